@@ -1,0 +1,140 @@
+/*
+ * pkv.h -- C ABI of the MI355X (gfx950) KV-cache data path.
+ *
+ * The reference (rouviere-german/paged-kv-serving) is pure Python + NumPy and has no FFI of its
+ * own. Each entry point below replaces one NumPy operation of the reference's data path; the
+ * comment above each names the reference code it replaces (paths are relative to the reference
+ * repository root).
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers (HIP global memory) unless stated otherwise. The caller owns
+ *     every buffer, including the attention workspace; the library never allocates.
+ *   - `device` is the HIP device ordinal the pointers live on. The library makes it current for
+ *     the duration of the call and restores the caller's device afterwards, so calls may come
+ *     from any host thread (the library keeps no per-thread state).
+ *   - `stream` is a hipStream_t passed as void*; NULL means the default stream. All work is
+ *     enqueued on it, asynchronously; nothing synchronises the host.
+ *   - Return value: PKV_OK (0) on success, a negative PKV_E* code otherwise. pkv_error_string()
+ *     maps a code to a constant message. Argument errors are detected before anything is
+ *     enqueued.
+ *   - Pools are laid out [num_layers, num_blocks, block_size, num_heads, head_dim], row-major,
+ *     exactly the shape of the reference's pools (src/paged_kv_serving/engine/runner.py:112-114).
+ *     A "slot" is block_id * block_size + offset (runner.py:158), so token row `slot` of layer l
+ *     starts at element ((l * num_blocks * block_size) + slot) * num_heads * head_dim.
+ */
+#ifndef PKV_H_
+#define PKV_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element type of a pool or of an input buffer. */
+typedef enum pkv_dtype {
+  PKV_F32 = 0,  /* IEEE binary32 */
+  PKV_BF16 = 1, /* bfloat16; written from float32 with round-to-nearest-even */
+} pkv_dtype;
+
+#define PKV_OK 0
+#define PKV_EINVAL (-1)       /* a size, stride, pointer or enum argument is out of range */
+#define PKV_EUNSUPPORTED (-2) /* a valid but unimplemented shape (e.g. head_dim 96) */
+#define PKV_EHIP (-3)         /* the HIP runtime reported an error while enqueueing */
+
+/* Version string of the library ("pkv <major>.<minor>"). Host-only, never fails. */
+const char* pkv_version(void);
+
+/* Constant, NUL-terminated description of a PKV_* return code. Host-only. */
+const char* pkv_error_string(int code);
+
+/*
+ * Slot-mapped append of one layer's new keys and values into the pools.
+ *
+ * Replaces src/paged_kv_serving/engine/runner.py:195-196:
+ *     key_pool.reshape(-1, H, D)[slots] = keys ; value_pool.reshape(-1, H, D)[slots] = values
+ *
+ *   key_pool, value_pool : the layer's pools, [num_slots, num_heads, head_dim] of pool_dtype
+ *                          (num_slots = num_blocks * block_size).
+ *   new_keys, new_values : [num_tokens, num_heads, head_dim] of src_dtype; token t starts at
+ *                          element t * src_token_stride (the H*D row itself is contiguous), so
+ *                          a view into a fused QKV output needs no copy.
+ *   slot_mapping         : int64 [num_tokens]. A slot outside [0, num_slots) is skipped (the
+ *                          host validates slots first; this only keeps a bad slot in bounds).
+ * A float32 source into a bfloat16 pool is rounded to nearest even; equal types copy bits.
+ * Duplicate slots in one call leave an unspecified one of the duplicate rows (the reference's
+ * fancy-index assignment keeps the last; the engine never produces duplicates).
+ */
+int pkv_append(void* key_pool, void* value_pool, pkv_dtype pool_dtype, int64_t num_slots,
+               const void* new_keys, const void* new_values, pkv_dtype src_dtype,
+               int64_t src_token_stride, const int64_t* slot_mapping, int64_t num_tokens,
+               int32_t num_heads, int32_t head_dim, int device, void* stream);
+
+/*
+ * Copy-on-write block copies, batched: for every pair (src, dst), block src is copied over block
+ * dst in every layer, for keys and values.
+ *
+ * Replaces src/paged_kv_serving/engine/runner.py:128-133 (ModelRunner.copy_block), called once
+ * per pair by BlockManager.prepare_for_write (src/paged_kv_serving/engine/blocks.py:162-164).
+ *
+ *   key_pool, value_pool : whole pools, [num_layers, num_blocks, block_elems] of dtype.
+ *   pairs                : int64 [num_pairs, 2] = (src, dst), device memory.
+ * All pairs of one call run concurrently, so no dst may appear twice and no dst may be the src
+ * of another pair in the same call (the Python host splits dependent sequences into several
+ * calls). Pairs with an id outside [0, num_blocks) or with src == dst are skipped.
+ */
+int pkv_copy_blocks(void* key_pool, void* value_pool, pkv_dtype dtype, const int64_t* pairs,
+                    int64_t num_pairs, int32_t num_layers, int64_t num_blocks, int64_t block_elems,
+                    int device, void* stream);
+
+/*
+ * Bytes of float32 workspace pkv_paged_attention needs for a batch (0 when no query can span
+ * more than one partition). Host-only.
+ */
+int64_t pkv_attention_workspace_bytes(int64_t num_queries, int32_t num_heads, int32_t head_dim,
+                                      int32_t max_context_len, int32_t partition_size);
+
+/*
+ * Paged causal attention of a ragged batch over one layer's pools: every query row attends to
+ * the keys at positions [0, min(context_len, position + 1)) of its sequence, read through the
+ * sequence's block table.
+ *
+ * Replaces src/paged_kv_serving/engine/attention.py:42-121 (paged_attention) together with the
+ * per-sequence loop of src/paged_kv_serving/engine/runner.py:198-212: one call covers every
+ * sequence of the batch, decode rows and prefill-chunk rows alike.
+ *
+ *   out              : float32 [num_queries, num_heads, head_dim], contiguous.
+ *   queries          : float32; query t starts at element t * query_token_stride, and its
+ *                      [num_heads, head_dim] block is contiguous.
+ *   query_positions  : int32 [num_queries], absolute position of each query (the causal mask:
+ *                      key position > query position is masked, attention.py:102-104).
+ *   query_seq        : int32 [num_queries], index of the sequence each query belongs to.
+ *   key_cache,
+ *   value_cache      : the layer's pools, [num_blocks, block_size, num_heads, head_dim], kv_dtype.
+ *   block_tables     : int32 [num_seqs, block_table_stride], physical block ids in logical order.
+ *   context_lens     : int32 [num_seqs], valid cached tokens of each sequence (runner.py:66-68).
+ *   max_context_len  : an upper bound of every context_len (sizes the grid).
+ *   partition_size   : keys per split-context partition, a positive multiple of 16, <= 1024;
+ *                      0 selects the library default.
+ *   workspace        : float32 scratch of pkv_attention_workspace_bytes(...) bytes (may be
+ *                      NULL when that is 0).
+ * A query whose every key is masked gets a zero output (attention.py:120-121).
+ * Block ids are read only for positions below the query's visible length, so table entries
+ * past a sequence's last used block may hold anything. Supported head_dim: 8, 16, 32, 64, 128,
+ * 256; any block_size >= 1; kv_dtype F32 or BF16 (accumulation is float32 either way).
+ */
+int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,
+                        const int32_t* query_positions, const int32_t* query_seq,
+                        int64_t num_queries, const void* key_cache, const void* value_cache,
+                        pkv_dtype kv_dtype, int64_t num_blocks, int32_t block_size,
+                        const int32_t* block_tables, int32_t block_table_stride,
+                        const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,
+                        int32_t head_dim, float scale, int32_t max_context_len,
+                        int32_t partition_size, float* workspace, int64_t workspace_bytes,
+                        int device, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PKV_H_ */

@@ -1,0 +1,178 @@
+"""Build and load the gfx950 C-ABI library ``libpkv.so`` (declared in ``include/pkv.h``).
+
+The library is compiled in-tree with ``hipcc --offload-arch=gfx950`` and loaded with ``ctypes``.
+There is no fallback: if the library is missing or fails to load, every operation of the data
+path raises :class:`NativeLibraryError`. Nothing here imports torch, so the loader can be
+exercised on a machine without a GPU (symbols resolve; no kernel is launched).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import shutil
+import subprocess
+import tempfile
+import threading
+from pathlib import Path
+
+__all__ = [
+    "HIPCC_FLAGS",
+    "LIB_PATH",
+    "SOURCES",
+    "EXPORTED_SYMBOLS",
+    "NativeLibraryError",
+    "PKV_BF16",
+    "PKV_F32",
+    "build",
+    "check",
+    "library",
+]
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+REPO_ROOT = PACKAGE_DIR.parent
+CSRC = PACKAGE_DIR / "csrc"
+INCLUDE = REPO_ROOT / "include"
+LIB_PATH = PACKAGE_DIR / "libpkv.so"
+SOURCES = (CSRC / "pkv_copy.hip", CSRC / "pkv_attention.hip")
+
+# gfx950 only. Packed-FP32 VALU instructions are disabled: the code relies on scalar fp32 FMA.
+HIPCC_FLAGS = (
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+)
+
+# pkv_dtype values (include/pkv.h).
+PKV_F32 = 0
+PKV_BF16 = 1
+
+PKV_OK = 0
+
+EXPORTED_SYMBOLS = (
+    "pkv_version",
+    "pkv_error_string",
+    "pkv_append",
+    "pkv_copy_blocks",
+    "pkv_attention_workspace_bytes",
+    "pkv_paged_attention",
+)
+
+
+class NativeLibraryError(RuntimeError):
+    """The HIP library is missing, failed to load, or returned an error code."""
+
+
+def _hipcc() -> str:
+    found = shutil.which("hipcc")
+    if found:
+        return found
+    candidate = Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "bin" / "hipcc"
+    if candidate.exists():
+        return str(candidate)
+    raise NativeLibraryError("hipcc not found: the gfx950 library cannot be built")
+
+
+def build(*, verbose: bool = False) -> Path:
+    """Compile every HIP source into ``libpkv.so`` next to this file. Always recompiles.
+
+    The output is written to a temporary file and renamed into place, so a concurrent loader
+    never sees a half-written library.
+    """
+    command = [_hipcc(), *HIPCC_FLAGS, "-I", str(INCLUDE)]
+    with tempfile.NamedTemporaryFile(
+        dir=PACKAGE_DIR, prefix=".libpkv.", suffix=".so.tmp", delete=False
+    ) as handle:
+        tmp = Path(handle.name)
+    try:
+        command += ["-o", str(tmp), *(str(source) for source in SOURCES)]
+        result = subprocess.run(command, capture_output=True, text=True, check=False)
+        if verbose or result.returncode != 0:
+            noise = "packed-fp32-ops"  # the host pass does not know this device feature
+            lines = [line for line in result.stderr.splitlines() if noise not in line]
+            if lines:
+                print("\n".join(lines))
+        if result.returncode != 0:
+            raise NativeLibraryError(f"hipcc failed with exit code {result.returncode}")
+        os.replace(tmp, LIB_PATH)
+    finally:
+        if tmp.exists():
+            tmp.unlink()
+    global _LIB
+    with _LOCK:
+        _LIB = None  # reload on next use
+    return LIB_PATH
+
+
+_LOCK = threading.Lock()
+_LIB: ctypes.CDLL | None = None
+
+_c_int = ctypes.c_int
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_ptr = ctypes.c_void_p
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.pkv_version.argtypes = []
+    lib.pkv_version.restype = ctypes.c_char_p
+    lib.pkv_error_string.argtypes = [_c_int]
+    lib.pkv_error_string.restype = ctypes.c_char_p
+    lib.pkv_append.argtypes = [
+        _ptr, _ptr, _c_int, _i64,  # key_pool, value_pool, pool_dtype, num_slots
+        _ptr, _ptr, _c_int, _i64,  # new_keys, new_values, src_dtype, src_token_stride
+        _ptr, _i64, _i32, _i32,  # slot_mapping, num_tokens, num_heads, head_dim
+        _c_int, _ptr,  # device, stream
+    ]
+    lib.pkv_append.restype = _c_int
+    lib.pkv_copy_blocks.argtypes = [
+        _ptr, _ptr, _c_int, _ptr, _i64,  # key_pool, value_pool, dtype, pairs, num_pairs
+        _i32, _i64, _i64,  # num_layers, num_blocks, block_elems
+        _c_int, _ptr,  # device, stream
+    ]
+    lib.pkv_copy_blocks.restype = _c_int
+    lib.pkv_attention_workspace_bytes.argtypes = [_i64, _i32, _i32, _i32, _i32]
+    lib.pkv_attention_workspace_bytes.restype = _i64
+    lib.pkv_paged_attention.argtypes = [
+        _ptr, _ptr, _i64,  # out, queries, query_token_stride
+        _ptr, _ptr, _i64,  # query_positions, query_seq, num_queries
+        _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size
+        _ptr, _i32, _ptr, _i32,  # block_tables, block_table_stride, context_lens, num_seqs
+        _i32, _i32, ctypes.c_float,  # num_heads, head_dim, scale
+        _i32, _i32,  # max_context_len, partition_size
+        _ptr, _i64,  # workspace, workspace_bytes
+        _c_int, _ptr,  # device, stream
+    ]
+    lib.pkv_paged_attention.restype = _c_int
+
+
+def library() -> ctypes.CDLL:
+    """The loaded library. Raises :class:`NativeLibraryError` if it has not been built."""
+    global _LIB
+    with _LOCK:
+        if _LIB is None:
+            if not LIB_PATH.exists():
+                raise NativeLibraryError(
+                    f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                    "(hipcc --offload-arch=gfx950)"
+                )
+            try:
+                lib = ctypes.CDLL(str(LIB_PATH))
+            except OSError as error:
+                raise NativeLibraryError(f"cannot load {LIB_PATH}: {error}") from error
+            _declare(lib)
+            _LIB = lib
+        return _LIB
+
+
+def check(code: int, what: str) -> None:
+    """Raise :class:`NativeLibraryError` for a non-zero PKV_* return code."""
+    if code != PKV_OK:
+        message = library().pkv_error_string(code).decode()
+        raise NativeLibraryError(f"{what} failed: {message} (code {code})")

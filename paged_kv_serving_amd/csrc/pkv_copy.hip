@@ -1,0 +1,232 @@
+// Byte-moving kernels of the KV data path: the slot-mapped append and the batched copy-on-write
+// block copy. Both are pure HBM streams: every thread moves one 16-byte vector per step, and the
+// grid is laid out so that one workgroup covers a contiguous 4 KiB (append) or 16 KiB (copy)
+// stretch of a token row or a block.
+#include "pkv_common.h"
+
+namespace pkv {
+namespace {
+
+constexpr int kCopyThreads = 256;
+
+// --------------------------------------------------------------------------------------------
+// Append. grid = (tokens * chunks of a token row, 2); y selects keys (0) or values (1).
+// Each thread converts/copies VEC consecutive elements of one token's [heads * head_dim] row.
+// --------------------------------------------------------------------------------------------
+template <typename SrcT, typename DstT>
+struct Mover;
+
+// float32 -> float32, 4 elements (16 bytes).
+template <>
+struct Mover<float, float> {
+  static constexpr int kVec = 4;
+  __device__ static void move(float* dst, const float* src) {
+    *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
+  }
+};
+
+// bfloat16 -> bfloat16, 8 elements (16 bytes); bits are copied unchanged.
+template <>
+struct Mover<uint16_t, uint16_t> {
+  static constexpr int kVec = 8;
+  __device__ static void move(uint16_t* dst, const uint16_t* src) {
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+  }
+};
+
+// float32 -> bfloat16, 8 elements (32 bytes in, 16 bytes out), round to nearest even.
+template <>
+struct Mover<float, uint16_t> {
+  static constexpr int kVec = 8;
+  __device__ static void move(uint16_t* dst, const float* src) {
+    const float4 a = reinterpret_cast<const float4*>(src)[0];
+    const float4 b = reinterpret_cast<const float4*>(src)[1];
+    uint4 o;
+    o.x = f32_to_bf16_bits(a.x) | (f32_to_bf16_bits(a.y) << 16);
+    o.y = f32_to_bf16_bits(a.z) | (f32_to_bf16_bits(a.w) << 16);
+    o.z = f32_to_bf16_bits(b.x) | (f32_to_bf16_bits(b.y) << 16);
+    o.w = f32_to_bf16_bits(b.z) | (f32_to_bf16_bits(b.w) << 16);
+    *reinterpret_cast<uint4*>(dst) = o;
+  }
+};
+
+__device__ __forceinline__ void move_one(float* d, const float* s) { *d = *s; }
+__device__ __forceinline__ void move_one(uint16_t* d, const uint16_t* s) { *d = *s; }
+__device__ __forceinline__ void move_one(uint16_t* d, const float* s) {
+  *d = static_cast<uint16_t>(f32_to_bf16_bits(*s));
+}
+
+template <typename SrcT, typename DstT, bool kVectorized>
+__global__ __launch_bounds__(kCopyThreads) void append_kernel(
+    DstT* __restrict__ key_pool, DstT* __restrict__ value_pool, int64_t num_slots,
+    const SrcT* __restrict__ new_keys, const SrcT* __restrict__ new_values, int64_t src_stride,
+    const int64_t* __restrict__ slots, int64_t row_elems, int64_t chunks) {
+  const int64_t token = blockIdx.x / chunks;
+  const int64_t chunk = blockIdx.x - token * chunks;
+  const int64_t slot = slots[token];
+  if (slot < 0 || slot >= num_slots) return;
+  const bool is_value = blockIdx.y != 0;
+  const SrcT* src = (is_value ? new_values : new_keys) + token * src_stride;
+  DstT* dst = (is_value ? value_pool : key_pool) + slot * row_elems;
+  constexpr int kVec = kVectorized ? Mover<SrcT, DstT>::kVec : 1;
+  const int64_t e = (chunk * kCopyThreads + threadIdx.x) * kVec;
+  if (e >= row_elems) return;
+  if constexpr (kVectorized) {
+    Mover<SrcT, DstT>::move(dst + e, src + e);
+  } else {
+    move_one(dst + e, src + e);
+  }
+}
+
+template <typename SrcT, typename DstT>
+int launch_append(void* key_pool, void* value_pool, int64_t num_slots, const void* new_keys,
+                  const void* new_values, int64_t src_stride, const int64_t* slots,
+                  int64_t num_tokens, int64_t row_elems, hipStream_t stream) {
+  constexpr int kVec = Mover<SrcT, DstT>::kVec;
+  const bool vectorized = row_elems % kVec == 0 && src_stride % kVec == 0 &&
+                          aligned16(key_pool) && aligned16(value_pool) && aligned16(new_keys) &&
+                          aligned16(new_values);
+  const int64_t per_block = static_cast<int64_t>(kCopyThreads) * (vectorized ? kVec : 1);
+  const int64_t chunks = (row_elems + per_block - 1) / per_block;
+  if (chunks * num_tokens > 0x7fffffff) return PKV_EUNSUPPORTED;
+  const dim3 grid(static_cast<uint32_t>(chunks * num_tokens), 2);
+  auto* kp = static_cast<DstT*>(key_pool);
+  auto* vp = static_cast<DstT*>(value_pool);
+  const auto* kn = static_cast<const SrcT*>(new_keys);
+  const auto* vn = static_cast<const SrcT*>(new_values);
+  if (vectorized) {
+    hipLaunchKernelGGL((append_kernel<SrcT, DstT, true>), grid, dim3(kCopyThreads), 0, stream, kp,
+                       vp, num_slots, kn, vn, src_stride, slots, row_elems, chunks);
+  } else {
+    hipLaunchKernelGGL((append_kernel<SrcT, DstT, false>), grid, dim3(kCopyThreads), 0, stream, kp,
+                       vp, num_slots, kn, vn, src_stride, slots, row_elems, chunks);
+  }
+  return check_launch();
+}
+
+// --------------------------------------------------------------------------------------------
+// Copy-on-write. grid = (pairs * chunks of one block, layers * 2); y = layer * 2 + (0 keys,
+// 1 values). Unit is the widest of 16/4/1 bytes that divides the block; each thread moves
+// kUnroll units, issuing every load before the first store.
+// --------------------------------------------------------------------------------------------
+template <typename UnitT, int kUnroll>
+__global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
+    char* __restrict__ key_pool, char* __restrict__ value_pool, const int64_t* __restrict__ pairs,
+    int64_t num_blocks, int64_t block_units, int64_t chunks) {
+  const int64_t pair = blockIdx.x / chunks;
+  const int64_t chunk = blockIdx.x - pair * chunks;
+  const int64_t src = pairs[2 * pair];
+  const int64_t dst = pairs[2 * pair + 1];
+  if (src == dst || src < 0 || dst < 0 || src >= num_blocks || dst >= num_blocks) return;
+  const int64_t layer = blockIdx.y >> 1;
+  char* pool = (blockIdx.y & 1) ? value_pool : key_pool;
+  UnitT* base = reinterpret_cast<UnitT*>(pool) + layer * num_blocks * block_units;
+  const UnitT* from = base + src * block_units;
+  UnitT* to = base + dst * block_units;
+  const int64_t first = chunk * (kCopyThreads * kUnroll) + threadIdx.x;
+  UnitT buf[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = first + static_cast<int64_t>(u) * kCopyThreads;
+    if (i < block_units) buf[u] = from[i];
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = first + static_cast<int64_t>(u) * kCopyThreads;
+    if (i < block_units) to[i] = buf[u];
+  }
+}
+
+template <typename UnitT>
+int launch_copy(void* key_pool, void* value_pool, const int64_t* pairs, int64_t num_pairs,
+                int32_t num_layers, int64_t num_blocks, int64_t block_bytes, hipStream_t stream) {
+  constexpr int kUnroll = 4;
+  const int64_t units = block_bytes / static_cast<int64_t>(sizeof(UnitT));
+  const int64_t per_group = static_cast<int64_t>(kCopyThreads) * kUnroll;
+  const int64_t chunks = (units + per_group - 1) / per_group;
+  if (chunks * num_pairs > 0x7fffffff || 2 * static_cast<int64_t>(num_layers) > 65535) {
+    return PKV_EUNSUPPORTED;
+  }
+  const dim3 grid(static_cast<uint32_t>(chunks * num_pairs), static_cast<uint32_t>(2 * num_layers));
+  hipLaunchKernelGGL((copy_blocks_kernel<UnitT, kUnroll>), grid, dim3(kCopyThreads), 0, stream,
+                     static_cast<char*>(key_pool), static_cast<char*>(value_pool), pairs,
+                     num_blocks, units, chunks);
+  return check_launch();
+}
+
+}  // namespace
+}  // namespace pkv
+
+extern "C" const char* pkv_version(void) { return "pkv 0.1"; }
+
+extern "C" const char* pkv_error_string(int code) {
+  switch (code) {
+    case PKV_OK:
+      return "ok";
+    case PKV_EINVAL:
+      return "invalid argument";
+    case PKV_EUNSUPPORTED:
+      return "unsupported shape or dtype";
+    case PKV_EHIP:
+      return "HIP runtime error while enqueueing";
+    default:
+      return "unknown error code";
+  }
+}
+
+extern "C" int pkv_append(void* key_pool, void* value_pool, pkv_dtype pool_dtype,
+                          int64_t num_slots, const void* new_keys, const void* new_values,
+                          pkv_dtype src_dtype, int64_t src_token_stride,
+                          const int64_t* slot_mapping, int64_t num_tokens, int32_t num_heads,
+                          int32_t head_dim, int device, void* stream) {
+  using namespace pkv;
+  if (num_tokens < 0 || num_heads < 1 || head_dim < 1 || num_slots < 1) return PKV_EINVAL;
+  if (dtype_size(pool_dtype) == 0 || dtype_size(src_dtype) == 0) return PKV_EINVAL;
+  if (src_dtype == PKV_BF16 && pool_dtype == PKV_F32) return PKV_EUNSUPPORTED;
+  const int64_t row = static_cast<int64_t>(num_heads) * head_dim;
+  if (src_token_stride < row) return PKV_EINVAL;
+  if (num_tokens == 0) return PKV_OK;
+  if (!key_pool || !value_pool || !new_keys || !new_values || !slot_mapping) return PKV_EINVAL;
+  DeviceGuard guard(device);
+  if (!guard.ok()) return PKV_EHIP;
+  (void)hipGetLastError();
+  auto s = static_cast<hipStream_t>(stream);
+  if (pool_dtype == PKV_F32) {
+    return launch_append<float, float>(key_pool, value_pool, num_slots, new_keys, new_values,
+                                       src_token_stride, slot_mapping, num_tokens, row, s);
+  }
+  if (src_dtype == PKV_F32) {
+    return launch_append<float, uint16_t>(key_pool, value_pool, num_slots, new_keys, new_values,
+                                          src_token_stride, slot_mapping, num_tokens, row, s);
+  }
+  return launch_append<uint16_t, uint16_t>(key_pool, value_pool, num_slots, new_keys, new_values,
+                                           src_token_stride, slot_mapping, num_tokens, row, s);
+}
+
+extern "C" int pkv_copy_blocks(void* key_pool, void* value_pool, pkv_dtype dtype,
+                               const int64_t* pairs, int64_t num_pairs, int32_t num_layers,
+                               int64_t num_blocks, int64_t block_elems, int device,
+                               void* stream) {
+  using namespace pkv;
+  if (num_pairs < 0 || num_layers < 1 || num_blocks < 1 || block_elems < 1) return PKV_EINVAL;
+  if (dtype_size(dtype) == 0) return PKV_EINVAL;
+  if (num_pairs == 0) return PKV_OK;
+  if (!key_pool || !value_pool || !pairs) return PKV_EINVAL;
+  DeviceGuard guard(device);
+  if (!guard.ok()) return PKV_EHIP;
+  (void)hipGetLastError();
+  auto s = static_cast<hipStream_t>(stream);
+  const int64_t bytes = block_elems * dtype_size(dtype);
+  const bool base_aligned = aligned16(key_pool) && aligned16(value_pool);
+  if (bytes % 16 == 0 && base_aligned) {
+    return launch_copy<uint4>(key_pool, value_pool, pairs, num_pairs, num_layers, num_blocks,
+                              bytes, s);
+  }
+  if (bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(key_pool) & 3u) == 0 &&
+      (reinterpret_cast<uintptr_t>(value_pool) & 3u) == 0) {
+    return launch_copy<uint32_t>(key_pool, value_pool, pairs, num_pairs, num_layers, num_blocks,
+                                 bytes, s);
+  }
+  return launch_copy<uint8_t>(key_pool, value_pool, pairs, num_pairs, num_layers, num_blocks,
+                              bytes, s);
+}

@@ -1,0 +1,229 @@
+"""Tensor-level entry points of the data path: torch device tensors in, HIP kernels out.
+
+Each function checks shapes, dtypes, devices and layouts on the host, then calls the matching
+``pkv_*`` function of ``libpkv.so`` on the caller's current HIP stream (torch's current stream of
+the tensors' device). Nothing here computes on the CPU: a missing library raises
+:class:`~paged_kv_serving_amd._native.NativeLibraryError`.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from paged_kv_serving_amd import _native
+
+__all__ = [
+    "append_kv",
+    "attention_workspace_bytes",
+    "copy_blocks",
+    "kv_dtype_code",
+    "paged_attention_ragged",
+]
+
+_DTYPE_CODES = {torch.float32: _native.PKV_F32, torch.bfloat16: _native.PKV_BF16}
+
+
+def kv_dtype_code(dtype: torch.dtype) -> int:
+    """``pkv_dtype`` of a torch dtype (float32 or bfloat16)."""
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported KV dtype {dtype}; use float32 or bfloat16") from None
+
+
+def _device_index(*tensors: torch.Tensor) -> int:
+    device = tensors[0].device
+    if device.type != "cuda":
+        raise ValueError("the KV data path runs on a HIP device; got a tensor on " + str(device))
+    for tensor in tensors[1:]:
+        if tensor.device != device:
+            raise ValueError("all tensors must be on the same device")
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def _stream(device: int) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _rows_contiguous(tensor: torch.Tensor, name: str) -> int:
+    """Token stride (elements) of a [T, H, D] tensor whose [H, D] block is contiguous."""
+    if tensor.dim() != 3:
+        raise ValueError(f"{name} must have shape (tokens, heads, head_dim)")
+    _, heads, dim = tensor.shape
+    if tensor.stride(2) != 1 or (heads > 1 and tensor.stride(1) != dim):
+        raise ValueError(f"{name}: each token's (heads, head_dim) block must be contiguous")
+    return tensor.stride(0) if tensor.shape[0] > 1 else heads * dim
+
+
+def append_kv(
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """Write ``keys[t]`` / ``values[t]`` to token row ``slot_mapping[t]`` of one layer's pools.
+
+    ``key_pool``/``value_pool``: contiguous ``[num_blocks, block_size, heads, head_dim]`` (or any
+    contiguous shape whose trailing dims are ``heads, head_dim``), float32 or bfloat16.
+    ``keys``/``values``: ``[T, heads, head_dim]`` float32 (or bfloat16 for a bfloat16 pool),
+    token-strided views allowed. ``slot_mapping``: int64 ``[T]`` on the same device.
+    Mirrors ``key_pool.reshape(-1, H, D)[slots] = keys`` (reference runner.py:195-196).
+    """
+    device = _device_index(key_pool, value_pool, keys, values, slot_mapping)
+    if key_pool.shape != value_pool.shape or key_pool.dtype != value_pool.dtype:
+        raise ValueError("key and value pools must have the same shape and dtype")
+    if not (key_pool.is_contiguous() and value_pool.is_contiguous()):
+        raise ValueError("pools must be contiguous")
+    if keys.shape != values.shape or keys.dtype != values.dtype:
+        raise ValueError("keys and values must have the same shape and dtype")
+    heads, dim = keys.shape[1], keys.shape[2]
+    if tuple(key_pool.shape[-2:]) != (heads, dim):
+        raise ValueError("pool rows and keys disagree on (heads, head_dim)")
+    stride = _rows_contiguous(keys, "keys")
+    if _rows_contiguous(values, "values") != stride:
+        raise ValueError("keys and values must share one token stride")
+    if slot_mapping.dtype != torch.int64 or slot_mapping.shape != (keys.shape[0],):
+        raise ValueError("slot_mapping must be int64 with one slot per token")
+    pool_code = kv_dtype_code(key_pool.dtype)
+    src_code = kv_dtype_code(keys.dtype)
+    num_slots = key_pool.numel() // (heads * dim)
+    rc = _native.library().pkv_append(
+        key_pool.data_ptr(), value_pool.data_ptr(), pool_code, num_slots,
+        keys.data_ptr(), values.data_ptr(), src_code, stride,
+        slot_mapping.data_ptr(), keys.shape[0], heads, dim,
+        device, _stream(device),
+    )  # fmt: skip
+    _native.check(rc, "pkv_append")
+
+
+def copy_blocks(key_pool: torch.Tensor, value_pool: torch.Tensor, pairs: torch.Tensor) -> None:
+    """Copy block ``src`` over block ``dst`` in every layer for each row ``(src, dst)`` of pairs.
+
+    ``key_pool``/``value_pool``: contiguous ``[layers, num_blocks, ...]``. ``pairs``: int64
+    ``[n, 2]`` on the device. The pairs must be independent (no repeated dst, no dst that is also
+    a src); :func:`independent_groups` splits an ordered list into such groups.
+    Mirrors ``K[:, dst] = K[:, src]; V[:, dst] = V[:, src]`` (reference runner.py:132-133).
+    """
+    device = _device_index(key_pool, value_pool, pairs)
+    if key_pool.shape != value_pool.shape or key_pool.dtype != value_pool.dtype:
+        raise ValueError("key and value pools must have the same shape and dtype")
+    if not (key_pool.is_contiguous() and value_pool.is_contiguous()):
+        raise ValueError("pools must be contiguous")
+    if pairs.dtype != torch.int64 or pairs.dim() != 2 or pairs.shape[1] != 2:
+        raise ValueError("pairs must be int64 of shape (n, 2)")
+    pairs = pairs.contiguous()
+    layers, num_blocks = key_pool.shape[0], key_pool.shape[1]
+    block_elems = key_pool[0, 0].numel()
+    rc = _native.library().pkv_copy_blocks(
+        key_pool.data_ptr(), value_pool.data_ptr(), kv_dtype_code(key_pool.dtype),
+        pairs.data_ptr(), pairs.shape[0], layers, num_blocks, block_elems,
+        device, _stream(device),
+    )  # fmt: skip
+    _native.check(rc, "pkv_copy_blocks")
+
+
+def independent_groups(pairs: list[tuple[int, int]]) -> list[list[tuple[int, int]]]:
+    """Split an ordered list of block copies into groups that may each run concurrently.
+
+    Applying the groups one after another gives the same pool as applying the copies one at a
+    time in list order: a copy starts a new group when it reads a block an earlier copy of the
+    group writes, or writes a block an earlier copy of the group reads or writes.
+    """
+    groups: list[list[tuple[int, int]]] = []
+    reads: set[int] = set()
+    writes: set[int] = set()
+    for src, dst in pairs:
+        if not groups or src in writes or dst in reads or dst in writes:
+            groups.append([])
+            reads, writes = set(), set()
+        groups[-1].append((src, dst))
+        reads.add(src)
+        writes.add(dst)
+    return groups
+
+
+def attention_workspace_bytes(
+    num_queries: int, num_heads: int, head_dim: int, max_context_len: int, partition_size: int = 0
+) -> int:
+    """Bytes of float32 split-context workspace :func:`paged_attention_ragged` needs."""
+    size = _native.library().pkv_attention_workspace_bytes(
+        num_queries, num_heads, head_dim, max_context_len, partition_size
+    )
+    if size < 0:
+        raise ValueError("invalid attention workspace query")
+    return int(size)
+
+
+def paged_attention_ragged(
+    queries: torch.Tensor,
+    query_positions: torch.Tensor,
+    query_seq: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    *,
+    max_context_len: int,
+    partition_size: int = 0,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Causal paged attention of every query row of a ragged batch, in one call.
+
+    ``queries``: float32 ``[T, H, D]`` (token-strided views allowed); ``query_positions`` and
+    ``query_seq``: int32 ``[T]``; ``key_cache``/``value_cache``: one layer's pools
+    ``[num_blocks, block_size, H, D]``; ``block_tables``: int32 ``[S, max_blocks]``;
+    ``context_lens``: int32 ``[S]``; ``max_context_len`` bounds every context length.
+    Returns float32 ``[T, H, D]``. Semantics of reference attention.py:42-121 for each query.
+    """
+    device = _device_index(
+        queries, query_positions, query_seq, key_cache, value_cache, block_tables, context_lens
+    )
+    if queries.dtype != torch.float32:
+        raise ValueError("queries must be float32")
+    stride = _rows_contiguous(queries, "queries")
+    num_queries, heads, dim = queries.shape
+    if key_cache.shape != value_cache.shape or key_cache.dtype != value_cache.dtype:
+        raise ValueError("key and value caches must have the same shape")
+    if key_cache.dim() != 4 or tuple(key_cache.shape[2:]) != (heads, dim):
+        raise ValueError("caches must have shape (num_blocks, block_size, heads, head_dim)")
+    if not (key_cache.is_contiguous() and value_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    for name, tensor in (("query_positions", query_positions), ("query_seq", query_seq)):
+        if tensor.dtype != torch.int32 or tensor.shape != (num_queries,):
+            raise ValueError(f"{name} must be int32 with one entry per query")
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2:
+        raise ValueError("block_tables must be int32 of shape (num_seqs, max_blocks)")
+    if not block_tables.is_contiguous():
+        raise ValueError("block_tables must be contiguous")
+    num_seqs = block_tables.shape[0]
+    if context_lens.dtype != torch.int32 or context_lens.shape != (num_seqs,):
+        raise ValueError("context_lens must be int32 with one entry per sequence")
+    if block_tables.shape[1] * key_cache.shape[1] < max_context_len:
+        raise ValueError("block_tables are too narrow for max_context_len")
+    if out is None:
+        out = torch.empty((num_queries, heads, dim), dtype=torch.float32, device=queries.device)
+    elif out.shape != (num_queries, heads, dim) or out.dtype != torch.float32:
+        raise ValueError("out must be float32 of shape (num_queries, heads, head_dim)")
+    elif not out.is_contiguous():
+        raise ValueError("out must be contiguous")
+    if num_queries == 0:
+        return out
+    need = attention_workspace_bytes(num_queries, heads, dim, max_context_len, partition_size)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need // 4, dtype=torch.float32, device=queries.device)
+    ws_ptr = workspace.data_ptr() if need else None
+    ws_bytes = workspace.numel() * workspace.element_size() if need else 0
+    rc = _native.library().pkv_paged_attention(
+        out.data_ptr(), queries.data_ptr(), stride,
+        query_positions.data_ptr(), query_seq.data_ptr(), num_queries,
+        key_cache.data_ptr(), value_cache.data_ptr(), kv_dtype_code(key_cache.dtype),
+        key_cache.shape[0], key_cache.shape[1],
+        block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(), num_seqs,
+        heads, dim, float(scale), max_context_len, partition_size,
+        ws_ptr, ws_bytes, device, _stream(device),
+    )  # fmt: skip
+    _native.check(rc, "pkv_paged_attention")
+    return out

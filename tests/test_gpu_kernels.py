@@ -1,0 +1,337 @@
+"""GPU parity of the three kernels against the CPU oracle, through the C ABI.
+
+Integer and byte work is bit-exact: the append (float32 and bfloat16 pools, strided sources),
+the copy-on-write block copy, and the bfloat16 rounding of the append. Attention is compared
+with the oracle's paged attention (reference attention.py:42-121) and with the float64 closed
+form; the tolerance is the north star's 1e-5 max abs for float32 KV, and for bfloat16 KV the
+same 1e-5 against the oracle run on the bf16-rounded keys and values (both sides then see
+identical inputs and differ only by float32 accumulation order).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import dense_attention, gather_context, paged_attention
+from oracle.bf16 import bf16_bits, bf16_round
+from paged_kv_serving_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+
+
+def say(*parts) -> None:
+    print(*parts, flush=True)
+
+
+# --- append ------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    ("blocks", "block", "heads", "dim", "tokens"),
+    [(7, 4, 2, 8, 11), (64, 16, 4, 32, 100), (300, 16, 32, 128, 64), (5, 3, 3, 6, 9)],
+)
+def test_append_float32_is_bit_exact(device, blocks, block, heads, dim, tokens) -> None:
+    say("append f32", blocks, block, heads, dim, tokens)
+    rng = np.random.default_rng(blocks + tokens)
+    pool_k = rng.standard_normal((blocks, block, heads, dim)).astype(np.float32)
+    pool_v = rng.standard_normal((blocks, block, heads, dim)).astype(np.float32)
+    slots = rng.permutation(blocks * block)[:tokens].astype(np.int64)
+    keys = rng.standard_normal((tokens, heads, dim)).astype(np.float32)
+    values = rng.standard_normal((tokens, heads, dim)).astype(np.float32)
+    dk, dv = torch.from_numpy(pool_k).to(device), torch.from_numpy(pool_v).to(device)
+    ops.append_kv(dk, dv, torch.from_numpy(keys).to(device), torch.from_numpy(values).to(device),
+                  torch.from_numpy(slots).to(device))  # fmt: skip
+    pool_k.reshape(-1, heads, dim)[slots] = keys
+    pool_v.reshape(-1, heads, dim)[slots] = values
+    assert np.array_equal(dk.cpu().numpy().view(np.uint32), pool_k.view(np.uint32))
+    assert np.array_equal(dv.cpu().numpy().view(np.uint32), pool_v.view(np.uint32))
+
+
+def test_append_from_a_fused_qkv_view(device) -> None:
+    """Keys and values as token-strided views of a (T, 3, H, D) projection, no copy."""
+    say("append strided")
+    rng = np.random.default_rng(5)
+    tokens, heads, dim, blocks, block = 13, 4, 16, 9, 8
+    fused = rng.standard_normal((tokens, 3, heads, dim)).astype(np.float32)
+    slots = rng.permutation(blocks * block)[:tokens].astype(np.int64)
+    dfused = torch.from_numpy(fused).to(device)
+    dk = torch.zeros((blocks, block, heads, dim), device=device)
+    dv = torch.zeros_like(dk)
+    ops.append_kv(dk, dv, dfused[:, 1], dfused[:, 2], torch.from_numpy(slots).to(device))
+    want_k = np.zeros((blocks * block, heads, dim), dtype=np.float32)
+    want_v = np.zeros_like(want_k)
+    want_k[slots] = fused[:, 1]
+    want_v[slots] = fused[:, 2]
+    assert np.array_equal(dk.cpu().numpy().reshape(-1, heads, dim), want_k)
+    assert np.array_equal(dv.cpu().numpy().reshape(-1, heads, dim), want_v)
+
+
+@pytest.mark.parametrize("dim", [8, 128, 6])
+def test_append_float32_into_bfloat16_rounds_to_nearest_even(device, dim) -> None:
+    say("append f32->bf16", dim)
+    rng = np.random.default_rng(dim)
+    tokens, heads, blocks, block = 21, 2, 6, 4
+    keys = (rng.standard_normal((tokens, heads, dim)) * 3).astype(np.float32)
+    values = (rng.standard_normal((tokens, heads, dim)) * 3).astype(np.float32)
+    keys[0, 0, :2] = [1.0 + 2.0**-8, 1.0 + 3 * 2.0**-8]  # ties: to even (down, up)
+    slots = rng.permutation(blocks * block)[:tokens].astype(np.int64)
+    dk = torch.zeros((blocks, block, heads, dim), dtype=torch.bfloat16, device=device)
+    dv = torch.zeros_like(dk)
+    ops.append_kv(dk, dv, torch.from_numpy(keys).to(device), torch.from_numpy(values).to(device),
+                  torch.from_numpy(slots).to(device))  # fmt: skip
+    got_k = dk.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1, heads, dim)
+    got_v = dv.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1, heads, dim)
+    assert np.array_equal(got_k[slots], bf16_bits(keys))
+    assert np.array_equal(got_v[slots], bf16_bits(values))
+    unused = np.setdiff1d(np.arange(blocks * block), slots)
+    assert not got_k[unused].any() and not got_v[unused].any()
+
+
+def test_append_bfloat16_into_bfloat16_copies_bits(device) -> None:
+    say("append bf16->bf16")
+    g = torch.Generator(device=device).manual_seed(3)
+    keys = torch.randn((10, 2, 64), generator=g, device=device).to(torch.bfloat16)
+    values = torch.randn((10, 2, 64), generator=g, device=device).to(torch.bfloat16)
+    slots = torch.tensor([3, 9, 0, 31, 17, 8, 22, 5, 14, 28], dtype=torch.int64, device=device)
+    dk = torch.zeros((8, 4, 2, 64), dtype=torch.bfloat16, device=device)
+    dv = torch.zeros_like(dk)
+    ops.append_kv(dk, dv, keys, values, slots)
+    assert torch.equal(dk.view(-1, 2, 64)[slots].view(torch.int16), keys.view(torch.int16))
+    assert torch.equal(dv.view(-1, 2, 64)[slots].view(torch.int16), values.view(torch.int16))
+
+
+def test_append_skips_slots_outside_the_pool(device) -> None:
+    say("append bad slots")
+    dk = torch.zeros((2, 4, 1, 8), device=device)
+    dv = torch.zeros_like(dk)
+    rows = torch.ones((3, 1, 8), device=device)
+    slots = torch.tensor([-1, 8, 5], dtype=torch.int64, device=device)
+    ops.append_kv(dk, dv, rows, rows, slots)
+    flat = dk.view(-1, 8).cpu().numpy()
+    assert flat[5].tolist() == [1.0] * 8
+    assert flat.sum() == 8.0
+
+
+# --- copy-on-write ----------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize(
+    ("layers", "blocks", "block", "heads", "dim", "dtype"),
+    [(2, 16, 4, 2, 8, torch.float32), (1, 600, 16, 32, 128, torch.float32),
+     (3, 40, 16, 4, 32, torch.bfloat16), (2, 9, 3, 1, 6, torch.float32)],
+)  # fmt: skip
+def test_copy_blocks_is_bit_exact(device, layers, blocks, block, heads, dim, dtype) -> None:
+    say("copy", layers, blocks, block, heads, dim, dtype)
+    g = torch.Generator(device=device).manual_seed(blocks)
+    keys = torch.randn((layers, blocks, block, heads, dim), generator=g, device=device).to(dtype)
+    values = torch.randn((layers, blocks, block, heads, dim), generator=g, device=device).to(dtype)
+    rng = np.random.default_rng(blocks)
+    ids = rng.permutation(blocks)
+    n = blocks // 3
+    pairs = np.stack([ids[:n], ids[n : 2 * n]], axis=1).astype(np.int64)
+    want_k, want_v = keys.clone(), values.clone()
+    for src, dst in pairs:
+        want_k[:, dst] = want_k[:, src]
+        want_v[:, dst] = want_v[:, src]
+    ops.copy_blocks(keys, values, torch.from_numpy(pairs).to(device))
+    assert torch.equal(keys.view(torch.uint8), want_k.view(torch.uint8))
+    assert torch.equal(values.view(torch.uint8), want_v.view(torch.uint8))
+
+
+def test_dependent_copies_apply_in_order(device) -> None:
+    """A -> B then B -> C: C must receive A's bytes (two groups, launched in order)."""
+    say("copy chain")
+    keys = torch.arange(1 * 4 * 2 * 1 * 4, dtype=torch.float32, device=device).view(1, 4, 2, 1, 4)
+    values = -keys
+    pairs = [(0, 1), (1, 2), (3, 0)]
+    groups = ops.independent_groups(pairs)
+    assert groups == [[(0, 1)], [(1, 2), (3, 0)]]
+    before = keys.clone()
+    for group in groups:
+        ops.copy_blocks(keys, values, torch.tensor(group, dtype=torch.int64, device=device))
+    assert torch.equal(keys[0, 1], before[0, 0])
+    assert torch.equal(keys[0, 2], before[0, 0])
+    assert torch.equal(keys[0, 0], before[0, 3])
+
+
+# --- attention --------------------------------------------------------------------------------
+
+
+def _ragged_case(rng, *, heads, dim, block, pool, seqs, max_ctx, prefill):
+    """Random ragged batch: each sequence gets 1 (decode) or several (prefill chunk) queries."""
+    kc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    vc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    contexts = rng.integers(1, max_ctx + 1, seqs)
+    need = [-(-int(c) // block) for c in contexts]
+    assert sum(need) <= pool
+    perm = rng.permutation(pool)
+    tables, offset = [], 0
+    for n in need:
+        tables.append(perm[offset : offset + n])
+        offset += n
+    positions, seq_of = [], []
+    for s, c in enumerate(contexts):
+        nq = int(rng.integers(1, min(int(c), 9) + 1)) if prefill else 1
+        positions += list(range(int(c) - nq, int(c)))
+        seq_of += [s] * nq
+    q = rng.standard_normal((len(positions), heads, dim)).astype(np.float32)
+    return kc, vc, tables, contexts, np.asarray(positions), np.asarray(seq_of), q
+
+
+def _run_kernel(device, kc, vc, tables, contexts, positions, seq_of, q, scale, *, partition=0,
+                dtype=torch.float32):  # fmt: skip
+    width = max(len(t) for t in tables)
+    padded = np.full((len(tables), width), -7, dtype=np.int32)  # padding is never read
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    dk = torch.from_numpy(kc).to(device).to(dtype)
+    dv = torch.from_numpy(vc).to(device).to(dtype)
+    out = ops.paged_attention_ragged(
+        torch.from_numpy(q).to(device),
+        torch.from_numpy(positions.astype(np.int32)).to(device),
+        torch.from_numpy(seq_of.astype(np.int32)).to(device),
+        dk, dv, torch.from_numpy(padded).to(device),
+        torch.from_numpy(contexts.astype(np.int32)).to(device),
+        scale, max_context_len=int(contexts.max()), partition_size=partition,
+    )  # fmt: skip
+    return out.cpu().numpy()
+
+
+def _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale):
+    out = np.zeros_like(q)
+    dense = np.zeros(q.shape, dtype=np.float64)
+    for s, (table, ctx) in enumerate(zip(tables, contexts)):
+        rows = np.nonzero(seq_of == s)[0]
+        out[rows] = paged_attention(q[rows], positions[rows], kc, vc, table, int(ctx), scale)
+        dense[rows] = dense_attention(q[rows], gather_context(kc, table, int(ctx)),
+                                      gather_context(vc, table, int(ctx)), scale, positions[rows])  # fmt: skip
+    return out, dense
+
+
+@pytest.mark.parametrize("dim", [8, 16, 32, 64, 128, 256])
+@pytest.mark.parametrize("block", [1, 3, 4, 16, 32])
+def test_ragged_attention_matches_the_oracle(device, dim, block) -> None:
+    say("ragged attention", dim, block)
+    rng = np.random.default_rng(dim * 100 + block)
+    heads = 2 if dim >= 128 else 3
+    max_ctx = 700 if block > 1 else 300
+    case = _ragged_case(rng, heads=heads, dim=dim, block=block, pool=5 * max_ctx // block + 8,
+                        seqs=5, max_ctx=max_ctx, prefill=True)  # fmt: skip
+    scale = dim**-0.5
+    for partition in (0, 16, 48, 1024):
+        got = _run_kernel(device, *case, scale, partition=partition)
+        want, dense = _oracle(*case, scale)
+        assert np.max(np.abs(got - want)) < FP32_TOL, partition
+        assert np.max(np.abs(got - dense)) < FP32_TOL, partition
+
+
+@pytest.mark.parametrize("dim", [8, 64, 128])
+def test_bfloat16_kv_matches_the_oracle_on_rounded_inputs(device, dim) -> None:
+    say("bf16 attention", dim)
+    rng = np.random.default_rng(dim + 1)
+    kc, vc, tables, contexts, positions, seq_of, q = _ragged_case(
+        rng, heads=2, dim=dim, block=16, pool=200, seqs=4, max_ctx=700, prefill=True
+    )
+    scale = dim**-0.5
+    got = _run_kernel(device, kc, vc, tables, contexts, positions, seq_of, q, scale, dtype=torch.bfloat16)
+    want, dense = _oracle(bf16_round(kc), bf16_round(vc), tables, contexts, positions, seq_of, q, scale)
+    assert np.max(np.abs(got - want)) < FP32_TOL
+    assert np.max(np.abs(got - dense)) < FP32_TOL
+
+
+def test_poisoned_slots_and_padding_are_never_read(device) -> None:
+    say("poison")
+    rng = np.random.default_rng(9)
+    heads, dim, block = 2, 8, 4
+    kc = np.full((6, block, heads, dim), np.inf, dtype=np.float32)
+    vc = np.full_like(kc, np.nan)
+    flat_k = rng.standard_normal((5, heads, dim)).astype(np.float32)
+    flat_v = rng.standard_normal((5, heads, dim)).astype(np.float32)
+    table = np.asarray([4, 1])
+    kc[4], vc[4] = flat_k[:4], flat_v[:4]
+    kc[1, 0], vc[1, 0] = flat_k[4], flat_v[4]
+    q = rng.standard_normal((2, heads, dim)).astype(np.float32)
+    got = _run_kernel(device, kc, vc, [table], np.asarray([5]), np.asarray([2, 4]), np.asarray([0, 0]),
+                      q, 0.35)  # fmt: skip
+    want = dense_attention(q, flat_k, flat_v, 0.35, np.asarray([2, 4]))
+    assert np.all(np.isfinite(got))
+    assert np.max(np.abs(got - want)) < FP32_TOL
+
+
+def test_a_fully_masked_query_is_zero(device) -> None:
+    say("masked")
+    rng = np.random.default_rng(2)
+    kc = rng.standard_normal((3, 4, 1, 16)).astype(np.float32)
+    got = _run_kernel(device, kc, kc.copy(), [np.asarray([2, 0])], np.asarray([6]),
+                      np.asarray([-1, 0]), np.asarray([0, 0]), np.ones((2, 1, 16), np.float32), 0.25)  # fmt: skip
+    assert np.array_equal(got[0], np.zeros((1, 16), np.float32))
+    assert np.allclose(got[1], kc[2, 0])
+
+
+# --- the benchmark configurations at full size ---------------------------------------------------
+
+
+def _torch_dense(batch, rows):
+    """float64 dense attention of selected query rows, on the device (torch reference)."""
+    out = {}
+    for t in rows:
+        s = int(batch.host_seq[t])
+        ctx = int(batch.host_context[s])
+        visible = min(ctx, int(batch.host_positions[t]) + 1)
+        table = torch.from_numpy(batch.host_tables[s].astype(np.int64)).to(batch.queries.device)
+        k = batch.key_cache[table].reshape(-1, *batch.key_cache.shape[2:])[:visible].double()
+        v = batch.value_cache[table].reshape(-1, *batch.value_cache.shape[2:])[:visible].double()
+        q = batch.queries[t].double()
+        scores = torch.einsum("hd,jhd->hj", q, k) * batch.scale
+        out[t] = torch.einsum("hj,jhd->hd", torch.softmax(scores, dim=1), v).float()
+    return out
+
+
+def _run_batch(batch, partition=0):
+    ops.append_kv(batch.key_cache, batch.value_cache, batch.new_keys, batch.new_values, batch.slot_mapping)
+    return ops.paged_attention_ragged(
+        batch.queries, batch.query_positions, batch.query_seq, batch.key_cache, batch.value_cache,
+        batch.block_tables, batch.context_lens, batch.scale, max_context_len=batch.max_context_len,
+        partition_size=partition,
+    )  # fmt: skip
+
+
+def test_config2_decode_64x4k_matches_the_oracle(device) -> None:
+    from paged_kv_serving_amd.workloads import decode_batch
+
+    say("config 2: build")
+    batch = decode_batch(seed=0, device=device)
+    say("config 2: run")
+    out = _run_batch(batch)
+    torch.cuda.synchronize()
+    # appended rows landed, bit-exact
+    slots = batch.slot_mapping
+    assert torch.equal(batch.key_cache.view(-1, 32, 128)[slots], batch.new_keys)
+    assert torch.equal(batch.value_cache.view(-1, 32, 128)[slots], batch.new_values)
+    # every sequence against the float64 torch reference
+    ref = _torch_dense(batch, range(batch.num_queries))
+    worst = max(float((out[t] - ref[t]).abs().max()) for t in ref)
+    say("config 2: worst vs float64 torch", worst)
+    assert worst < FP32_TOL
+    # a sample of sequences against the CPU oracle (reference algorithm, tile_blocks 8)
+    got = out.cpu().numpy()
+    for s in (0, 17, 63):
+        keys, values, q, pos = batch.host_rows(s)
+        pool_k = keys.reshape(1, -1, 32, 128)
+        pool_v = values.reshape(1, -1, 32, 128)
+        want = paged_attention(q, pos, pool_k.transpose(1, 0, 2, 3), pool_v.transpose(1, 0, 2, 3),
+                               np.arange(keys.shape[0]), int(batch.host_context[s]), batch.scale,
+                               tile_blocks=128)  # fmt: skip
+        assert np.max(np.abs(got[s] - want[0])) < FP32_TOL, s
+    # partition size changes nothing beyond rounding
+    for partition in (64, 256, 1024):
+        other = ops.paged_attention_ragged(
+            batch.queries, batch.query_positions, batch.query_seq, batch.key_cache,
+            batch.value_cache, batch.block_tables, batch.context_lens, batch.scale,
+            max_context_len=batch.max_context_len, partition_size=partition,
+        )  # fmt: skip
+        assert float((other - out).abs().max()) < FP32_TOL, partition

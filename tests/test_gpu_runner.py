@@ -1,0 +1,237 @@
+"""The GPU ModelRunner against the cache-free recompute (the reference's central claim).
+
+Ports the properties of the reference's tests/property/test_equivalence.py (chunk splits,
+scattered block tables, tile size, batch composition, a shared prefix) with seeded cases
+instead of hypothesis draws, at its tolerance of 1e-4 on logits and BLOCK_SIZE 8, plus the
+runner surface: copy-on-write through BlockManager with real bytes, the block fingerprint,
+reset, the weight-swap hazard and the reference's error messages.
+"""
+
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.model import OracleModel
+from oracle.runner import OracleRunner
+from paged_kv_serving_amd.blocks import BlockManager
+from paged_kv_serving_amd.config import ModelConfig
+from paged_kv_serving_amd.kvcache import KVCacheManager
+from paged_kv_serving_amd.model import LanguageModel, random_weights
+from paged_kv_serving_amd.prefix_cache import PrefixCache
+from paged_kv_serving_amd.runner import BatchEntry, ExecutionBatch, ModelRunner
+from paged_kv_serving_amd.sequence import Request, Sequence
+
+pytestmark = pytest.mark.gpu
+
+TOLERANCE = 1e-4
+BLOCK_SIZE = 8
+#: The reference's tiny test model (its tests/conftest.py:42-44).
+TINY_MODEL = dict(vocab_size=64, d_model=32, n_layers=2, n_heads=2, d_ff=64, max_seq_len=192)
+
+
+@pytest.fixture(scope="module")
+def models():
+    config = ModelConfig(**TINY_MODEL)
+    weights = random_weights(config, seed=11)
+    return LanguageModel(config, weights), OracleModel(config, weights)
+
+
+def split_sizes(total: int, chunk: int) -> list[int]:
+    sizes = [chunk] * (total // chunk)
+    if total % chunk:
+        sizes.append(total % chunk)
+    return sizes
+
+
+def chunked_logits(model, tokens, *, chunks=None, block_order=None, tile_blocks=8, device=None):
+    """Last-position logits through the GPU runner, chunk by chunk (equivalence.py:49-92)."""
+    sizes = chunks or [len(tokens)]
+    needed = -(-len(tokens) // BLOCK_SIZE)
+    table = tuple(block_order) if block_order is not None else tuple(range(needed))
+    runner = ModelRunner(model, num_blocks=max(table) + 1, block_size=BLOCK_SIZE,
+                         tile_blocks=tile_blocks, device=device)  # fmt: skip
+    start, logits = 0, None
+    for size in sizes:
+        stop = start + size
+        entry = BatchEntry("s", tuple(tokens[start:stop]), tuple(range(start, stop)), table,
+                           size - 1 if stop == len(tokens) else None)  # fmt: skip
+        result = runner.execute(ExecutionBatch((entry,)))
+        logits = result.get("s", logits)
+        start = stop
+    return logits
+
+
+def token_cases(count: int, seed: int, low: int = 1, high: int = 40):
+    rng = np.random.default_rng(seed)
+    return [[int(t) for t in rng.integers(0, 64, int(rng.integers(low, high + 1)))] for _ in range(count)]
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_chunked_prefill_matches_a_cache_free_recompute(device, models, case) -> None:
+    model, oracle = models
+    tokens = token_cases(12, 1)[case]
+    chunk = 1 + case % 13
+    got = chunked_logits(model, tokens, chunks=split_sizes(len(tokens), chunk), device=device)
+    want = oracle.reference_forward(tokens)[-1]
+    gap = float(np.max(np.abs(got - want)))
+    print("chunked", case, len(tokens), chunk, gap, flush=True)
+    assert gap < TOLERANCE
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_a_scattered_block_table_gives_the_same_logits(device, models, case) -> None:
+    model, oracle = models
+    tokens = token_cases(8, 2)[case]
+    needed = -(-len(tokens) // BLOCK_SIZE)
+    order = [int(v) for v in np.random.default_rng(case).permutation(needed * 2 + 3)[:needed]]
+    got = chunked_logits(model, tokens, block_order=order, device=device)
+    assert float(np.max(np.abs(got - oracle.reference_forward(tokens)[-1]))) < TOLERANCE
+
+
+@pytest.mark.parametrize("tile", [1, 2, 6])
+def test_tile_size_does_not_change_the_result(device, models, tile) -> None:
+    model, oracle = models
+    for tokens in token_cases(3, 3 + tile):
+        got = chunked_logits(model, tokens, chunks=split_sizes(len(tokens), 5), tile_blocks=tile, device=device)
+        assert float(np.max(np.abs(got - oracle.reference_forward(tokens)[-1]))) < TOLERANCE
+
+
+@pytest.mark.parametrize("decode_first", [False, True])
+def test_batch_composition_does_not_change_a_sequences_logits(device, models, decode_first) -> None:
+    model, _ = models
+    sequences = token_cases(4, 4)
+    per_seq = [-(-len(t) // BLOCK_SIZE) for t in sequences]
+    runner = ModelRunner(model, num_blocks=sum(per_seq), block_size=BLOCK_SIZE, device=device)
+    order = list(range(len(sequences)))[:: -1 if decode_first else 1]
+    entries = []
+    for i in order:
+        start = sum(per_seq[:i])
+        entries.append(BatchEntry(f"s{i}", tuple(sequences[i]), tuple(range(len(sequences[i]))),
+                                  tuple(range(start, start + per_seq[i])), len(sequences[i]) - 1))  # fmt: skip
+    batched = runner.execute(ExecutionBatch(tuple(entries)))
+    for i, tokens in enumerate(sequences):
+        alone = chunked_logits(model, tokens, device=device)
+        assert float(np.max(np.abs(batched[f"s{i}"] - alone))) < TOLERANCE
+
+
+def test_mixed_decode_and_prefill_rows_match_the_numpy_runner(device, models) -> None:
+    """One ragged batch of decode rows and chunk rows: GPU logits vs the NumPy runner's."""
+    model, oracle = models
+    gpu = ModelRunner(model, num_blocks=40, block_size=BLOCK_SIZE, device=device)
+    cpu = OracleRunner(oracle, num_blocks=40, block_size=BLOCK_SIZE)
+    rng = np.random.default_rng(7)
+    prompts = [[int(t) for t in rng.integers(0, 64, n)] for n in (17, 9, 30)]
+    tables = [tuple(range(0, 5)), tuple(range(10, 15)), tuple(range(20, 25))]
+    first = ExecutionBatch(tuple(
+        BatchEntry(f"s{i}", tuple(p), tuple(range(len(p))), tables[i], len(p) - 1)
+        for i, p in enumerate(prompts)
+    ))  # fmt: skip
+    for runner in (gpu, cpu):
+        runner.execute(first)
+    entries = (
+        BatchEntry("s0", (5,), (17,), tables[0], 0),  # decode
+        BatchEntry("s1", (1, 2, 3, 4), (9, 10, 11, 12), tables[1], 3),  # chunk
+        BatchEntry("s2", (8,), (30,), tables[2], 0),  # decode
+    )
+    got = gpu.execute(ExecutionBatch(entries))
+    want = cpu.execute(ExecutionBatch(entries))
+    for name in want:
+        assert float(np.max(np.abs(got[name] - want[name]))) < TOLERANCE
+    # and the pools hold the same keys/values (float32 rounding only)
+    for layer in range(2):
+        gk, gv = gpu.block_view(layer)
+        assert float(np.max(np.abs(gk.cpu().numpy() - cpu.keys[layer]))) < 1e-5
+        assert float(np.max(np.abs(gv.cpu().numpy() - cpu.values[layer]))) < 1e-5
+
+
+def test_sharing_a_prefix_block_does_not_change_either_continuation(device, models) -> None:
+    model, oracle = models
+    rng = np.random.default_rng(12)
+    prefix = [int(t) for t in rng.integers(0, 64, 16)]
+    a = [*prefix, *[int(t) for t in rng.integers(0, 64, 7)]]
+    b = [*prefix, *[int(t) for t in rng.integers(0, 64, 11)]]
+    runner = ModelRunner(model, num_blocks=8, block_size=BLOCK_SIZE, device=device)
+    shared = (0, 1)
+    runner.execute(ExecutionBatch((BatchEntry("p", tuple(prefix), tuple(range(16)), shared),)))
+    for name, seq, own in (("a", a, (2,)), ("b", b, (4, 5))):
+        result = runner.execute(ExecutionBatch((BatchEntry(
+            name, tuple(seq[16:]), tuple(range(16, len(seq))), shared + own, len(seq) - 17),)))  # fmt: skip
+        assert float(np.max(np.abs(result[name] - oracle.reference_forward(seq)[-1]))) < TOLERANCE
+
+
+def test_copy_on_write_moves_real_bytes_and_keeps_the_original(device, models) -> None:
+    """Fork, then the child's first write: BlockManager asks the runner for one copy."""
+    model, oracle = models
+    runner = ModelRunner(model, num_blocks=16, block_size=4, device=device)
+    blocks = BlockManager(num_blocks=16, block_size=4, store=runner)
+    cache = KVCacheManager(blocks, PrefixCache(blocks))
+    parent = Sequence.from_request(Request("p", (1, 2, 3, 4, 5, 6)), 0)
+    cache.reserve(parent, 6)
+    runner.execute(ExecutionBatch((BatchEntry("p", (1, 2, 3, 4, 5, 6), tuple(range(6)),
+                                              tuple(parent.block_table), 5),)))  # fmt: skip
+    parent.num_computed_tokens = 6
+    child = Sequence.from_request(Request("c", (1, 2, 3, 4, 5, 6)), 0)
+    cache.fork(parent, child)
+    shared = parent.block_table[1]
+    before = runner.block_fingerprint(shared)
+    child.append_token(9)
+    cache.reserve(child, 7)  # copy-on-write of the partial block, queued in the runner
+    private = child.block_table[1]
+    assert private != shared
+    result = runner.execute(ExecutionBatch((BatchEntry("c", (9,), (6,), tuple(child.block_table), 0),)))
+    assert runner.block_fingerprint(shared) == before, "the original block changed"
+    k, v = runner.block_view(0)
+    assert torch.equal(k[private, :2], k[shared, :2]) and torch.equal(v[private, :2], v[shared, :2])
+    want = oracle.reference_forward([1, 2, 3, 4, 5, 6, 9])[-1]
+    assert float(np.max(np.abs(result["c"] - want))) < TOLERANCE
+
+
+def test_fingerprint_matches_the_reference_byte_layout(device, models) -> None:
+    model, _ = models
+    runner = ModelRunner(model, num_blocks=4, block_size=4, device=device)
+    runner.execute(ExecutionBatch((BatchEntry("s", (3, 1, 4, 1, 5), tuple(range(5)), (2, 0)),)))
+    keys = runner.key_cache.cpu().numpy()
+    values = runner.value_cache.cpu().numpy()
+    digest = hashlib.blake2b(digest_size=16)
+    digest.update(np.ascontiguousarray(keys[:, 2]).tobytes())
+    digest.update(np.ascontiguousarray(values[:, 2]).tobytes())
+    assert runner.block_fingerprint(2) == digest.digest()
+    runner.reset_cache()
+    assert not runner.key_cache.any() and not runner.value_cache.any()
+
+
+def test_a_weight_swap_is_picked_up(device, models) -> None:
+    model, _ = models
+    config = model.config
+    swapped = LanguageModel(config, random_weights(config, seed=11))
+    runner = ModelRunner(swapped, num_blocks=4, block_size=8, device=device)
+    entry = BatchEntry("s", (1, 2, 3), (0, 1, 2), (0,), 2)
+    first = runner.execute(ExecutionBatch((entry,)))["s"]
+    swapped.weights = random_weights(config, seed=12)  # what the reference's admin swap does
+    runner.reset_cache()
+    second = runner.execute(ExecutionBatch((entry,)))["s"]
+    oracle = OracleModel(config, swapped.weights)
+    assert float(np.max(np.abs(second - oracle.reference_forward([1, 2, 3])[-1]))) < TOLERANCE
+    assert not np.allclose(first, second)
+
+
+def test_reference_error_messages(device, models) -> None:
+    model, _ = models
+    with pytest.raises(ValueError, match="num_blocks and block_size must be >= 1"):
+        ModelRunner(model, num_blocks=0, block_size=4, device=device)
+    with pytest.raises(ValueError, match="tile_blocks must be >= 1"):
+        ModelRunner(model, num_blocks=4, block_size=4, tile_blocks=0, device=device)
+    runner = ModelRunner(model, num_blocks=4, block_size=4, device=device)
+    with pytest.raises(ValueError, match="token id outside the vocabulary"):
+        runner.execute(ExecutionBatch((BatchEntry("s", (64,), (0,), (0,)),)))
+    with pytest.raises(ValueError, match="position beyond max_seq_len"):
+        runner.execute(ExecutionBatch((BatchEntry("s", (1,), (192,), (0,)),)))
+    with pytest.raises(ValueError, match="sequence s: position 4 has no block in the table"):
+        runner.execute(ExecutionBatch((BatchEntry("s", (1,), (4,), (0,)),)))
+    with pytest.raises(ValueError, match="onto itself"):
+        runner.copy_block(1, 1)
+    assert runner.execute(ExecutionBatch(())) == {}

@@ -1,0 +1,93 @@
+"""The C-ABI library builds for gfx950, loads, and exports exactly what include/pkv.h declares.
+
+Runs without a GPU: only host-side entry points are called (version, error strings, workspace
+sizing) plus argument checks that return before any HIP call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from paged_kv_serving_amd import _native
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> list[str]:
+    text = (ROOT / "include" / "pkv.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pkv_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _native.LIB_PATH.exists():
+        _native.build()
+    return _native.library()
+
+
+def test_every_declared_function_is_exported(lib) -> None:
+    names = declared_functions()
+    assert names == sorted(_native.EXPORTED_SYMBOLS)
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.LIB_PATH)], capture_output=True, text=True, check=True)
+    exported = {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
+    for name in names:
+        assert name in exported, name
+        assert getattr(lib, name) is not None
+
+
+def test_the_library_holds_gfx950_code_only() -> None:
+    blob = _native.LIB_PATH.read_bytes()  # built in-tree from csrc/ by _native.build()
+    assert b"amdgcn-amd-amdhsa--gfx950" in blob
+    for other in (b"gfx942", b"gfx90a", b"gfx908", b"sm_"):
+        assert b"amdgcn-amd-amdhsa--" + other not in blob
+
+
+def test_version_and_error_strings(lib) -> None:
+    assert lib.pkv_version().decode().startswith("pkv ")
+    assert lib.pkv_error_string(0) == b"ok"
+    assert lib.pkv_error_string(-1) == b"invalid argument"
+    assert lib.pkv_error_string(-2) == b"unsupported shape or dtype"
+    assert lib.pkv_error_string(-3).startswith(b"HIP")
+    assert lib.pkv_error_string(7) == b"unknown error code"
+
+
+def test_workspace_sizing(lib) -> None:
+    # one partition -> no workspace
+    assert lib.pkv_attention_workspace_bytes(64, 32, 128, 512, 512) == 0
+    # 4096 / 512 = 8 partitions of (128 + 2) floats per (query, head)
+    assert lib.pkv_attention_workspace_bytes(64, 32, 128, 4096, 512) == 64 * 32 * 8 * 130 * 4
+    assert lib.pkv_attention_workspace_bytes(64, 32, 128, 4097, 0) == 64 * 32 * 9 * 130 * 4
+    assert lib.pkv_attention_workspace_bytes(1, 1, 128, 100, 17) == -1  # not a multiple of 16
+    assert lib.pkv_attention_workspace_bytes(1, 1, 128, 100, 2048) == -1  # above 1024
+
+
+def test_bad_arguments_are_refused_before_any_device_work(lib) -> None:
+    null = None
+    # num_heads = 0
+    assert lib.pkv_append(null, null, 0, 10, null, null, 0, 8, null, 1, 0, 8, 0, null) == -1
+    # bf16 source into a float32 pool is not a supported conversion
+    assert lib.pkv_append(null, null, 0, 10, null, null, 1, 8, null, 1, 1, 8, 0, null) == -2
+    # zero tokens is a no-op
+    assert lib.pkv_append(null, null, 0, 10, null, null, 0, 8, null, 0, 1, 8, 0, null) == 0
+    # unknown dtype
+    assert lib.pkv_copy_blocks(null, null, 9, null, 1, 1, 4, 16, 0, null) == -1
+    assert lib.pkv_copy_blocks(null, null, 0, null, 0, 1, 4, 16, 0, null) == 0
+    # partition size not a multiple of 16
+    args = [null, null, 8, null, null, 1, null, null, 0, 4, 4, null, 1, null, 1, 1, 8,
+            ctypes.c_float(0.5), 8, 17, null, 0, 0, null]  # fmt: skip
+    assert lib.pkv_paged_attention(*args) == -1
+    args[19] = 16
+    assert lib.pkv_paged_attention(*args) == -1  # null pointers
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch) -> None:
+    monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "absent.so")
+    monkeypatch.setattr(_native, "_LIB", None)
+    with pytest.raises(_native.NativeLibraryError, match="missing"):
+        _native.library()
