@@ -56,9 +56,10 @@ const char* pkv_error_string(int code);
  *
  *   key_pool, value_pool : the layer's pools, [num_slots, num_heads, head_dim] of pool_dtype
  *                          (num_slots = num_blocks * block_size).
- *   new_keys, new_values : [num_tokens, num_heads, head_dim] of src_dtype; token t starts at
- *                          element t * src_token_stride (the H*D row itself is contiguous), so
- *                          a view into a fused QKV output needs no copy.
+ *   new_keys, new_values : [num_tokens, num_heads, head_dim] of src_dtype; token t of the keys
+ *                          starts at element t * key_token_stride, of the values at
+ *                          t * value_token_stride (each H*D row itself is contiguous), so views
+ *                          into a fused QKV output need no copy.
  *   slot_mapping         : int64 [num_tokens]. A slot outside [0, num_slots) is skipped (the
  *                          host validates slots first; this only keeps a bad slot in bounds).
  * A float32 source into a bfloat16 pool is rounded to nearest even; equal types copy bits.
@@ -67,8 +68,9 @@ const char* pkv_error_string(int code);
  */
 int pkv_append(void* key_pool, void* value_pool, pkv_dtype pool_dtype, int64_t num_slots,
                const void* new_keys, const void* new_values, pkv_dtype src_dtype,
-               int64_t src_token_stride, const int64_t* slot_mapping, int64_t num_tokens,
-               int32_t num_heads, int32_t head_dim, int device, void* stream);
+               int64_t key_token_stride, int64_t value_token_stride,
+               const int64_t* slot_mapping, int64_t num_tokens, int32_t num_heads,
+               int32_t head_dim, int device, void* stream);
 
 /*
  * Copy-on-write block copies, batched: for every pair (src, dst), block src is copied over block
@@ -113,7 +115,9 @@ int64_t pkv_attention_workspace_bytes(int64_t num_queries, int32_t num_heads, in
  *   value_cache      : the layer's pools, [num_blocks, block_size, num_heads, head_dim], kv_dtype.
  *   block_tables     : int32 [num_seqs, block_table_stride], physical block ids in logical order.
  *   context_lens     : int32 [num_seqs], valid cached tokens of each sequence (runner.py:66-68).
- *   max_context_len  : an upper bound of every context_len (sizes the grid).
+ *   max_context_len  : an upper bound of every context_len; it sizes the grid, and visible
+ *                      lengths are clamped to it, so block_table_stride * block_size must be
+ *                      >= max_context_len (checked).
  *   partition_size   : keys per split-context partition, a positive multiple of 16, <= 1024;
  *                      0 selects the library default.
  *   workspace        : float32 scratch of pkv_attention_workspace_bytes(...) bytes (may be

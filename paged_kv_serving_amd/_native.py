@@ -126,7 +126,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pkv_error_string.restype = ctypes.c_char_p
     lib.pkv_append.argtypes = [
         _ptr, _ptr, _c_int, _i64,  # key_pool, value_pool, pool_dtype, num_slots
-        _ptr, _ptr, _c_int, _i64,  # new_keys, new_values, src_dtype, src_token_stride
+        _ptr, _ptr, _c_int,  # new_keys, new_values, src_dtype
+        _i64, _i64,  # key_token_stride, value_token_stride
         _ptr, _i64, _i32, _i32,  # slot_mapping, num_tokens, num_heads, head_dim
         _c_int, _ptr,  # device, stream
     ]

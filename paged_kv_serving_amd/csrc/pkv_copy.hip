@@ -59,14 +59,14 @@ __device__ __forceinline__ void move_one(uint16_t* d, const float* s) {
 template <typename SrcT, typename DstT, bool kVectorized>
 __global__ __launch_bounds__(kCopyThreads) void append_kernel(
     DstT* __restrict__ key_pool, DstT* __restrict__ value_pool, int64_t num_slots,
-    const SrcT* __restrict__ new_keys, const SrcT* __restrict__ new_values, int64_t src_stride,
-    const int64_t* __restrict__ slots, int64_t row_elems, int64_t chunks) {
+    const SrcT* __restrict__ new_keys, const SrcT* __restrict__ new_values, int64_t key_stride,
+    int64_t value_stride, const int64_t* __restrict__ slots, int64_t row_elems, int64_t chunks) {
   const int64_t token = blockIdx.x / chunks;
   const int64_t chunk = blockIdx.x - token * chunks;
   const int64_t slot = slots[token];
   if (slot < 0 || slot >= num_slots) return;
   const bool is_value = blockIdx.y != 0;
-  const SrcT* src = (is_value ? new_values : new_keys) + token * src_stride;
+  const SrcT* src = is_value ? new_values + token * value_stride : new_keys + token * key_stride;
   DstT* dst = (is_value ? value_pool : key_pool) + slot * row_elems;
   constexpr int kVec = kVectorized ? Mover<SrcT, DstT>::kVec : 1;
   const int64_t e = (chunk * kCopyThreads + threadIdx.x) * kVec;
@@ -80,10 +80,12 @@ __global__ __launch_bounds__(kCopyThreads) void append_kernel(
 
 template <typename SrcT, typename DstT>
 int launch_append(void* key_pool, void* value_pool, int64_t num_slots, const void* new_keys,
-                  const void* new_values, int64_t src_stride, const int64_t* slots,
-                  int64_t num_tokens, int64_t row_elems, hipStream_t stream) {
+                  const void* new_values, int64_t key_stride, int64_t value_stride,
+                  const int64_t* slots, int64_t num_tokens, int64_t row_elems,
+                  hipStream_t stream) {
   constexpr int kVec = Mover<SrcT, DstT>::kVec;
-  const bool vectorized = row_elems % kVec == 0 && src_stride % kVec == 0 &&
+  const bool vectorized = row_elems % kVec == 0 && key_stride % kVec == 0 &&
+                          value_stride % kVec == 0 &&
                           aligned16(key_pool) && aligned16(value_pool) && aligned16(new_keys) &&
                           aligned16(new_values);
   const int64_t per_block = static_cast<int64_t>(kCopyThreads) * (vectorized ? kVec : 1);
@@ -96,10 +98,10 @@ int launch_append(void* key_pool, void* value_pool, int64_t num_slots, const voi
   const auto* vn = static_cast<const SrcT*>(new_values);
   if (vectorized) {
     hipLaunchKernelGGL((append_kernel<SrcT, DstT, true>), grid, dim3(kCopyThreads), 0, stream, kp,
-                       vp, num_slots, kn, vn, src_stride, slots, row_elems, chunks);
+                       vp, num_slots, kn, vn, key_stride, value_stride, slots, row_elems, chunks);
   } else {
     hipLaunchKernelGGL((append_kernel<SrcT, DstT, false>), grid, dim3(kCopyThreads), 0, stream, kp,
-                       vp, num_slots, kn, vn, src_stride, slots, row_elems, chunks);
+                       vp, num_slots, kn, vn, key_stride, value_stride, slots, row_elems, chunks);
   }
   return check_launch();
 }
@@ -176,15 +178,16 @@ extern "C" const char* pkv_error_string(int code) {
 
 extern "C" int pkv_append(void* key_pool, void* value_pool, pkv_dtype pool_dtype,
                           int64_t num_slots, const void* new_keys, const void* new_values,
-                          pkv_dtype src_dtype, int64_t src_token_stride,
-                          const int64_t* slot_mapping, int64_t num_tokens, int32_t num_heads,
-                          int32_t head_dim, int device, void* stream) {
+                          pkv_dtype src_dtype, int64_t key_token_stride,
+                          int64_t value_token_stride, const int64_t* slot_mapping,
+                          int64_t num_tokens, int32_t num_heads, int32_t head_dim, int device,
+                          void* stream) {
   using namespace pkv;
   if (num_tokens < 0 || num_heads < 1 || head_dim < 1 || num_slots < 1) return PKV_EINVAL;
   if (dtype_size(pool_dtype) == 0 || dtype_size(src_dtype) == 0) return PKV_EINVAL;
   if (src_dtype == PKV_BF16 && pool_dtype == PKV_F32) return PKV_EUNSUPPORTED;
   const int64_t row = static_cast<int64_t>(num_heads) * head_dim;
-  if (src_token_stride < row) return PKV_EINVAL;
+  if (key_token_stride < row || value_token_stride < row) return PKV_EINVAL;
   if (num_tokens == 0) return PKV_OK;
   if (!key_pool || !value_pool || !new_keys || !new_values || !slot_mapping) return PKV_EINVAL;
   DeviceGuard guard(device);
@@ -193,14 +196,17 @@ extern "C" int pkv_append(void* key_pool, void* value_pool, pkv_dtype pool_dtype
   auto s = static_cast<hipStream_t>(stream);
   if (pool_dtype == PKV_F32) {
     return launch_append<float, float>(key_pool, value_pool, num_slots, new_keys, new_values,
-                                       src_token_stride, slot_mapping, num_tokens, row, s);
+                                       key_token_stride, value_token_stride, slot_mapping,
+                                       num_tokens, row, s);
   }
   if (src_dtype == PKV_F32) {
     return launch_append<float, uint16_t>(key_pool, value_pool, num_slots, new_keys, new_values,
-                                          src_token_stride, slot_mapping, num_tokens, row, s);
+                                          key_token_stride, value_token_stride, slot_mapping,
+                                          num_tokens, row, s);
   }
   return launch_append<uint16_t, uint16_t>(key_pool, value_pool, num_slots, new_keys, new_values,
-                                           src_token_stride, slot_mapping, num_tokens, row, s);
+                                           key_token_stride, value_token_stride, slot_mapping,
+                                           num_tokens, row, s);
 }
 
 extern "C" int pkv_copy_blocks(void* key_pool, void* value_pool, pkv_dtype dtype,

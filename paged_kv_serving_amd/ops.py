@@ -80,9 +80,8 @@ def append_kv(
     heads, dim = keys.shape[1], keys.shape[2]
     if tuple(key_pool.shape[-2:]) != (heads, dim):
         raise ValueError("pool rows and keys disagree on (heads, head_dim)")
-    stride = _rows_contiguous(keys, "keys")
-    if _rows_contiguous(values, "values") != stride:
-        raise ValueError("keys and values must share one token stride")
+    key_stride = _rows_contiguous(keys, "keys")
+    value_stride = _rows_contiguous(values, "values")
     if slot_mapping.dtype != torch.int64 or slot_mapping.shape != (keys.shape[0],):
         raise ValueError("slot_mapping must be int64 with one slot per token")
     pool_code = kv_dtype_code(key_pool.dtype)
@@ -90,7 +89,7 @@ def append_kv(
     num_slots = key_pool.numel() // (heads * dim)
     rc = _native.library().pkv_append(
         key_pool.data_ptr(), value_pool.data_ptr(), pool_code, num_slots,
-        keys.data_ptr(), values.data_ptr(), src_code, stride,
+        keys.data_ptr(), values.data_ptr(), src_code, key_stride, value_stride,
         slot_mapping.data_ptr(), keys.shape[0], heads, dim,
         device, _stream(device),
     )  # fmt: skip

@@ -59,15 +59,17 @@ def test_append_from_a_fused_qkv_view(device) -> None:
     fused = rng.standard_normal((tokens, 3, heads, dim)).astype(np.float32)
     slots = rng.permutation(blocks * block)[:tokens].astype(np.int64)
     dfused = torch.from_numpy(fused).to(device)
-    dk = torch.zeros((blocks, block, heads, dim), device=device)
-    dv = torch.zeros_like(dk)
-    ops.append_kv(dk, dv, dfused[:, 1], dfused[:, 2], torch.from_numpy(slots).to(device))
     want_k = np.zeros((blocks * block, heads, dim), dtype=np.float32)
     want_v = np.zeros_like(want_k)
     want_k[slots] = fused[:, 1]
     want_v[slots] = fused[:, 2]
-    assert np.array_equal(dk.cpu().numpy().reshape(-1, heads, dim), want_k)
-    assert np.array_equal(dv.cpu().numpy().reshape(-1, heads, dim), want_v)
+    # both strided; then contiguous keys (as after RoPE) with strided values
+    for keys in (dfused[:, 1], dfused[:, 1].contiguous()):
+        dk = torch.zeros((blocks, block, heads, dim), device=device)
+        dv = torch.zeros_like(dk)
+        ops.append_kv(dk, dv, keys, dfused[:, 2], torch.from_numpy(slots).to(device))
+        assert np.array_equal(dk.cpu().numpy().reshape(-1, heads, dim), want_k)
+        assert np.array_equal(dv.cpu().numpy().reshape(-1, heads, dim), want_v)
 
 
 @pytest.mark.parametrize("dim", [8, 128, 6])

@@ -70,11 +70,13 @@ def test_workspace_sizing(lib) -> None:
 def test_bad_arguments_are_refused_before_any_device_work(lib) -> None:
     null = None
     # num_heads = 0
-    assert lib.pkv_append(null, null, 0, 10, null, null, 0, 8, null, 1, 0, 8, 0, null) == -1
+    assert lib.pkv_append(null, null, 0, 10, null, null, 0, 8, 8, null, 1, 0, 8, 0, null) == -1
     # bf16 source into a float32 pool is not a supported conversion
-    assert lib.pkv_append(null, null, 0, 10, null, null, 1, 8, null, 1, 1, 8, 0, null) == -2
+    assert lib.pkv_append(null, null, 0, 10, null, null, 1, 8, 8, null, 1, 1, 8, 0, null) == -2
+    # a value stride shorter than a row
+    assert lib.pkv_append(null, null, 0, 10, null, null, 0, 8, 4, null, 1, 1, 8, 0, null) == -1
     # zero tokens is a no-op
-    assert lib.pkv_append(null, null, 0, 10, null, null, 0, 8, null, 0, 1, 8, 0, null) == 0
+    assert lib.pkv_append(null, null, 0, 10, null, null, 0, 8, 8, null, 0, 1, 8, 0, null) == 0
     # unknown dtype
     assert lib.pkv_copy_blocks(null, null, 9, null, 1, 1, 4, 16, 0, null) == -1
     assert lib.pkv_copy_blocks(null, null, 0, null, 0, 1, 4, 16, 0, null) == 0
