@@ -23,7 +23,19 @@
 namespace pkv {
 namespace {
 
-constexpr int kWaves = 4;             // wavefronts per workgroup
+// Tunables (compile-time): wavefronts per workgroup, key rows loaded per wavefront before any
+// of them is used, and whether K/V rows are loaded non-temporally (read-once streams).
+#ifndef PKV_ATTN_WAVES
+#define PKV_ATTN_WAVES 4
+#endif
+#ifndef PKV_ATTN_ITER_TOKENS
+#define PKV_ATTN_ITER_TOKENS 32
+#endif
+#ifndef PKV_ATTN_NONTEMPORAL
+#define PKV_ATTN_NONTEMPORAL 1
+#endif
+
+constexpr int kWaves = PKV_ATTN_WAVES;  // wavefronts per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kMaxPartition = 1024;   // keys per partition, upper bound
 constexpr int kDefaultPartition = 512;
@@ -53,7 +65,7 @@ struct Layout {
   static constexpr int kEpv = 16 / kEsize;  // elements per 16-byte vector
   static constexpr int kDpl = kVpl * kEpv;
   static constexpr int kTpr = kWave / kLpt;
-  static constexpr int kRounds = kTpr >= 16 ? 1 : 16 / kTpr;
+  static constexpr int kRounds = kTpr >= PKV_ATTN_ITER_TOKENS ? 1 : PKV_ATTN_ITER_TOKENS / kTpr;
   static constexpr int kIterTok = kTpr * kRounds;
   static constexpr int kGroups = kWaves * kTpr;  // lane groups per workgroup
 };
@@ -74,6 +86,17 @@ __device__ __forceinline__ void widen(const uint4& raw, float* out, uint16_t) {
   out[5] = bf16_hi(raw.z);
   out[6] = bf16_lo(raw.w);
   out[7] = bf16_hi(raw.w);
+}
+
+// One 16-byte vector of a key or value row.
+__device__ __forceinline__ uint4 load_row(const uint4* p) {
+#if PKV_ATTN_NONTEMPORAL
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return *p;
+#endif
 }
 
 // Visible key count of a query: keys at positions 0 .. min(context_len, position + 1) - 1.
@@ -170,9 +193,9 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
         const uint4* kp = reinterpret_cast<const uint4*>(kcache + row);
         const uint4* vp = reinterpret_cast<const uint4*>(vcache + row);
 #pragma unroll
-        for (int i = 0; i < L::kVpl; ++i) kraw[r][i] = kp[i * L::kLpt + j];
+        for (int i = 0; i < L::kVpl; ++i) kraw[r][i] = load_row(kp + i * L::kLpt + j);
 #pragma unroll
-        for (int i = 0; i < L::kVpl; ++i) vraw[r][i] = vp[i * L::kLpt + j];
+        for (int i = 0; i < L::kVpl; ++i) vraw[r][i] = load_row(vp + i * L::kLpt + j);
       } else {
 #pragma unroll
         for (int i = 0; i < L::kVpl; ++i) {

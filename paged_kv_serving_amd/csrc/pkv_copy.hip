@@ -111,6 +111,38 @@ int launch_append(void* key_pool, void* value_pool, int64_t num_slots, const voi
 // 1 values). Unit is the widest of 16/4/1 bytes that divides the block; each thread moves
 // kUnroll units, issuing every load before the first store.
 // --------------------------------------------------------------------------------------------
+#ifndef PKV_COPY_NT_LOAD
+#define PKV_COPY_NT_LOAD 1
+#endif
+#ifndef PKV_COPY_NT_STORE
+#define PKV_COPY_NT_STORE 0
+#endif
+#ifndef PKV_COPY_UNROLL
+#define PKV_COPY_UNROLL 4
+#endif
+
+// 16-byte unit of the block copy, as a vector type the non-temporal builtins accept.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// The source block is read once, so it is loaded non-temporally; the destination is read again
+// by the same step's attention, so by default it is stored normally and may stay in the caches.
+template <typename UnitT>
+__device__ __forceinline__ UnitT load_unit(const UnitT* p) {
+#if PKV_COPY_NT_LOAD
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+template <typename UnitT>
+__device__ __forceinline__ void store_unit(UnitT* p, UnitT v) {
+#if PKV_COPY_NT_STORE
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
+
 template <typename UnitT, int kUnroll>
 __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
     char* __restrict__ key_pool, char* __restrict__ value_pool, const int64_t* __restrict__ pairs,
@@ -130,19 +162,19 @@ __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t i = first + static_cast<int64_t>(u) * kCopyThreads;
-    if (i < block_units) buf[u] = from[i];
+    if (i < block_units) buf[u] = load_unit(from + i);
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     const int64_t i = first + static_cast<int64_t>(u) * kCopyThreads;
-    if (i < block_units) to[i] = buf[u];
+    if (i < block_units) store_unit(to + i, buf[u]);
   }
 }
 
 template <typename UnitT>
 int launch_copy(void* key_pool, void* value_pool, const int64_t* pairs, int64_t num_pairs,
                 int32_t num_layers, int64_t num_blocks, int64_t block_bytes, hipStream_t stream) {
-  constexpr int kUnroll = 4;
+  constexpr int kUnroll = PKV_COPY_UNROLL;
   const int64_t units = block_bytes / static_cast<int64_t>(sizeof(UnitT));
   const int64_t per_group = static_cast<int64_t>(kCopyThreads) * kUnroll;
   const int64_t chunks = (units + per_group - 1) / per_group;
@@ -225,7 +257,7 @@ extern "C" int pkv_copy_blocks(void* key_pool, void* value_pool, pkv_dtype dtype
   const int64_t bytes = block_elems * dtype_size(dtype);
   const bool base_aligned = aligned16(key_pool) && aligned16(value_pool);
   if (bytes % 16 == 0 && base_aligned) {
-    return launch_copy<uint4>(key_pool, value_pool, pairs, num_pairs, num_layers, num_blocks,
+    return launch_copy<u32x4>(key_pool, value_pool, pairs, num_pairs, num_layers, num_blocks,
                               bytes, s);
   }
   if (bytes % 4 == 0 && (reinterpret_cast<uintptr_t>(key_pool) & 3u) == 0 &&
