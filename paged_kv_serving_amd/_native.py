@@ -177,3 +177,7 @@ def check(code: int, what: str) -> None:
     if code != PKV_OK:
         message = library().pkv_error_string(code).decode()
         raise NativeLibraryError(f"{what} failed: {message} (code {code})")
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

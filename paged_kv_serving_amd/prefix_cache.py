@@ -80,6 +80,15 @@ class PrefixCacheStats:
     def hit_ratio(self) -> float:
         return self.hit_blocks / self.queried_blocks if self.queried_blocks else 0.0
 
+    def as_dict(self) -> dict[str, float]:
+        return {
+            "queried_blocks": float(self.queried_blocks),
+            "hit_blocks": float(self.hit_blocks),
+            "registered_blocks": float(self.registered_blocks),
+            "evicted_blocks": float(self.evicted_blocks),
+            "hit_ratio": self.hit_ratio,
+        }
+
 
 class PrefixCache:
     """LRU map from chained block hash to block id, one reference per entry."""

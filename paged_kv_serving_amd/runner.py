@@ -31,7 +31,7 @@ import torch
 
 from paged_kv_serving_amd import ops
 
-__all__ = ["DEFAULT_TILE_BLOCKS", "BatchEntry", "ExecutionBatch", "ModelRunner"]
+__all__ = ["DEFAULT_TILE_BLOCKS", "BatchEntry", "ExecutionBatch", "ModelRunner", "compute_slots"]
 
 #: Accepted for API compatibility (reference attention.py:39). The kernels tile the context in
 #: their own units, and results do not depend on this value.
@@ -86,6 +86,25 @@ class ExecutionBatch:
     @property
     def num_prefill_tokens(self) -> int:
         return sum(entry.num_tokens for entry in self.entries if entry.num_tokens > 1)
+
+
+def compute_slots(entries, block_size: int) -> np.ndarray:
+    """Flat slot ``block_table[p // B] * B + p % B`` of every token of a batch, int64.
+
+    The slot mapping of runner.py:149-159 and :184-186, vectorised per entry; a position past
+    the entry's table raises the reference's ValueError, naming the first such position.
+    """
+    parts = []
+    for entry in entries:
+        positions = np.asarray(entry.positions, dtype=np.int64)
+        table = np.asarray(entry.block_table, dtype=np.int64)
+        index = positions // block_size
+        missing = np.nonzero(index >= table.size)[0]
+        if missing.size:
+            position = int(positions[missing[0]])
+            raise ValueError(f"sequence {entry.seq_id}: position {position} has no block in the table")
+        parts.append(table[index] * block_size + positions % block_size)
+    return np.concatenate(parts) if parts else np.zeros(0, dtype=np.int64)
 
 
 def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -240,20 +259,6 @@ class ModelRunner:
             self._weights = _DeviceWeights(self.model, self.device)
         return self._weights
 
-    def _slots(self, entry: BatchEntry) -> list[int]:
-        """Flat slot of every position of an entry (runner.py:149-159)."""
-        size = self.block_size
-        table = entry.block_table
-        out = []
-        for position in entry.positions:
-            index = position // size
-            if index >= len(table):
-                raise ValueError(
-                    f"sequence {entry.seq_id}: position {position} has no block in the table"
-                )
-            out.append(table[index] * size + position % size)
-        return out
-
     def execute(self, batch: ExecutionBatch) -> dict[str, np.ndarray]:
         """Run one iteration; return host float32 logits for the entries that ask for them.
 
@@ -271,11 +276,11 @@ class ModelRunner:
         positions = np.fromiter((p for e in entries for p in e.positions), dtype=np.int64, count=total)
         if np.any(positions >= config.max_seq_len):
             raise ValueError("position beyond max_seq_len")
-        slots = np.asarray([s for e in entries for s in self._slots(e)], dtype=np.int64)
-        if slots.size and (slots.min() < 0 or slots.max() >= self.capacity_tokens):
-            raise IndexError("a block table names a block outside the pool")
         if np.any(positions < 0):
             raise ValueError("positions must be >= 0")
+        slots = compute_slots(entries, self.block_size)
+        if slots.size and (slots.min() < 0 or slots.max() >= self.capacity_tokens):
+            raise IndexError("a block table names a block outside the pool")
 
         num_seqs = len(entries)
         width = max(max(len(e.block_table) for e in entries), 1)
