@@ -97,6 +97,12 @@ int64_t pkv_attention_workspace_bytes(int64_t num_queries, int32_t num_heads, in
                                       int32_t max_context_len, int32_t partition_size);
 
 /*
+ * Nonzero when the MFMA tile path of pkv_paged_attention supports this head_dim (32, 64, 128,
+ * 256). Host-only.
+ */
+int pkv_tile_head_dim_supported(int32_t head_dim);
+
+/*
  * Paged causal attention of a ragged batch over one layer's pools: every query row attends to
  * the keys at positions [0, min(context_len, position + 1)) of its sequence, read through the
  * sequence's block table.
@@ -111,15 +117,25 @@ int64_t pkv_attention_workspace_bytes(int64_t num_queries, int32_t num_heads, in
  *   query_positions  : int32 [num_queries], absolute position of each query (the causal mask:
  *                      key position > query position is masked, attention.py:102-104).
  *   query_seq        : int32 [num_queries], index of the sequence each query belongs to.
+ *   rows, num_rows   : the plan's row list, int32 [num_rows]: query rows computed by the
+ *                      row-streaming pass (one workgroup per row, head and partition; the right
+ *                      pass for decode rows).
+ *   tiles, num_tiles : the plan's tile list, int32 [num_tiles, 2] = (first row, row count <= 64):
+ *                      runs of consecutive rows of ONE sequence computed by the fp32 MFMA tile
+ *                      pass (the right pass for prefill chunks). Needs
+ *                      pkv_tile_head_dim_supported(head_dim).
+ *                      Every query row must be in exactly one of the two lists. With rows and
+ *                      tiles both NULL, every row goes through the row-streaming pass.
  *   key_cache,
- *   value_cache      : the layer's pools, [num_blocks, block_size, num_heads, head_dim], kv_dtype.
+ *   value_cache      : the layer's pools, [num_blocks, block_size, num_heads, head_dim], kv_dtype,
+ *                      16-byte aligned.
  *   block_tables     : int32 [num_seqs, block_table_stride], physical block ids in logical order.
  *   context_lens     : int32 [num_seqs], valid cached tokens of each sequence (runner.py:66-68).
  *   max_context_len  : an upper bound of every context_len; it sizes the grid, and visible
  *                      lengths are clamped to it, so block_table_stride * block_size must be
  *                      >= max_context_len (checked).
  *   partition_size   : keys per split-context partition, a positive multiple of 16, <= 1024;
- *                      0 selects the library default.
+ *                      0 selects the library default (512).
  *   workspace        : float32 scratch of pkv_attention_workspace_bytes(...) bytes (may be
  *                      NULL when that is 0).
  * A query whose every key is masked gets a zero output (attention.py:120-121).
@@ -129,13 +145,14 @@ int64_t pkv_attention_workspace_bytes(int64_t num_queries, int32_t num_heads, in
  */
 int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,
                         const int32_t* query_positions, const int32_t* query_seq,
-                        int64_t num_queries, const void* key_cache, const void* value_cache,
-                        pkv_dtype kv_dtype, int64_t num_blocks, int32_t block_size,
-                        const int32_t* block_tables, int32_t block_table_stride,
-                        const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,
-                        int32_t head_dim, float scale, int32_t max_context_len,
-                        int32_t partition_size, float* workspace, int64_t workspace_bytes,
-                        int device, void* stream);
+                        int64_t num_queries, const int32_t* rows, int64_t num_rows,
+                        const int32_t* tiles, int64_t num_tiles, const void* key_cache,
+                        const void* value_cache, pkv_dtype kv_dtype, int64_t num_blocks,
+                        int32_t block_size, const int32_t* block_tables,
+                        int32_t block_table_stride, const int32_t* context_lens,
+                        int32_t num_seqs, int32_t num_heads, int32_t head_dim, float scale,
+                        int32_t max_context_len, int32_t partition_size, float* workspace,
+                        int64_t workspace_bytes, int device, void* stream);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,7 @@ EXPORTED_SYMBOLS = (
     "pkv_append",
     "pkv_copy_blocks",
     "pkv_attention_workspace_bytes",
+    "pkv_tile_head_dim_supported",
     "pkv_paged_attention",
 )
 
@@ -140,9 +141,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pkv_copy_blocks.restype = _c_int
     lib.pkv_attention_workspace_bytes.argtypes = [_i64, _i32, _i32, _i32, _i32]
     lib.pkv_attention_workspace_bytes.restype = _i64
+    lib.pkv_tile_head_dim_supported.argtypes = [_i32]
+    lib.pkv_tile_head_dim_supported.restype = _c_int
     lib.pkv_paged_attention.argtypes = [
         _ptr, _ptr, _i64,  # out, queries, query_token_stride
         _ptr, _ptr, _i64,  # query_positions, query_seq, num_queries
+        _ptr, _i64, _ptr, _i64,  # rows, num_rows, tiles, num_tiles
         _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size
         _ptr, _i32, _ptr, _i32,  # block_tables, block_table_stride, context_lens, num_seqs
         _i32, _i32, ctypes.c_float,  # num_heads, head_dim, scale

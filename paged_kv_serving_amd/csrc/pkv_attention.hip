@@ -1,21 +1,28 @@
-// Paged causal attention over block tables, for ragged batches (decode rows and prefill-chunk
-// rows alike), as two passes:
+// Paged causal attention over block tables for ragged batches: decode rows and prefill-chunk
+// rows of many sequences in one call. Three kernels, launched in order on one stream:
 //
-//  1. partial: one workgroup of kWaves wavefronts per (query row, head, context partition).
-//     The partition's block-table slice is staged in LDS; each wavefront streams whole key and
-//     value token rows of its share of the partition with 16-byte loads (kLpt lanes cover one
-//     token's head row, so one load instruction reads kTpr rows of up to 128 contiguous bytes),
-//     and keeps an online softmax (running max m, running sum l, unnormalised accumulator) per
-//     lane group in registers. The groups are merged through LDS at the end. A query whose
-//     visible context fits one partition writes its final output here.
-//  2. reduce: for queries spanning several partitions, merge the per-partition (m, l, acc)
-//     with the same max-rescaled sum and write the normalised output.
+//  1. row_partial (memory-bound rows, e.g. decode): one workgroup of kWaves wavefronts per
+//     (query row, head, context partition). The partition's slice of the block table is staged
+//     in LDS; each wavefront streams whole key and value token rows of its share of the
+//     partition with non-temporal 16-byte loads (kLpt lanes cover one token's head row) and keeps
+//     an online softmax (running max, running sum, unnormalised accumulator) per lane group in
+//     registers. The lane groups are merged through LDS at the end.
+//  2. tile_partial (compute-bound rows: a run of consecutive prefill rows of one sequence): one
+//     workgroup per (tile of <= 64 rows, head, context partition). Key and value tiles of 16 rows
+//     are staged in padded LDS and shared by 4 wavefronts of 16 queries each; the scores are
+//     computed as S^T = K Q^T and the output as O = P V with v_mfma_f32_16x16x4f32, so every
+//     lane owns one query's four scores per tile and the P operand of the second product is the
+//     lane's own registers.
+//  3. reduce: rows whose visible context spans several partitions merge the per-partition
+//     (max, sum, acc) and write the normalised output. Rows that fit one partition were written
+//     by pass 1 or 2 directly.
 //
 // Scores are kept in base 2: q is pre-multiplied by scale * log2(e), so every exponential is a
-// single v_exp_f32. Softmax is invariant under that change of base.
+// single v_exp_f32; softmax is invariant under the change of base.
 //
-// Every key position a query may read is below min(context_len, position + 1); rows at or
-// beyond it are never loaded, and table entries past the last visible block are never read.
+// Every key position a query may read is below min(context_len, position + 1), clamped to
+// max_context_len; rows at or beyond it are never loaded, and table entries past the last
+// visible block are never read.
 #include <math.h>
 
 #include "pkv_common.h"
@@ -23,8 +30,9 @@
 namespace pkv {
 namespace {
 
-// Tunables (compile-time): wavefronts per workgroup, key rows loaded per wavefront before any
-// of them is used, and whether K/V rows are loaded non-temporally (read-once streams).
+// Tunables (compile-time): wavefronts per row_partial workgroup, key rows loaded per wavefront
+// before any of them is used, and whether row_partial loads K/V rows non-temporally (each row is
+// read once there).
 #ifndef PKV_ATTN_WAVES
 #define PKV_ATTN_WAVES 4
 #endif
@@ -35,11 +43,16 @@ namespace {
 #define PKV_ATTN_NONTEMPORAL 1
 #endif
 
-constexpr int kWaves = PKV_ATTN_WAVES;  // wavefronts per workgroup
+constexpr int kWaves = PKV_ATTN_WAVES;  // wavefronts per row_partial workgroup
 constexpr int kThreads = kWaves * kWave;
-constexpr int kMaxPartition = 1024;   // keys per partition, upper bound
+constexpr int kMaxPartition = 1024;     // keys per partition, upper bound
 constexpr int kDefaultPartition = 512;
 constexpr int kTableSlots = kMaxPartition + 4;  // ceil(P / B) + 1 entries at most
+constexpr int kTileRows = 64;           // query rows per tile_partial workgroup (4 x 16)
+constexpr int kTileKeys = 16;           // keys per LDS tile in tile_partial
+constexpr int kTileThreads = 256;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <typename KVT>
 struct KVTraits;
@@ -52,9 +65,37 @@ struct KVTraits<uint16_t> {  // bfloat16 bits
   static constexpr int kEsize = 2;
 };
 
-// How one wavefront maps onto token rows of a head: kLpt lanes per row, kVpl 16-byte vectors per
-// lane, so each lane owns kDpl = D / kLpt dimensions and a wavefront covers kTpr rows per load
-// round. kRounds rounds (kIterTok rows) are loaded before any of them is used.
+// Everything the three kernels read, passed by value.
+struct Params {
+  float* out;              // [T, H, D]
+  float* ws_acc;           // [T, H, max_parts, D]
+  float* ws_ml;            // [T, H, max_parts, 2]
+  const float* queries;    // row t at t * q_stride
+  int64_t q_stride;
+  const int32_t* q_pos;    // [T]
+  const int32_t* q_seq;    // [T]
+  const int32_t* rows;     // row_partial: grid row -> query row (null: identity)
+  const int32_t* tiles;    // tile_partial: [n, 2] = (first row, row count <= 64)
+  const void* kcache;      // [N, B, H, D]
+  const void* vcache;
+  int64_t num_queries;
+  int64_t num_blocks;
+  const int32_t* tables;   // [S, table_stride]
+  const int32_t* ctx_lens; // [S]
+  int32_t table_stride;
+  int32_t num_seqs;
+  int32_t num_heads;
+  int32_t block_size;
+  int32_t block_shift;     // log2(block_size) when it is a power of two
+  int32_t part_size;
+  int32_t max_parts;
+  int32_t max_ctx;
+  float scale_log2;        // scale * log2(e)
+};
+
+// How one wavefront of row_partial maps onto token rows of a head: kLpt lanes per row, kVpl
+// 16-byte vectors per lane, so each lane owns kDpl = D / kLpt dimensions and a wavefront covers
+// kTpr rows per load round. kRounds rounds (kIterTok rows) are loaded before any is used.
 template <typename KVT, int D>
 struct Layout {
   static constexpr int kEsize = KVTraits<KVT>::kEsize;
@@ -70,7 +111,7 @@ struct Layout {
   static constexpr int kGroups = kWaves * kTpr;  // lane groups per workgroup
 };
 
-// Widen one 16-byte vector into kEpv floats.
+// Widen one 16-byte vector into 4 (float) or 8 (bfloat16) floats.
 __device__ __forceinline__ void widen(const uint4& raw, float* out, float) {
   out[0] = __uint_as_float(raw.x);
   out[1] = __uint_as_float(raw.y);
@@ -88,8 +129,8 @@ __device__ __forceinline__ void widen(const uint4& raw, float* out, uint16_t) {
   out[7] = bf16_hi(raw.w);
 }
 
-// One 16-byte vector of a key or value row.
-__device__ __forceinline__ uint4 load_row(const uint4* p) {
+// One 16-byte vector of a key or value row that is read exactly once.
+__device__ __forceinline__ uint4 load_stream(const uint4* p) {
 #if PKV_ATTN_NONTEMPORAL
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -105,43 +146,76 @@ __device__ __forceinline__ int visible_len(int ctx, int pos) {
   return pos >= ctx ? ctx : pos + 1;
 }
 
+__device__ __forceinline__ int row_visible(const Params& a, int64_t t) {
+  const int seq = a.q_seq[t];
+  if (seq < 0 || seq >= a.num_seqs) return 0;
+  return min(visible_len(a.ctx_lens[seq], a.q_pos[t]), a.max_ctx);
+}
+
+__device__ __forceinline__ int parts_of(int visible, int part_size) {
+  return visible > part_size ? (visible + part_size - 1) / part_size : 1;
+}
+
+template <bool kPow2Block>
+__device__ __forceinline__ int block_of(int pos, const Params& a) {
+  return kPow2Block ? (pos >> a.block_shift) : (pos / a.block_size);
+}
+
+// Stage table entries of blocks [b0, b0 + nb) of sequence `seq` into LDS.
+__device__ __forceinline__ void stage_table(int* s_table, const Params& a, int seq, int b0, int nb,
+                                            int threads) {
+  const int32_t* table = a.tables + static_cast<int64_t>(seq) * a.table_stride + b0;
+  for (int i = threadIdx.x; i < nb; i += threads) s_table[i] = table[i];
+}
+
+// Write one query row's partition result: final output when the row fits one partition,
+// otherwise the unnormalised (max, sum, acc) for the reduce pass.
+__device__ __forceinline__ void store_result(const Params& a, int64_t t, int h, int p, int nparts,
+                                             int d, int D, float acc, float big, float sum,
+                                             bool write_ml) {
+  const int64_t qh = t * a.num_heads + h;
+  if (nparts == 1) {
+    a.out[qh * D + d] = acc / (sum > 0.f ? sum : 1.f);
+  } else {
+    const int64_t slot = qh * a.max_parts + p;
+    a.ws_acc[slot * D + d] = acc;
+    if (write_ml) {
+      a.ws_ml[2 * slot] = big;
+      a.ws_ml[2 * slot + 1] = sum;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Pass 1: row_partial.
+// ---------------------------------------------------------------------------------------------
 template <typename KVT, int D, bool kPow2Block>
-__global__ __launch_bounds__(kThreads) void attention_partial_kernel(
-    float* __restrict__ out, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
-    const float* __restrict__ queries, int64_t q_stride, const int32_t* __restrict__ q_pos,
-    const int32_t* __restrict__ q_seq, const KVT* __restrict__ kcache,
-    const KVT* __restrict__ vcache, int64_t num_blocks, int32_t block_size, int32_t block_shift,
-    const int32_t* __restrict__ tables, int32_t table_stride, const int32_t* __restrict__ ctx_lens,
-    int32_t num_seqs, int32_t num_heads, float scale_log2, int32_t part_size, int32_t max_parts,
-    int32_t max_ctx) {
+__global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   using L = Layout<KVT, D>;
   __shared__ int s_table[kTableSlots];
   __shared__ float s_m[L::kGroups];
   __shared__ float s_l[L::kGroups];
   __shared__ float s_acc[L::kGroups * D];
 
-  // Grid: heads fastest, then partitions, then query rows.
-  const int64_t bid = blockIdx.x;
-  const int h = static_cast<int>(bid % num_heads);
-  const int64_t rest = bid / num_heads;
-  const int p = static_cast<int>(rest % max_parts);
-  const int64_t t = rest / max_parts;
+  // Grid: heads fastest, then partitions, then rows.
+  const uint32_t bid = blockIdx.x;
+  const int h = static_cast<int>(bid % static_cast<uint32_t>(a.num_heads));
+  const uint32_t rest = bid / static_cast<uint32_t>(a.num_heads);
+  const int p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
+  const int64_t r = rest / static_cast<uint32_t>(a.max_parts);
+  const int64_t t = a.rows ? a.rows[r] : r;
+  if (t < 0 || t >= a.num_queries) return;  // a row outside the batch is skipped
 
-  const int seq = q_seq[t];
-  const bool seq_ok = seq >= 0 && seq < num_seqs;
-  const int kv_len = seq_ok ? min(visible_len(ctx_lens[seq], q_pos[t]), max_ctx) : 0;
-  const int nparts = kv_len > part_size ? (kv_len + part_size - 1) / part_size : 1;
+  const int seq = a.q_seq[t];
+  const int kv_len = row_visible(a, t);
+  const int nparts = parts_of(kv_len, a.part_size);
   if (p >= nparts) return;
-  const int kbeg = p * part_size;
-  const int kend = min(kbeg + part_size, kv_len);
+  const int kbeg = p * a.part_size;
+  const int kend = min(kbeg + a.part_size, kv_len);
 
-  // Stage the partition's slice of the block table.
-  const int b0 = kPow2Block ? (kbeg >> block_shift) : (kbeg / block_size);
-  const int nb = kend > kbeg ? (kPow2Block ? ((kend - 1) >> block_shift) : ((kend - 1) / block_size)) - b0 + 1 : 0;
-  if (nb > 0) {
-    const int32_t* table = tables + static_cast<int64_t>(seq) * table_stride + b0;
-    for (int i = threadIdx.x; i < nb; i += kThreads) s_table[i] = table[i];
-  }
+  const int b0 = block_of<kPow2Block>(kbeg, a);
+  const int nb = kend > kbeg ? block_of<kPow2Block>(kend - 1, a) - b0 + 1 : 0;
+  if (nb > 0) stage_table(s_table, a, seq, b0, nb, kThreads);
   __syncthreads();
 
   const int lane = threadIdx.x & (kWave - 1);
@@ -151,12 +225,12 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
 
   float qv[L::kDpl];
   {
-    const float* qrow = queries + t * q_stride + static_cast<int64_t>(h) * D;
+    const float* qrow = a.queries + t * a.q_stride + static_cast<int64_t>(h) * D;
 #pragma unroll
     for (int i = 0; i < L::kVpl; ++i) {
 #pragma unroll
       for (int e = 0; e < L::kEpv; ++e) {
-        qv[i * L::kEpv + e] = qrow[(i * L::kLpt + j) * L::kEpv + e] * scale_log2;
+        qv[i * L::kEpv + e] = qrow[(i * L::kLpt + j) * L::kEpv + e] * a.scale_log2;
       }
     }
   }
@@ -167,8 +241,10 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
 #pragma unroll
   for (int d = 0; d < L::kDpl; ++d) acc[d] = 0.f;
 
+  const KVT* kcache = static_cast<const KVT*>(a.kcache);
+  const KVT* vcache = static_cast<const KVT*>(a.vcache);
   const int64_t head_off = static_cast<int64_t>(h) * D;
-  const int64_t row_stride = static_cast<int64_t>(num_heads) * D;  // elements per token row
+  const int64_t row_stride = static_cast<int64_t>(a.num_heads) * D;  // elements per token row
   const int n_iter = (kend - kbeg + L::kIterTok - 1) / L::kIterTok;
 
   for (int it = wave; it < n_iter; it += kWaves) {
@@ -177,30 +253,30 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
     uint4 vraw[L::kRounds][L::kVpl];
     bool valid[L::kRounds];
 #pragma unroll
-    for (int r = 0; r < L::kRounds; ++r) {
-      const int kpos = base + r * L::kTpr + g;
+    for (int rr = 0; rr < L::kRounds; ++rr) {
+      const int kpos = base + rr * L::kTpr + g;
       bool ok = kpos < kend;
       int64_t row = 0;
       if (ok) {
-        const int lb = (kPow2Block ? (kpos >> block_shift) : (kpos / block_size)) - b0;
-        const int off = kPow2Block ? (kpos & (block_size - 1)) : (kpos - (lb + b0) * block_size);
+        const int lb = block_of<kPow2Block>(kpos, a) - b0;
+        const int off = kpos - (lb + b0) * a.block_size;
         const int blk = s_table[lb];
-        ok = blk >= 0 && blk < num_blocks;
-        row = (static_cast<int64_t>(blk) * block_size + off) * row_stride + head_off;
+        ok = blk >= 0 && blk < a.num_blocks;
+        row = (static_cast<int64_t>(blk) * a.block_size + off) * row_stride + head_off;
       }
-      valid[r] = ok;
+      valid[rr] = ok;
       if (ok) {
         const uint4* kp = reinterpret_cast<const uint4*>(kcache + row);
         const uint4* vp = reinterpret_cast<const uint4*>(vcache + row);
 #pragma unroll
-        for (int i = 0; i < L::kVpl; ++i) kraw[r][i] = load_row(kp + i * L::kLpt + j);
+        for (int i = 0; i < L::kVpl; ++i) kraw[rr][i] = load_stream(kp + i * L::kLpt + j);
 #pragma unroll
-        for (int i = 0; i < L::kVpl; ++i) vraw[r][i] = load_row(vp + i * L::kLpt + j);
+        for (int i = 0; i < L::kVpl; ++i) vraw[rr][i] = load_stream(vp + i * L::kLpt + j);
       } else {
 #pragma unroll
         for (int i = 0; i < L::kVpl; ++i) {
-          kraw[r][i] = make_uint4(0, 0, 0, 0);
-          vraw[r][i] = make_uint4(0, 0, 0, 0);
+          kraw[rr][i] = make_uint4(0, 0, 0, 0);
+          vraw[rr][i] = make_uint4(0, 0, 0, 0);
         }
       }
     }
@@ -208,44 +284,44 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
     // Scores of this lane group's rows (base-2 units), reduced over the kLpt lanes of a row.
     float s[L::kRounds];
 #pragma unroll
-    for (int r = 0; r < L::kRounds; ++r) {
+    for (int rr = 0; rr < L::kRounds; ++rr) {
       float dot = 0.f;
 #pragma unroll
       for (int i = 0; i < L::kVpl; ++i) {
         float kf[L::kEpv];
-        widen(kraw[r][i], kf, KVT{});
+        widen(kraw[rr][i], kf, KVT{});
 #pragma unroll
         for (int e = 0; e < L::kEpv; ++e) dot = fmaf(qv[i * L::kEpv + e], kf[e], dot);
       }
       dot = group_sum<L::kLpt>(dot);
-      s[r] = valid[r] ? dot : -INFINITY;
+      s[rr] = valid[rr] ? dot : -INFINITY;
     }
 
     // Online softmax update.
     float mx = m;
 #pragma unroll
-    for (int r = 0; r < L::kRounds; ++r) mx = fmaxf(mx, s[r]);
+    for (int rr = 0; rr < L::kRounds; ++rr) mx = fmaxf(mx, s[rr]);
     const float shift = mx == -INFINITY ? 0.f : mx;
     const float alpha = fast_exp2(m - shift);
     float pr[L::kRounds];
     float psum = 0.f;
 #pragma unroll
-    for (int r = 0; r < L::kRounds; ++r) {
-      pr[r] = fast_exp2(s[r] - shift);
-      psum += pr[r];
+    for (int rr = 0; rr < L::kRounds; ++rr) {
+      pr[rr] = fast_exp2(s[rr] - shift);
+      psum += pr[rr];
     }
     l = fmaf(l, alpha, psum);
 #pragma unroll
     for (int d = 0; d < L::kDpl; ++d) acc[d] *= alpha;
 #pragma unroll
-    for (int r = 0; r < L::kRounds; ++r) {
+    for (int rr = 0; rr < L::kRounds; ++rr) {
 #pragma unroll
       for (int i = 0; i < L::kVpl; ++i) {
         float vf[L::kEpv];
-        widen(vraw[r][i], vf, KVT{});
+        widen(vraw[rr][i], vf, KVT{});
 #pragma unroll
         for (int e = 0; e < L::kEpv; ++e) {
-          acc[i * L::kEpv + e] = fmaf(pr[r], vf[e], acc[i * L::kEpv + e]);
+          acc[i * L::kEpv + e] = fmaf(pr[rr], vf[e], acc[i * L::kEpv + e]);
         }
       }
     }
@@ -272,129 +348,280 @@ __global__ __launch_bounds__(kThreads) void attention_partial_kernel(
     for (int k = 0; k < L::kGroups; ++k) big = fmaxf(big, s_m[k]);
     const float shift = big == -INFINITY ? 0.f : big;
     float lsum = 0.f;
-    float a = 0.f;
+    float sum_acc = 0.f;
     for (int k = 0; k < L::kGroups; ++k) {
       const float w = fast_exp2(s_m[k] - shift);
       lsum = fmaf(s_l[k], w, lsum);
-      a = fmaf(s_acc[k * D + d], w, a);
+      sum_acc = fmaf(s_acc[k * D + d], w, sum_acc);
     }
-    const int64_t qh = t * num_heads + h;
-    if (nparts == 1) {
-      out[qh * D + d] = a / (lsum > 0.f ? lsum : 1.f);
-    } else {
-      const int64_t slot = qh * max_parts + p;
-      ws_acc[slot * D + d] = a;
-      if (d == 0) {
-        ws_ml[2 * slot] = big;
-        ws_ml[2 * slot + 1] = lsum;
+    store_result(a, t, h, p, nparts, d, D, sum_acc, big, lsum, d == 0);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Pass 2: tile_partial (fp32 MFMA). Lane l of a wavefront is (c = l / 16, n = l % 16).
+//
+//   S^T = K Q^T  with v_mfma_f32_16x16x4f32, kD4 = D / 4 steps. In step s, the k index of lane
+//                group c stands for head dimension c * kD4 + s, so lane (c, n) supplies
+//                A = K[key n][c * kD4 + s] (from LDS) and B = Q[query n][c * kD4 + s] (from
+//                registers). The result holds S[query n][key 4c + r] in register r.
+//   O = P V      four steps per 16-key tile; in step m the k index of lane group c stands for key
+//                4c + m, so A = P[query n][key 4c + m] is the lane's own register m and
+//                B = V[key 4c + m][16b + n] for output tile b. Register r of output tile b holds
+//                O[query 4c + r][16b + n].
+// ---------------------------------------------------------------------------------------------
+template <typename KVT, int D, bool kPow2Block>
+__global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params a) {
+  static_assert(D % 16 == 0 && D >= 32, "the MFMA tile needs whole 16-wide output tiles");
+  constexpr int kRow = D + 4;        // padded LDS row (floats): conflict-free operand reads
+  constexpr int kD4 = D / 4;         // MFMA steps of S^T per key tile
+  constexpr int kNb = D / 16;        // output tiles of 16 dimensions
+  constexpr int kEsize = KVTraits<KVT>::kEsize;
+  constexpr int kEpv = 16 / kEsize;  // elements per 16-byte vector
+  constexpr int kVecPerRow = D / kEpv;
+  __shared__ int s_table[kTableSlots];
+  __shared__ float s_k[kTileKeys * kRow];
+  __shared__ float s_v[kTileKeys * kRow];
+  __shared__ int s_vis[kTileRows];
+
+  const uint32_t bid = blockIdx.x;
+  const int h = static_cast<int>(bid % static_cast<uint32_t>(a.num_heads));
+  const uint32_t rest = bid / static_cast<uint32_t>(a.num_heads);
+  const int p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
+  const int64_t tile = rest / static_cast<uint32_t>(a.max_parts);
+  const int64_t t0 = a.tiles[2 * tile];
+  if (t0 < 0 || t0 >= a.num_queries) return;  // a tile outside the batch is skipped
+  const int nrows = static_cast<int>(min<int64_t>(min(a.tiles[2 * tile + 1], kTileRows), a.num_queries - t0));
+  const int seq = a.q_seq[t0];
+
+  if (threadIdx.x < kTileRows) {
+    s_vis[threadIdx.x] = static_cast<int>(threadIdx.x) < nrows ? row_visible(a, t0 + threadIdx.x) : 0;
+  }
+  __syncthreads();
+  int tile_vis = 0;
+  for (int i = 0; i < kTileRows; ++i) tile_vis = max(tile_vis, s_vis[i]);
+  const int nparts = parts_of(tile_vis, a.part_size);
+  if (p >= nparts) return;
+  const int kbeg = p * a.part_size;
+  const int kend = min(kbeg + a.part_size, tile_vis);
+  const int b0 = block_of<kPow2Block>(kbeg, a);
+  const int nb = kend > kbeg ? block_of<kPow2Block>(kend - 1, a) - b0 + 1 : 0;
+  if (nb > 0) stage_table(s_table, a, seq, b0, nb, kTileThreads);
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int c = lane >> 4;
+  const int n = lane & 15;
+  const int qi = wave * 16 + n;  // this lane's query in the S^T layout
+  const int my_vis = s_vis[qi];
+  const bool q_ok = qi < nrows;
+
+  float qreg[kD4];
+  {
+    const int64_t row = t0 + (q_ok ? qi : 0);  // lanes past the tile read row t0, then drop it
+    const float* qrow = a.queries + row * a.q_stride + static_cast<int64_t>(h) * D + c * kD4;
+#pragma unroll
+    for (int s = 0; s < kD4; ++s) qreg[s] = q_ok ? qrow[s] * a.scale_log2 : 0.f;
+  }
+
+  floatx4 o[kNb];
+#pragma unroll
+  for (int b = 0; b < kNb; ++b) o[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY;
+  float l = 0.f;
+
+  const KVT* kcache = static_cast<const KVT*>(a.kcache);
+  const KVT* vcache = static_cast<const KVT*>(a.vcache);
+  const int64_t head_off = static_cast<int64_t>(h) * D;
+  const int64_t row_stride = static_cast<int64_t>(a.num_heads) * D;
+  __syncthreads();  // s_table ready
+
+  for (int k0 = kbeg; k0 < kend; k0 += kTileKeys) {
+    // Stage kTileKeys key and value rows (zeros past kend) as float32.
+    for (int v = threadIdx.x; v < kTileKeys * kVecPerRow; v += kTileThreads) {
+      const int row = v / kVecPerRow;
+      const int col = (v - row * kVecPerRow) * kEpv;
+      const int kpos = k0 + row;
+      float kf[kEpv];
+      float vf[kEpv];
+      bool ok = kpos < kend;
+      int64_t off = 0;
+      if (ok) {
+        const int lb = block_of<kPow2Block>(kpos, a) - b0;
+        const int blk = s_table[lb];
+        ok = blk >= 0 && blk < a.num_blocks;
+        off = (static_cast<int64_t>(blk) * a.block_size + (kpos - (lb + b0) * a.block_size)) *
+                  row_stride + head_off + col;
       }
+      if (ok) {
+        widen(*reinterpret_cast<const uint4*>(kcache + off), kf, KVT{});
+        widen(*reinterpret_cast<const uint4*>(vcache + off), vf, KVT{});
+      } else {
+#pragma unroll
+        for (int e = 0; e < kEpv; ++e) kf[e] = vf[e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < kEpv; e += 4) {
+        *reinterpret_cast<float4*>(&s_k[row * kRow + col + e]) =
+            make_float4(kf[e], kf[e + 1], kf[e + 2], kf[e + 3]);
+        *reinterpret_cast<float4*>(&s_v[row * kRow + col + e]) =
+            make_float4(vf[e], vf[e + 1], vf[e + 2], vf[e + 3]);
+      }
+    }
+    __syncthreads();
+
+    // S^T tile: register r = S[query n][key 4c + r].
+    floatx4 st = {0.f, 0.f, 0.f, 0.f};
+    const float* krow = &s_k[n * kRow + c * kD4];
+#pragma unroll
+    for (int s = 0; s < kD4; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[s], qreg[s], st, 0, 0, 0);
+
+    const int lim = min(my_vis, kend);
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = (k0 + 4 * c + r) < lim ? st[r] : -INFINITY;
+    float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float shift = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2(m - shift);
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sc[r] - shift);
+    float ps = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l = fmaf(l, alpha, ps);
+    m = m_new;
+
+    // Rescale the output rows (queries 4c + r) by their queries' alpha.
+    float ar[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * c + r);
+#pragma unroll
+    for (int b = 0; b < kNb; ++b) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[b][r] *= ar[r];
+    }
+
+    // O += P V.
+#pragma unroll
+    for (int step = 0; step < 4; ++step) {
+      const float* vrow = &s_v[(4 * c + step) * kRow + n];
+#pragma unroll
+      for (int b = 0; b < kNb; ++b) {
+        o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[step], vrow[16 * b], o[b], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: register r of tile b is O[query 4c + r][16b + n].
+  float lr[4];
+  float mr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    lr[r] = __shfl(l, 4 * c + r);
+    mr[r] = __shfl(m, 4 * c + r);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int qq = wave * 16 + 4 * c + r;
+    if (qq >= nrows) continue;
+    const int row_parts = parts_of(s_vis[qq], a.part_size);
+    if (p >= row_parts) continue;
+#pragma unroll
+    for (int b = 0; b < kNb; ++b) {
+      store_result(a, t0 + qq, h, p, row_parts, 16 * b + n, D, o[b][r], mr[r], lr[r],
+                   b == 0 && n == 0);
     }
   }
 }
 
-// One workgroup per (query row, head); thread d owns output dimension d.
+// ---------------------------------------------------------------------------------------------
+// Pass 3: reduce. One workgroup per (query row, head); thread d owns output dimension d.
+// ---------------------------------------------------------------------------------------------
 template <int D>
-__global__ __launch_bounds__(D < kWave ? kWave : D) void attention_reduce_kernel(
-    float* __restrict__ out, const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
-    const int32_t* __restrict__ q_pos, const int32_t* __restrict__ q_seq,
-    const int32_t* __restrict__ ctx_lens, int32_t num_seqs, int32_t num_heads, int32_t part_size,
-    int32_t max_parts, int32_t max_ctx) {
+__global__ __launch_bounds__(D < kWave ? kWave : D) void reduce_kernel(const Params a) {
   const int64_t qh = blockIdx.x;
-  const int64_t t = qh / num_heads;
-  const int seq = q_seq[t];
-  const bool seq_ok = seq >= 0 && seq < num_seqs;
-  const int kv_len = seq_ok ? min(visible_len(ctx_lens[seq], q_pos[t]), max_ctx) : 0;
-  const int nparts = kv_len > part_size ? (kv_len + part_size - 1) / part_size : 1;
+  const int64_t t = qh / a.num_heads;
+  const int nparts = parts_of(row_visible(a, t), a.part_size);
   if (nparts == 1) return;  // written by the partial pass
   const int d = threadIdx.x;
   if (d >= D) return;
-  const float* ml = ws_ml + 2 * qh * max_parts;
+  const float* ml = a.ws_ml + 2 * qh * a.max_parts;
   float big = -INFINITY;
   for (int k = 0; k < nparts; ++k) big = fmaxf(big, ml[2 * k]);
   const float shift = big == -INFINITY ? 0.f : big;
   float lsum = 0.f;
-  float a = 0.f;
-  const float* acc = ws_acc + qh * max_parts * D;
+  float acc = 0.f;
+  const float* part = a.ws_acc + qh * a.max_parts * D;
   for (int k = 0; k < nparts; ++k) {
     const float w = fast_exp2(ml[2 * k] - shift);
     lsum = fmaf(ml[2 * k + 1], w, lsum);
-    a = fmaf(acc[static_cast<int64_t>(k) * D + d], w, a);
+    acc = fmaf(part[static_cast<int64_t>(k) * D + d], w, acc);
   }
-  out[qh * D + d] = a / (lsum > 0.f ? lsum : 1.f);
+  a.out[qh * D + d] = acc / (lsum > 0.f ? lsum : 1.f);
 }
 
-struct AttnArgs {
-  float* out;
-  const float* queries;
-  int64_t q_stride;
-  const int32_t* q_pos;
-  const int32_t* q_seq;
-  int64_t num_queries;
-  const void* kcache;
-  const void* vcache;
-  int64_t num_blocks;
-  int32_t block_size;
-  const int32_t* tables;
-  int32_t table_stride;
-  const int32_t* ctx_lens;
-  int32_t num_seqs;
-  int32_t num_heads;
-  float scale_log2;
-  int32_t part_size;
-  int32_t max_parts;
-  int32_t max_ctx;
-  float* ws_acc;
-  float* ws_ml;
-};
-
 template <typename KVT, int D>
-int launch_attention(const AttnArgs& a, hipStream_t stream) {
-  const int64_t groups = a.num_queries * a.max_parts * a.num_heads;
-  if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
-  const int bs = a.block_size;
-  const bool pow2 = (bs & (bs - 1)) == 0;
-  int shift = 0;
-  while ((1 << shift) < bs) ++shift;
-  const auto* kc = static_cast<const KVT*>(a.kcache);
-  const auto* vc = static_cast<const KVT*>(a.vcache);
-  if (pow2) {
-    hipLaunchKernelGGL((attention_partial_kernel<KVT, D, true>), dim3(static_cast<uint32_t>(groups)),
-                       dim3(kThreads), 0, stream, a.out, a.ws_acc, a.ws_ml, a.queries, a.q_stride,
-                       a.q_pos, a.q_seq, kc, vc, a.num_blocks, bs, shift, a.tables,
-                       a.table_stride, a.ctx_lens, a.num_seqs, a.num_heads, a.scale_log2,
-                       a.part_size, a.max_parts, a.max_ctx);
-  } else {
-    hipLaunchKernelGGL((attention_partial_kernel<KVT, D, false>),
-                       dim3(static_cast<uint32_t>(groups)), dim3(kThreads), 0, stream, a.out,
-                       a.ws_acc, a.ws_ml, a.queries, a.q_stride, a.q_pos, a.q_seq, kc, vc,
-                       a.num_blocks, bs, 0, a.tables, a.table_stride, a.ctx_lens, a.num_seqs,
-                       a.num_heads, a.scale_log2, a.part_size, a.max_parts, a.max_ctx);
+int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t num_tiles,
+               hipStream_t stream) {
+  const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
+  const int64_t per_row = static_cast<int64_t>(a.max_parts) * a.num_heads;
+  if (num_tiles > 0) {
+    if constexpr (D % 16 == 0 && D >= 32) {
+      const int64_t groups = num_tiles * per_row;
+      if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
+      const dim3 grid(static_cast<uint32_t>(groups));
+      if (pow2) {
+        hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true>), grid, dim3(kTileThreads), 0, stream, a);
+      } else {
+        hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false>), grid, dim3(kTileThreads), 0, stream, a);
+      }
+      if (check_launch() != PKV_OK) return PKV_EHIP;
+    } else {
+      return PKV_EUNSUPPORTED;
+    }
   }
-  int rc = check_launch();
-  if (rc != PKV_OK || a.max_parts == 1) return rc;
-  const int64_t rows = a.num_queries * a.num_heads;
-  hipLaunchKernelGGL((attention_reduce_kernel<D>), dim3(static_cast<uint32_t>(rows)),
-                     dim3(D < kWave ? kWave : D), 0, stream, a.out, a.ws_acc, a.ws_ml, a.q_pos,
-                     a.q_seq, a.ctx_lens, a.num_seqs, a.num_heads, a.part_size, a.max_parts,
-                     a.max_ctx);
-  return check_launch();
+  if (num_rows > 0) {
+    const int64_t groups = num_rows * per_row;
+    if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
+    const dim3 grid(static_cast<uint32_t>(groups));
+    if (pow2) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, true>), grid, dim3(kThreads), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, false>), grid, dim3(kThreads), 0, stream, a);
+    }
+    if (check_launch() != PKV_OK) return PKV_EHIP;
+  }
+  if (a.max_parts > 1) {
+    const int64_t groups = num_queries * a.num_heads;
+    if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
+    hipLaunchKernelGGL((reduce_kernel<D>), dim3(static_cast<uint32_t>(groups)),
+                       dim3(D < kWave ? kWave : D), 0, stream, a);
+    if (check_launch() != PKV_OK) return PKV_EHIP;
+  }
+  return PKV_OK;
 }
 
 template <typename KVT>
-int dispatch_head_dim(int head_dim, const AttnArgs& a, hipStream_t stream) {
+int dispatch_head_dim(int head_dim, const Params& a, int64_t num_queries, int64_t num_rows,
+                      int64_t num_tiles, hipStream_t stream) {
   switch (head_dim) {
     case 8:
-      return launch_attention<KVT, 8>(a, stream);
+      return launch_all<KVT, 8>(a, num_queries, num_rows, num_tiles, stream);
     case 16:
-      return launch_attention<KVT, 16>(a, stream);
+      return launch_all<KVT, 16>(a, num_queries, num_rows, num_tiles, stream);
     case 32:
-      return launch_attention<KVT, 32>(a, stream);
+      return launch_all<KVT, 32>(a, num_queries, num_rows, num_tiles, stream);
     case 64:
-      return launch_attention<KVT, 64>(a, stream);
+      return launch_all<KVT, 64>(a, num_queries, num_rows, num_tiles, stream);
     case 128:
-      return launch_attention<KVT, 128>(a, stream);
+      return launch_all<KVT, 128>(a, num_queries, num_rows, num_tiles, stream);
     case 256:
-      return launch_attention<KVT, 256>(a, stream);
+      return launch_all<KVT, 256>(a, num_queries, num_rows, num_tiles, stream);
     default:
       return PKV_EUNSUPPORTED;
   }
@@ -428,9 +655,14 @@ extern "C" int64_t pkv_attention_workspace_bytes(int64_t num_queries, int32_t nu
          static_cast<int64_t>(sizeof(float));
 }
 
+extern "C" int pkv_tile_head_dim_supported(int32_t head_dim) {
+  return head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
+}
+
 extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,
                                    const int32_t* query_positions, const int32_t* query_seq,
-                                   int64_t num_queries, const void* key_cache,
+                                   int64_t num_queries, const int32_t* rows, int64_t num_rows,
+                                   const int32_t* tiles, int64_t num_tiles, const void* key_cache,
                                    const void* value_cache, pkv_dtype kv_dtype, int64_t num_blocks,
                                    int32_t block_size, const int32_t* block_tables,
                                    int32_t block_table_stride, const int32_t* context_lens,
@@ -441,8 +673,9 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   using namespace pkv;
   const int part = resolve_partition(partition_size);
   if (part < 0) return PKV_EINVAL;
-  if (num_queries < 0 || num_blocks < 1 || block_size < 1 || block_table_stride < 0 ||
-      num_seqs < 0 || num_heads < 1 || head_dim < 1 || max_context_len < 0) {
+  if (num_queries < 0 || num_rows < 0 || num_tiles < 0 || num_blocks < 1 || block_size < 1 ||
+      block_table_stride < 0 || num_seqs < 0 || num_heads < 1 || head_dim < 1 ||
+      max_context_len < 0) {
     return PKV_EINVAL;
   }
   if (dtype_size(kv_dtype) == 0) return PKV_EINVAL;
@@ -456,6 +689,15 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
     return PKV_EINVAL;
   }
   if (!aligned16(key_cache) || !aligned16(value_cache)) return PKV_EINVAL;
+  // Without a plan (rows and tiles both null) every query goes through the row pass.
+  if (!rows && !tiles) {
+    num_rows = num_queries;
+    num_tiles = 0;
+  }
+  if ((num_rows > 0 && !rows && num_rows != num_queries) || (num_tiles > 0 && !tiles)) {
+    return PKV_EINVAL;
+  }
+  if (num_tiles > 0 && !pkv_tile_head_dim_supported(head_dim)) return PKV_EUNSUPPORTED;
   const int64_t parts = parts_for(max_context_len, part);
   if (parts > 0x7fffffff) return PKV_EUNSUPPORTED;
   float* ws_acc = nullptr;
@@ -470,29 +712,34 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   DeviceGuard guard(device);
   if (!guard.ok()) return PKV_EHIP;
   (void)hipGetLastError();
-  const double log2e = 1.4426950408889634;
-  AttnArgs a{out,
-             queries,
-             query_token_stride,
-             query_positions,
-             query_seq,
-             num_queries,
-             key_cache,
-             value_cache,
-             num_blocks,
-             block_size,
-             block_tables,
-             block_table_stride,
-             context_lens,
-             num_seqs,
-             num_heads,
-             static_cast<float>(static_cast<double>(scale) * log2e),
-             part,
-             static_cast<int32_t>(parts),
-             max_context_len,
-             ws_acc,
-             ws_ml};
+  int shift = 0;
+  while ((1 << shift) < block_size) ++shift;
+  Params a{};
+  a.out = out;
+  a.ws_acc = ws_acc;
+  a.ws_ml = ws_ml;
+  a.queries = queries;
+  a.q_stride = query_token_stride;
+  a.q_pos = query_positions;
+  a.q_seq = query_seq;
+  a.rows = rows;
+  a.tiles = tiles;
+  a.kcache = key_cache;
+  a.vcache = value_cache;
+  a.num_queries = num_queries;
+  a.num_blocks = num_blocks;
+  a.tables = block_tables;
+  a.ctx_lens = context_lens;
+  a.table_stride = block_table_stride;
+  a.num_seqs = num_seqs;
+  a.num_heads = num_heads;
+  a.block_size = block_size;
+  a.block_shift = shift;
+  a.part_size = part;
+  a.max_parts = static_cast<int32_t>(parts);
+  a.max_ctx = max_context_len;
+  a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   auto s = static_cast<hipStream_t>(stream);
-  if (kv_dtype == PKV_F32) return dispatch_head_dim<float>(head_dim, a, s);
-  return dispatch_head_dim<uint16_t>(head_dim, a, s);
+  if (kv_dtype == PKV_F32) return dispatch_head_dim<float>(head_dim, a, num_queries, num_rows, num_tiles, s);
+  return dispatch_head_dim<uint16_t>(head_dim, a, num_queries, num_rows, num_tiles, s);
 }

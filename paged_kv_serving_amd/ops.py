@@ -8,17 +8,32 @@ the tensors' device). Nothing here computes on the CPU: a missing library raises
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
+import numpy as np
 import torch
 
 from paged_kv_serving_amd import _native
 
 __all__ = [
+    "AttentionPlan",
+    "MIN_TILE_ROWS",
+    "TILE_ROWS",
     "append_kv",
     "attention_workspace_bytes",
     "copy_blocks",
+    "independent_groups",
     "kv_dtype_code",
     "paged_attention_ragged",
+    "plan_rows",
+    "upload_plan",
 ]
+
+#: Rows per MFMA tile (4 wavefronts x 16 queries).
+TILE_ROWS = 64
+#: A run of at least this many consecutive rows of one sequence is computed as MFMA tiles; the
+#: row-streaming pass reads a sequence's keys once per row, the tile pass once per 64 rows.
+MIN_TILE_ROWS = 8
 
 _DTYPE_CODES = {torch.float32: _native.PKV_F32, torch.bfloat16: _native.PKV_BF16}
 
@@ -142,6 +157,60 @@ def independent_groups(pairs: list[tuple[int, int]]) -> list[list[tuple[int, int
     return groups
 
 
+@dataclass(frozen=True)
+class AttentionPlan:
+    """Which query rows go to which attention pass, as int32 device tensors.
+
+    ``rows``: rows for the row-streaming pass; ``tiles``: ``[n, 2]`` (first row, row count) runs
+    of consecutive rows of one sequence for the MFMA tile pass. Every query row is in exactly
+    one of them.
+    """
+
+    rows: torch.Tensor
+    tiles: torch.Tensor
+
+    @property
+    def num_rows(self) -> int:
+        return int(self.rows.shape[0])
+
+    @property
+    def num_tiles(self) -> int:
+        return int(self.tiles.shape[0])
+
+
+def plan_rows(
+    query_seq: np.ndarray, head_dim: int, *, min_tile_rows: int = MIN_TILE_ROWS
+) -> tuple[np.ndarray, np.ndarray]:
+    """Split a ragged batch's rows between the two attention passes (host, int32).
+
+    Runs of at least ``min_tile_rows`` consecutive rows with the same sequence index become
+    tiles of at most ``TILE_ROWS`` rows (when the head_dim has a tile kernel); every other row
+    goes to the row-streaming pass. Returns ``(rows [R], tiles [n, 2])``.
+    """
+    seq = np.asarray(query_seq, dtype=np.int64)
+    total = seq.size
+    tiled = bool(_native.library().pkv_tile_head_dim_supported(head_dim))
+    if total == 0:
+        return np.zeros(0, np.int32), np.zeros((0, 2), np.int32)
+    starts = np.flatnonzero(np.concatenate([[True], seq[1:] != seq[:-1]]))
+    ends = np.concatenate([starts[1:], [total]])
+    rows, tiles = [], []
+    for start, end in zip(starts.tolist(), ends.tolist()):
+        if tiled and end - start >= min_tile_rows:
+            for first in range(start, end, TILE_ROWS):
+                tiles.append((first, min(TILE_ROWS, end - first)))
+        else:
+            rows.extend(range(start, end))
+    return np.asarray(rows, dtype=np.int32), np.asarray(tiles, dtype=np.int32).reshape(-1, 2)
+
+
+def upload_plan(rows: np.ndarray, tiles: np.ndarray, device: torch.device) -> AttentionPlan:
+    """Copy a host plan to the device in one transfer."""
+    packed = np.concatenate([rows.astype(np.int32), tiles.astype(np.int32).ravel()])
+    data = torch.from_numpy(packed).to(device)
+    return AttentionPlan(rows=data[: rows.size], tiles=data[rows.size :].view(-1, 2))
+
+
 def attention_workspace_bytes(
     num_queries: int, num_heads: int, head_dim: int, max_context_len: int, partition_size: int = 0
 ) -> int:
@@ -168,6 +237,7 @@ def paged_attention_ragged(
     partition_size: int = 0,
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    plan: AttentionPlan | None = None,
 ) -> torch.Tensor:
     """Causal paged attention of every query row of a ragged batch, in one call.
 
@@ -175,6 +245,8 @@ def paged_attention_ragged(
     ``query_seq``: int32 ``[T]``; ``key_cache``/``value_cache``: one layer's pools
     ``[num_blocks, block_size, H, D]``; ``block_tables``: int32 ``[S, max_blocks]``;
     ``context_lens``: int32 ``[S]``; ``max_context_len`` bounds every context length.
+    ``plan`` (from :func:`plan_rows` + :func:`upload_plan`) routes prefill runs to the MFMA tile
+    pass; without one every row takes the row-streaming pass.
     Returns float32 ``[T, H, D]``. Semantics of reference attention.py:42-121 for each query.
     """
     device = _device_index(
@@ -215,9 +287,25 @@ def paged_attention_ragged(
         workspace = torch.empty(need // 4, dtype=torch.float32, device=queries.device)
     ws_ptr = workspace.data_ptr() if need else None
     ws_bytes = workspace.numel() * workspace.element_size() if need else 0
+    rows_ptr = tiles_ptr = None
+    num_rows = num_tiles = 0
+    if plan is not None:
+        for name, tensor in (("rows", plan.rows), ("tiles", plan.tiles)):
+            if tensor.dtype != torch.int32 or tensor.device != queries.device:
+                raise ValueError(f"plan.{name} must be an int32 tensor on the queries' device")
+        if plan.tiles.dim() != 2 or plan.tiles.shape[1] != 2 or not plan.tiles.is_contiguous():
+            raise ValueError("plan.tiles must be contiguous int32 of shape (n, 2)")
+        if plan.num_rows + 0 > num_queries:
+            raise ValueError("plan.rows lists more rows than the batch has")
+        num_rows, num_tiles = plan.num_rows, plan.num_tiles
+        rows_ptr = plan.rows.data_ptr() if num_rows else None
+        tiles_ptr = plan.tiles.data_ptr() if num_tiles else None
+        if num_rows == 0 and num_tiles == 0:
+            return out
     rc = _native.library().pkv_paged_attention(
         out.data_ptr(), queries.data_ptr(), stride,
         query_positions.data_ptr(), query_seq.data_ptr(), num_queries,
+        rows_ptr, num_rows, tiles_ptr, num_tiles,
         key_cache.data_ptr(), value_cache.data_ptr(), kv_dtype_code(key_cache.dtype),
         key_cache.shape[0], key_cache.shape[1],
         block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(), num_seqs,

@@ -7,8 +7,9 @@ exactly like the reference's NumPy pools (runner.py:112-114), and is both the re
 
     torch (hipBLASLt) : RMSNorm, fused QKV projection, RoPE on q and k
     pkv_append        : scatter this iteration's keys/values into their slots (one launch)
-    pkv_paged_attention : every query of the ragged batch against its block table (one launch,
-                          plus the split-context reduce when a context spans partitions)
+    pkv_paged_attention : every query of the ragged batch against its block table in one call:
+                          decode rows stream K/V per row, prefill runs go to the fp32 MFMA tile
+                          pass, then the split-context reduce when a context spans partitions
     torch             : output projection, SwiGLU
 
 Slot mappings are computed on the host with the reference's closed form and validation
@@ -289,15 +290,24 @@ class ModelRunner:
             tables[row, : len(entry.block_table)] = entry.block_table
         context = np.fromiter((e.positions[-1] + 1 for e in entries), dtype=np.int32, count=num_seqs)
         query_seq = np.repeat(np.arange(num_seqs, dtype=np.int32), [len(e.token_ids) for e in entries])
+        plan_rows, plan_tiles = ops.plan_rows(query_seq, config.head_dim)
         meta64 = torch.from_numpy(np.concatenate([tokens, positions, slots])).to(self.device)
         meta32 = torch.from_numpy(
-            np.concatenate([positions.astype(np.int32), query_seq, context, tables.ravel()])
+            np.concatenate([
+                positions.astype(np.int32), query_seq, context, tables.ravel(),
+                plan_rows, plan_tiles.ravel(),
+            ])  # fmt: skip
         ).to(self.device)
         tokens_d, positions_d, slots_d = meta64[:total], meta64[total : 2 * total], meta64[2 * total :]
         qpos_d = meta32[:total]
         qseq_d = meta32[total : 2 * total]
         context_d = meta32[2 * total : 2 * total + num_seqs]
-        tables_d = meta32[2 * total + num_seqs :].view(num_seqs, width)
+        end_tables = 2 * total + num_seqs + num_seqs * width
+        tables_d = meta32[2 * total + num_seqs : end_tables].view(num_seqs, width)
+        plan = ops.AttentionPlan(
+            rows=meta32[end_tables : end_tables + plan_rows.size],
+            tiles=meta32[end_tables + plan_rows.size :].view(-1, 2),
+        )
         max_context = int(context.max())
 
         self.flush_copies()
@@ -322,7 +332,7 @@ class ModelRunner:
             ops.paged_attention_ragged(
                 queries, qpos_d, qseq_d, self._keys[index], self._values[index], tables_d,
                 context_d, scale, max_context_len=max_context,
-                partition_size=self.partition_size, out=attended, workspace=workspace,
+                partition_size=self.partition_size, out=attended, workspace=workspace, plan=plan,
             )  # fmt: skip
             hidden = hidden + attended.view(total, d_model) @ out_proj
             normed = _rms_norm(hidden, ffn_norm, eps)

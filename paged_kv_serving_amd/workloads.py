@@ -18,6 +18,8 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
+from paged_kv_serving_amd import ops
+
 __all__ = [
     "AttentionBatch",
     "decode_batch",
@@ -42,6 +44,7 @@ class AttentionBatch:
     context_lens: torch.Tensor  # int32 [S]
     max_context_len: int
     scale: float
+    plan: ops.AttentionPlan | None = None  # prefill runs -> MFMA tiles, other rows -> row pass
     # Host copies of the integer metadata (bit-exact with the device tensors).
     host_tables: list[np.ndarray] = field(default_factory=list)
     host_context: np.ndarray | None = None
@@ -135,6 +138,7 @@ def _assemble(
     padded = np.zeros((len(tables), width), dtype=np.int32)
     for i, table in enumerate(tables):
         padded[i, : len(table)] = table
+    plan = ops.upload_plan(*ops.plan_rows(seq, head_dim), device)
     return AttentionBatch(
         key_cache=key_cache,
         value_cache=value_cache,
@@ -148,6 +152,7 @@ def _assemble(
         context_lens=torch.from_numpy(context.astype(np.int32)).to(device),
         max_context_len=int(context.max()),
         scale=float(head_dim) ** -0.5,
+        plan=plan,
         host_tables=tables,
         host_context=context.astype(np.int64),
         host_positions=positions.astype(np.int64),

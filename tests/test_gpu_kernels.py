@@ -163,7 +163,7 @@ def test_dependent_copies_apply_in_order(device) -> None:
 # --- attention --------------------------------------------------------------------------------
 
 
-def _ragged_case(rng, *, heads, dim, block, pool, seqs, max_ctx, prefill):
+def _ragged_case(rng, *, heads, dim, block, pool, seqs, max_ctx, prefill, max_rows=9):
     """Random ragged batch: each sequence gets 1 (decode) or several (prefill chunk) queries."""
     kc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
     vc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
@@ -177,7 +177,7 @@ def _ragged_case(rng, *, heads, dim, block, pool, seqs, max_ctx, prefill):
         offset += n
     positions, seq_of = [], []
     for s, c in enumerate(contexts):
-        nq = int(rng.integers(1, min(int(c), 9) + 1)) if prefill else 1
+        nq = int(rng.integers(1, min(int(c), max_rows) + 1)) if prefill else 1
         positions += list(range(int(c) - nq, int(c)))
         seq_of += [s] * nq
     q = rng.standard_normal((len(positions), heads, dim)).astype(np.float32)
@@ -185,20 +185,23 @@ def _ragged_case(rng, *, heads, dim, block, pool, seqs, max_ctx, prefill):
 
 
 def _run_kernel(device, kc, vc, tables, contexts, positions, seq_of, q, scale, *, partition=0,
-                dtype=torch.float32):  # fmt: skip
+                dtype=torch.float32, tiles=False):  # fmt: skip
     width = max(len(t) for t in tables)
     padded = np.full((len(tables), width), -7, dtype=np.int32)  # padding is never read
     for i, t in enumerate(tables):
         padded[i, : len(t)] = t
     dk = torch.from_numpy(kc).to(device).to(dtype)
     dv = torch.from_numpy(vc).to(device).to(dtype)
+    plan = None
+    if tiles:  # runs of >= 2 rows of one sequence go to the MFMA tile pass
+        plan = ops.upload_plan(*ops.plan_rows(seq_of, q.shape[2], min_tile_rows=2), device)
     out = ops.paged_attention_ragged(
         torch.from_numpy(q).to(device),
         torch.from_numpy(positions.astype(np.int32)).to(device),
         torch.from_numpy(seq_of.astype(np.int32)).to(device),
         dk, dv, torch.from_numpy(padded).to(device),
         torch.from_numpy(contexts.astype(np.int32)).to(device),
-        scale, max_context_len=int(contexts.max()), partition_size=partition,
+        scale, max_context_len=int(contexts.max()), partition_size=partition, plan=plan,
     )  # fmt: skip
     return out.cpu().numpy()
 
@@ -214,21 +217,64 @@ def _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale):
     return out, dense
 
 
+@pytest.mark.parametrize("tiles", [False, True], ids=["rows", "tiles"])
 @pytest.mark.parametrize("dim", [8, 16, 32, 64, 128, 256])
 @pytest.mark.parametrize("block", [1, 3, 4, 16, 32])
-def test_ragged_attention_matches_the_oracle(device, dim, block) -> None:
-    say("ragged attention", dim, block)
+def test_ragged_attention_matches_the_oracle(device, dim, block, tiles) -> None:
+    say("ragged attention", dim, block, tiles)
     rng = np.random.default_rng(dim * 100 + block)
     heads = 2 if dim >= 128 else 3
     max_ctx = 700 if block > 1 else 300
     case = _ragged_case(rng, heads=heads, dim=dim, block=block, pool=5 * max_ctx // block + 8,
                         seqs=5, max_ctx=max_ctx, prefill=True)  # fmt: skip
     scale = dim**-0.5
+    want, dense = _oracle(*case, scale)
     for partition in (0, 16, 48, 1024):
-        got = _run_kernel(device, *case, scale, partition=partition)
-        want, dense = _oracle(*case, scale)
+        got = _run_kernel(device, *case, scale, partition=partition, tiles=tiles)
         assert np.max(np.abs(got - want)) < FP32_TOL, partition
         assert np.max(np.abs(got - dense)) < FP32_TOL, partition
+
+
+@pytest.mark.parametrize("dim", [32, 64, 128, 256])
+@pytest.mark.parametrize("kv", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_long_prefill_runs_through_the_mfma_tiles(device, dim, kv) -> None:
+    """Runs of up to 150 rows: several full and partial 64-row tiles, causal inside the chunk,
+    mixed with decode rows, across partition sizes."""
+    say("mfma tiles", dim, kv)
+    rng = np.random.default_rng(dim + 7)
+    case = _ragged_case(rng, heads=2, dim=dim, block=16, pool=300, seqs=6, max_ctx=700,
+                        prefill=True, max_rows=150)  # fmt: skip
+    kc, vc, tables, contexts, positions, seq_of, q = case
+    scale = dim**-0.5
+    if kv == torch.bfloat16:
+        kc, vc = bf16_round(kc), bf16_round(vc)
+    want, dense = _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale)
+    rows, tile_list = ops.plan_rows(seq_of, dim, min_tile_rows=2)
+    assert len(tile_list) >= 3 and any(n < 64 for _, n in tile_list)
+    for partition in (0, 128, 1024):
+        got = _run_kernel(device, kc, vc, tables, contexts, positions, seq_of, q, scale,
+                          partition=partition, dtype=kv, tiles=True)  # fmt: skip
+        assert np.max(np.abs(got - want)) < FP32_TOL, partition
+        assert np.max(np.abs(got - dense)) < FP32_TOL, partition
+
+
+def test_tile_rows_with_arbitrary_positions_and_no_visible_keys(device) -> None:
+    """A tile's rows need not be consecutive positions; a row with position < 0 sees nothing."""
+    say("tile positions")
+    rng = np.random.default_rng(5)
+    heads, dim, block = 2, 64, 16
+    kc = rng.standard_normal((20, block, heads, dim)).astype(np.float32)
+    vc = rng.standard_normal((20, block, heads, dim)).astype(np.float32)
+    table = rng.permutation(20)[:12]
+    positions = np.asarray([150, -1, 3, 190, 0, 77, 77, 12, 160, 5, 100, 130], dtype=np.int64)
+    seq_of = np.zeros(positions.size, dtype=np.int64)
+    q = rng.standard_normal((positions.size, heads, dim)).astype(np.float32)
+    case = (kc, vc, [table], np.asarray([191]), positions, seq_of, q)
+    want, dense = _oracle(*case, 0.125)
+    for partition in (0, 64):
+        got = _run_kernel(device, *case, 0.125, partition=partition, tiles=True)
+        assert np.array_equal(got[1], np.zeros_like(got[1]))
+        assert np.max(np.abs(got - dense)) < FP32_TOL
 
 
 @pytest.mark.parametrize("dim", [8, 64, 128])
@@ -293,13 +339,27 @@ def _torch_dense(batch, rows):
     return out
 
 
-def _run_batch(batch, partition=0):
+def _run_batch(batch, partition=0, plan=True):
     ops.append_kv(batch.key_cache, batch.value_cache, batch.new_keys, batch.new_values, batch.slot_mapping)
     return ops.paged_attention_ragged(
         batch.queries, batch.query_positions, batch.query_seq, batch.key_cache, batch.value_cache,
         batch.block_tables, batch.context_lens, batch.scale, max_context_len=batch.max_context_len,
-        partition_size=partition,
+        partition_size=partition, plan=batch.plan if plan else None,
     )  # fmt: skip
+
+
+def _oracle_rows(batch, out, seqs, tol):
+    """CPU oracle (reference algorithm, 128-key tiles) on every row of the chosen sequences."""
+    got = out.cpu().numpy()
+    heads, dim = batch.key_cache.shape[2], batch.key_cache.shape[3]
+    for s in seqs:
+        keys, values, q, pos = batch.host_rows(s)
+        pool_k = keys.reshape(-1, 1, heads, dim)
+        pool_v = values.reshape(-1, 1, heads, dim)
+        want = paged_attention(q, pos, pool_k, pool_v, np.arange(keys.shape[0]),
+                               int(batch.host_context[s]), batch.scale, tile_blocks=128)  # fmt: skip
+        rows = np.nonzero(batch.host_seq == s)[0]
+        assert np.max(np.abs(got[rows] - want)) < tol, s
 
 
 def test_config2_decode_64x4k_matches_the_oracle(device) -> None:
@@ -337,3 +397,44 @@ def test_config2_decode_64x4k_matches_the_oracle(device) -> None:
             max_context_len=batch.max_context_len, partition_size=partition,
         )  # fmt: skip
         assert float((other - out).abs().max()) < FP32_TOL, partition
+
+
+def test_config3_mixed_prefill_and_decode_matches_the_oracle(device) -> None:
+    """8 chunked-prefill rows of 512 tokens at offsets U[0, 2048] (MFMA tiles) plus 120 decode
+    rows with contexts U[256, 4096] (row pass), 32 heads x 128, fp32, one ragged call."""
+    from paged_kv_serving_amd.workloads import mixed_batch
+
+    say("config 3: build")
+    batch = mixed_batch(seed=0, device=device)
+    assert batch.plan.num_tiles == 64 and batch.plan.num_rows == 120
+    say("config 3: run")
+    out = _run_batch(batch)
+    torch.cuda.synchronize()
+    # every 8th prefill row and every decode row against float64 torch
+    rows = list(range(0, 4096, 8)) + list(range(4096, batch.num_queries))
+    ref = _torch_dense(batch, rows)
+    worst = max(float((out[t] - ref[t]).abs().max()) for t in ref)
+    say("config 3: worst vs float64 torch", worst)
+    assert worst < FP32_TOL
+    _oracle_rows(batch, out, (0, 5, 8, 100), FP32_TOL)
+    # the row pass alone computes the same thing
+    rows_only = _run_batch(batch, plan=False)
+    assert float((rows_only - out).abs().max()) < FP32_TOL
+
+
+def test_config5_long_context_bf16_matches_the_oracle(device) -> None:
+    """16 sequences at 32,768 context, bf16 K/V, 40k-block shuffled pool, split-context."""
+    from paged_kv_serving_amd.workloads import long_context_batch
+
+    say("config 5: build")
+    batch = long_context_batch(seed=0, device=device)
+    out = _run_batch(batch)
+    torch.cuda.synchronize()
+    slots = batch.slot_mapping
+    want_bits = batch.new_keys.to(torch.bfloat16).view(torch.int16)
+    assert torch.equal(batch.key_cache.view(-1, 32, 128)[slots].view(torch.int16), want_bits)
+    ref = _torch_dense(batch, range(batch.num_queries))  # on the stored (bf16) K/V, in float64
+    worst = max(float((out[t] - ref[t]).abs().max()) for t in ref)
+    say("config 5: worst vs float64 torch on bf16 K/V", worst)
+    assert worst < FP32_TOL
+    _oracle_rows(batch, out, (0, 15), FP32_TOL)

@@ -81,11 +81,13 @@ def test_bad_arguments_are_refused_before_any_device_work(lib) -> None:
     assert lib.pkv_copy_blocks(null, null, 9, null, 1, 1, 4, 16, 0, null) == -1
     assert lib.pkv_copy_blocks(null, null, 0, null, 0, 1, 4, 16, 0, null) == 0
     # partition size not a multiple of 16
-    args = [null, null, 8, null, null, 1, null, null, 0, 4, 4, null, 1, null, 1, 1, 8,
-            ctypes.c_float(0.5), 8, 17, null, 0, 0, null]  # fmt: skip
+    args = [null, null, 8, null, null, 1, null, 0, null, 0, null, null, 0, 4, 4, null, 1, null,
+            1, 1, 8, ctypes.c_float(0.5), 8, 17, null, 0, 0, null]  # fmt: skip
     assert lib.pkv_paged_attention(*args) == -1
-    args[19] = 16
+    args[23] = 16
     assert lib.pkv_paged_attention(*args) == -1  # null pointers
+    assert lib.pkv_tile_head_dim_supported(128) == 1
+    assert lib.pkv_tile_head_dim_supported(16) == 0
 
 
 def test_missing_library_fails_loudly(tmp_path, monkeypatch) -> None:
