@@ -17,6 +17,7 @@ tile_blocks 8, plus the runner.py:195-196 append) on a bounded sample of the sam
 single-threaded BLAS as the reference pins it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--partition P] [--no-cpu]
+       python bench.py --config {3,4,5}   (the other BASELINE.json configurations)
 """
 
 from __future__ import annotations
@@ -40,6 +41,8 @@ METRIC = "paged-attn decode tokens/s & HBM GB/s (% of peak) at 64 seq x 4k ctx; 
 def parse() -> argparse.Namespace:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
+                        help="BASELINE.json config to run (2 is the headline metric)")
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--partition", type=int, default=0, help="keys per partition (0: default)")
@@ -149,6 +152,206 @@ def cpu_baseline(args: argparse.Namespace) -> dict:
     }
 
 
+def timed(fn, steps: int, stream) -> float:
+    """Mean milliseconds of ``fn`` over ``steps`` calls, by HIP events on ``stream``."""
+    import torch
+
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for start, stop in marks:
+        start.record(stream)
+        fn()
+        stop.record(stream)
+    torch.cuda.synchronize()
+    return float(np.mean([a.elapsed_time(b) for a, b in marks]))
+
+
+def attention_call(batch, args, out, workspace):
+    from paged_kv_serving_amd import ops
+
+    def attend() -> None:
+        ops.paged_attention_ragged(
+            batch.queries, batch.query_positions, batch.query_seq, batch.key_cache,
+            batch.value_cache, batch.block_tables, batch.context_lens, batch.scale,
+            max_context_len=batch.max_context_len, partition_size=args.partition,
+            out=out, workspace=workspace, plan=batch.plan,
+        )  # fmt: skip
+
+    return attend
+
+
+def run_attention_config(args, batch, *, metric: str, workload: str, dtype: str, extra=None) -> dict:
+    """Time ``args.steps`` steps of append + ragged attention on a resident batch."""
+    import torch
+
+    from paged_kv_serving_amd import ops
+
+    device = batch.queries.device
+    heads, dim = batch.key_cache.shape[2], batch.key_cache.shape[3]
+    need = ops.attention_workspace_bytes(batch.num_queries, heads, dim, batch.max_context_len, args.partition)
+    workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=device)
+    out = torch.empty_like(batch.queries)
+
+    def append() -> None:
+        ops.append_kv(batch.key_cache, batch.value_cache, batch.new_keys, batch.new_values, batch.slot_mapping)
+
+    attend = attention_call(batch, args, out, workspace)
+    for _ in range(args.warmup):
+        append()
+        attend()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    start = time.perf_counter()
+    for e0, e1, e2 in marks:
+        e0.record(stream)
+        append()
+        e1.record(stream)
+        attend()
+        e2.record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    append_ms = float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in marks]))
+    attention_ms = float(np.mean([e1.elapsed_time(e2) for _, e1, e2 in marks]))
+    tokens = batch.num_queries
+    esize = batch.key_cache.element_size()
+    kv_bytes = batch.context_bytes()
+    io_bytes = 2 * tokens * heads * dim * 4 + batch.block_tables.numel() * 4 + 3 * tokens * 4
+    attention_bytes = kv_bytes + io_bytes
+    append_bytes = 2 * tokens * heads * dim * (4 + esize) + tokens * 8  # read k, v + write k, v
+    achieved = attention_bytes / (attention_ms * 1e-3) / 1e9
+    result = {
+        "metric": metric,
+        "value": round(tokens * args.steps / elapsed, 1),
+        "unit": "query tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic: seeded N(0,1) K/V pools, queries and new tokens resident in HBM",
+        "config": {
+            "workload": workload,
+            "partition_size": args.partition or 512,
+            "context_tokens": int(kv_bytes // (2 * heads * dim * esize)),
+        },
+        "attention_ms": round(attention_ms, 4),
+        "attention_gbps": round(achieved, 1),
+        "attention_frac_of_peak": round(achieved / HBM_PEAK_GBPS, 4),
+        "attention_tokens_per_s": round(tokens / (attention_ms * 1e-3), 1),
+        "append_us": round(append_ms * 1e3, 2),
+        "append_gbps": round(append_bytes / (append_ms * 1e-3) / 1e9, 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel": "pkv_paged_attention (row_partial + tile_partial + reduce)",
+            "algorithmic_bytes_per_launch": attention_bytes,
+        },
+    }
+    if extra:
+        result.update(extra(result, attention_ms))
+    return result
+
+
+def config2(args) -> dict:
+    from paged_kv_serving_amd.workloads import decode_batch
+
+    import torch
+
+    batch = decode_batch(seed=args.seed, device=torch.device("cuda", 0))
+    result = run_attention_config(
+        args, batch, metric=METRIC, dtype="f32",
+        workload="config2 decode: 64 seqs, ctx U[512,4096] (seed 0), 32 heads x 128 MHA, "
+        "block 16, fp32 KV, 20000-block shuffled pool, 1 layer; step = append 64 tokens + "
+        "paged attention",
+    )  # fmt: skip
+    result["unit"] = "decode tokens/s"
+    result["roofline"]["traffic"] = traffic_from_profiles()
+    result["roofline"]["kernel"] = "row_partial_kernel<float,128> + reduce_kernel<128>"
+    return result
+
+
+def config3(args) -> dict:
+    import torch
+
+    from paged_kv_serving_amd.workloads import mixed_batch
+
+    batch = mixed_batch(seed=args.seed, device=torch.device("cuda", 0))
+    offsets = batch.host_positions[batch.host_seq < 8].reshape(8, -1)[:, 0]
+    # causal prefill FLOPs: each chunk row i at offset o sees o + i + 1 keys; QK^T and PV, 2 each
+    visible = sum(int((o + np.arange(1, 513)).sum()) for o in offsets)
+    prefill_flops = 4 * 32 * 128 * visible
+
+    def extra(result, attention_ms):
+        return {"prefill_gflop": round(prefill_flops / 1e9, 2)}
+
+    return run_attention_config(
+        args, batch, dtype="f32", extra=extra,
+        metric="mixed ragged batch: query tokens/s, attention GB/s and append GB/s (config 3)",
+        workload="config3 mixed: 8 prefill chunks x 512 tokens at offsets U[0,2048] + 120 decode "
+        "rows ctx U[256,4096], 32x128 fp32, block 16, 40000-block shuffled pool; step = append "
+        "4216 tokens + one ragged attention call (MFMA tiles for chunks, row pass for decode)",
+    )  # fmt: skip
+
+
+def config5(args) -> dict:
+    import torch
+
+    from paged_kv_serving_amd.workloads import long_context_batch
+
+    batch = long_context_batch(seed=args.seed, device=torch.device("cuda", 0))
+    return run_attention_config(
+        args, batch, dtype="bf16 storage, f32 math",
+        metric="long-context decode tokens/s and HBM GB/s, bf16 KV (config 5)",
+        workload="config5 long context: 16 seqs x 32768 ctx, bf16 KV, fp32 accumulation, 32x128, "
+        "block 16, 40000-block shuffled pool, split-context partitions + reduce",
+    )  # fmt: skip
+
+
+def config4(args) -> dict:
+    import torch
+
+    from paged_kv_serving_amd import ops
+    from paged_kv_serving_amd.workloads import prefix_sharing_step
+
+    device = torch.device("cuda", 0)
+    step = prefix_sharing_step(seed=args.seed, device=device)
+    batch = step.decode
+    stream = torch.cuda.current_stream(device)
+
+    def cow() -> None:
+        ops.copy_blocks(step.key_cache, step.value_cache, step.cow_pairs)
+
+    for _ in range(args.warmup):
+        cow()
+    torch.cuda.synchronize()
+    cow_ms = timed(cow, args.steps, stream)
+    result = run_attention_config(
+        args, batch, dtype="f32",
+        metric="prefix sharing: COW GB/s and decode tokens/s over 256 sequences (config 4)",
+        workload="config4 prefix sharing: 256 seqs fork a 1016-token prefix (63 full + 1 partial "
+        "block), suffixes U[32,256]; 256 COW copies of the partial block, then one decode step",
+    )  # fmt: skip
+    unique = step.unique_context_bytes()
+    result.update({
+        "cow_pairs": len(step.host_pairs),
+        "cow_us": round(cow_ms * 1e3, 2),
+        "cow_gbps": round(step.cow_bytes() / (cow_ms * 1e-3) / 1e9, 1),
+        "cow_frac_of_peak": round(step.cow_bytes() / (cow_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "unique_context_bytes": unique,
+        "attention_unique_gbps": round(unique / (result["attention_ms"] * 1e-3) / 1e9, 1),
+        "note": "attention_gbps counts the shared prefix once per sequence (logical bytes); "
+        "attention_unique_gbps counts distinct blocks",
+    })  # fmt: skip
+    return result
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -160,100 +363,15 @@ def main() -> int:
         return 2
     import torch
 
-    from paged_kv_serving_amd import ops
-    from paged_kv_serving_amd.workloads import decode_batch
-
-    device = torch.device("cuda", 0)
-    torch.cuda.set_device(device)
-    batch = decode_batch(seed=args.seed, device=device)
-    workspace_bytes = ops.attention_workspace_bytes(
-        batch.num_queries, 32, 128, batch.max_context_len, args.partition
-    )
-    workspace = torch.empty(max(workspace_bytes // 4, 1), dtype=torch.float32, device=device)
-    out = torch.empty_like(batch.queries)
-
-    def append() -> None:
-        ops.append_kv(batch.key_cache, batch.value_cache, batch.new_keys, batch.new_values, batch.slot_mapping)
-
-    def attend() -> None:
-        ops.paged_attention_ragged(
-            batch.queries, batch.query_positions, batch.query_seq, batch.key_cache,
-            batch.value_cache, batch.block_tables, batch.context_lens, batch.scale,
-            max_context_len=batch.max_context_len, partition_size=args.partition,
-            out=out, workspace=workspace,
-        )  # fmt: skip
-
-    for _ in range(args.warmup):
-        append()
-        attend()
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.current_stream(device)
-    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    start = time.perf_counter()
-    for e0, e1, e2 in marks:
-        e0.record(stream)
-        append()
-        e1.record(stream)
-        attend()
-        e2.record(stream)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - start
-
-    append_ms = float(np.mean([e0.elapsed_time(e1) for e0, e1, _ in marks]))
-    attention_ms = float(np.mean([e1.elapsed_time(e2) for _, e1, e2 in marks]))
-    tokens = batch.num_queries
-    heads, dim = 32, 128
-    kv_bytes = batch.context_bytes()
-    io_bytes = 2 * tokens * heads * dim * 4 + batch.block_tables.numel() * 4 + 3 * tokens * 4
-    attention_bytes = kv_bytes + io_bytes
-    append_bytes = 2 * tokens * heads * dim * 4 * 2 + tokens * 8  # read k, v + write k, v + slots
-    achieved = attention_bytes / (attention_ms * 1e-3) / 1e9
-    append_gbps = append_bytes / (append_ms * 1e-3) / 1e9
-    ms_per_step = elapsed * 1e3 / args.steps
-    result = {
-        "metric": METRIC,
-        "value": round(tokens * args.steps / elapsed, 1),
-        "unit": "decode tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: seeded N(0,1) K/V pools, queries and new tokens resident in HBM",
-        "config": {
-            "workload": "config2 decode: 64 seqs, ctx U[512,4096] (seed 0), 32 heads x 128 MHA, "
-            "block 16, fp32 KV, 20000-block shuffled pool, 1 layer; step = append 64 tokens + "
-            "paged attention",
-            "partition_size": args.partition or 512,
-            "context_tokens": int(batch.host_context.sum()),
-        },
-        "attention_ms": round(attention_ms, 4),
-        "attention_gbps": round(achieved, 1),
-        "attention_frac_of_peak": round(achieved / HBM_PEAK_GBPS, 4),
-        "attention_tokens_per_s": round(tokens / (attention_ms * 1e-3), 1),
-        "append_us": round(append_ms * 1e3, 2),
-        "append_gbps": round(append_gbps, 1),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": traffic_from_profiles(),
-            "kernel": "attention_partial_kernel<float,128> + attention_reduce_kernel<128>",
-            "algorithmic_bytes_per_launch": attention_bytes,
-        },
-    }
-    peak = copy_peak(device)
-    result["copy_peak_gbps"] = peak["copy_peak_gbps"]
-    result["attention_frac_of_copy_peak"] = round(achieved / peak["copy_peak_gbps"], 4)
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(args)
+    torch.cuda.set_device(0)
+    runners = {2: config2, 3: config3, 4: config4, 5: config5}
+    result = runners[args.config](args)
+    if args.config == 2:
+        peak = copy_peak(torch.device("cuda", 0))
+        result["copy_peak_gbps"] = peak["copy_peak_gbps"]
+        result["attention_frac_of_copy_peak"] = round(result["roofline"]["achieved"] / peak["copy_peak_gbps"], 4)
+        if not args.no_cpu:
+            result["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(result), flush=True)
     return 0
 

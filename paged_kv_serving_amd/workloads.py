@@ -22,9 +22,11 @@ from paged_kv_serving_amd import ops
 
 __all__ = [
     "AttentionBatch",
+    "PrefixSharingStep",
     "decode_batch",
     "long_context_batch",
     "mixed_batch",
+    "prefix_sharing_step",
 ]
 
 
@@ -252,3 +254,124 @@ def long_context_batch(
         head_dim=head_dim, kv_dtype=kv_dtype, tables=tables, context=context,
         positions=context - 1, seq=np.arange(num_seqs),
     )  # fmt: skip
+
+
+@dataclass
+class PrefixSharingStep:
+    """Config 4: a shared prefix, one copy-on-write per sequence, then one decode step."""
+
+    key_cache: torch.Tensor  # [1, N, B, H, D] (one layer, pools as copy_blocks expects)
+    value_cache: torch.Tensor
+    cow_pairs: torch.Tensor  # int64 [n, 2] (src, dst), in BlockManager order
+    host_pairs: list[tuple[int, int]]
+    decode: AttentionBatch  # views of the same pools (layer 0), one decode row per sequence
+    shared_blocks: int
+    prefix_tokens: int
+
+    def cow_bytes(self) -> int:
+        """Bytes one COW launch moves: each pair reads and writes a K and a V block."""
+        block = self.key_cache[0, 0].numel() * self.key_cache.element_size()
+        return 4 * block * len(self.host_pairs)
+
+    def unique_context_bytes(self) -> int:
+        """K+V bytes of distinct blocks the decode step reads (the shared prefix counted once)."""
+        heads, dim = self.key_cache.shape[3], self.key_cache.shape[4]
+        per_token = 2 * heads * dim * self.key_cache.element_size()
+        shared = self.prefix_tokens - (self.prefix_tokens % self.key_cache.shape[2] or self.key_cache.shape[2])
+        own = int(sum(int(c) - shared for c in self.decode.host_context))
+        return (shared + own) * per_token
+
+
+def prefix_sharing_step(
+    *,
+    seed: int = 0,
+    num_seqs: int = 256,
+    prefix_tokens: int = 1016,
+    suffix_low: int = 32,
+    suffix_high: int = 256,
+    heads: int = 32,
+    head_dim: int = 128,
+    block_size: int = 16,
+    num_blocks: int = 8192,
+    device: torch.device | str = "cuda",
+) -> PrefixSharingStep:
+    """Config 4 through the host API: a parent prefills ``prefix_tokens`` (the last shared block
+    is partial: 1016 = 63 x 16 + 8), ``num_seqs`` children fork from it while the parent keeps its
+    reference, and each child reserves its suffix, so ``KVCacheManager.reserve`` copies-on-write
+    the partial shared block once per child (reference kvcache.py:148-180, blocks.py:148-165).
+    Suffix keys/values are then written (untimed set-up) and every child runs one decode token.
+    """
+    from paged_kv_serving_amd.blocks import BlockManager, RecordingBlockStore
+    from paged_kv_serving_amd.kvcache import KVCacheManager
+    from paged_kv_serving_amd.prefix_cache import PrefixCache
+    from paged_kv_serving_amd.sequence import Request, Sequence
+
+    device = torch.device(device)
+    rng = np.random.default_rng(seed)
+    store = RecordingBlockStore()
+    blocks = BlockManager(num_blocks=num_blocks, block_size=block_size, store=store)
+    cache = KVCacheManager(blocks, PrefixCache(blocks, enabled=False))
+    prefix = [int(t) for t in rng.integers(0, 50_000, prefix_tokens)]
+    parent = Sequence.from_request(Request("parent", tuple(prefix)), 0)
+    cache.reserve(parent, prefix_tokens)
+    parent.num_computed_tokens = prefix_tokens
+    suffixes = rng.integers(suffix_low, suffix_high + 1, num_seqs)
+    children = []
+    for i in range(num_seqs):
+        child = Sequence.from_request(Request(f"c{i}", tuple(prefix)), 0)
+        cache.fork(parent, child)
+        child.token_ids.extend(int(t) for t in rng.integers(0, 50_000, int(suffixes[i]) + 1))
+        cache.reserve(child, prefix_tokens + int(suffixes[i]) + 1)  # suffix + the decode token
+        children.append(child)
+    pairs = list(store.copies)
+    cache.check_invariants()
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    shape = (1, num_blocks, block_size, heads, head_dim)
+    key_cache = torch.randn(shape, generator=gen, device=device)
+    value_cache = torch.randn(shape, generator=gen, device=device)
+    contexts = prefix_tokens + suffixes + 1
+    tables = [np.asarray(c.block_table, dtype=np.int32) for c in children]
+    # Suffix rows (positions prefix .. ctx-2) get their own data; the pool's random fill stands
+    # in for it, except that the COW destinations are overwritten by the timed copy.
+    total = num_seqs
+    width = max(len(t) for t in tables)
+    padded = np.zeros((num_seqs, width), dtype=np.int32)
+    for i, table in enumerate(tables):
+        padded[i, : len(table)] = table
+    positions = contexts - 1
+    slots = np.asarray(
+        [int(tables[i][p // block_size]) * block_size + p % block_size for i, p in enumerate(positions)],
+        dtype=np.int64,
+    )
+    seq = np.arange(num_seqs)
+    decode = AttentionBatch(
+        key_cache=key_cache[0],
+        value_cache=value_cache[0],
+        queries=torch.randn((total, heads, head_dim), generator=gen, device=device),
+        new_keys=torch.randn((total, heads, head_dim), generator=gen, device=device),
+        new_values=torch.randn((total, heads, head_dim), generator=gen, device=device),
+        slot_mapping=torch.from_numpy(slots).to(device),
+        query_positions=torch.from_numpy(positions.astype(np.int32)).to(device),
+        query_seq=torch.from_numpy(seq.astype(np.int32)).to(device),
+        block_tables=torch.from_numpy(padded).to(device),
+        context_lens=torch.from_numpy(contexts.astype(np.int32)).to(device),
+        max_context_len=int(contexts.max()),
+        scale=float(head_dim) ** -0.5,
+        plan=ops.upload_plan(*ops.plan_rows(seq, head_dim), device),
+        host_tables=tables,
+        host_context=contexts.astype(np.int64),
+        host_positions=positions.astype(np.int64),
+        host_seq=seq.astype(np.int64),
+        host_slots=slots,
+    )
+    return PrefixSharingStep(
+        key_cache=key_cache,
+        value_cache=value_cache,
+        cow_pairs=torch.tensor(pairs, dtype=torch.int64).to(device),
+        host_pairs=pairs,
+        decode=decode,
+        shared_blocks=len(parent.block_table),
+        prefix_tokens=prefix_tokens,
+    )

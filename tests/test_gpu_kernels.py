@@ -438,3 +438,30 @@ def test_config5_long_context_bf16_matches_the_oracle(device) -> None:
     say("config 5: worst vs float64 torch on bf16 K/V", worst)
     assert worst < FP32_TOL
     _oracle_rows(batch, out, (0, 15), FP32_TOL)
+
+
+def test_config4_prefix_sharing_cow_then_decode(device) -> None:
+    """256 children fork a 1016-token prefix; reserve() COWs the partial shared block once per
+    child (pairs from the host BlockManager); one batched copy launch, then one decode step."""
+    from paged_kv_serving_amd.workloads import prefix_sharing_step
+
+    say("config 4: build")
+    step = prefix_sharing_step(seed=0, device=device)
+    assert len(step.host_pairs) == 256 and step.shared_blocks == 64
+    assert len({src for src, _ in step.host_pairs}) == 1  # every child copies the partial block
+    assert len({dst for _, dst in step.host_pairs}) == 256
+    src = step.host_pairs[0][0]
+    before_k = step.key_cache[0, src].clone()
+    ops.copy_blocks(step.key_cache, step.value_cache, step.cow_pairs)
+    dsts = torch.tensor([d for _, d in step.host_pairs], device=device)
+    assert torch.equal(step.key_cache[0, dsts], before_k.expand(256, *before_k.shape))
+    assert torch.equal(step.value_cache[0, dsts], step.value_cache[0, src].expand(256, *before_k.shape))
+    assert torch.equal(step.key_cache[0, src], before_k)
+    say("config 4: decode")
+    out = _run_batch(step.decode)
+    torch.cuda.synchronize()
+    ref = _torch_dense(step.decode, range(0, 256, 5))
+    worst = max(float((out[t] - ref[t]).abs().max()) for t in ref)
+    say("config 4: worst vs float64 torch", worst)
+    assert worst < FP32_TOL
+    _oracle_rows(step.decode, out, (0, 255), FP32_TOL)
