@@ -17,7 +17,7 @@ tile_blocks 8, plus the runner.py:195-196 append) on a bounded sample of the sam
 single-threaded BLAS as the reference pins it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--partition P] [--no-cpu]
-       python bench.py --config {3,4,5}   (the other BASELINE.json configurations)
+       python bench.py --config {1,3,4,5}   (the other BASELINE.json configurations)
 """
 
 from __future__ import annotations
@@ -41,7 +41,7 @@ METRIC = "paged-attn decode tokens/s & HBM GB/s (% of peak) at 64 seq x 4k ctx; 
 def parse() -> argparse.Namespace:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
+    parser.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
                         help="BASELINE.json config to run (2 is the headline metric)")
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
@@ -352,6 +352,67 @@ def config4(args) -> dict:
     return result
 
 
+def config1(args) -> dict:
+    """The whole engine (config 1): continuous batching + chunked prefill over the GPU runner."""
+    import torch
+
+    from paged_kv_serving_amd.config import EngineConfig, ModelConfig
+    from paged_kv_serving_amd.engine import Engine
+    from paged_kv_serving_amd.model import LanguageModel, random_weights
+    from paged_kv_serving_amd.sequence import Request, SamplingParams
+
+    config = ModelConfig(vocab_size=256, d_model=128, n_layers=2, n_heads=4, d_ff=320, max_seq_len=1024)
+    model = LanguageModel(config, random_weights(config, seed=0))
+
+    def requests():
+        rng = np.random.default_rng(args.seed)
+        out = []
+        for i in range(32):
+            length = int(rng.integers(16, 129))
+            tokens = tuple(int(t) for t in rng.integers(0, 256, length))
+            out.append(Request(f"req{i}", tokens, SamplingParams(max_new_tokens=32, seed=i)))
+        return out
+
+    for _ in range(max(1, args.warmup // 5)):
+        Engine(model, EngineConfig()).generate(requests())
+    torch.cuda.synchronize()
+    runs = max(1, args.steps // 10)
+    seconds, iterations, generated = [], 0, 0
+    for _ in range(runs):
+        engine = Engine(model, EngineConfig())
+        start = time.perf_counter()
+        outputs = engine.generate(requests())
+        torch.cuda.synchronize()
+        seconds.append(time.perf_counter() - start)
+        iterations = engine.iterations
+        generated = sum(len(s) for samples in outputs.values() for s in samples)
+    elapsed = float(np.median(seconds))
+    return {
+        "metric": "engine output tokens/s, continuous batching + chunked prefill (config 1)",
+        "value": round(generated / elapsed, 1),
+        "unit": "output tokens/s",
+        "n_gpus": 1,
+        "steps": iterations,
+        "warmup": max(1, args.warmup // 5),
+        "ms_per_step": round(elapsed * 1e3 / iterations, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: random_weights(seed 0), 32 prompts U[16,128] random tokens (seed 0)",
+        "config": {
+            "workload": "config1: fp32 decoder vocab 256, d_model 128, 2 layers, 4 heads x 32, d_ff "
+            "320; 32 requests, 32 greedy tokens each; EngineConfig defaults (block 16, 512 blocks, "
+            "budget 256, 32 running)",
+            "runs": runs,
+        },
+        "seconds_per_run": round(elapsed, 4),
+        "generated_tokens": generated,
+        "reference_published": "1453.36 output tok/s (engine_throughput_24_requests, i5-8500, "
+        "bench/results/latest.json:46-53; a different workload, for orientation only)",
+    }
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -364,7 +425,7 @@ def main() -> int:
     import torch
 
     torch.cuda.set_device(0)
-    runners = {2: config2, 3: config3, 4: config4, 5: config5}
+    runners = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
     result = runners[args.config](args)
     if args.config == 2:
         peak = copy_peak(torch.device("cuda", 0))

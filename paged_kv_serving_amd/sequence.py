@@ -14,7 +14,15 @@ import itertools
 from dataclasses import dataclass, field
 from enum import Enum
 
-__all__ = ["Request", "SamplingParams", "Sequence", "SequenceStatus", "new_sequence_id"]
+__all__ = [
+    "FinishReason",
+    "Request",
+    "SamplingParams",
+    "Sequence",
+    "SequenceStatus",
+    "finish_reason_for",
+    "new_sequence_id",
+]
 
 _ORDER = itertools.count()
 
@@ -28,6 +36,12 @@ class SequenceStatus(Enum):
     RUNNING = "running"
     PREEMPTED = "preempted"
     FINISHED = "finished"
+
+
+class FinishReason(Enum):
+    LENGTH = "length"
+    STOP = "stop"
+    CONTEXT_LIMIT = "context_limit"
 
 
 @dataclass(frozen=True)
@@ -71,8 +85,11 @@ class Sequence:
     num_computed_tokens: int = 0
     status: SequenceStatus = SequenceStatus.WAITING
     cached_prefix_blocks: int = 0
+    # Running slots held for the samples that fork from this one once its prompt is computed.
+    fork_slots: int = 0
     block_hashes: list[bytes] = field(default_factory=list)
     preemption_count: int = 0
+    finish_reason: FinishReason | None = None
     admission_order: int = field(default_factory=lambda: next(_ORDER))
 
     @classmethod
@@ -120,6 +137,23 @@ class Sequence:
         self.status = SequenceStatus.PREEMPTED
         self.preemption_count += 1
 
+    def finish(self, reason: FinishReason) -> None:
+        self.status = SequenceStatus.FINISHED
+        self.finish_reason = reason
+
     def priority_key(self) -> tuple[int, float, int]:
         """One service class, no deadlines: arrival order (sequence.py:230-241)."""
         return (0, float("inf"), self.admission_order)
+
+
+def finish_reason_for(
+    sequence: Sequence, token: int, *, eos_token_id: int | None, max_context_tokens: int
+) -> FinishReason | None:
+    """Stop token, then the output cap, then the context cap (sequence.py:244-262)."""
+    if eos_token_id is not None and token == eos_token_id:
+        return FinishReason.STOP
+    if sequence.num_output_tokens >= sequence.request.sampling.max_new_tokens:
+        return FinishReason.LENGTH
+    if sequence.num_tokens >= max_context_tokens:
+        return FinishReason.CONTEXT_LIMIT
+    return None
