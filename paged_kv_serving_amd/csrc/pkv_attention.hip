@@ -25,6 +25,8 @@
 // visible block are never read.
 #include <math.h>
 
+#include <mutex>
+
 #include "pkv_common.h"
 
 namespace pkv {
@@ -41,6 +43,17 @@ namespace {
 #endif
 #ifndef PKV_ATTN_NONTEMPORAL
 #define PKV_ATTN_NONTEMPORAL 1
+#endif
+// tile_partial: prefetch the next key tile during the MFMAs of the current one; and run the tile
+// pass on a second stream beside the row pass when a call has both.
+#ifndef PKV_TILE_PIPELINE
+#define PKV_TILE_PIPELINE 1
+#endif
+#ifndef PKV_ATTN_OVERLAP
+#define PKV_ATTN_OVERLAP 1
+#endif
+#ifndef PKV_ATTN_ROWS_FIRST
+#define PKV_ATTN_ROWS_FIRST 0
 #endif
 
 constexpr int kWaves = PKV_ATTN_WAVES;  // wavefronts per row_partial workgroup
@@ -436,39 +449,68 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
   const int64_t row_stride = static_cast<int64_t>(a.num_heads) * D;
   __syncthreads();  // s_table ready
 
+  // Software pipeline: the raw vectors of key tile k0 + kTileKeys are loaded into registers while
+  // tile k0 is being multiplied; at the top of each step they are widened into LDS.
+  constexpr int kVecs = kTileKeys * kVecPerRow;  // 16-byte vectors per K (or V) tile
+  constexpr int kPerThread = (kVecs + kTileThreads - 1) / kTileThreads;
+  uint4 kraw[kPerThread];
+  uint4 vraw[kPerThread];
+  auto prefetch = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u) {
+      const int v = threadIdx.x + u * kTileThreads;
+      kraw[u] = make_uint4(0, 0, 0, 0);
+      vraw[u] = make_uint4(0, 0, 0, 0);
+      if (v < kVecs) {
+        const int row = v / kVecPerRow;
+        const int kpos = k0 + row;
+        if (kpos < kend) {
+          const int lb = block_of<kPow2Block>(kpos, a) - b0;
+          const int blk = s_table[lb];
+          if (blk >= 0 && blk < a.num_blocks) {
+            const int col = (v - row * kVecPerRow) * kEpv;
+            const int64_t off =
+                (static_cast<int64_t>(blk) * a.block_size + (kpos - (lb + b0) * a.block_size)) *
+                    row_stride + head_off + col;
+            kraw[u] = *reinterpret_cast<const uint4*>(kcache + off);
+            vraw[u] = *reinterpret_cast<const uint4*>(vcache + off);
+          }
+        }
+      }
+    }
+  };
+#if PKV_TILE_PIPELINE
+  if (kbeg < kend) prefetch(kbeg);
+#endif
+
   for (int k0 = kbeg; k0 < kend; k0 += kTileKeys) {
-    // Stage kTileKeys key and value rows (zeros past kend) as float32.
-    for (int v = threadIdx.x; v < kTileKeys * kVecPerRow; v += kTileThreads) {
-      const int row = v / kVecPerRow;
-      const int col = (v - row * kVecPerRow) * kEpv;
-      const int kpos = k0 + row;
-      float kf[kEpv];
-      float vf[kEpv];
-      bool ok = kpos < kend;
-      int64_t off = 0;
-      if (ok) {
-        const int lb = block_of<kPow2Block>(kpos, a) - b0;
-        const int blk = s_table[lb];
-        ok = blk >= 0 && blk < a.num_blocks;
-        off = (static_cast<int64_t>(blk) * a.block_size + (kpos - (lb + b0) * a.block_size)) *
-                  row_stride + head_off + col;
-      }
-      if (ok) {
-        widen(*reinterpret_cast<const uint4*>(kcache + off), kf, KVT{});
-        widen(*reinterpret_cast<const uint4*>(vcache + off), vf, KVT{});
-      } else {
+#if !PKV_TILE_PIPELINE
+    prefetch(k0);
+#endif
+    // Widen the prefetched tile (zeros past kend) into LDS as float32.
 #pragma unroll
-        for (int e = 0; e < kEpv; ++e) kf[e] = vf[e] = 0.f;
-      }
+    for (int u = 0; u < kPerThread; ++u) {
+      const int v = threadIdx.x + u * kTileThreads;
+      if (v < kVecs) {
+        const int row = v / kVecPerRow;
+        const int col = (v - row * kVecPerRow) * kEpv;
+        float kf[kEpv];
+        float vf[kEpv];
+        widen(kraw[u], kf, KVT{});
+        widen(vraw[u], vf, KVT{});
 #pragma unroll
-      for (int e = 0; e < kEpv; e += 4) {
-        *reinterpret_cast<float4*>(&s_k[row * kRow + col + e]) =
-            make_float4(kf[e], kf[e + 1], kf[e + 2], kf[e + 3]);
-        *reinterpret_cast<float4*>(&s_v[row * kRow + col + e]) =
-            make_float4(vf[e], vf[e + 1], vf[e + 2], vf[e + 3]);
+        for (int e = 0; e < kEpv; e += 4) {
+          *reinterpret_cast<float4*>(&s_k[row * kRow + col + e]) =
+              make_float4(kf[e], kf[e + 1], kf[e + 2], kf[e + 3]);
+          *reinterpret_cast<float4*>(&s_v[row * kRow + col + e]) =
+              make_float4(vf[e], vf[e + 1], vf[e + 2], vf[e + 3]);
+        }
       }
     }
     __syncthreads();
+#if PKV_TILE_PIPELINE
+    if (k0 + kTileKeys < kend) prefetch(k0 + kTileKeys);
+#endif
 
     // S^T tile: register r = S[query n][key 4c + r].
     floatx4 st = {0.f, 0.f, 0.f, 0.f};
@@ -565,27 +607,71 @@ __global__ __launch_bounds__(D < kWave ? kWave : D) void reduce_kernel(const Par
   a.out[qh * D + d] = acc / (lsum > 0.f ? lsum : 1.f);
 }
 
-template <typename KVT, int D>
-int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t num_tiles,
-               hipStream_t stream) {
-  const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
-  const int64_t per_row = static_cast<int64_t>(a.max_parts) * a.num_heads;
-  if (num_tiles > 0) {
-    if constexpr (D % 16 == 0 && D >= 32) {
-      const int64_t groups = num_tiles * per_row;
-      if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
-      const dim3 grid(static_cast<uint32_t>(groups));
-      if (pow2) {
-        hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true>), grid, dim3(kTileThreads), 0, stream, a);
-      } else {
-        hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false>), grid, dim3(kTileThreads), 0, stream, a);
-      }
-      if (check_launch() != PKV_OK) return PKV_EHIP;
-    } else {
-      return PKV_EUNSUPPORTED;
+// A second stream per device, with fork/join events, so the compute-bound tile pass runs beside
+// the memory-bound row pass of the same call. Created once per device (default priority,
+// non-blocking) and kept for the life of the process; the enqueue sequence that uses the events
+// runs under one mutex, so calls from several host threads cannot interleave their records.
+constexpr int kMaxDevices = 64;
+
+struct Overlap {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t join = nullptr;
+  bool failed = false;
+};
+
+std::mutex g_overlap_mutex;
+Overlap g_overlap[kMaxDevices];
+
+// The current device's overlap stream and events (created on first use), or null when they
+// cannot be created; callers then run both passes on their own stream. Caller holds the mutex.
+Overlap* overlap_locked(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  Overlap& o = g_overlap[device];
+  if (o.failed) return nullptr;
+  if (o.stream == nullptr) {
+    if (hipStreamCreateWithFlags(&o.stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&o.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&o.join, hipEventDisableTiming) != hipSuccess) {
+      o.failed = true;
+      (void)hipGetLastError();
+      return nullptr;
     }
   }
-  if (num_rows > 0) {
+  return &o;
+}
+
+template <typename KVT, int D>
+int launch_tiles(const Params& a, int64_t num_tiles, hipStream_t stream) {
+  if constexpr (D % 16 == 0 && D >= 32) {
+    const int64_t groups = num_tiles * static_cast<int64_t>(a.max_parts) * a.num_heads;
+    if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
+    const dim3 grid(static_cast<uint32_t>(groups));
+    if ((a.block_size & (a.block_size - 1)) == 0) {
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true>), grid, dim3(kTileThreads), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false>), grid, dim3(kTileThreads), 0, stream, a);
+    }
+    return check_launch();
+  } else {
+    return PKV_EUNSUPPORTED;
+  }
+}
+
+template <typename KVT, int D>
+int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t num_tiles,
+               int device, hipStream_t stream) {
+  const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
+  const int64_t per_row = static_cast<int64_t>(a.max_parts) * a.num_heads;
+  std::unique_lock<std::mutex> overlap_lock(g_overlap_mutex, std::defer_lock);
+  Overlap* overlap = nullptr;
+  if (PKV_ATTN_OVERLAP && num_tiles > 0 && num_rows > 0) {
+    overlap_lock.lock();
+    overlap = overlap_locked(device);
+    if (overlap == nullptr) overlap_lock.unlock();
+  }
+  auto launch_rows = [&]() -> int {
+    if (num_rows == 0) return PKV_OK;
     const int64_t groups = num_rows * per_row;
     if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
     const dim3 grid(static_cast<uint32_t>(groups));
@@ -594,7 +680,36 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     } else {
       hipLaunchKernelGGL((row_partial_kernel<KVT, D, false>), grid, dim3(kThreads), 0, stream, a);
     }
-    if (check_launch() != PKV_OK) return PKV_EHIP;
+    return check_launch();
+  };
+  if (PKV_ATTN_ROWS_FIRST || overlap == nullptr) {
+    // Without overlap the order does not matter; with it, rows first takes the CUs first.
+    if (overlap != nullptr && hipEventRecord(overlap->fork, stream) != hipSuccess) return PKV_EHIP;
+    const int rc = launch_rows();
+    if (rc != PKV_OK) return rc;
+  } else if (hipEventRecord(overlap->fork, stream) != hipSuccess) {
+    return PKV_EHIP;
+  }
+  if (num_tiles > 0) {
+    if (overlap != nullptr) {
+      // fork: the tile pass starts when the caller's stream reaches the fork point
+      if (hipStreamWaitEvent(overlap->stream, overlap->fork, 0) != hipSuccess) return PKV_EHIP;
+      const int rc = launch_tiles<KVT, D>(a, num_tiles, overlap->stream);
+      if (rc != PKV_OK) return rc;
+      if (hipEventRecord(overlap->join, overlap->stream) != hipSuccess) return PKV_EHIP;
+    } else {
+      const int rc = launch_tiles<KVT, D>(a, num_tiles, stream);
+      if (rc != PKV_OK) return rc;
+    }
+  }
+  if (!PKV_ATTN_ROWS_FIRST && overlap != nullptr) {
+    const int rc = launch_rows();
+    if (rc != PKV_OK) return rc;
+  }
+  if (overlap != nullptr) {
+    // join: everything after this (the reduce, the caller's next work) waits for the tile pass
+    if (hipStreamWaitEvent(stream, overlap->join, 0) != hipSuccess) return PKV_EHIP;
+    overlap_lock.unlock();
   }
   if (a.max_parts > 1) {
     const int64_t groups = num_queries * a.num_heads;
@@ -608,20 +723,20 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
 
 template <typename KVT>
 int dispatch_head_dim(int head_dim, const Params& a, int64_t num_queries, int64_t num_rows,
-                      int64_t num_tiles, hipStream_t stream) {
+                      int64_t num_tiles, int device, hipStream_t stream) {
   switch (head_dim) {
     case 8:
-      return launch_all<KVT, 8>(a, num_queries, num_rows, num_tiles, stream);
+      return launch_all<KVT, 8>(a, num_queries, num_rows, num_tiles, device, stream);
     case 16:
-      return launch_all<KVT, 16>(a, num_queries, num_rows, num_tiles, stream);
+      return launch_all<KVT, 16>(a, num_queries, num_rows, num_tiles, device, stream);
     case 32:
-      return launch_all<KVT, 32>(a, num_queries, num_rows, num_tiles, stream);
+      return launch_all<KVT, 32>(a, num_queries, num_rows, num_tiles, device, stream);
     case 64:
-      return launch_all<KVT, 64>(a, num_queries, num_rows, num_tiles, stream);
+      return launch_all<KVT, 64>(a, num_queries, num_rows, num_tiles, device, stream);
     case 128:
-      return launch_all<KVT, 128>(a, num_queries, num_rows, num_tiles, stream);
+      return launch_all<KVT, 128>(a, num_queries, num_rows, num_tiles, device, stream);
     case 256:
-      return launch_all<KVT, 256>(a, num_queries, num_rows, num_tiles, stream);
+      return launch_all<KVT, 256>(a, num_queries, num_rows, num_tiles, device, stream);
     default:
       return PKV_EUNSUPPORTED;
   }
@@ -740,6 +855,8 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   a.max_ctx = max_context_len;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   auto s = static_cast<hipStream_t>(stream);
-  if (kv_dtype == PKV_F32) return dispatch_head_dim<float>(head_dim, a, num_queries, num_rows, num_tiles, s);
-  return dispatch_head_dim<uint16_t>(head_dim, a, num_queries, num_rows, num_tiles, s);
+  if (kv_dtype == PKV_F32) {
+    return dispatch_head_dim<float>(head_dim, a, num_queries, num_rows, num_tiles, device, s);
+  }
+  return dispatch_head_dim<uint16_t>(head_dim, a, num_queries, num_rows, num_tiles, device, s);
 }
