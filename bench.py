@@ -234,7 +234,8 @@ def run_attention_config(args, batch, *, metric: str, workload: str, dtype: str,
         "data": "synthetic: seeded N(0,1) K/V pools, queries and new tokens resident in HBM",
         "config": {
             "workload": workload,
-            "partition_size": args.partition or 512,
+            "partition_size": args.partition or batch.plan.partition_size or 512,
+            "kv_loads": "cached" if batch.plan.shared_kv else "streaming",
             "context_tokens": int(kv_bytes // (2 * heads * dim * esize)),
         },
         "attention_ms": round(attention_ms, 4),

@@ -37,6 +37,11 @@ typedef enum pkv_dtype {
   PKV_BF16 = 1, /* bfloat16; written from float32 with round-to-nearest-even */
 } pkv_dtype;
 
+/* pkv_paged_attention flags. */
+#define PKV_ATTN_SHARED_KV 1 /* blocks are shared between sequences of the batch (a common
+                                prefix): load K/V rows through the caches instead of streaming
+                                them past, so the other readers hit L2 / the Infinity Cache */
+
 #define PKV_OK 0
 #define PKV_EINVAL (-1)       /* a size, stride, pointer or enum argument is out of range */
 #define PKV_EUNSUPPORTED (-2) /* a valid but unimplemented shape (e.g. head_dim 96) */
@@ -136,6 +141,7 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *                      >= max_context_len (checked).
  *   partition_size   : keys per split-context partition, a positive multiple of 16, <= 1024;
  *                      0 selects the library default (512).
+ *   flags            : 0 or PKV_ATTN_SHARED_KV.
  *   workspace        : float32 scratch of pkv_attention_workspace_bytes(...) bytes (may be
  *                      NULL when that is 0).
  * A query whose every key is masked gets a zero output (attention.py:120-121).
@@ -151,8 +157,8 @@ int pkv_paged_attention(float* out, const float* queries, int64_t query_token_st
                         int32_t block_size, const int32_t* block_tables,
                         int32_t block_table_stride, const int32_t* context_lens,
                         int32_t num_seqs, int32_t num_heads, int32_t head_dim, float scale,
-                        int32_t max_context_len, int32_t partition_size, float* workspace,
-                        int64_t workspace_bytes, int device, void* stream);
+                        int32_t max_context_len, int32_t partition_size, int32_t flags,
+                        float* workspace, int64_t workspace_bytes, int device, void* stream);
 
 #ifdef __cplusplus
 }

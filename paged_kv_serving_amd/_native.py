@@ -49,9 +49,10 @@ HIPCC_FLAGS = (
     "-packed-fp32-ops",
 )
 
-# pkv_dtype values (include/pkv.h).
+# pkv_dtype values and pkv_paged_attention flags (include/pkv.h).
 PKV_F32 = 0
 PKV_BF16 = 1
+PKV_ATTN_SHARED_KV = 1
 
 PKV_OK = 0
 
@@ -150,7 +151,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size
         _ptr, _i32, _ptr, _i32,  # block_tables, block_table_stride, context_lens, num_seqs
         _i32, _i32, ctypes.c_float,  # num_heads, head_dim, scale
-        _i32, _i32,  # max_context_len, partition_size
+        _i32, _i32, _i32,  # max_context_len, partition_size, flags
         _ptr, _i64,  # workspace, workspace_bytes
         _c_int, _ptr,  # device, stream
     ]

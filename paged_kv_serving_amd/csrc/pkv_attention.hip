@@ -142,15 +142,18 @@ __device__ __forceinline__ void widen(const uint4& raw, float* out, uint16_t) {
   out[7] = bf16_hi(raw.w);
 }
 
-// One 16-byte vector of a key or value row that is read exactly once.
-__device__ __forceinline__ uint4 load_stream(const uint4* p) {
-#if PKV_ATTN_NONTEMPORAL
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
-#else
-  return *p;
-#endif
+// One 16-byte vector of a key or value row. Rows read once by the whole call stream past the
+// caches (non-temporal); rows shared by several sequences of the batch are loaded normally so
+// the other readers hit L2 / the Infinity Cache.
+template <bool kStream>
+__device__ __forceinline__ uint4 load_row(const uint4* p) {
+  if constexpr (kStream && PKV_ATTN_NONTEMPORAL) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *p;
+  }
 }
 
 // Visible key count of a query: keys at positions 0 .. min(context_len, position + 1) - 1.
@@ -202,7 +205,7 @@ __device__ __forceinline__ void store_result(const Params& a, int64_t t, int h, 
 // ---------------------------------------------------------------------------------------------
 // Pass 1: row_partial.
 // ---------------------------------------------------------------------------------------------
-template <typename KVT, int D, bool kPow2Block>
+template <typename KVT, int D, bool kPow2Block, bool kStream>
 __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   using L = Layout<KVT, D>;
   __shared__ int s_table[kTableSlots];
@@ -282,9 +285,9 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
         const uint4* kp = reinterpret_cast<const uint4*>(kcache + row);
         const uint4* vp = reinterpret_cast<const uint4*>(vcache + row);
 #pragma unroll
-        for (int i = 0; i < L::kVpl; ++i) kraw[rr][i] = load_stream(kp + i * L::kLpt + j);
+        for (int i = 0; i < L::kVpl; ++i) kraw[rr][i] = load_row<kStream>(kp + i * L::kLpt + j);
 #pragma unroll
-        for (int i = 0; i < L::kVpl; ++i) vraw[rr][i] = load_stream(vp + i * L::kLpt + j);
+        for (int i = 0; i < L::kVpl; ++i) vraw[rr][i] = load_row<kStream>(vp + i * L::kLpt + j);
       } else {
 #pragma unroll
         for (int i = 0; i < L::kVpl; ++i) {
@@ -660,7 +663,7 @@ int launch_tiles(const Params& a, int64_t num_tiles, hipStream_t stream) {
 
 template <typename KVT, int D>
 int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t num_tiles,
-               int device, hipStream_t stream) {
+               bool stream_kv, int device, hipStream_t stream) {
   const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
   const int64_t per_row = static_cast<int64_t>(a.max_parts) * a.num_heads;
   std::unique_lock<std::mutex> overlap_lock(g_overlap_mutex, std::defer_lock);
@@ -675,10 +678,14 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     const int64_t groups = num_rows * per_row;
     if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
     const dim3 grid(static_cast<uint32_t>(groups));
-    if (pow2) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, true>), grid, dim3(kThreads), 0, stream, a);
+    if (pow2 && stream_kv) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, true, true>), grid, dim3(kThreads), 0, stream, a);
+    } else if (pow2) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, true, false>), grid, dim3(kThreads), 0, stream, a);
+    } else if (stream_kv) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, false, true>), grid, dim3(kThreads), 0, stream, a);
     } else {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, false, false>), grid, dim3(kThreads), 0, stream, a);
     }
     return check_launch();
   };
@@ -723,20 +730,20 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
 
 template <typename KVT>
 int dispatch_head_dim(int head_dim, const Params& a, int64_t num_queries, int64_t num_rows,
-                      int64_t num_tiles, int device, hipStream_t stream) {
+                      int64_t num_tiles, bool stream_kv, int device, hipStream_t stream) {
   switch (head_dim) {
     case 8:
-      return launch_all<KVT, 8>(a, num_queries, num_rows, num_tiles, device, stream);
+      return launch_all<KVT, 8>(a, num_queries, num_rows, num_tiles, stream_kv, device, stream);
     case 16:
-      return launch_all<KVT, 16>(a, num_queries, num_rows, num_tiles, device, stream);
+      return launch_all<KVT, 16>(a, num_queries, num_rows, num_tiles, stream_kv, device, stream);
     case 32:
-      return launch_all<KVT, 32>(a, num_queries, num_rows, num_tiles, device, stream);
+      return launch_all<KVT, 32>(a, num_queries, num_rows, num_tiles, stream_kv, device, stream);
     case 64:
-      return launch_all<KVT, 64>(a, num_queries, num_rows, num_tiles, device, stream);
+      return launch_all<KVT, 64>(a, num_queries, num_rows, num_tiles, stream_kv, device, stream);
     case 128:
-      return launch_all<KVT, 128>(a, num_queries, num_rows, num_tiles, device, stream);
+      return launch_all<KVT, 128>(a, num_queries, num_rows, num_tiles, stream_kv, device, stream);
     case 256:
-      return launch_all<KVT, 256>(a, num_queries, num_rows, num_tiles, device, stream);
+      return launch_all<KVT, 256>(a, num_queries, num_rows, num_tiles, stream_kv, device, stream);
     default:
       return PKV_EUNSUPPORTED;
   }
@@ -783,11 +790,13 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
                                    int32_t block_table_stride, const int32_t* context_lens,
                                    int32_t num_seqs, int32_t num_heads, int32_t head_dim,
                                    float scale, int32_t max_context_len, int32_t partition_size,
-                                   float* workspace, int64_t workspace_bytes, int device,
-                                   void* stream) {
+                                   int32_t flags, float* workspace, int64_t workspace_bytes,
+                                   int device, void* stream) {
   using namespace pkv;
   const int part = resolve_partition(partition_size);
   if (part < 0) return PKV_EINVAL;
+  if (flags & ~PKV_ATTN_SHARED_KV) return PKV_EINVAL;
+  const bool stream_kv = (flags & PKV_ATTN_SHARED_KV) == 0;
   if (num_queries < 0 || num_rows < 0 || num_tiles < 0 || num_blocks < 1 || block_size < 1 ||
       block_table_stride < 0 || num_seqs < 0 || num_heads < 1 || head_dim < 1 ||
       max_context_len < 0) {
@@ -856,7 +865,7 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
   auto s = static_cast<hipStream_t>(stream);
   if (kv_dtype == PKV_F32) {
-    return dispatch_head_dim<float>(head_dim, a, num_queries, num_rows, num_tiles, device, s);
+    return dispatch_head_dim<float>(head_dim, a, num_queries, num_rows, num_tiles, stream_kv, device, s);
   }
-  return dispatch_head_dim<uint16_t>(head_dim, a, num_queries, num_rows, num_tiles, device, s);
+  return dispatch_head_dim<uint16_t>(head_dim, a, num_queries, num_rows, num_tiles, stream_kv, device, s);
 }

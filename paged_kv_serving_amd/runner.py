@@ -163,6 +163,7 @@ class ModelRunner:
         device: torch.device | str | int | None = None,
         partition_size: int = 0,
     ) -> None:
+        """``partition_size`` 0 lets each call choose (``ops.batch_hints``)."""
         if num_blocks < 1 or block_size < 1:
             raise ValueError("num_blocks and block_size must be >= 1")
         if tile_blocks < 1:
@@ -291,6 +292,10 @@ class ModelRunner:
         context = np.fromiter((e.positions[-1] + 1 for e in entries), dtype=np.int32, count=num_seqs)
         query_seq = np.repeat(np.arange(num_seqs, dtype=np.int32), [len(e.token_ids) for e in entries])
         plan_rows, plan_tiles = ops.plan_rows(query_seq, config.head_dim)
+        hint_partition, shared_kv = ops.batch_hints(
+            [e.block_table for e in entries], context, config.n_heads, self.block_size, total
+        )
+        partition = self.partition_size or hint_partition
         meta64 = torch.from_numpy(np.concatenate([tokens, positions, slots])).to(self.device)
         meta32 = torch.from_numpy(
             np.concatenate([
@@ -307,6 +312,8 @@ class ModelRunner:
         plan = ops.AttentionPlan(
             rows=meta32[end_tables : end_tables + plan_rows.size],
             tiles=meta32[end_tables + plan_rows.size :].view(-1, 2),
+            partition_size=partition,
+            shared_kv=shared_kv,
         )
         max_context = int(context.max())
 
@@ -327,12 +334,12 @@ class ModelRunner:
             values = fused[:, 2]
             ops.append_kv(self._keys[index], self._values[index], keys, values, slots_d)
             if workspace is None:
-                need = ops.attention_workspace_bytes(total, heads, dim, max_context, self.partition_size)
+                need = ops.attention_workspace_bytes(total, heads, dim, max_context, partition)
                 workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=self.device)
             ops.paged_attention_ragged(
                 queries, qpos_d, qseq_d, self._keys[index], self._values[index], tables_d,
                 context_d, scale, max_context_len=max_context,
-                partition_size=self.partition_size, out=attended, workspace=workspace, plan=plan,
+                partition_size=partition, out=attended, workspace=workspace, plan=plan,
             )  # fmt: skip
             hidden = hidden + attended.view(total, d_model) @ out_proj
             normed = _rms_norm(hidden, ffn_norm, eps)

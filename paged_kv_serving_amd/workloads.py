@@ -140,7 +140,8 @@ def _assemble(
     padded = np.zeros((len(tables), width), dtype=np.int32)
     for i, table in enumerate(tables):
         padded[i, : len(table)] = table
-    plan = ops.upload_plan(*ops.plan_rows(seq, head_dim), device)
+    partition, shared = ops.batch_hints(tables, context, heads, block_size, positions.size)
+    plan = ops.upload_plan(*ops.plan_rows(seq, head_dim), device, partition_size=partition, shared_kv=shared)
     return AttentionBatch(
         key_cache=key_cache,
         value_cache=value_cache,
@@ -359,7 +360,10 @@ def prefix_sharing_step(
         context_lens=torch.from_numpy(contexts.astype(np.int32)).to(device),
         max_context_len=int(contexts.max()),
         scale=float(head_dim) ** -0.5,
-        plan=ops.upload_plan(*ops.plan_rows(seq, head_dim), device),
+        plan=ops.upload_plan(
+            *ops.plan_rows(seq, head_dim), device,
+            **dict(zip(("partition_size", "shared_kv"), ops.batch_hints(tables, contexts, heads, block_size))),
+        ),  # fmt: skip
         host_tables=tables,
         host_context=contexts.astype(np.int64),
         host_positions=positions.astype(np.int64),

@@ -397,6 +397,14 @@ def test_config2_decode_64x4k_matches_the_oracle(device) -> None:
             max_context_len=batch.max_context_len, partition_size=partition,
         )  # fmt: skip
         assert float((other - out).abs().max()) < FP32_TOL, partition
+    # cached loads (the shared-prefix hint) give the same bits as the streaming loads
+    assert not batch.plan.shared_kv and batch.plan.partition_size == 512
+    cached = ops.paged_attention_ragged(
+        batch.queries, batch.query_positions, batch.query_seq, batch.key_cache, batch.value_cache,
+        batch.block_tables, batch.context_lens, batch.scale, max_context_len=batch.max_context_len,
+        plan=batch.plan, shared_kv=True,
+    )  # fmt: skip
+    assert torch.equal(cached, out)
 
 
 def test_config3_mixed_prefill_and_decode_matches_the_oracle(device) -> None:
@@ -465,3 +473,20 @@ def test_config4_prefix_sharing_cow_then_decode(device) -> None:
     say("config 4: worst vs float64 torch", worst)
     assert worst < FP32_TOL
     _oracle_rows(step.decode, out, (0, 255), FP32_TOL)
+    # the shared-prefix hint only changes how K/V rows are loaded: same bits either way
+    assert step.decode.plan.shared_kv and step.decode.plan.partition_size == 1024
+    d = step.decode
+    for partition in (0, 512):
+        streamed = ops.paged_attention_ragged(
+            d.queries, d.query_positions, d.query_seq, d.key_cache, d.value_cache, d.block_tables,
+            d.context_lens, d.scale, max_context_len=d.max_context_len, partition_size=partition,
+            plan=d.plan, shared_kv=False,
+        )  # fmt: skip
+        cached = ops.paged_attention_ragged(
+            d.queries, d.query_positions, d.query_seq, d.key_cache, d.value_cache, d.block_tables,
+            d.context_lens, d.scale, max_context_len=d.max_context_len, partition_size=partition,
+            plan=d.plan, shared_kv=True,
+        )  # fmt: skip
+        assert torch.equal(streamed, cached), partition
+        if partition == 0:
+            assert torch.equal(cached, out)
