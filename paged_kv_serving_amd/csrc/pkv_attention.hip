@@ -1,5 +1,7 @@
 // Paged causal attention over block tables for ragged batches: decode rows and prefill-chunk
-// rows of many sequences in one call. Three kernels, launched in order on one stream:
+// rows of many sequences in one call. Three kernels; passes 1 and 2 cover disjoint query rows and
+// run side by side (pass 2 on a second stream forked from and joined back to the caller's), and
+// pass 3 runs on the caller's stream after both:
 //
 //  1. row_partial (memory-bound rows, e.g. decode): one workgroup of kWaves wavefronts per
 //     (query row, head, context partition). The partition's slice of the block table is staged
