@@ -315,8 +315,10 @@ def config3(args) -> dict:
     visible = sum(int((o + np.arange(1, 513)).sum()) for o in offsets)
     prefill_flops = 4 * 32 * 128 * visible
 
+    rope = rope_append_timing(args, batch)
+
     def extra(result, attention_ms):
-        return {"prefill_gflop": round(prefill_flops / 1e9, 2)}
+        return {"prefill_gflop": round(prefill_flops / 1e9, 2), **rope}
 
     return run_attention_config(
         args, batch, dtype="f32", extra=extra,
@@ -325,6 +327,44 @@ def config3(args) -> dict:
         "rows ctx U[256,4096], 32x128 fp32, block 16, 40000-block shuffled pool; step = append "
         "4216 tokens + one ragged attention call (MFMA tiles for chunks, row pass for decode)",
     )  # fmt: skip
+
+
+def rope_append_timing(args, batch) -> dict:
+    """The fused RoPE + append kernel on the batch's tokens (a [T, 3, H, D] projection output),
+    timed on its own: it is what ModelRunner.execute runs in place of the append."""
+    import torch
+
+    from paged_kv_serving_amd import ops
+    from paged_kv_serving_amd.model import rope_tables
+
+    device = batch.queries.device
+    tokens, heads, dim = batch.queries.shape
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed)
+    fused = torch.randn((tokens, 3, heads, dim), generator=gen, device=device)
+    cos, sin = (torch.from_numpy(t).to(device) for t in rope_tables(4096, dim, 10_000.0))
+    positions = batch.slot_mapping.remainder(4096)
+    out = torch.empty((tokens, heads, dim), device=device)
+
+    def run() -> None:
+        ops.rope_append(
+            batch.key_cache, batch.value_cache, fused[:, 0], fused[:, 1], fused[:, 2],
+            positions, cos, sin, batch.slot_mapping, out=out,
+        )  # fmt: skip
+
+    for _ in range(max(args.warmup, 1)):
+        run()
+    torch.cuda.synchronize()
+    ms = timed(run, args.steps, torch.cuda.current_stream(device))
+    esize = batch.key_cache.element_size()
+    row = heads * dim
+    # read q, k, v and the two table rows; write q', k' and v
+    moved = tokens * (3 * row * 4 + dim * 4 + row * 4 + 2 * row * esize + 16)
+    return {
+        "rope_append_us": round(ms * 1e3, 2),
+        "rope_append_gbps": round(moved / (ms * 1e-3) / 1e9, 1),
+        "rope_append_bytes": moved,
+    }
 
 
 def config5(args) -> dict:

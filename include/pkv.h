@@ -95,6 +95,41 @@ int pkv_copy_blocks(void* key_pool, void* value_pool, pkv_dtype dtype, const int
                     int device, void* stream);
 
 /*
+ * Rotary embedding of one layer's queries and keys fused with the slot-mapped append of the
+ * rotated keys and the values.
+ *
+ * Replaces src/paged_kv_serving/engine/model.py:251-252 (apply_rope, model.py:70-81, on the q
+ * and k of the fused projection) followed by runner.py:195-196 (the append), for float32
+ * activations:
+ *     q' = rope(q, positions) ; key_pool[slots] = rope(k, positions) ; value_pool[slots] = v
+ * with rope(x)[i] = x[i]*cos - x[i+D/2]*sin and rope(x)[i+D/2] = x[i+D/2]*cos + x[i]*sin,
+ * cos/sin = table[position][i]; each product and sum is rounded separately, so the results
+ * equal the reference's float32 NumPy expressions bit for bit.
+ *
+ *   rotated_queries      : float32 [num_tokens, num_heads, head_dim], token stride
+ *                          rotated_token_stride. May be `queries` itself (same stride) to rotate
+ *                          in place; must not otherwise overlap an input.
+ *   queries, keys, values: float32 [num_tokens, num_heads, head_dim] with their own token
+ *                          strides (>= num_heads * head_dim), e.g. the three slices of a fused
+ *                          [num_tokens, 3, num_heads, head_dim] projection output.
+ *   positions            : int64 [num_tokens], absolute token positions.
+ *   cos_table, sin_table : float32 [table_rows, head_dim / 2] (model.py:60-67).
+ *   key_pool, value_pool : the layer's pools, [num_slots, num_heads, head_dim] of pool_dtype.
+ *   slot_mapping         : int64 [num_tokens].
+ * head_dim must be even. A token whose position is outside [0, table_rows) is skipped entirely
+ * (its rotated query is not written); a slot outside [0, num_slots) skips only that token's
+ * pool writes. The host validates both first; the checks only keep a bad index in bounds.
+ * Into a bfloat16 pool the rotated keys and the values are rounded to nearest even.
+ */
+int pkv_rope_append(float* rotated_queries, int64_t rotated_token_stride, const float* queries,
+                    const float* keys, const float* values, int64_t query_token_stride,
+                    int64_t key_token_stride, int64_t value_token_stride,
+                    const int64_t* positions, const float* cos_table, const float* sin_table,
+                    int64_t table_rows, void* key_pool, void* value_pool, pkv_dtype pool_dtype,
+                    int64_t num_slots, const int64_t* slot_mapping, int64_t num_tokens,
+                    int32_t num_heads, int32_t head_dim, int device, void* stream);
+
+/*
  * Bytes of float32 workspace pkv_paged_attention needs for a batch (0 when no query can span
  * more than one partition). Host-only.
  */

@@ -52,8 +52,10 @@ def rope_tables(max_seq_len: int, head_dim: int, theta: float) -> tuple[np.ndarr
     if head_dim % 2:
         raise ValueError("head_dim must be even for rotary embeddings")
     half = head_dim // 2
-    frequencies = theta ** (-(np.arange(half, dtype=np.float64) * 2.0 / head_dim))
-    angles = np.arange(max_seq_len, dtype=np.float64)[:, None] * frequencies[None, :]
+    # 1 / theta^x rather than theta^-x: the two differ in the last float64 bit for some i, which
+    # flips float32 table entries at head_dim >= 64.
+    frequencies = 1.0 / (theta ** (np.arange(half, dtype=np.float64) * 2.0 / head_dim))
+    angles = np.outer(np.arange(max_seq_len, dtype=np.float64), frequencies)
     return np.cos(angles).astype(np.float32), np.sin(angles).astype(np.float32)
 
 

@@ -34,7 +34,7 @@ REPO_ROOT = PACKAGE_DIR.parent
 CSRC = PACKAGE_DIR / "csrc"
 INCLUDE = REPO_ROOT / "include"
 LIB_PATH = PACKAGE_DIR / "libpkv.so"
-SOURCES = (CSRC / "pkv_copy.hip", CSRC / "pkv_attention.hip")
+SOURCES = (CSRC / "pkv_copy.hip", CSRC / "pkv_rope.hip", CSRC / "pkv_attention.hip")
 
 # gfx950 only. Packed-FP32 VALU instructions are disabled: the code relies on scalar fp32 FMA.
 HIPCC_FLAGS = (
@@ -61,6 +61,7 @@ EXPORTED_SYMBOLS = (
     "pkv_error_string",
     "pkv_append",
     "pkv_copy_blocks",
+    "pkv_rope_append",
     "pkv_attention_workspace_bytes",
     "pkv_tile_head_dim_supported",
     "pkv_paged_attention",
@@ -140,6 +141,16 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_int, _ptr,  # device, stream
     ]
     lib.pkv_copy_blocks.restype = _c_int
+    lib.pkv_rope_append.argtypes = [
+        _ptr, _i64,  # rotated_queries, rotated_token_stride
+        _ptr, _ptr, _ptr,  # queries, keys, values
+        _i64, _i64, _i64,  # query/key/value token strides
+        _ptr, _ptr, _ptr, _i64,  # positions, cos_table, sin_table, table_rows
+        _ptr, _ptr, _c_int, _i64,  # key_pool, value_pool, pool_dtype, num_slots
+        _ptr, _i64, _i32, _i32,  # slot_mapping, num_tokens, num_heads, head_dim
+        _c_int, _ptr,  # device, stream
+    ]
+    lib.pkv_rope_append.restype = _c_int
     lib.pkv_attention_workspace_bytes.argtypes = [_i64, _i32, _i32, _i32, _i32]
     lib.pkv_attention_workspace_bytes.restype = _i64
     lib.pkv_tile_head_dim_supported.argtypes = [_i32]

@@ -27,6 +27,7 @@ __all__ = [
     "paged_attention_ragged",
     "batch_hints",
     "plan_rows",
+    "rope_append",
     "upload_plan",
 ]
 
@@ -110,6 +111,73 @@ def append_kv(
         device, _stream(device),
     )  # fmt: skip
     _native.check(rc, "pkv_append")
+
+
+def rope_append(
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    queries: torch.Tensor,
+    keys: torch.Tensor,
+    values: torch.Tensor,
+    positions: torch.Tensor,
+    cos_table: torch.Tensor,
+    sin_table: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    *,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Rotate ``queries`` and ``keys`` by their positions and append the rotated keys and the
+    ``values`` to one layer's pools, in one kernel; returns the rotated queries.
+
+    Mirrors ``apply_rope`` on q and k (reference model.py:70-81, 251-252) followed by
+    ``key_pool.reshape(-1, H, D)[slots] = k; value_pool...[slots] = v`` (runner.py:195-196), bit
+    for bit in float32. ``queries``/``keys``/``values``: float32 ``[T, heads, head_dim]``,
+    token-strided views allowed (the slices of a fused projection). ``positions``, ``slot_mapping``:
+    int64 ``[T]``. ``cos_table``/``sin_table``: float32 ``[rows, head_dim / 2]``. ``out``: where
+    to write the rotated queries (``[T, heads, head_dim]`` float32 with contiguous rows; may be
+    ``queries`` itself); a new contiguous tensor when None.
+    """
+    device = _device_index(key_pool, value_pool, queries, keys, values, positions, cos_table, sin_table, slot_mapping)
+    if key_pool.shape != value_pool.shape or key_pool.dtype != value_pool.dtype:
+        raise ValueError("key and value pools must have the same shape and dtype")
+    if not (key_pool.is_contiguous() and value_pool.is_contiguous()):
+        raise ValueError("pools must be contiguous")
+    if queries.dim() != 3 or queries.shape != keys.shape or keys.shape != values.shape:
+        raise ValueError("queries, keys and values must all be [T, heads, head_dim]")
+    if any(t.dtype != torch.float32 for t in (queries, keys, values, cos_table, sin_table)):
+        raise ValueError("queries, keys, values and the rope tables must be float32")
+    tokens, heads, dim = queries.shape
+    if dim % 2:
+        raise ValueError("head_dim must be even for rotary embeddings")
+    if tuple(key_pool.shape[-2:]) != (heads, dim):
+        raise ValueError("pool rows and keys disagree on (heads, head_dim)")
+    if cos_table.shape != sin_table.shape or cos_table.dim() != 2 or cos_table.shape[1] != dim // 2:
+        raise ValueError("rope tables must both be [rows, head_dim / 2]")
+    if not (cos_table.is_contiguous() and sin_table.is_contiguous()):
+        raise ValueError("rope tables must be contiguous")
+    for name, index in (("positions", positions), ("slot_mapping", slot_mapping)):
+        if index.dtype != torch.int64 or index.shape != (tokens,):
+            raise ValueError(f"{name} must be int64 with one entry per token")
+    q_stride = _rows_contiguous(queries, "queries")
+    k_stride = _rows_contiguous(keys, "keys")
+    v_stride = _rows_contiguous(values, "values")
+    if out is None:
+        out = torch.empty((tokens, heads, dim), dtype=torch.float32, device=queries.device)
+    elif out.shape != queries.shape or out.dtype != torch.float32 or out.device != queries.device:
+        raise ValueError("out must be float32 [T, heads, head_dim] on the queries' device")
+    out_stride = _rows_contiguous(out, "out")
+    if tokens == 0:
+        return out
+    num_slots = key_pool.numel() // (heads * dim)
+    rc = _native.library().pkv_rope_append(
+        out.data_ptr(), out_stride, queries.data_ptr(), keys.data_ptr(), values.data_ptr(),
+        q_stride, k_stride, v_stride, positions.data_ptr(), cos_table.data_ptr(),
+        sin_table.data_ptr(), cos_table.shape[0], key_pool.data_ptr(), value_pool.data_ptr(),
+        kv_dtype_code(key_pool.dtype), num_slots, slot_mapping.data_ptr(), tokens, heads, dim,
+        device, _stream(device),
+    )  # fmt: skip
+    _native.check(rc, "pkv_rope_append")
+    return out
 
 
 def copy_blocks(key_pool: torch.Tensor, value_pool: torch.Tensor, pairs: torch.Tensor) -> None:

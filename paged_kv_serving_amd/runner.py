@@ -5,8 +5,9 @@ exactly like the reference's NumPy pools (runner.py:112-114), and is both the re
 ``EngineExecutor`` (``execute(batch) -> {seq_id: float32[vocab]}``, engine.py:64-73) and its
 ``BlockStore`` (``copy_block(src, dst)``, blocks.py:43-48). Per layer of :meth:`execute`:
 
-    torch (hipBLASLt) : RMSNorm, fused QKV projection, RoPE on q and k
-    pkv_append        : scatter this iteration's keys/values into their slots (one launch)
+    torch (hipBLASLt) : RMSNorm, fused QKV projection
+    pkv_rope_append   : RoPE on q (in place) and k, and the scatter of the rotated keys and the
+                        values into their slots, in one launch
     pkv_paged_attention : every query of the ragged batch against its block table in one call:
                           decode rows stream K/V per row, prefill runs go to the fp32 MFMA tile
                           pass, then the split-context reduce when a context spans partitions
@@ -110,13 +111,6 @@ def compute_slots(entries, block_size: int) -> np.ndarray:
 
 def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return x / torch.sqrt(torch.mean(x * x, dim=-1, keepdim=True) + eps) * weight
-
-
-def _rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """Half-split rotation of (T, H, D) by per-token (T, 1, D/2) tables."""
-    half = x.shape[-1] // 2
-    first, second = x[..., :half], x[..., half:]
-    return torch.cat([first * cos - second * sin, second * cos + first * sin], dim=-1)
 
 
 def _silu(x: torch.Tensor) -> torch.Tensor:
@@ -322,17 +316,17 @@ class ModelRunner:
         heads, dim, d_model = config.n_heads, config.head_dim, config.d_model
         eps = config.norm_eps
         scale = self.model.attention_scale
-        cos = w.cos[positions_d][:, None, :]
-        sin = w.sin[positions_d][:, None, :]
         hidden = w.embedding[tokens_d]
         workspace = None
         attended = torch.empty((total, heads, dim), dtype=torch.float32, device=self.device)
         for index, (attn_norm, qkv, out_proj, ffn_norm, gate, up, down) in enumerate(w.layers):
             fused = (_rms_norm(hidden, attn_norm, eps) @ qkv).view(total, 3, heads, dim)
-            queries = _rope(fused[:, 0], cos, sin)
-            keys = _rope(fused[:, 1], cos, sin)
-            values = fused[:, 2]
-            ops.append_kv(self._keys[index], self._values[index], keys, values, slots_d)
+            # RoPE on q (in place) and k, and the append of k and v, in one kernel
+            # (reference model.py:251-252 then runner.py:195-196).
+            queries = ops.rope_append(
+                self._keys[index], self._values[index], fused[:, 0], fused[:, 1], fused[:, 2],
+                positions_d, w.cos, w.sin, slots_d, out=fused[:, 0],
+            )  # fmt: skip
             if workspace is None:
                 need = ops.attention_workspace_bytes(total, heads, dim, max_context, partition)
                 workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=self.device)

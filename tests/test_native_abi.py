@@ -93,6 +93,29 @@ def test_bad_arguments_are_refused_before_any_device_work(lib) -> None:
     assert lib.pkv_tile_head_dim_supported(16) == 0
 
 
+def test_rope_append_arguments_are_refused_before_any_device_work(lib) -> None:
+    # Placeholder addresses: every call below returns before touching them or the device.
+    fake = [ctypes.c_void_p(4096 * (i + 1)) for i in range(9)]
+    rot, q, k, v, pos, cos, sin, kp, vp = fake
+    slots = ctypes.c_void_p(4096 * 20)
+
+    def call(rot_stride=64, strides=(64, 64, 64), dtype=0, tokens=2, heads=2, dim=32, q_ptr=q, **kw):
+        return lib.pkv_rope_append(
+            kw.get("rot", rot), rot_stride, q_ptr, k, v, *strides, pos, cos, sin, 16, kp, vp,
+            dtype, 100, slots, tokens, heads, dim, 0, None,
+        )  # fmt: skip
+
+    assert call(dim=31) == -1  # odd head_dim
+    assert call(heads=0) == -1
+    assert call(dtype=7) == -1  # unknown pool dtype
+    assert call(tokens=-1) == -1
+    assert call(tokens=0) == 0  # nothing to do
+    assert call(strides=(63, 64, 64)) == -1  # a token stride shorter than a row
+    assert call(rot_stride=32) == -1
+    assert call(rot=q, rot_stride=64, strides=(192, 192, 192)) == -1  # in place needs equal strides
+    assert call(q_ptr=None) == -1  # null pointer
+
+
 def test_missing_library_fails_loudly(tmp_path, monkeypatch) -> None:
     monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "absent.so")
     monkeypatch.setattr(_native, "_LIB", None)

@@ -75,6 +75,21 @@ def test_rope_at_position_zero_is_the_identity_and_tables_agree() -> None:
         rope_tables(8, 7, 10_000.0)
 
 
+@pytest.mark.parametrize("head_dim", [32, 128, 256])
+def test_rope_tables_follow_the_closed_form(head_dim) -> None:
+    """cos/sin(p * theta^(-2i/D)) to float32 rounding; column 0 is cos(p); bit-equal to the
+    package's tables, which use the reference's 1 / theta^x form (model.py:64-66)."""
+    cos, sin = rope_tables(4096, head_dim, 10_000.0)
+    assert cos.shape == (4096, head_dim // 2) and cos.dtype == np.float32
+    p = np.arange(4096, dtype=np.float64)[:, None]
+    i = np.arange(head_dim // 2, dtype=np.float64)[None, :]
+    angle = p * np.exp(-np.log(10_000.0) * 2.0 * i / head_dim)
+    assert np.max(np.abs(cos - np.cos(angle))) < 1e-6 and np.max(np.abs(sin - np.sin(angle))) < 1e-6
+    assert np.array_equal(cos[:, 0], np.cos(np.arange(4096, dtype=np.float64)).astype(np.float32))
+    pcos, psin = package_rope_tables(4096, head_dim, 10_000.0)
+    assert np.array_equal(cos, pcos) and np.array_equal(sin, psin)
+
+
 def test_random_weights_are_deterministic_and_match_the_package() -> None:
     a, b = random_weights(TINY, seed=1), random_weights(TINY, seed=1)
     assert np.array_equal(a.token_embedding, b.token_embedding)
