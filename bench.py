@@ -494,7 +494,8 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this build has no "
-            "multi-GPU path; see DESIGN.md for how the data path would shard)",
+            "multi-GPU path; the data path shards by heads with no exchange, which one GPU's "
+            "share at its real shape already measures)",
             file=sys.stderr,
         )
         return 2

@@ -195,6 +195,21 @@ int pkv_paged_attention(float* out, const float* queries, int64_t query_token_st
                         int32_t max_context_len, int32_t partition_size, int32_t flags,
                         float* workspace, int64_t workspace_bytes, int device, void* stream);
 
+/*
+ * Greedy sampling: the argmax of each logits row, on the device.
+ *
+ * Replaces src/paged_kv_serving/engine/sampling.py:28-30 (greedy_token: int(np.argmax(logits)))
+ * applied to every row the engine samples from, so one int32 per row crosses PCIe instead of
+ * the whole row. NumPy's rules: ties resolve to the lowest id; a NaN beats every number and the
+ * first NaN wins; -0.0 and +0.0 tie.
+ *
+ *   token_ids  : int32 [num_rows], output.
+ *   logits     : float32 rows of vocab_size values; row r starts at element r * row_stride
+ *                (row_stride >= vocab_size).
+ */
+int pkv_greedy_tokens(int32_t* token_ids, const float* logits, int64_t row_stride,
+                      int64_t num_rows, int64_t vocab_size, int device, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,6 @@ Modules:
     runner     -- slots, append, copy-on-write and the paged forward (runner.py:95-227)
     bf16       -- round-to-nearest-even float32 -> bfloat16 for the bf16-KV tolerance oracle
 
-How each function is pinned (closed forms, invariants, brute force) is recorded in DESIGN.md and
-exercised by ``tests/test_oracle_*.py``.
+Each function is pinned (closed forms, invariants, brute force on tiny inputs, planted mistakes)
+by ``tests/test_oracle_*.py``.
 """

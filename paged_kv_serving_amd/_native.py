@@ -34,7 +34,9 @@ REPO_ROOT = PACKAGE_DIR.parent
 CSRC = PACKAGE_DIR / "csrc"
 INCLUDE = REPO_ROOT / "include"
 LIB_PATH = PACKAGE_DIR / "libpkv.so"
-SOURCES = (CSRC / "pkv_copy.hip", CSRC / "pkv_rope.hip", CSRC / "pkv_attention.hip")
+SOURCES = (
+    CSRC / "pkv_copy.hip", CSRC / "pkv_rope.hip", CSRC / "pkv_attention.hip", CSRC / "pkv_sample.hip"
+)
 
 # gfx950 only. Packed-FP32 VALU instructions are disabled: the code relies on scalar fp32 FMA.
 HIPCC_FLAGS = (
@@ -65,6 +67,7 @@ EXPORTED_SYMBOLS = (
     "pkv_attention_workspace_bytes",
     "pkv_tile_head_dim_supported",
     "pkv_paged_attention",
+    "pkv_greedy_tokens",
 )
 
 
@@ -167,6 +170,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_int, _ptr,  # device, stream
     ]
     lib.pkv_paged_attention.restype = _c_int
+    lib.pkv_greedy_tokens.argtypes = [
+        _ptr, _ptr, _i64, _i64, _i64,  # token_ids, logits, row_stride, num_rows, vocab_size
+        _c_int, _ptr,  # device, stream
+    ]
+    lib.pkv_greedy_tokens.restype = _c_int
 
 
 def library() -> ctypes.CDLL:

@@ -2,7 +2,7 @@
 
 The scheduler and engine are callers of the data path, not part of it. This module restates
 their behaviour for a single service class with no deadlines, so the path can run end to end
-without the reference's code:
+(the config-1 workload) without the reference's code:
 
 * ``Scheduler.schedule`` follows src/paged_kv_serving/engine/scheduler.py:209-425:
   - decode rows first, one token per decoding sequence in priority order;
@@ -17,7 +17,9 @@ their behaviour for a single service class with no deadlines, so the path can ru
   returned rows, fork the remaining samples of an n-way request, and free finished sequences.
 
 Sampling is greedy (``argmax``, ties to the lowest id, sampling.py:28-30), the only policy the
-data-path runs use.
+data-path runs use. With the GPU runner it runs on the device (``ModelRunner.execute_greedy``,
+one int32 per row back to the host); an executor with only ``execute`` (the NumPy runner, a
+recording wrapper) is sampled on the host with the same rule.
 """
 
 from __future__ import annotations
@@ -39,7 +41,7 @@ from paged_kv_serving_amd.sequence import (
     finish_reason_for,
 )
 
-__all__ = ["Engine", "RecordingExecutor", "Scheduler", "ScheduledSequence", "SchedulerOutput"]
+__all__ = ["Engine", "RecordingExecutor", "Scheduler", "ScheduledSequence", "SchedulerOutput", "greedy_token"]
 
 
 @dataclass(frozen=True)
@@ -218,6 +220,13 @@ class Scheduler:
         )
 
 
+def greedy_token(logits: np.ndarray) -> int:
+    """Highest-scoring token id, ties to the lowest id (reference sampling.py:28-30, 62-65)."""
+    if logits.ndim != 1:
+        raise ValueError("logits must be a 1-D array over the vocabulary")
+    return int(np.argmax(logits))
+
+
 @dataclass
 class RecordingExecutor:
     """Executes on a runner and keeps a copy of every logits row (equivalence.py:120-139)."""
@@ -305,37 +314,40 @@ class Engine:
         if output.is_empty:
             return output
         self.iterations += 1
-        logits = self.executor.execute(output.batch)
+        # An executor that samples on the device (ModelRunner.execute_greedy) returns token ids;
+        # any other returns host logits rows, sampled here with the same argmax rule.
+        device_greedy = getattr(self.executor, "execute_greedy", None)
+        if device_greedy is not None:
+            tokens = device_greedy(output.batch)
+        else:
+            tokens = {seq_id: greedy_token(row) for seq_id, row in self.executor.execute(output.batch).items()}
         for item in output.scheduled:
             seq = item.sequence
             seq.num_computed_tokens += item.num_tokens
             self.cache.publish_full_blocks(seq)
             if not item.produces_token:
                 continue
-            row = logits[seq.seq_id]
-            self._fork_pending(seq, row)
-            self._emit(seq, row)
+            token = tokens[seq.seq_id]
+            self._fork_pending(seq, token)
+            self._emit(seq, token)
         for seq in self.scheduler.drop_finished():
             state = self._requests.get(seq.request.request_id)
             if state is not None:
                 state.finished[seq.sample_index] = tuple(seq.output_token_ids)
         return output
 
-    def _fork_pending(self, seq: Sequence, row: np.ndarray) -> None:
+    def _fork_pending(self, seq: Sequence, token: int) -> None:
         state = self._requests.get(seq.request.request_id)
         if state is None or seq.sample_index != 0 or seq.num_output_tokens:
             return
         for child in state.pending_forks:
             self.cache.fork(seq, child)
             self.scheduler.add_running(child)
-            self._emit(child, row)
+            self._emit(child, token)
         state.pending_forks.clear()
         seq.fork_slots = 0
 
-    def _emit(self, seq: Sequence, row: np.ndarray) -> None:
-        if row.ndim != 1:
-            raise ValueError("logits must be a 1-D array over the vocabulary")
-        token = int(np.argmax(row))
+    def _emit(self, seq: Sequence, token: int) -> None:
         seq.append_token(token)
         reason = finish_reason_for(
             seq, token, eos_token_id=self.eos_token_id, max_context_tokens=self.config.max_context_tokens

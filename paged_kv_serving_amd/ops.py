@@ -22,6 +22,7 @@ __all__ = [
     "append_kv",
     "attention_workspace_bytes",
     "copy_blocks",
+    "greedy_tokens",
     "independent_groups",
     "kv_dtype_code",
     "paged_attention_ragged",
@@ -177,6 +178,34 @@ def rope_append(
         device, _stream(device),
     )  # fmt: skip
     _native.check(rc, "pkv_rope_append")
+    return out
+
+
+def greedy_tokens(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Argmax of each row of float32 ``logits [rows, vocab]`` as int32 ``[rows]``, on the device.
+
+    Mirrors ``int(np.argmax(row))`` (reference sampling.py:28-30) row by row: ties go to the
+    lowest id, the first NaN wins.
+    """
+    device = _device_index(logits)
+    if logits.dim() != 2 or logits.dtype != torch.float32:
+        raise ValueError("logits must be float32 of shape (rows, vocab)")
+    rows, vocab = logits.shape
+    if vocab < 1:
+        raise ValueError("logits need at least one column")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    elif out.shape != (rows,) or out.dtype != torch.int32 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous int32 tensor with one entry per row")
+    if rows == 0:
+        return out
+    stride = logits.stride(0) if rows > 1 else vocab
+    rc = _native.library().pkv_greedy_tokens(
+        out.data_ptr(), logits.data_ptr(), stride, rows, vocab, device, _stream(device)
+    )
+    _native.check(rc, "pkv_greedy_tokens")
     return out
 
 

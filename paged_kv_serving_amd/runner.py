@@ -261,9 +261,27 @@ class ModelRunner:
         Keys and values of every token are written into the pool as a side effect, so the
         blocks named by each entry's block table must have been allocated first.
         """
+        names, logits = self._forward(batch)
+        if not names:
+            return {}
+        host = logits.cpu().numpy()
+        return {name: host[i] for i, name in enumerate(names)}
+
+    def execute_greedy(self, batch: ExecutionBatch) -> dict[str, int]:
+        """:meth:`execute` followed by greedy sampling on the device: the argmax token id of each
+        logits row (reference sampling.py:28-30), one int32 per row copied to the host."""
+        names, logits = self._forward(batch)
+        if not names:
+            return {}
+        tokens = ops.greedy_tokens(logits).cpu().numpy()
+        return {name: int(tokens[i]) for i, name in enumerate(names)}
+
+    def _forward(self, batch: ExecutionBatch) -> tuple[list[str], torch.Tensor | None]:
+        """The forward pass of one iteration: (seq ids, device logits [rows, vocab]) of the
+        entries that ask for logits, in batch order."""
         entries = batch.entries
         if not entries:
-            return {}
+            return [], None
         config = self.model.config
         total = sum(len(entry.token_ids) for entry in entries)
         tokens = np.fromiter((t for e in entries for t in e.token_ids), dtype=np.int64, count=total)
@@ -346,8 +364,6 @@ class ModelRunner:
                 names.append(entry.seq_id)
             offset += len(entry.token_ids)
         if not wanted:
-            return {}
+            return [], None
         rows = torch.tensor(wanted, dtype=torch.int64).to(self.device)
-        logits = _rms_norm(hidden[rows], w.final_norm, eps) @ w.embedding.T
-        host = logits.cpu().numpy()
-        return {name: host[i] for i, name in enumerate(names)}
+        return names, _rms_norm(hidden[rows], w.final_norm, eps) @ w.embedding.T

@@ -116,6 +116,15 @@ def test_rope_append_arguments_are_refused_before_any_device_work(lib) -> None:
     assert call(q_ptr=None) == -1  # null pointer
 
 
+def test_greedy_tokens_arguments_are_refused_before_any_device_work(lib) -> None:
+    out, logits = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
+    assert lib.pkv_greedy_tokens(out, logits, 8, 2, 0, 0, None) == -1  # empty vocabulary
+    assert lib.pkv_greedy_tokens(out, logits, 7, 2, 8, 0, None) == -1  # stride shorter than a row
+    assert lib.pkv_greedy_tokens(out, logits, 8, -1, 8, 0, None) == -1
+    assert lib.pkv_greedy_tokens(out, logits, 8, 0, 8, 0, None) == 0  # no rows: nothing to do
+    assert lib.pkv_greedy_tokens(None, logits, 8, 2, 8, 0, None) == -1
+
+
 def test_missing_library_fails_loudly(tmp_path, monkeypatch) -> None:
     monkeypatch.setattr(_native, "LIB_PATH", tmp_path / "absent.so")
     monkeypatch.setattr(_native, "_LIB", None)
