@@ -314,9 +314,13 @@ SHARED_KV_FRACTION = 0.25
 
 
 def batch_hints(
-    tables: list, context_lens: np.ndarray, num_heads: int, block_size: int, num_rows: int | None = None
-) -> tuple[int, bool]:
+    tables: list | None, context_lens: np.ndarray, num_heads: int, block_size: int,
+    num_rows: int | None = None, *, used_ids: np.ndarray | None = None,
+) -> tuple[int, bool]:  # fmt: skip
     """``(partition_size, shared_kv)`` for a batch, from its host block tables and contexts.
+
+    ``used_ids`` (every sequence's first ``ceil(context / block_size)`` table entries,
+    concatenated) may be passed instead of ``tables``.
 
     Partition size: 1024 when ``rows x heads x ceil(context / 1024)`` reaches
     ``WIDE_PARTITION_ITEMS``, else 512 (measured on MI355X: long contexts and large batches gain
@@ -331,10 +335,18 @@ def batch_hints(
     per_seq_rows = 1 if num_rows is None else max(1, num_rows // contexts.size)
     wide = int(np.sum(-(-contexts // 1024))) * per_seq_rows * num_heads
     partition = 1024 if wide >= WIDE_PARTITION_ITEMS else 512
-    used = [np.asarray(t[: -(-int(c) // block_size)]) for t, c in zip(tables, contexts)]
-    ids = np.concatenate(used) if used else np.zeros(0, np.int64)
-    repeated = ids.size - np.unique(ids).size
-    shared = ids.size > 0 and repeated >= SHARED_KV_FRACTION * ids.size
+    if used_ids is None:
+        used = [np.asarray(t[: -(-int(c) // block_size)]) for t, c in zip(tables, contexts)]
+        used_ids = np.concatenate(used) if used else np.zeros(0, np.int64)
+    ids = np.asarray(used_ids)
+    if ids.size == 0:
+        return partition, False
+    low, high = int(ids.min()), int(ids.max())
+    if 0 <= low and high < (1 << 26):  # block ids: a histogram is cheaper than a sort
+        distinct = int(np.count_nonzero(np.bincount(ids, minlength=0)))
+    else:
+        distinct = int(np.unique(ids).size)
+    shared = ids.size - distinct >= SHARED_KV_FRACTION * ids.size
     return partition, bool(shared)
 
 

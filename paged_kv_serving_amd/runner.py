@@ -32,6 +32,7 @@ import numpy as np
 import torch
 
 from paged_kv_serving_amd import ops
+from paged_kv_serving_amd.tables import BlockTableArena
 
 __all__ = ["DEFAULT_TILE_BLOCKS", "BatchEntry", "ExecutionBatch", "ModelRunner", "compute_slots"]
 
@@ -96,17 +97,34 @@ def compute_slots(entries, block_size: int) -> np.ndarray:
     The slot mapping of runner.py:149-159 and :184-186, vectorised per entry; a position past
     the entry's table raises the reference's ValueError, naming the first such position.
     """
-    parts = []
+    total = sum(len(entry.positions) for entry in entries)
+    out = np.empty(total, dtype=np.int64)
+    offset = 0
     for entry in entries:
-        positions = np.asarray(entry.positions, dtype=np.int64)
-        table = np.asarray(entry.block_table, dtype=np.int64)
-        index = positions // block_size
-        missing = np.nonzero(index >= table.size)[0]
+        positions, table = entry.positions, entry.block_table
+        if len(positions) == 1:  # a decode row: one lookup, no array conversion of the table
+            position = positions[0]
+            index = position // block_size
+            if index >= len(table):
+                raise ValueError(f"sequence {entry.seq_id}: position {position} has no block in the table")
+            out[offset] = table[index] * block_size + position % block_size
+            offset += 1
+            continue
+        where = np.asarray(positions, dtype=np.int64)
+        index = where // block_size
+        missing = np.nonzero(index >= len(table))[0]
         if missing.size:
-            position = int(positions[missing[0]])
+            position = int(where[missing[0]])
             raise ValueError(f"sequence {entry.seq_id}: position {position} has no block in the table")
-        parts.append(table[index] * block_size + positions % block_size)
-    return np.concatenate(parts) if parts else np.zeros(0, dtype=np.int64)
+        low = int(index.min())
+        if low >= 0:  # convert only the stretch of the table the chunk touches
+            blocks = np.asarray(table[low : int(index.max()) + 1], dtype=np.int64)
+            index = index - low
+        else:  # negative positions index from the end, as the reference's tuple lookup does
+            blocks = np.asarray(table, dtype=np.int64)
+        out[offset : offset + where.size] = blocks[index] * block_size + where % block_size
+        offset += where.size
+    return out
 
 
 def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -179,6 +197,7 @@ class ModelRunner:
         self._values = torch.zeros(shape, dtype=kv_dtype, device=self.device)
         self._pending: list[tuple[int, int]] = []
         self._weights: _DeviceWeights | None = None
+        self._tables = BlockTableArena(self.device)
 
     # --- pool ---------------------------------------------------------------------------
 
@@ -297,33 +316,39 @@ class ModelRunner:
             raise IndexError("a block table names a block outside the pool")
 
         num_seqs = len(entries)
-        width = max(max(len(e.block_table) for e in entries), 1)
-        tables = np.zeros((num_seqs, width), dtype=np.int32)
-        for row, entry in enumerate(entries):
-            tables[row, : len(entry.block_table)] = entry.block_table
+        # Block tables live in a device arena between calls; only changed entries travel.
+        update = self._tables.update(entries)
+        arena_rows = self._tables.num_rows
         context = np.fromiter((e.positions[-1] + 1 for e in entries), dtype=np.int32, count=num_seqs)
-        query_seq = np.repeat(np.arange(num_seqs, dtype=np.int32), [len(e.token_ids) for e in entries])
+        contexts_by_row = np.zeros(arena_rows, dtype=np.int32)
+        contexts_by_row[update.rows] = context
+        per_entry = np.fromiter((len(e.token_ids) for e in entries), dtype=np.int64, count=num_seqs)
+        query_seq = np.repeat(update.rows, per_entry)
         plan_rows, plan_tiles = ops.plan_rows(query_seq, config.head_dim)
+        used = self._tables.used_blocks(update.rows, -(-context.astype(np.int64) // self.block_size))
         hint_partition, shared_kv = ops.batch_hints(
-            [e.block_table for e in entries], context, config.n_heads, self.block_size, total
+            None, context, config.n_heads, self.block_size, total, used_ids=used
         )
         partition = self.partition_size or hint_partition
-        meta64 = torch.from_numpy(np.concatenate([tokens, positions, slots])).to(self.device)
+        changed = update.index.size
+        meta64 = torch.from_numpy(np.concatenate([tokens, positions, slots, update.index])).to(self.device)
         meta32 = torch.from_numpy(
             np.concatenate([
-                positions.astype(np.int32), query_seq, context, tables.ravel(),
+                positions.astype(np.int32), query_seq, contexts_by_row, update.values,
                 plan_rows, plan_tiles.ravel(),
             ])  # fmt: skip
         ).to(self.device)
-        tokens_d, positions_d, slots_d = meta64[:total], meta64[total : 2 * total], meta64[2 * total :]
+        tokens_d, positions_d = meta64[:total], meta64[total : 2 * total]
+        slots_d = meta64[2 * total : 3 * total]
         qpos_d = meta32[:total]
         qseq_d = meta32[total : 2 * total]
-        context_d = meta32[2 * total : 2 * total + num_seqs]
-        end_tables = 2 * total + num_seqs + num_seqs * width
-        tables_d = meta32[2 * total + num_seqs : end_tables].view(num_seqs, width)
+        context_d = meta32[2 * total : 2 * total + arena_rows]
+        end_values = 2 * total + arena_rows + changed
+        self._tables.apply(meta64[3 * total :], meta32[2 * total + arena_rows : end_values])
+        tables_d = self._tables.tables
         plan = ops.AttentionPlan(
-            rows=meta32[end_tables : end_tables + plan_rows.size],
-            tiles=meta32[end_tables + plan_rows.size :].view(-1, 2),
+            rows=meta32[end_values : end_values + plan_rows.size],
+            tiles=meta32[end_values + plan_rows.size :].view(-1, 2),
             partition_size=partition,
             shared_kv=shared_kv,
         )

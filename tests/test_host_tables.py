@@ -1,0 +1,118 @@
+"""The device block-table arena (paged_kv_serving_amd.tables), on the CPU.
+
+After every update + apply, each entry's arena row must start with exactly its block table (the
+rest of the row is never read: attention reads only a sequence's first ceil(context / B)
+entries), on the host mirror and on the "device" tensor (a CPU tensor here; the GPU runner tests
+run the same code on the GPU). Only entries that differ from what a row holds may travel.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from paged_kv_serving_amd.tables import BlockTableArena, _common_prefix
+
+
+@dataclass(frozen=True)
+class Entry:
+    seq_id: str
+    block_table: tuple[int, ...]
+
+
+def step(arena: BlockTableArena, entries):
+    update = arena.update(entries)
+    arena.apply(torch.from_numpy(update.index), torch.from_numpy(update.values))
+    for entry, row in zip(entries, update.rows.tolist()):
+        n = len(entry.block_table)
+        assert tuple(arena.host[row, :n].tolist()) == entry.block_table
+        assert tuple(arena.tables[row, :n].tolist()) == entry.block_table
+    assert len(set(update.rows.tolist())) == len(entries), "one row per entry"
+    return update
+
+
+def test_only_changed_entries_travel() -> None:
+    arena = BlockTableArena("cpu", rows=4, width=8)
+    first = step(arena, [Entry("a", (5, 6, 7)), Entry("b", (9,))])
+    assert first.index.size == 4  # both tables are new
+    assert step(arena, [Entry("a", (5, 6, 7)), Entry("b", (9,))]).index.size == 0
+    grown = step(arena, [Entry("a", (5, 6, 7, 8)), Entry("b", (9,))])  # a decode step's new block
+    assert grown.index.tolist() == [first.rows[0] * arena.width + 3] and grown.values.tolist() == [8]
+    cow = step(arena, [Entry("a", (5, 6, 11, 8))])  # copy-on-write swapped one block
+    assert cow.values.tolist() == [11, 8]
+    shrunk = step(arena, [Entry("a", (5, 6))])  # a prefix of what the row holds: nothing to send
+    assert shrunk.index.size == 0
+
+
+def test_least_recently_used_rows_are_reclaimed_and_refilled() -> None:
+    arena = BlockTableArena("cpu", rows=2, width=4)
+    rows_a = step(arena, [Entry("a", (1, 2))]).rows
+    step(arena, [Entry("b", (3, 4))])
+    step(arena, [Entry("a", (1, 2))])  # b is now the least recently used
+    rows_c = step(arena, [Entry("c", (7,))]).rows
+    assert rows_c[0] != rows_a[0]
+    back = step(arena, [Entry("b", (3, 4))])  # b lost its row: the whole table travels again
+    assert back.index.size == 2 and back.rows[0] != step(arena, [Entry("a", (1, 2))]).rows[0]
+
+
+def test_growth_keeps_contents() -> None:
+    arena = BlockTableArena("cpu", rows=2, width=2)
+    step(arena, [Entry("a", (1, 2)), Entry("b", (3,))])
+    many = [Entry(f"s{i}", tuple(range(i, i + 2 + i))) for i in range(7)]
+    step(arena, many)  # more entries than rows, longer tables than the width
+    assert arena.num_rows >= 7 and arena.width >= 8
+    again = step(arena, many)
+    assert again.index.size == 0, "growth kept every row's contents"
+
+
+def test_a_sequence_twice_in_one_batch_gets_two_rows() -> None:
+    arena = BlockTableArena("cpu", rows=4, width=4)
+    update = step(arena, [Entry("a", (1, 2)), Entry("a", (1, 3))])
+    assert update.rows[0] != update.rows[1]
+
+
+def test_used_blocks_concatenates_the_visible_prefix() -> None:
+    arena = BlockTableArena("cpu", rows=4, width=6)
+    update = step(arena, [Entry("a", (1, 2, 3, 4)), Entry("b", (7, 8))])
+    assert arena.used_blocks(update.rows, np.asarray([3, 1])).tolist() == [1, 2, 3, 7]
+
+
+@pytest.mark.parametrize(
+    ("old", "new", "want"),
+    [((), (1,), 0), ((1, 2, 3), (1, 2, 3), 3), ((1, 2, 3), (1, 9, 3), 1), ((1, 2), (1, 2, 5), 2), ((4,), (5,), 0)],
+)
+def test_common_prefix(old, new, want) -> None:
+    assert _common_prefix(old, new) == want
+
+
+@settings(max_examples=60, deadline=None)
+@given(st.data())
+def test_random_table_histories_read_back(data) -> None:
+    """Random sequences join, grow, copy-on-write a block, leave and come back, over many steps;
+    every step's entries read back exactly from both mirrors."""
+    arena = BlockTableArena("cpu", rows=data.draw(st.integers(1, 4)), width=data.draw(st.integers(1, 4)))
+    tables: dict[str, list[int]] = {}
+    next_block = 0
+    for _ in range(data.draw(st.integers(1, 25))):
+        names = data.draw(st.lists(st.sampled_from("abcdefg"), min_size=1, max_size=6, unique=True))
+        entries = []
+        for name in names:
+            table = tables.setdefault(name, [])
+            action = data.draw(st.sampled_from(["grow", "cow", "keep", "reset"]))
+            if action == "grow" or not table:
+                for _ in range(data.draw(st.integers(1, 3))):
+                    table.append(next_block)
+                    next_block += 1
+            elif action == "cow":
+                table[data.draw(st.integers(0, len(table) - 1))] = next_block
+                next_block += 1
+            elif action == "reset":  # preempted and recomputed with fresh blocks
+                table[:] = [next_block]
+                next_block += 1
+            entries.append(Entry(name, tuple(table)))
+        step(arena, entries)
