@@ -151,7 +151,8 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  * per-sequence loop of src/paged_kv_serving/engine/runner.py:198-212: one call covers every
  * sequence of the batch, decode rows and prefill-chunk rows alike.
  *
- *   out              : float32 [num_queries, num_heads, head_dim], contiguous.
+ *   out              : float32 [num_queries, num_heads, head_dim], contiguous; 16-byte aligned
+ *                      when num_tiles > 0.
  *   queries          : float32; query t starts at element t * query_token_stride, and its
  *                      [num_heads, head_dim] block is contiguous.
  *   query_positions  : int32 [num_queries], absolute position of each query (the causal mask:
@@ -178,7 +179,7 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *                      0 selects the library default (512).
  *   flags            : 0 or PKV_ATTN_SHARED_KV.
  *   workspace        : float32 scratch of pkv_attention_workspace_bytes(...) bytes (may be
- *                      NULL when that is 0).
+ *                      NULL when that is 0); 16-byte aligned when num_tiles > 0.
  * A query whose every key is masked gets a zero output (attention.py:120-121).
  * Block ids are read only for positions below the query's visible length, so table entries
  * past a sequence's last used block may hold anything. Supported head_dim: 8, 16, 32, 64, 128,

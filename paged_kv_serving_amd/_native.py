@@ -39,6 +39,9 @@ SOURCES = (
 )
 
 # gfx950 only. Packed-FP32 VALU instructions are disabled: the code relies on scalar fp32 FMA.
+# MFMA accumulators are kept in VGPRs rather than AGPRs: the tile pass rescales its output rows
+# with VALU multiplies, which on AGPRs costs a copy out and back per key tile (measured: the
+# config-3 tile pass 0.84 -> 0.78 ms).
 HIPCC_FLAGS = (
     "--offload-arch=gfx950",
     "-O3",
@@ -49,6 +52,8 @@ HIPCC_FLAGS = (
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    "-mllvm",
+    "-amdgpu-mfma-vgpr-form",
 )
 
 # pkv_dtype values and pkv_paged_attention flags (include/pkv.h).

@@ -10,11 +10,11 @@
 //     an online softmax (running max, running sum, unnormalised accumulator) per lane group in
 //     registers. The lane groups are merged through LDS at the end.
 //  2. tile_partial (compute-bound rows: a run of consecutive prefill rows of one sequence): one
-//     workgroup per (tile of <= 64 rows, head, context partition). Key and value tiles of 16 rows
-//     are staged in padded LDS and shared by 4 wavefronts of 16 queries each; the scores are
-//     computed as S^T = K Q^T and the output as O = P V with v_mfma_f32_16x16x4f32, so every
-//     lane owns one query's four scores per tile and the P operand of the second product is the
-//     lane's own registers.
+//     workgroup per (tile of <= 64 rows, head, context partition). Key and value tiles of 32 rows
+//     (16 at head_dim 256) are staged in padded LDS and shared by 4 wavefronts of 16 queries
+//     each; the scores are computed as S^T = K Q^T and the output as O = P V with
+//     v_mfma_f32_16x16x4f32, so every lane owns four scores of one query per 16 keys and the P
+//     operand of the second product is the lane's own registers.
 //  3. reduce: rows whose visible context spans several partitions merge the per-partition
 //     (max, sum, acc) and write the normalised output. Rows that fit one partition were written
 //     by pass 1 or 2 directly.
@@ -46,11 +46,7 @@ namespace {
 #ifndef PKV_ATTN_NONTEMPORAL
 #define PKV_ATTN_NONTEMPORAL 1
 #endif
-// tile_partial: prefetch the next key tile during the MFMAs of the current one; and run the tile
-// pass on a second stream beside the row pass when a call has both.
-#ifndef PKV_TILE_PIPELINE
-#define PKV_TILE_PIPELINE 1
-#endif
+// Run the tile pass on a second stream beside the row pass when a call has both.
 #ifndef PKV_ATTN_OVERLAP
 #define PKV_ATTN_OVERLAP 1
 #endif
@@ -64,7 +60,6 @@ constexpr int kMaxPartition = 1024;     // keys per partition, upper bound
 constexpr int kDefaultPartition = 512;
 constexpr int kTableSlots = kMaxPartition + 4;  // ceil(P / B) + 1 entries at most
 constexpr int kTileRows = 64;           // query rows per tile_partial workgroup (4 x 16)
-constexpr int kTileKeys = 16;           // keys per LDS tile in tile_partial
 constexpr int kTileThreads = 256;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -377,29 +372,72 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Pass 2: tile_partial (fp32 MFMA). Lane l of a wavefront is (c = l / 16, n = l % 16).
+// Pass 2: tile_partial (fp32 MFMA). Lane l of a wavefront is (c = l / 16, n = l % 16); wavefront
+// w owns the tile's queries 16w .. 16w + 15. Keys are staged in LDS kKeys at a time, as kSub
+// column blocks of 16 keys.
 //
-//   S^T = K Q^T  with v_mfma_f32_16x16x4f32, kD4 = D / 4 steps. In step s, the k index of lane
-//                group c stands for head dimension c * kD4 + s, so lane (c, n) supplies
-//                A = K[key n][c * kD4 + s] (from LDS) and B = Q[query n][c * kD4 + s] (from
-//                registers). The result holds S[query n][key 4c + r] in register r.
-//   O = P V      four steps per 16-key tile; in step m the k index of lane group c stands for key
-//                4c + m, so A = P[query n][key 4c + m] is the lane's own register m and
-//                B = V[key 4c + m][16b + n] for output tile b. Register r of output tile b holds
-//                O[query 4c + r][16b + n].
+//   S^T = K Q^T  with v_mfma_f32_16x16x4f32, kD4 = D / 4 steps per 16-key block j. In step s, the
+//                k index of lane group c stands for head dimension c * kD4 + s, so lane (c, n)
+//                supplies A = K[key 16j + n][c * kD4 + s] (from LDS) and B = Q[query n][c * kD4
+//                + s] (from registers). Register r of block j holds S[query n][key 16j + 4c + r].
+//                The kSub chains are independent and interleaved.
+//   O^T = V^T P^T  four steps per 16-key block; in step m the k index of lane group c stands for
+//                key 16j + 4c + m, so lane (c, n) supplies A = V[key 16j + 4c + m][16b + n] for
+//                output tile b (from LDS) and B = P[query n][key 16j + 4c + m], its own register
+//                m. Register r of output tile b holds O[query n][16b + 4c + r]: every lane owns
+//                four dimensions of its own query's output row, so rescaling a row needs only the
+//                lane's own factor.
+//
+// Online softmax with a lazy reference: probabilities are exp2(s - m_ref), where m_ref is a
+// running maximum that is only raised when some score of a query exceeds it by more than
+// kLazyLog2 (then every p stays <= 2^kLazyLog2, far from float overflow). Raising it rescales the
+// query's output row and sum; the branch is taken by the whole wavefront only when one of its
+// queries needs it, which after the first key tile is rare. A query's four lanes keep partial
+// sums of their own keys, summed once at the end. The result is acc / l relative to the same
+// m_ref, which the reduce pass merges like any other (max, sum, acc) triple.
 // ---------------------------------------------------------------------------------------------
+constexpr float kLazyLog2 = 8.f;
+
+// Maximum / sum over the four lanes {n, n + 16, n + 32, n + 48} of a wavefront. With the same
+// register as both operands, v_permlane16_swap returns in each lane the two values of the lane
+// pair {l, l ^ 16} (one per result) and v_permlane32_swap those of {l, l ^ 32}.
+__device__ __forceinline__ float column_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float column_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int D>
+struct TileShape {
+  static constexpr int kKeys = D <= 128 ? 32 : 16;  // keys per LDS tile (registers bound D = 256)
+  static constexpr int kSub = kKeys / 16;
+  static constexpr int kRow = D + 4;                 // padded LDS row (floats): conflict-free reads
+  static constexpr int kD4 = D / 4;
+  static constexpr int kNb = D / 16;
+};
+
 template <typename KVT, int D, bool kPow2Block>
 __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params a) {
   static_assert(D % 16 == 0 && D >= 32, "the MFMA tile needs whole 16-wide output tiles");
-  constexpr int kRow = D + 4;        // padded LDS row (floats): conflict-free operand reads
-  constexpr int kD4 = D / 4;         // MFMA steps of S^T per key tile
-  constexpr int kNb = D / 16;        // output tiles of 16 dimensions
+  using S = TileShape<D>;
+  constexpr int kKeys = S::kKeys;
+  constexpr int kSub = S::kSub;
+  constexpr int kRow = S::kRow;
+  constexpr int kD4 = S::kD4;
+  constexpr int kNb = S::kNb;
   constexpr int kEsize = KVTraits<KVT>::kEsize;
   constexpr int kEpv = 16 / kEsize;  // elements per 16-byte vector
   constexpr int kVecPerRow = D / kEpv;
   __shared__ int s_table[kTableSlots];
-  __shared__ float s_k[kTileKeys * kRow];
-  __shared__ float s_v[kTileKeys * kRow];
+  __shared__ float s_k[kKeys * kRow];
+  __shared__ float s_v[kKeys * kRow];
   __shared__ int s_vis[kTileRows];
 
   const uint32_t bid = blockIdx.x;
@@ -412,12 +450,16 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
   const int nrows = static_cast<int>(min<int64_t>(min(a.tiles[2 * tile + 1], kTileRows), a.num_queries - t0));
   const int seq = a.q_seq[t0];
 
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
   if (threadIdx.x < kTileRows) {
     s_vis[threadIdx.x] = static_cast<int>(threadIdx.x) < nrows ? row_visible(a, t0 + threadIdx.x) : 0;
   }
   __syncthreads();
-  int tile_vis = 0;
-  for (int i = 0; i < kTileRows; ++i) tile_vis = max(tile_vis, s_vis[i]);
+  // The tile's longest visible row bounds its partitions (every wavefront reads all 64 entries).
+  int tile_vis = s_vis[lane];
+#pragma unroll
+  for (int mask = 32; mask > 0; mask >>= 1) tile_vis = max(tile_vis, __shfl_xor(tile_vis, mask));
   const int nparts = parts_of(tile_vis, a.part_size);
   if (p >= nparts) return;
   const int kbeg = p * a.part_size;
@@ -426,8 +468,6 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
   const int nb = kend > kbeg ? block_of<kPow2Block>(kend - 1, a) - b0 + 1 : 0;
   if (nb > 0) stage_table(s_table, a, seq, b0, nb, kTileThreads);
 
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
   const int c = lane >> 4;
   const int n = lane & 15;
   const int qi = wave * 16 + n;  // this lane's query in the S^T layout
@@ -436,17 +476,22 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
 
   float qreg[kD4];
   {
-    const int64_t row = t0 + (q_ok ? qi : 0);  // lanes past the tile read row t0, then drop it
+    // Lanes past the tile read row t0 (always in the batch) and drop it, so every load is
+    // unconditional and the 32 loads of a lane can all be in flight together.
+    const int64_t row = t0 + (q_ok ? qi : 0);
     const float* qrow = a.queries + row * a.q_stride + static_cast<int64_t>(h) * D + c * kD4;
+    float raw[kD4];
 #pragma unroll
-    for (int s = 0; s < kD4; ++s) qreg[s] = q_ok ? qrow[s] * a.scale_log2 : 0.f;
+    for (int s = 0; s < kD4; ++s) raw[s] = qrow[s];
+#pragma unroll
+    for (int s = 0; s < kD4; ++s) qreg[s] = q_ok ? raw[s] * a.scale_log2 : 0.f;
   }
 
   floatx4 o[kNb];
 #pragma unroll
   for (int b = 0; b < kNb; ++b) o[b] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY;
-  float l = 0.f;
+  float m_ref = -INFINITY;  // the same in the four lanes of a query
+  float l_part = 0.f;       // this lane's share of the query's sum
 
   const KVT* kcache = static_cast<const KVT*>(a.kcache);
   const KVT* vcache = static_cast<const KVT*>(a.vcache);
@@ -454,9 +499,9 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
   const int64_t row_stride = static_cast<int64_t>(a.num_heads) * D;
   __syncthreads();  // s_table ready
 
-  // Software pipeline: the raw vectors of key tile k0 + kTileKeys are loaded into registers while
+  // Software pipeline: the raw vectors of key tile k0 + kKeys are loaded into registers while
   // tile k0 is being multiplied; at the top of each step they are widened into LDS.
-  constexpr int kVecs = kTileKeys * kVecPerRow;  // 16-byte vectors per K (or V) tile
+  constexpr int kVecs = kKeys * kVecPerRow;  // 16-byte vectors per K (or V) tile
   constexpr int kPerThread = (kVecs + kTileThreads - 1) / kTileThreads;
   uint4 kraw[kPerThread];
   uint4 vraw[kPerThread];
@@ -484,14 +529,10 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
       }
     }
   };
-#if PKV_TILE_PIPELINE
   if (kbeg < kend) prefetch(kbeg);
-#endif
 
-  for (int k0 = kbeg; k0 < kend; k0 += kTileKeys) {
-#if !PKV_TILE_PIPELINE
-    prefetch(k0);
-#endif
+  const int lim = min(my_vis, kend);
+  for (int k0 = kbeg; k0 < kend; k0 += kKeys) {
     // Widen the prefetched tile (zeros past kend) into LDS as float32.
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
@@ -513,75 +554,91 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
       }
     }
     __syncthreads();
-#if PKV_TILE_PIPELINE
-    if (k0 + kTileKeys < kend) prefetch(k0 + kTileKeys);
-#endif
+    if (k0 + kKeys < kend) prefetch(k0 + kKeys);
 
-    // S^T tile: register r = S[query n][key 4c + r].
-    floatx4 st = {0.f, 0.f, 0.f, 0.f};
-    const float* krow = &s_k[n * kRow + c * kD4];
+    // S^T blocks: register r of st[j] = S[query n][key k0 + 16j + 4c + r].
+    floatx4 st[kSub];
 #pragma unroll
-    for (int s = 0; s < kD4; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(krow[s], qreg[s], st, 0, 0, 0);
-
-    const int lim = min(my_vis, kend);
-    float sc[4];
+    for (int j = 0; j < kSub; ++j) st[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = (k0 + 4 * c + r) < lim ? st[r] : -INFINITY;
-    float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float shift = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = fast_exp2(m - shift);
-    float pr[4];
+    for (int s = 0; s < kD4; ++s) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sc[r] - shift);
-    float ps = (pr[0] + pr[1]) + (pr[2] + pr[3]);
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
-    l = fmaf(l, alpha, ps);
-    m = m_new;
-
-    // Rescale the output rows (queries 4c + r) by their queries' alpha.
-    float ar[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * c + r);
-#pragma unroll
-    for (int b = 0; b < kNb; ++b) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o[b][r] *= ar[r];
+      for (int j = 0; j < kSub; ++j) {
+        st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(s_k[(16 * j + n) * kRow + c * kD4 + s], qreg[s], st[j], 0, 0, 0);
+      }
     }
 
-    // O += P V.
+    float sc[kSub][4];
+    float mx = -INFINITY;
 #pragma unroll
-    for (int step = 0; step < 4; ++step) {
-      const float* vrow = &s_v[(4 * c + step) * kRow + n];
+    for (int j = 0; j < kSub; ++j) {
 #pragma unroll
-      for (int b = 0; b < kNb; ++b) {
-        o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[step], vrow[16 * b], o[b], 0, 0, 0);
+      for (int r = 0; r < 4; ++r) {
+        sc[j][r] = (k0 + 16 * j + 4 * c + r) < lim ? st[j][r] : -INFINITY;
+        mx = fmaxf(mx, sc[j][r]);
+      }
+    }
+    mx = column_max(mx);
+    // Raise the reference only when a score passes it by more than kLazyLog2 (or it is unset).
+    const bool raise = mx > m_ref + kLazyLog2 || (m_ref == -INFINITY && mx > -INFINITY);
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+      const float m_next = raise ? mx : m_ref;
+      const float alpha = raise ? fast_exp2(m_ref - m_next) : 1.f;  // exp2(-inf) = 0
+      l_part *= alpha;
+#pragma unroll
+      for (int b = 0; b < kNb; ++b) o[b] *= alpha;
+      m_ref = m_next;
+    }
+    const float shift = m_ref == -INFINITY ? 0.f : m_ref;
+    float pr[kSub][4];
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[j][r] = fast_exp2(sc[j][r] - shift);
+        l_part += pr[j][r];
+      }
+    }
+
+    // O^T += V^T P^T.
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+      for (int step = 0; step < 4; ++step) {
+        const float* vrow = &s_v[(16 * j + 4 * c + step) * kRow + n];
+#pragma unroll
+        for (int b = 0; b < kNb; ++b) {
+          o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * b], pr[j][step], o[b], 0, 0, 0);
+        }
       }
     }
     __syncthreads();
   }
 
-  // Epilogue: register r of tile b is O[query 4c + r][16b + n].
-  float lr[4];
-  float mr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    lr[r] = __shfl(l, 4 * c + r);
-    mr[r] = __shfl(m, 4 * c + r);
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int qq = wave * 16 + 4 * c + r;
-    if (qq >= nrows) continue;
-    const int row_parts = parts_of(s_vis[qq], a.part_size);
-    if (p >= row_parts) continue;
+  // Epilogue: register r of tile b is O[query n][16b + 4c + r].
+  const float l = column_sum(l_part);
+  if (!q_ok) return;
+  const int row_parts = parts_of(my_vis, a.part_size);
+  if (p >= row_parts) return;
+  const int64_t qh = (t0 + qi) * a.num_heads + h;
+  if (row_parts == 1) {
+    const float sum = l > 0.f ? l : 1.f;
+    float* dst = a.out + qh * D + 4 * c;
 #pragma unroll
     for (int b = 0; b < kNb; ++b) {
-      store_result(a, t0 + qq, h, p, row_parts, 16 * b + n, D, o[b][r], mr[r], lr[r],
-                   b == 0 && n == 0);
+      *reinterpret_cast<float4*>(dst + 16 * b) =
+          make_float4(o[b][0] / sum, o[b][1] / sum, o[b][2] / sum, o[b][3] / sum);
+    }
+  } else {
+    const int64_t slot = qh * a.max_parts + p;
+    float* dst = a.ws_acc + slot * D + 4 * c;
+#pragma unroll
+    for (int b = 0; b < kNb; ++b) {
+      *reinterpret_cast<float4*>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
+    }
+    if (c == 0) {
+      a.ws_ml[2 * slot] = m_ref;
+      a.ws_ml[2 * slot + 1] = l;
     }
   }
 }
@@ -835,6 +892,8 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
     ws_acc = workspace;
     ws_ml = workspace + num_queries * num_heads * parts * head_dim;
   }
+  // The tile pass writes four dimensions of a row at a time.
+  if (num_tiles > 0 && (!aligned16(out) || (ws_acc && !aligned16(ws_acc)))) return PKV_EINVAL;
   DeviceGuard guard(device);
   if (!guard.ok()) return PKV_EHIP;
   (void)hipGetLastError();
