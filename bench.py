@@ -198,8 +198,7 @@ def attention_call(batch, args, out, workspace):
         ops.paged_attention_ragged(
             batch.queries, batch.query_positions, batch.query_seq, batch.key_cache,
             batch.value_cache, batch.block_tables, batch.context_lens, batch.scale,
-            max_context_len=batch.max_context_len, partition_size=args.partition,
-            out=out, workspace=workspace, plan=batch.plan,
+            max_context_len=batch.max_context_len, out=out, workspace=workspace, plan=batch.plan,
         )  # fmt: skip
 
     return attend
@@ -211,9 +210,14 @@ def run_attention_config(args, batch, *, metric: str, workload: str, dtype: str,
 
     from paged_kv_serving_amd import ops
 
+    if args.partition:
+        batch.replan(args.partition)
+
     device = batch.queries.device
     heads, dim = batch.key_cache.shape[2], batch.key_cache.shape[3]
-    need = ops.attention_workspace_bytes(batch.num_queries, heads, dim, batch.max_context_len, args.partition)
+    need = ops.attention_workspace_bytes(
+        batch.num_queries, heads, dim, batch.max_context_len, batch.plan.partition_size
+    )
     workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=device)
     out = torch.empty_like(batch.queries)
 
@@ -260,7 +264,8 @@ def run_attention_config(args, batch, *, metric: str, workload: str, dtype: str,
         "data": "synthetic: seeded N(0,1) K/V pools, queries and new tokens resident in HBM",
         "config": {
             "workload": workload,
-            "partition_size": args.partition or batch.plan.partition_size or 512,
+            "partition_size": batch.plan.partition_size or 512,
+            "shared_prefix_tiles": int(batch.plan.tiles[:, 3].gt(0).sum()) if batch.plan.num_tiles else 0,
             "kv_loads": "cached" if batch.plan.shared_kv else "streaming",
             "context_tokens": int(kv_bytes // (2 * heads * dim * esize)),
         },

@@ -158,14 +158,20 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *   query_positions  : int32 [num_queries], absolute position of each query (the causal mask:
  *                      key position > query position is masked, attention.py:102-104).
  *   query_seq        : int32 [num_queries], index of the sequence each query belongs to.
- *   rows, num_rows   : the plan's row list, int32 [num_rows]: query rows computed by the
- *                      row-streaming pass (one workgroup per row, head and partition; the right
- *                      pass for decode rows).
- *   tiles, num_tiles : the plan's tile list, int32 [num_tiles, 2] = (first row, row count <= 64):
- *                      runs of consecutive rows of ONE sequence computed by the fp32 MFMA tile
- *                      pass (the right pass for prefill chunks). Needs
+ *   rows, num_rows   : the plan's row list, int32 [num_rows, 2] = (query row, first partition):
+ *                      query rows computed by the row-streaming pass (one workgroup per row,
+ *                      head and partition; the right pass for decode rows), from their first
+ *                      partition on.
+ *   tiles, num_tiles : the plan's tile list, int32 [num_tiles, 4] = (first row, row count <= 64,
+ *                      first partition, end partition; end <= first means through the last):
+ *                      runs of consecutive rows computed by the fp32 MFMA tile pass over those
+ *                      partitions. Keys are read through the table of the tile's first row, so
+ *                      the rows are either one sequence's (a prefill chunk) or rows of several
+ *                      sequences whose tables hold the same block ids over the tile's
+ *                      partitions (a shared prefix; those rows then also appear in the row list
+ *                      with the first partition after the tile's). Needs
  *                      pkv_tile_head_dim_supported(head_dim).
- *                      Every query row must be in exactly one of the two lists. With rows and
+ *                      Every (query row, partition) must be covered exactly once. With rows and
  *                      tiles both NULL, every row goes through the row-streaming pass.
  *   key_cache,
  *   value_cache      : the layer's pools, [num_blocks, block_size, num_heads, head_dim], kv_dtype,

@@ -9,8 +9,11 @@
 //     partition with non-temporal 16-byte loads (kLpt lanes cover one token's head row) and keeps
 //     an online softmax (running max, running sum, unnormalised accumulator) per lane group in
 //     registers. The lane groups are merged through LDS at the end.
-//  2. tile_partial (compute-bound rows: a run of consecutive prefill rows of one sequence): one
-//     workgroup per (tile of <= 64 rows, head, context partition). Key and value tiles of 32 rows
+//  2. tile_partial (compute-bound rows: a run of consecutive prefill rows of one sequence, or
+//     decode rows of several sequences over the partitions of a prefix they share): one
+//     workgroup per (tile of <= 64 rows, head, context partition). Keys are read through the
+//     table of the tile's first row, which the planner only allows where every row of the tile
+//     has the same blocks. Key and value tiles of 32 rows
 //     (16 at head_dim 256) are staged in padded LDS and shared by 4 wavefronts of 16 queries
 //     each; the scores are computed as S^T = K Q^T and the output as O = P V with
 //     v_mfma_f32_16x16x4f32, so every lane owns four scores of one query per 16 keys and the P
@@ -84,8 +87,9 @@ struct Params {
   int64_t q_stride;
   const int32_t* q_pos;    // [T]
   const int32_t* q_seq;    // [T]
-  const int32_t* rows;     // row_partial: grid row -> query row (null: identity)
-  const int32_t* tiles;    // tile_partial: [n, 2] = (first row, row count <= 64)
+  const int32_t* rows;     // row_partial: [R, 2] = (query row, first partition); null: identity
+  const int32_t* tiles;    // tile_partial: [n, 4] = (first row, row count <= 64, first
+                           // partition, end partition; end <= first: through the last)
   const void* kcache;      // [N, B, H, D]
   const void* vcache;
   int64_t num_queries;
@@ -216,8 +220,11 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   const uint32_t rest = bid / static_cast<uint32_t>(a.num_heads);
   const int p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
   const int64_t r = rest / static_cast<uint32_t>(a.max_parts);
-  const int64_t t = a.rows ? a.rows[r] : r;
+  const int64_t t = a.rows ? a.rows[2 * r] : r;
   if (t < 0 || t >= a.num_queries) return;  // a row outside the batch is skipped
+  // Partitions before the row's first one are computed by a tile (a prefix shared with the
+  // other rows of the tile).
+  if (a.rows && p < a.rows[2 * r + 1]) return;
 
   const int seq = a.q_seq[t];
   const int kv_len = row_visible(a, t);
@@ -445,9 +452,11 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
   const uint32_t rest = bid / static_cast<uint32_t>(a.num_heads);
   const int p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
   const int64_t tile = rest / static_cast<uint32_t>(a.max_parts);
-  const int64_t t0 = a.tiles[2 * tile];
+  const int32_t* entry = a.tiles + 4 * tile;
+  const int64_t t0 = entry[0];
   if (t0 < 0 || t0 >= a.num_queries) return;  // a tile outside the batch is skipped
-  const int nrows = static_cast<int>(min<int64_t>(min(a.tiles[2 * tile + 1], kTileRows), a.num_queries - t0));
+  if (p < entry[2] || (entry[3] > entry[2] && p >= entry[3])) return;  // outside its partitions
+  const int nrows = static_cast<int>(min<int64_t>(min(entry[1], kTileRows), a.num_queries - t0));
   const int seq = a.q_seq[t0];
 
   const int lane = threadIdx.x & (kWave - 1);

@@ -26,8 +26,12 @@ __all__ = [
     "independent_groups",
     "kv_dtype_code",
     "paged_attention_ragged",
+    "BatchPlan",
     "batch_hints",
+    "plan_batch",
     "plan_rows",
+    "tiles_supported",
+    "upload_batch_plan",
     "rope_append",
     "upload_plan",
 ]
@@ -257,12 +261,15 @@ def independent_groups(pairs: list[tuple[int, int]]) -> list[list[tuple[int, int
 
 @dataclass(frozen=True)
 class AttentionPlan:
-    """Which query rows go to which attention pass, as int32 device tensors, plus batch hints.
+    """Which (query row, partition) goes to which attention pass, as int32 device tensors, plus
+    the launch hints.
 
-    ``rows``: rows for the row-streaming pass; ``tiles``: ``[n, 2]`` (first row, row count) runs
-    of consecutive rows of one sequence for the MFMA tile pass. Every query row is in exactly
-    one of them. ``partition_size`` (0: library default) and ``shared_kv`` come from
-    :func:`batch_hints`.
+    ``rows``: ``[R, 2]`` = (query row, first partition) for the row-streaming pass. ``tiles``:
+    ``[n, 4]`` = (first row, row count, first partition, end partition; end <= first: through
+    the last) for the MFMA tile pass: a run of consecutive rows of one sequence, or decode rows
+    of several sequences over the partitions of a prefix whose blocks they share. Every (row,
+    partition) is covered exactly once. ``partition_size`` (0: library default) and
+    ``shared_kv`` choose the launch.
     """
 
     rows: torch.Tensor
@@ -279,30 +286,38 @@ class AttentionPlan:
         return int(self.tiles.shape[0])
 
 
+def tiles_supported(head_dim: int) -> bool:
+    """Whether the MFMA tile pass exists for this head_dim."""
+    return bool(_native.library().pkv_tile_head_dim_supported(head_dim))
+
+
 def plan_rows(
     query_seq: np.ndarray, head_dim: int, *, min_tile_rows: int = MIN_TILE_ROWS
 ) -> tuple[np.ndarray, np.ndarray]:
     """Split a ragged batch's rows between the two attention passes (host, int32).
 
     Runs of at least ``min_tile_rows`` consecutive rows with the same sequence index become
-    tiles of at most ``TILE_ROWS`` rows (when the head_dim has a tile kernel); every other row
-    goes to the row-streaming pass. Returns ``(rows [R], tiles [n, 2])``.
+    tiles of at most ``TILE_ROWS`` rows over all partitions (when the head_dim has a tile
+    kernel); every other row goes to the row-streaming pass from partition 0. Returns
+    ``(rows [R, 2], tiles [n, 4])``.
     """
     seq = np.asarray(query_seq, dtype=np.int64)
     total = seq.size
-    tiled = bool(_native.library().pkv_tile_head_dim_supported(head_dim))
     if total == 0:
-        return np.zeros(0, np.int32), np.zeros((0, 2), np.int32)
+        return np.zeros((0, 2), np.int32), np.zeros((0, 4), np.int32)
+    tiled = tiles_supported(head_dim)
     starts = np.flatnonzero(np.concatenate([[True], seq[1:] != seq[:-1]]))
     ends = np.concatenate([starts[1:], [total]])
     rows, tiles = [], []
     for start, end in zip(starts.tolist(), ends.tolist()):
         if tiled and end - start >= min_tile_rows:
             for first in range(start, end, TILE_ROWS):
-                tiles.append((first, min(TILE_ROWS, end - first)))
+                tiles.append((first, min(TILE_ROWS, end - first), 0, 0))
         else:
             rows.extend(range(start, end))
-    return np.asarray(rows, dtype=np.int32), np.asarray(tiles, dtype=np.int32).reshape(-1, 2)
+    row_array = np.zeros((len(rows), 2), dtype=np.int32)
+    row_array[:, 0] = rows
+    return row_array, np.asarray(tiles, dtype=np.int32).reshape(-1, 4)
 
 
 #: Partition work items (row x head x partition) above which 1024-key partitions pay off: fewer,
@@ -311,6 +326,30 @@ WIDE_PARTITION_ITEMS = 8192
 #: Fraction of a batch's used table entries that repeat across sequences above which the K/V
 #: rows are loaded through the caches (PKV_ATTN_SHARED_KV) rather than streamed past them.
 SHARED_KV_FRACTION = 0.25
+#: Row-pass rows of different sequences whose tables share at least this many leading tokens'
+#: blocks, at least MIN_SHARED_ROWS of them in a row, compute that prefix as MFMA tiles.
+MIN_SHARED_TOKENS = 512
+MIN_SHARED_ROWS = 16
+#: Shared-prefix tile workgroups the partition choice aims for (two per CU of 256), and the
+#: smallest partition it will choose for them.
+TARGET_PREFIX_GROUPS = 512
+MIN_PREFIX_PARTITION = 256
+
+
+def _wide_partition(contexts: np.ndarray, num_heads: int, rows_per_seq: int) -> int:
+    wide = int(np.sum(-(-contexts // 1024))) * rows_per_seq * num_heads
+    return 1024 if wide >= WIDE_PARTITION_ITEMS else 512
+
+
+def _repeated_fraction_reached(ids: np.ndarray) -> bool:
+    if ids.size == 0:
+        return False
+    low, high = int(ids.min()), int(ids.max())
+    if 0 <= low and high < (1 << 26):  # block ids: a histogram is cheaper than a sort
+        distinct = int(np.count_nonzero(np.bincount(ids, minlength=0)))
+    else:
+        distinct = int(np.unique(ids).size)
+    return ids.size - distinct >= SHARED_KV_FRACTION * ids.size
 
 
 def batch_hints(
@@ -333,34 +372,157 @@ def batch_hints(
     if contexts.size == 0:
         return 0, False
     per_seq_rows = 1 if num_rows is None else max(1, num_rows // contexts.size)
-    wide = int(np.sum(-(-contexts // 1024))) * per_seq_rows * num_heads
-    partition = 1024 if wide >= WIDE_PARTITION_ITEMS else 512
+    partition = _wide_partition(contexts, num_heads, per_seq_rows)
     if used_ids is None:
         used = [np.asarray(t[: -(-int(c) // block_size)]) for t, c in zip(tables, contexts)]
         used_ids = np.concatenate(used) if used else np.zeros(0, np.int64)
-    ids = np.asarray(used_ids)
-    if ids.size == 0:
-        return partition, False
-    low, high = int(ids.min()), int(ids.max())
-    if 0 <= low and high < (1 << 26):  # block ids: a histogram is cheaper than a sort
-        distinct = int(np.count_nonzero(np.bincount(ids, minlength=0)))
-    else:
-        distinct = int(np.unique(ids).size)
-    shared = ids.size - distinct >= SHARED_KV_FRACTION * ids.size
-    return partition, bool(shared)
+    return partition, _repeated_fraction_reached(np.asarray(used_ids))
+
+
+@dataclass(frozen=True)
+class BatchPlan:
+    """A host plan: ``rows [R, 2]``, ``tiles [n, 4]`` (int32, the :class:`AttentionPlan` layout),
+    the partition size and the load hint."""
+
+    rows: np.ndarray
+    tiles: np.ndarray
+    partition_size: int
+    shared_kv: bool
+
+
+def _common_prefix(a: np.ndarray, b: np.ndarray) -> int:
+    n = min(a.size, b.size)
+    if n == 0:
+        return 0
+    differ = np.flatnonzero(a[:n] != b[:n])
+    return int(differ[0]) if differ.size else n
+
+
+def _prefix_groups(
+    rows: np.ndarray, seq: np.ndarray, tables, used_blocks: np.ndarray, min_blocks: int
+) -> list:
+    """Runs of consecutive row-pass rows whose sequences' used tables agree over a common
+    prefix of at least ``min_blocks`` blocks. Returns
+    ``[(first index into rows, row count, common blocks)]``; a member whose whole used table is
+    a prefix of the first row's constrains nothing (its visible keys end inside the prefix)."""
+    groups = []
+    count = rows.shape[0]
+    i = 0
+    while i < count:
+        t0 = int(rows[i, 0])
+        s0 = int(seq[t0])
+        first = np.asarray(tables[s0][: used_blocks[s0]])
+        common = int(used_blocks[s0])
+        j = i + 1
+        while j < count and int(rows[j, 0]) == int(rows[j - 1, 0]) + 1:
+            sj = int(seq[int(rows[j, 0])])
+            if used_blocks[sj] and first.size and tables[sj][0] != first[0]:
+                break  # nothing shared (the common case, without an array comparison)
+            mine = np.asarray(tables[sj][: used_blocks[sj]])
+            shared = _common_prefix(first, mine)
+            limit = common if shared == mine.size else min(common, shared)
+            if limit < min_blocks:
+                break
+            common = limit
+            j += 1
+        if j - i >= MIN_SHARED_ROWS and common >= min_blocks:
+            groups.append((i, j - i, common))
+            i = j
+        else:
+            i += 1
+    return groups
+
+
+def _prefix_partition(shared_tokens: int, tiles: int, num_heads: int) -> int:
+    """Partition size for a shared prefix: whole partitions should cover the prefix (at most
+    1024 keys each) and give the tile pass about TARGET_PREFIX_GROUPS workgroups."""
+    best = 0
+    k = max(1, -(-shared_tokens // 1024))
+    while True:
+        size = min(1024, (shared_tokens // k) // 16 * 16)
+        if size < MIN_PREFIX_PARTITION:
+            break
+        best = size
+        if tiles * num_heads * k >= TARGET_PREFIX_GROUPS:
+            break
+        k += 1
+    return best
+
+
+def plan_batch(
+    query_seq: np.ndarray, head_dim: int, num_heads: int, tables, context_lens: np.ndarray,
+    block_size: int, *, partition_size: int = 0, min_tile_rows: int = MIN_TILE_ROWS,
+) -> BatchPlan:  # fmt: skip
+    """The full host plan of a ragged call: the row/tile split of :func:`plan_rows`, shared-prefix
+    tiles, the partition size and the load hint.
+
+    ``tables[s]`` / ``context_lens[s]``: block table (any int sequence) and context length of
+    the sequence index ``s`` used in ``query_seq``. Row-pass rows of consecutive queries whose
+    sequences share at least MIN_SHARED_TOKENS of leading blocks, MIN_SHARED_ROWS or more of
+    them, read that prefix once per head as MFMA tiles over its whole partitions, and start the
+    row pass at the first partition after it. A nonzero ``partition_size`` is kept as given.
+    """
+    seq = np.asarray(query_seq, dtype=np.int64)
+    contexts = np.asarray(context_lens, dtype=np.int64)
+    rows, tiles = plan_rows(seq, head_dim, min_tile_rows=min_tile_rows)
+    if seq.size == 0:
+        return BatchPlan(rows, tiles, partition_size or 0, False)
+    used_blocks = -(-contexts // block_size)
+    groups = []
+    if rows.shape[0] >= MIN_SHARED_ROWS and tiles_supported(head_dim):
+        groups = _prefix_groups(rows, seq, tables, used_blocks, -(-MIN_SHARED_TOKENS // block_size))
+    present = np.unique(seq)
+    partition = partition_size
+    if partition == 0:
+        if groups:
+            largest = max(groups, key=lambda g: g[1] * g[2])
+            tile_count = sum(-(-g[1] // TILE_ROWS) for g in groups)
+            partition = _prefix_partition(largest[2] * block_size, tile_count, num_heads)
+        if partition == 0:
+            partition = _wide_partition(contexts[present], num_heads, max(1, seq.size // present.size))
+    prefix_tiles = []
+    for start, count, common in groups:
+        parts = common * block_size // partition
+        if parts < 1:
+            continue
+        rows[start : start + count, 1] = parts
+        first_row = int(rows[start, 0])
+        for offset in range(0, count, TILE_ROWS):
+            prefix_tiles.append((first_row + offset, min(TILE_ROWS, count - offset), 0, parts))
+    if prefix_tiles:
+        tiles = np.concatenate([tiles, np.asarray(prefix_tiles, dtype=np.int32)])
+    # The load hint looks at what the row pass still reads: each row-pass sequence's blocks from
+    # its first partition on (tiles read their keys once per 64 rows either way).
+    row_seqs = seq[rows[:, 0]] if rows.size else np.zeros(0, np.int64)
+    firsts = rows[:, 1].astype(np.int64) * partition // block_size
+    seen = set()
+    parts = []
+    for s, f in zip(row_seqs.tolist(), firsts.tolist()):
+        if (s, f) in seen:
+            continue
+        seen.add((s, f))
+        parts.append(np.asarray(tables[s][f : used_blocks[s]]))
+    ids = np.concatenate(parts) if parts else np.zeros(0, np.int64)
+    return BatchPlan(rows, tiles, int(partition), _repeated_fraction_reached(ids))
 
 
 def upload_plan(
     rows: np.ndarray, tiles: np.ndarray, device: torch.device, *, partition_size: int = 0,
     shared_kv: bool = False,
 ) -> AttentionPlan:
-    """Copy a host plan to the device in one transfer."""
-    packed = np.concatenate([rows.astype(np.int32), tiles.astype(np.int32).ravel()])
+    """Copy a host plan (``rows [R, 2]``, ``tiles [n, 4]``) to the device in one transfer."""
+    rows = np.asarray(rows, dtype=np.int32).reshape(-1, 2)
+    tiles = np.asarray(tiles, dtype=np.int32).reshape(-1, 4)
+    packed = np.concatenate([rows.ravel(), tiles.ravel()])
     data = torch.from_numpy(packed).to(device)
     return AttentionPlan(
-        rows=data[: rows.size], tiles=data[rows.size :].view(-1, 2),
+        rows=data[: rows.size].view(-1, 2), tiles=data[rows.size :].view(-1, 4),
         partition_size=partition_size, shared_kv=shared_kv,
     )  # fmt: skip
+
+
+def upload_batch_plan(plan: BatchPlan, device: torch.device) -> AttentionPlan:
+    return upload_plan(plan.rows, plan.tiles, device, partition_size=plan.partition_size, shared_kv=plan.shared_kv)
 
 
 def attention_workspace_bytes(
@@ -398,7 +560,8 @@ def paged_attention_ragged(
     ``query_seq``: int32 ``[T]``; ``key_cache``/``value_cache``: one layer's pools
     ``[num_blocks, block_size, H, D]``; ``block_tables``: int32 ``[S, max_blocks]``;
     ``context_lens``: int32 ``[S]``; ``max_context_len`` bounds every context length.
-    ``plan`` (from :func:`plan_rows` + :func:`upload_plan`) routes prefill runs to the MFMA tile
+    ``plan`` (from :func:`plan_batch` + :func:`upload_batch_plan`) routes prefill runs and shared
+    prefixes to the MFMA tile
     pass; without one every row takes the row-streaming pass. An explicit ``partition_size``
     overrides the plan's; so does ``shared_kv`` when not None.
     Returns float32 ``[T, H, D]``. Semantics of reference attention.py:42-121 for each query.
@@ -436,7 +599,12 @@ def paged_attention_ragged(
         raise ValueError("out must be contiguous")
     if num_queries == 0:
         return out
-    if plan is not None and partition_size == 0:
+    if plan is not None and plan.partition_size:
+        if partition_size not in (0, plan.partition_size):
+            raise ValueError(
+                f"the plan's partitions were laid out for partition_size {plan.partition_size}, "
+                f"not {partition_size}"
+            )
         partition_size = plan.partition_size
     if shared_kv is None:
         shared_kv = plan.shared_kv if plan is not None else False
@@ -451,8 +619,10 @@ def paged_attention_ragged(
         for name, tensor in (("rows", plan.rows), ("tiles", plan.tiles)):
             if tensor.dtype != torch.int32 or tensor.device != queries.device:
                 raise ValueError(f"plan.{name} must be an int32 tensor on the queries' device")
-        if plan.tiles.dim() != 2 or plan.tiles.shape[1] != 2 or not plan.tiles.is_contiguous():
-            raise ValueError("plan.tiles must be contiguous int32 of shape (n, 2)")
+        if plan.rows.dim() != 2 or plan.rows.shape[1] != 2 or not plan.rows.is_contiguous():
+            raise ValueError("plan.rows must be contiguous int32 of shape (R, 2)")
+        if plan.tiles.dim() != 2 or plan.tiles.shape[1] != 4 or not plan.tiles.is_contiguous():
+            raise ValueError("plan.tiles must be contiguous int32 of shape (n, 4)")
         if plan.num_rows + 0 > num_queries:
             raise ValueError("plan.rows lists more rows than the batch has")
         num_rows, num_tiles = plan.num_rows, plan.num_tiles

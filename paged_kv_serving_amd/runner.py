@@ -175,7 +175,7 @@ class ModelRunner:
         device: torch.device | str | int | None = None,
         partition_size: int = 0,
     ) -> None:
-        """``partition_size`` 0 lets each call choose (``ops.batch_hints``)."""
+        """``partition_size`` 0 lets each call choose (``ops.plan_batch``)."""
         if num_blocks < 1 or block_size < 1:
             raise ValueError("num_blocks and block_size must be >= 1")
         if tile_blocks < 1:
@@ -324,18 +324,18 @@ class ModelRunner:
         contexts_by_row[update.rows] = context
         per_entry = np.fromiter((len(e.token_ids) for e in entries), dtype=np.int64, count=num_seqs)
         query_seq = np.repeat(update.rows, per_entry)
-        plan_rows, plan_tiles = ops.plan_rows(query_seq, config.head_dim)
-        used = self._tables.used_blocks(update.rows, -(-context.astype(np.int64) // self.block_size))
-        hint_partition, shared_kv = ops.batch_hints(
-            None, context, config.n_heads, self.block_size, total, used_ids=used
-        )
-        partition = self.partition_size or hint_partition
+        host_plan = ops.plan_batch(
+            query_seq, config.head_dim, config.n_heads, self._tables.host, contexts_by_row,
+            self.block_size, partition_size=self.partition_size,
+        )  # fmt: skip
+        partition = host_plan.partition_size
+        plan_rows, plan_tiles = host_plan.rows, host_plan.tiles
         changed = update.index.size
         meta64 = torch.from_numpy(np.concatenate([tokens, positions, slots, update.index])).to(self.device)
         meta32 = torch.from_numpy(
             np.concatenate([
                 positions.astype(np.int32), query_seq, contexts_by_row, update.values,
-                plan_rows, plan_tiles.ravel(),
+                plan_rows.ravel(), plan_tiles.ravel(),
             ])  # fmt: skip
         ).to(self.device)
         tokens_d, positions_d = meta64[:total], meta64[total : 2 * total]
@@ -347,10 +347,10 @@ class ModelRunner:
         self._tables.apply(meta64[3 * total :], meta32[2 * total + arena_rows : end_values])
         tables_d = self._tables.tables
         plan = ops.AttentionPlan(
-            rows=meta32[end_values : end_values + plan_rows.size],
-            tiles=meta32[end_values + plan_rows.size :].view(-1, 2),
+            rows=meta32[end_values : end_values + plan_rows.size].view(-1, 2),
+            tiles=meta32[end_values + plan_rows.size :].view(-1, 4),
             partition_size=partition,
-            shared_kv=shared_kv,
+            shared_kv=host_plan.shared_kv,
         )
         max_context = int(context.max())
 

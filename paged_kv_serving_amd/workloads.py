@@ -58,6 +58,15 @@ class AttentionBatch:
     def num_queries(self) -> int:
         return int(self.queries.shape[0])
 
+    def replan(self, partition_size: int) -> None:
+        """Rebuild the plan for a given partition size (0: the planner's choice)."""
+        heads, dim = self.key_cache.shape[2], self.key_cache.shape[3]
+        host = ops.plan_batch(
+            self.host_seq, dim, heads, self.host_tables, self.host_context, self.key_cache.shape[1],
+            partition_size=partition_size,
+        )  # fmt: skip
+        self.plan = ops.upload_batch_plan(host, self.queries.device)
+
     @property
     def num_seqs(self) -> int:
         return int(self.context_lens.shape[0])
@@ -140,8 +149,7 @@ def _assemble(
     padded = np.zeros((len(tables), width), dtype=np.int32)
     for i, table in enumerate(tables):
         padded[i, : len(table)] = table
-    partition, shared = ops.batch_hints(tables, context, heads, block_size, positions.size)
-    plan = ops.upload_plan(*ops.plan_rows(seq, head_dim), device, partition_size=partition, shared_kv=shared)
+    plan = ops.upload_batch_plan(ops.plan_batch(seq, head_dim, heads, tables, context, block_size), device)
     return AttentionBatch(
         key_cache=key_cache,
         value_cache=value_cache,
@@ -360,10 +368,7 @@ def prefix_sharing_step(
         context_lens=torch.from_numpy(contexts.astype(np.int32)).to(device),
         max_context_len=int(contexts.max()),
         scale=float(head_dim) ** -0.5,
-        plan=ops.upload_plan(
-            *ops.plan_rows(seq, head_dim), device,
-            **dict(zip(("partition_size", "shared_kv"), ops.batch_hints(tables, contexts, heads, block_size))),
-        ),  # fmt: skip
+        plan=ops.upload_batch_plan(ops.plan_batch(seq, head_dim, heads, tables, contexts, block_size), device),
         host_tables=tables,
         host_context=contexts.astype(np.int64),
         host_positions=positions.astype(np.int64),

@@ -250,12 +250,66 @@ def test_long_prefill_runs_through_the_mfma_tiles(device, dim, kv) -> None:
         kc, vc = bf16_round(kc), bf16_round(vc)
     want, dense = _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale)
     rows, tile_list = ops.plan_rows(seq_of, dim, min_tile_rows=2)
-    assert len(tile_list) >= 3 and any(n < 64 for _, n in tile_list)
+    assert len(tile_list) >= 3 and any(n < 64 for _, n, _, _ in tile_list)
     for partition in (0, 128, 1024):
         got = _run_kernel(device, kc, vc, tables, contexts, positions, seq_of, q, scale,
                           partition=partition, dtype=kv, tiles=True)  # fmt: skip
         assert np.max(np.abs(got - want)) < FP32_TOL, partition
         assert np.max(np.abs(got - dense)) < FP32_TOL, partition
+
+
+@pytest.mark.parametrize("kv", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_shared_prefix_tiles_match_the_oracle(device, kv) -> None:
+    """Decode rows of 40 sequences: 24 share 70 leading blocks (one of them ends inside the
+    prefix), 16 share 33 others; the planner turns each prefix into tiles over whole partitions
+    and starts those rows' row pass after it. Same results as the plain plan and the oracle."""
+    say("shared prefix", kv)
+    rng = np.random.default_rng(21)
+    heads, dim, block = 4, 128, 16
+    pool = 1200
+    kc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    vc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    if kv == torch.bfloat16:
+        kc, vc = bf16_round(kc), bf16_round(vc)
+    ids = iter(rng.permutation(pool).tolist())
+    prefix_a = [next(ids) for _ in range(70)]
+    prefix_b = [next(ids) for _ in range(33)]
+    tables, contexts = [], []
+    for i in range(40):
+        prefix = prefix_a if i < 24 else prefix_b
+        ctx = len(prefix) * block + int(rng.integers(1, 300))
+        if i == 5:
+            ctx = 600  # ends inside prefix a
+        need = -(-ctx // block)
+        table = prefix[:need] + [next(ids) for _ in range(max(0, need - len(prefix)))]
+        tables.append(np.asarray(table))
+        contexts.append(ctx)
+    contexts = np.asarray(contexts)
+    positions = contexts - 1
+    seq_of = np.arange(40)
+    q = rng.standard_normal((40, heads, dim)).astype(np.float32)
+    plan = ops.plan_batch(seq_of, dim, heads, tables, contexts, block)
+    assert plan.tiles.shape[0] >= 2 and np.count_nonzero(plan.rows[:, 1]) == 40
+    want, dense = _oracle(kc, vc, tables, contexts, positions, seq_of, q, 0.09)
+    width = max(len(t) for t in tables)
+    padded = np.full((40, width), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    args = [
+        torch.from_numpy(q).to(device), torch.from_numpy(positions.astype(np.int32)).to(device),
+        torch.from_numpy(seq_of.astype(np.int32)).to(device),
+        torch.from_numpy(kc).to(device).to(kv), torch.from_numpy(vc).to(device).to(kv),
+        torch.from_numpy(padded).to(device), torch.from_numpy(contexts.astype(np.int32)).to(device), 0.09,
+    ]  # fmt: skip
+    got = ops.paged_attention_ragged(
+        *args, max_context_len=int(contexts.max()), plan=ops.upload_batch_plan(plan, device)
+    ).cpu().numpy()
+    plain = ops.paged_attention_ragged(
+        *args, max_context_len=int(contexts.max()), partition_size=plan.partition_size
+    ).cpu().numpy()
+    assert np.max(np.abs(got - want)) < FP32_TOL
+    assert np.max(np.abs(got - dense)) < FP32_TOL
+    assert np.max(np.abs(got - plain)) < FP32_TOL
 
 
 def test_tile_rows_with_arbitrary_positions_and_no_visible_keys(device) -> None:
@@ -473,20 +527,22 @@ def test_config4_prefix_sharing_cow_then_decode(device) -> None:
     say("config 4: worst vs float64 torch", worst)
     assert worst < FP32_TOL
     _oracle_rows(step.decode, out, (0, 255), FP32_TOL)
-    # the shared-prefix hint only changes how K/V rows are loaded: same bits either way
-    assert step.decode.plan.shared_kv and step.decode.plan.partition_size == 1024
+    # the planner computed the shared 1008-token prefix as tiles over three 336-key partitions
+    plan = step.decode.plan
+    assert plan.partition_size == 336 and not plan.shared_kv
+    assert plan.tiles.cpu().tolist() == [[64 * i, 64, 0, 3] for i in range(4)]
     d = step.decode
-    for partition in (0, 512):
-        streamed = ops.paged_attention_ragged(
-            d.queries, d.query_positions, d.query_seq, d.key_cache, d.value_cache, d.block_tables,
-            d.context_lens, d.scale, max_context_len=d.max_context_len, partition_size=partition,
-            plan=d.plan, shared_kv=False,
-        )  # fmt: skip
-        cached = ops.paged_attention_ragged(
-            d.queries, d.query_positions, d.query_seq, d.key_cache, d.value_cache, d.block_tables,
-            d.context_lens, d.scale, max_context_len=d.max_context_len, partition_size=partition,
-            plan=d.plan, shared_kv=True,
-        )  # fmt: skip
-        assert torch.equal(streamed, cached), partition
-        if partition == 0:
-            assert torch.equal(cached, out)
+    common = (d.queries, d.query_positions, d.query_seq, d.key_cache, d.value_cache, d.block_tables,
+              d.context_lens, d.scale)  # fmt: skip
+    # the plain plan (every row streams its whole context) agrees within rounding
+    plain = ops.paged_attention_ragged(*common, max_context_len=d.max_context_len, partition_size=336)
+    assert float((plain - out).abs().max()) < FP32_TOL
+    # the load hint only changes how K/V rows are loaded: same bits either way
+    runs = [
+        ops.paged_attention_ragged(*common, max_context_len=d.max_context_len, plan=plan, shared_kv=flag)
+        for flag in (False, True)
+    ]
+    assert torch.equal(runs[0], runs[1]) and torch.equal(runs[0], out)
+    # a plan's partition indices belong to its partition size
+    with pytest.raises(ValueError, match="partition"):
+        ops.paged_attention_ragged(*common, max_context_len=d.max_context_len, plan=plan, partition_size=512)

@@ -14,8 +14,10 @@ from paged_kv_serving_amd import ops
 
 
 def _check_split(seq: np.ndarray, rows: np.ndarray, tiles: np.ndarray, min_rows: int) -> None:
-    covered = list(rows.tolist())
-    for first, count in tiles.tolist():
+    assert rows.shape[1] == 2 and tiles.shape[1] == 4
+    assert np.all(rows[:, 1] == 0) and np.all(tiles[:, 2:] == 0), "no shared-prefix split here"
+    covered = list(rows[:, 0].tolist())
+    for first, count, _, _ in tiles.tolist():
         assert 1 <= count <= ops.TILE_ROWS
         assert len(set(seq[first : first + count].tolist())) == 1, "a tile spans one sequence"
         covered += range(first, first + count)
@@ -24,7 +26,7 @@ def _check_split(seq: np.ndarray, rows: np.ndarray, tiles: np.ndarray, min_rows:
     starts = np.flatnonzero(np.concatenate([[True], seq[1:] != seq[:-1]]))
     lengths = np.diff(np.concatenate([starts, [seq.size]]))
     run_len = np.repeat(lengths, lengths)
-    assert np.all(run_len[rows] < min_rows)
+    assert np.all(run_len[rows[:, 0]] < min_rows)
 
 
 @pytest.mark.parametrize("seed", range(6))
@@ -40,13 +42,13 @@ def test_every_row_goes_to_exactly_one_pass(seed) -> None:
 def test_known_splits() -> None:
     seq = np.array([0] * 130 + [1] + [2] * 8 + [3] * 7, np.int32)
     rows, tiles = ops.plan_rows(seq, 64)
-    assert tiles.tolist() == [[0, 64], [64, 64], [128, 2], [131, 8]]
-    assert rows.tolist() == [130, *range(139, 146)]
+    assert tiles.tolist() == [[0, 64, 0, 0], [64, 64, 0, 0], [128, 2, 0, 0], [131, 8, 0, 0]]
+    assert rows[:, 0].tolist() == [130, *range(139, 146)]
     # head dims without a tile kernel keep everything in the row pass
     rows, tiles = ops.plan_rows(seq, 8)
-    assert tiles.shape == (0, 2) and rows.tolist() == list(range(146))
+    assert tiles.shape == (0, 4) and rows[:, 0].tolist() == list(range(146))
     rows, tiles = ops.plan_rows(np.zeros(0, np.int32), 128)
-    assert rows.size == 0 and tiles.shape == (0, 2)
+    assert rows.shape == (0, 2) and tiles.shape == (0, 4)
 
 
 def _tables(contexts, block_size, rng, shared_prefix=0):
@@ -81,3 +83,85 @@ def test_shared_hint_counts_repeated_block_ids() -> None:
     # entries past a sequence's context are padding and never count
     tables = [np.concatenate([[i], np.full(10, 5)]) for i in range(100)]
     assert not ops.batch_hints(tables, np.full(100, 16), 32, 16)[1]
+
+
+# --- shared prefixes -----------------------------------------------------------------------------
+
+
+def _covered(plan, seq, contexts, block_size):
+    """(row, partition) pairs each pass computes; every visible partition exactly once."""
+    P = plan.partition_size
+    seen = {}
+    for first, count, pb, pe in plan.tiles.tolist():
+        for t in range(first, first + count):
+            parts = max(1, -(-int(contexts[seq[t]]) // P))
+            for p in range(pb, pe if pe > pb else parts):
+                if p < parts:
+                    seen[(t, p)] = seen.get((t, p), 0) + 1
+    for t, f in plan.rows.tolist():
+        parts = max(1, -(-int(contexts[seq[t]]) // P))
+        for p in range(f, parts):
+            seen[(t, p)] = seen.get((t, p), 0) + 1
+    want = {(t, p) for t in range(seq.size) for p in range(max(1, -(-int(contexts[seq[t]]) // P)))}
+    assert set(seen) == want and all(v == 1 for v in seen.values())
+
+
+def test_a_shared_prefix_becomes_tiles_over_whole_partitions() -> None:
+    """256 decode rows sharing 63 leading blocks (1008 tokens, the prefix-sharing workload's
+    shape): the prefix goes to four 64-row tiles over three 336-key partitions."""
+    rng = np.random.default_rng(3)
+    contexts = 1016 + rng.integers(32, 257, 256) + 1
+    tables = _tables(contexts, 16, rng, shared_prefix=63)
+    seq = np.arange(256)
+    plan = ops.plan_batch(seq, 128, 32, tables, contexts, 16)
+    assert plan.partition_size == 336
+    assert plan.tiles.tolist() == [[64 * i, 64, 0, 3] for i in range(4)]
+    assert np.all(plan.rows[:, 1] == 3)
+    assert not plan.shared_kv, "what the row pass still reads is private"
+    _covered(plan, seq, contexts, 16)
+
+
+def test_prefix_groups_split_where_tables_diverge_and_skip_small_groups() -> None:
+    rng = np.random.default_rng(4)
+    a = _tables(np.full(40, 2000), 16, rng, shared_prefix=100)  # 40 rows share 100 blocks
+    b = _tables(np.full(10, 2000), 16, rng, shared_prefix=100)  # only 10: too few to tile
+    c = _tables(np.full(30, 900), 16, rng, shared_prefix=40)  # 30 rows share 40 blocks (640 tokens)
+    tables = a + b + c
+    contexts = np.asarray([2000] * 50 + [900] * 30)
+    seq = np.arange(80)
+    plan = ops.plan_batch(seq, 128, 8, tables, contexts, 16)
+    P = plan.partition_size
+    groups = {(f, n, pb, pe) for f, n, pb, pe in plan.tiles.tolist()}
+    assert {f for f, _, _, _ in groups} == {0, 50}
+    assert all(pe * P <= 100 * 16 for f, _, _, pe in groups if f == 0)
+    assert all(pe * P <= 40 * 16 for f, _, _, pe in groups if f == 50)
+    assert np.all(plan.rows[40:50, 1] == 0), "the small group stays in the row pass"
+    _covered(plan, seq, contexts, 16)
+
+
+def test_a_member_whose_table_ends_inside_the_prefix_still_joins() -> None:
+    rng = np.random.default_rng(5)
+    tables = _tables(np.full(20, 3000), 16, rng, shared_prefix=150)
+    contexts = np.full(20, 3000)
+    contexts[7] = 700  # its visible keys end inside the shared prefix
+    tables[7] = tables[7][:44]
+    seq = np.arange(20)
+    plan = ops.plan_batch(seq, 64, 4, tables, contexts, 16)
+    assert plan.tiles.shape[0] == 1 and plan.tiles[0, 0] == 0 and plan.tiles[0, 1] == 20
+    _covered(plan, seq, contexts, 16)
+
+
+def test_no_sharing_keeps_the_plain_plan() -> None:
+    rng = np.random.default_rng(6)
+    contexts = rng.integers(512, 4097, 64)
+    tables = _tables(contexts, 16, rng)
+    plan = ops.plan_batch(np.arange(64), 128, 32, tables, contexts, 16)
+    assert plan.tiles.shape == (0, 4) and np.all(plan.rows[:, 1] == 0)
+    assert (plan.partition_size, plan.shared_kv) == ops.batch_hints(tables, contexts, 32, 16)
+
+
+def test_every_public_name_of_ops_exists_and_the_workspace_helper_answers() -> None:
+    missing = [name for name in ops.__all__ if not hasattr(ops, name)]
+    assert not missing
+    assert ops.attention_workspace_bytes(64, 32, 128, 4096, 512) == 64 * 32 * 8 * 130 * 4
+    assert ops.attention_workspace_bytes(64, 32, 128, 512, 512) == 0
