@@ -198,6 +198,8 @@ class ModelRunner:
         self._pending: list[tuple[int, int]] = []
         self._weights: _DeviceWeights | None = None
         self._tables = BlockTableArena(self.device)
+        #: The host plan of the last ``execute`` (rows, tiles, partition size, load hint).
+        self.last_plan: ops.BatchPlan | None = None
 
     # --- pool ---------------------------------------------------------------------------
 
@@ -328,6 +330,7 @@ class ModelRunner:
             query_seq, config.head_dim, config.n_heads, self._tables.host, contexts_by_row,
             self.block_size, partition_size=self.partition_size,
         )  # fmt: skip
+        self.last_plan = host_plan
         partition = host_plan.partition_size
         plan_rows, plan_tiles = host_plan.rows, host_plan.tiles
         changed = update.index.size

@@ -148,6 +148,43 @@ def test_mixed_decode_and_prefill_rows_match_the_numpy_runner(device, models) ->
         assert float(np.max(np.abs(gv.cpu().numpy() - cpu.values[layer]))) < 1e-5
 
 
+def test_a_shared_prompt_decodes_through_prefix_tiles(device) -> None:
+    """20 sequences share a 544-token prompt's blocks; their decode step reads the prompt as
+    MFMA tiles over whole partitions (head_dim 32) and matches the NumPy runner."""
+    config = ModelConfig(vocab_size=64, d_model=64, n_layers=1, n_heads=2, d_ff=64, max_seq_len=1024)
+    weights = random_weights(config, seed=3)
+    model, oracle = LanguageModel(config, weights), OracleModel(config, weights)
+    block = 16
+    gpu = ModelRunner(model, num_blocks=120, block_size=block, device=device)
+    cpu = OracleRunner(oracle, num_blocks=120, block_size=block)
+    rng = np.random.default_rng(11)
+    prompt = [int(t) for t in rng.integers(0, 64, 544)]
+    shared = tuple(range(34))
+    fill = ExecutionBatch((BatchEntry("p", tuple(prompt), tuple(range(544)), shared, None),))
+    suffixes = [int(n) for n in rng.integers(3, 20, 20)]
+    tables = [shared + (34 + 2 * i, 35 + 2 * i) for i in range(20)]
+    children = ExecutionBatch(tuple(
+        BatchEntry(f"c{i}", tuple(int(t) for t in rng.integers(0, 64, n)), tuple(range(544, 544 + n)),
+                   tables[i], n - 1)
+        for i, n in enumerate(suffixes)
+    ))  # fmt: skip
+    decode = ExecutionBatch(tuple(
+        BatchEntry(f"c{i}", (int(rng.integers(0, 64)),), (544 + n,), tables[i], 0)
+        for i, n in enumerate(suffixes)
+    ))  # fmt: skip
+    for batch in (fill, children):
+        gpu.execute(batch)
+        cpu.execute(batch)
+    got = gpu.execute(decode)
+    plan = gpu.last_plan
+    assert plan.tiles.shape[0] == 1 and plan.tiles[0, 1] == 20 and plan.tiles[0, 3] >= 1
+    assert np.all(plan.rows[:, 1] == plan.tiles[0, 3])
+    want = cpu.execute(decode)
+    assert set(got) == set(want)
+    for name in want:
+        assert float(np.max(np.abs(got[name] - want[name]))) < TOLERANCE, name
+
+
 def test_sharing_a_prefix_block_does_not_change_either_continuation(device, models) -> None:
     model, oracle = models
     rng = np.random.default_rng(12)
