@@ -37,14 +37,17 @@
 namespace pkv {
 namespace {
 
-// Tunables (compile-time): wavefronts per row_partial workgroup, key rows loaded per wavefront
-// before any of them is used, and whether row_partial loads K/V rows non-temporally (each row is
-// read once there).
+// Tunables (compile-time): wavefronts per row_partial workgroup; bytes of one head row each lane
+// covers; bytes of key rows a wavefront loads (and as many value bytes) before it uses any of
+// them; and whether row_partial loads K/V rows non-temporally (each row is read once there).
 #ifndef PKV_ATTN_WAVES
 #define PKV_ATTN_WAVES 4
 #endif
-#ifndef PKV_ATTN_ITER_TOKENS
-#define PKV_ATTN_ITER_TOKENS 32
+#ifndef PKV_ATTN_LANE_BYTES
+#define PKV_ATTN_LANE_BYTES 16
+#endif
+#ifndef PKV_ATTN_ITER_BYTES
+#define PKV_ATTN_ITER_BYTES 16384
 #endif
 #ifndef PKV_ATTN_NONTEMPORAL
 #define PKV_ATTN_NONTEMPORAL 1
@@ -55,6 +58,13 @@ namespace {
 #endif
 #ifndef PKV_ATTN_ROWS_FIRST
 #define PKV_ATTN_ROWS_FIRST 0
+#endif
+// Workgroup order of the row pass: 0 = the hardware's round robin over the 8 XCDs (consecutive
+// workgroups, i.e. neighbouring heads of one token, on different XCDs); 1 = each XCD walks one
+// contiguous eighth of the grid. Measured on MI355X (64 x 4k decode): 0 reads at 6.79 TB/s,
+// 1 at 6.26 TB/s.
+#ifndef PKV_ATTN_XCD_REMAP
+#define PKV_ATTN_XCD_REMAP 0
 #endif
 
 constexpr int kWaves = PKV_ATTN_WAVES;  // wavefronts per row_partial workgroup
@@ -107,20 +117,39 @@ struct Params {
   float scale_log2;        // scale * log2(e)
 };
 
-// How one wavefront of row_partial maps onto token rows of a head: kLpt lanes per row, kVpl
-// 16-byte vectors per lane, so each lane owns kDpl = D / kLpt dimensions and a wavefront covers
-// kTpr rows per load round. kRounds rounds (kIterTok rows) are loaded before any is used.
+constexpr uint32_t kXcds = 8;  // MI355X: workgroup i runs on XCD i % 8
+
+// Logical workgroup index of this workgroup under the XCD order chosen above.
+__device__ __forceinline__ uint32_t logical_block() {
+  const uint32_t bid = blockIdx.x;
+  if constexpr (PKV_ATTN_XCD_REMAP) {
+    const uint32_t full = gridDim.x - gridDim.x % kXcds;
+    if (bid < full) return (bid % kXcds) * (full / kXcds) + bid / kXcds;
+  }
+  return bid;
+}
+
+// How one wavefront of row_partial maps onto token rows of a head: kLpt lanes per row (so that
+// each lane covers about PKV_ATTN_LANE_BYTES of it, 1 to 8 lanes), kVpl 16-byte vectors per
+// lane, so each lane owns kDpl = D / kLpt dimensions and a wavefront covers kTpr rows per load
+// round. kRounds rounds (kIterTok rows, about PKV_ATTN_ITER_BYTES of keys, at most 64 rows) are
+// loaded before any is used: a bfloat16 row is half a float32 one, so twice as many are in
+// flight. Measured on MI355X: 16-byte lanes (8 lanes per 512-byte row) beat 64-byte lanes for
+// bfloat16 by 18% (register pressure halves occupancy otherwise); 16 KiB per round is within
+// 1-3% of 8 and 24 KiB on configs 2-5 and best overall.
 template <typename KVT, int D>
 struct Layout {
   static constexpr int kEsize = KVTraits<KVT>::kEsize;
   static constexpr int kRowBytes = D * kEsize;
   static_assert(kRowBytes >= 16 && kRowBytes % 16 == 0, "head row must be whole 16-byte vectors");
-  static constexpr int kLpt = kRowBytes / 16 < 8 ? kRowBytes / 16 : 8;
+  static constexpr int kLptWanted = kRowBytes / PKV_ATTN_LANE_BYTES;
+  static constexpr int kLpt = kLptWanted < 1 ? 1 : (kLptWanted > 8 ? 8 : kLptWanted);
   static constexpr int kVpl = kRowBytes / (16 * kLpt);
   static constexpr int kEpv = 16 / kEsize;  // elements per 16-byte vector
   static constexpr int kDpl = kVpl * kEpv;
   static constexpr int kTpr = kWave / kLpt;
-  static constexpr int kRounds = kTpr >= PKV_ATTN_ITER_TOKENS ? 1 : PKV_ATTN_ITER_TOKENS / kTpr;
+  static constexpr int kIterWanted = PKV_ATTN_ITER_BYTES / kRowBytes < 64 ? PKV_ATTN_ITER_BYTES / kRowBytes : 64;
+  static constexpr int kRounds = kTpr >= kIterWanted ? 1 : kIterWanted / kTpr;
   static constexpr int kIterTok = kTpr * kRounds;
   static constexpr int kGroups = kWaves * kTpr;  // lane groups per workgroup
 };
@@ -215,7 +244,7 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   __shared__ float s_acc[L::kGroups * D];
 
   // Grid: heads fastest, then partitions, then rows.
-  const uint32_t bid = blockIdx.x;
+  const uint32_t bid = logical_block();
   const int h = static_cast<int>(bid % static_cast<uint32_t>(a.num_heads));
   const uint32_t rest = bid / static_cast<uint32_t>(a.num_heads);
   const int p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
