@@ -4,10 +4,11 @@
 // pass 3 runs on the caller's stream after both:
 //
 //  1. row_partial (memory-bound rows, e.g. decode): one workgroup of kWaves wavefronts per
-//     (query row, head, context partition). The partition's slice of the block table is staged
-//     in LDS; each wavefront streams whole key and value token rows of its share of the
-//     partition with non-temporal 16-byte loads (kLpt lanes cover one token's head row) and keeps
-//     an online softmax (running max, running sum, unnormalised accumulator) per lane group in
+//     (query row, group of HPW adjacent heads, context partition), HPW = 2 where one head row is
+//     at most 256 bytes. The partition's slice of the block table is staged in LDS; each
+//     wavefront streams the group's slice of whole key and value token rows of its share of the
+//     partition with non-temporal 16-byte loads (kLpt lanes cover one slice) and keeps an online
+//     softmax (running max, running sum, unnormalised accumulator) per lane group and head in
 //     registers. The lane groups are merged through LDS at the end.
 //  2. tile_partial (compute-bound rows: a run of consecutive prefill rows of one sequence, or
 //     decode rows of several sequences over the partitions of a prefix they share): one
@@ -31,6 +32,7 @@
 #include <math.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "pkv_common.h"
 
@@ -129,30 +131,46 @@ __device__ __forceinline__ uint32_t logical_block() {
   return bid;
 }
 
-// How one wavefront of row_partial maps onto token rows of a head: kLpt lanes per row (so that
-// each lane covers about PKV_ATTN_LANE_BYTES of it, 1 to 8 lanes), kVpl 16-byte vectors per
-// lane, so each lane owns kDpl = D / kLpt dimensions and a wavefront covers kTpr rows per load
-// round. kRounds rounds (kIterTok rows, about PKV_ATTN_ITER_BYTES of keys, at most 64 rows) are
-// loaded before any is used: a bfloat16 row is half a float32 one, so twice as many are in
-// flight. Measured on MI355X: 16-byte lanes (8 lanes per 512-byte row) beat 64-byte lanes for
-// bfloat16 by 18% (register pressure halves occupancy otherwise); 16 KiB per round is within
-// 1-3% of 8 and 24 KiB on configs 2-5 and best overall.
-template <typename KVT, int D>
+// How one wavefront of row_partial maps onto token rows. A workgroup serves HPW consecutive
+// heads, so each token row it reads is one contiguous slice of HPW * D elements. kLpt lanes
+// cover a slice (about PKV_ATTN_LANE_BYTES each, 1 to 8 lanes, never more than the 16-byte
+// vectors of one head), each with kVpl 16-byte vectors: lane j's vector i is vector i * kLpt + j
+// of the slice and belongs to head i / kVph. A lane therefore owns kDph dimensions of each of
+// the HPW heads, and a wavefront covers kTpr token rows per load round. kRounds rounds (kIterTok
+// rows, about PKV_ATTN_ITER_BYTES of keys, at most 64 rows) are loaded before any is used.
+// Measured on MI355X: 16-byte lanes beat 64-byte lanes for bfloat16 by 18% (register pressure
+// halves occupancy otherwise); 16 KiB per round is within 1-3% of 8 and 24 KiB on configs 2-5
+// and best overall. Slices of at least 512 contiguous bytes per token row stream faster than
+// 256-byte ones from a shuffled pool (a load-only probe of the bfloat16 head_dim-128 pattern:
+// 6.65 TB/s at one head per workgroup, 6.97 TB/s at two), which is what HPW = 2 is for.
+template <typename KVT, int D, int HPW>
 struct Layout {
   static constexpr int kEsize = KVTraits<KVT>::kEsize;
-  static constexpr int kRowBytes = D * kEsize;
-  static_assert(kRowBytes >= 16 && kRowBytes % 16 == 0, "head row must be whole 16-byte vectors");
-  static constexpr int kLptWanted = kRowBytes / PKV_ATTN_LANE_BYTES;
-  static constexpr int kLpt = kLptWanted < 1 ? 1 : (kLptWanted > 8 ? 8 : kLptWanted);
-  static constexpr int kVpl = kRowBytes / (16 * kLpt);
+  static constexpr int kHeadBytes = D * kEsize;
+  static_assert(kHeadBytes >= 16 && kHeadBytes % 16 == 0, "head row must be whole 16-byte vectors");
+  static constexpr int kVecPerHead = kHeadBytes / 16;
+  static constexpr int kSliceBytes = HPW * kHeadBytes;
+  static constexpr int kLptWanted = kSliceBytes / PKV_ATTN_LANE_BYTES;
+  static constexpr int kLptCap = kVecPerHead < 8 ? kVecPerHead : 8;
+  static constexpr int kLpt = kLptWanted < 1 ? 1 : (kLptWanted > kLptCap ? kLptCap : kLptWanted);
+  static_assert(kVecPerHead % kLpt == 0, "the lanes of a row split every head alike");
+  static constexpr int kVph = kVecPerHead / kLpt;  // vectors per lane per head
+  static constexpr int kVpl = HPW * kVph;
   static constexpr int kEpv = 16 / kEsize;  // elements per 16-byte vector
+  static constexpr int kDph = kVph * kEpv;  // dimensions per lane per head
   static constexpr int kDpl = kVpl * kEpv;
   static constexpr int kTpr = kWave / kLpt;
-  static constexpr int kIterWanted = PKV_ATTN_ITER_BYTES / kRowBytes < 64 ? PKV_ATTN_ITER_BYTES / kRowBytes : 64;
+  static constexpr int kIterWanted =
+      PKV_ATTN_ITER_BYTES / kSliceBytes < 64 ? PKV_ATTN_ITER_BYTES / kSliceBytes : 64;
   static constexpr int kRounds = kTpr >= kIterWanted ? 1 : kIterWanted / kTpr;
   static constexpr int kIterTok = kTpr * kRounds;
   static constexpr int kGroups = kWaves * kTpr;  // lane groups per workgroup
 };
+
+// Heads per row_partial workgroup: two when one head row is at most 256 bytes and the heads pair
+// up, so every token row is read as a slice of at least 512 contiguous bytes.
+template <typename KVT, int D>
+constexpr bool kPairHeads = D * KVTraits<KVT>::kEsize <= 256;
 
 // Widen one 16-byte vector into 4 (float) or 8 (bfloat16) floats.
 __device__ __forceinline__ void widen(const uint4& raw, float* out, float) {
@@ -235,18 +253,20 @@ __device__ __forceinline__ void store_result(const Params& a, int64_t t, int h, 
 // ---------------------------------------------------------------------------------------------
 // Pass 1: row_partial.
 // ---------------------------------------------------------------------------------------------
-template <typename KVT, int D, bool kPow2Block, bool kStream>
+template <typename KVT, int D, int HPW, bool kPow2Block, bool kStream>
 __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
-  using L = Layout<KVT, D>;
+  using L = Layout<KVT, D, HPW>;
+  constexpr int kSlice = HPW * D;  // elements of the token-row slice this workgroup reads
   __shared__ int s_table[kTableSlots];
-  __shared__ float s_m[L::kGroups];
-  __shared__ float s_l[L::kGroups];
-  __shared__ float s_acc[L::kGroups * D];
+  __shared__ float s_m[L::kGroups * HPW];
+  __shared__ float s_l[L::kGroups * HPW];
+  __shared__ float s_acc[L::kGroups * kSlice];
 
-  // Grid: heads fastest, then partitions, then rows.
+  // Grid: head groups fastest, then partitions, then rows.
   const uint32_t bid = logical_block();
-  const int h = static_cast<int>(bid % static_cast<uint32_t>(a.num_heads));
-  const uint32_t rest = bid / static_cast<uint32_t>(a.num_heads);
+  const uint32_t head_groups = static_cast<uint32_t>(a.num_heads / HPW);
+  const int h = static_cast<int>(bid % head_groups) * HPW;  // first head of the group
+  const uint32_t rest = bid / head_groups;
   const int p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
   const int64_t r = rest / static_cast<uint32_t>(a.max_parts);
   const int64_t t = a.rows ? a.rows[2 * r] : r;
@@ -270,8 +290,10 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int g = lane / L::kLpt;  // token slot inside a load round
-  const int j = lane % L::kLpt;  // position inside the row
+  const int j = lane % L::kLpt;  // position inside the slice
 
+  // Element (i * kLpt + j) * kEpv + e of the slice is dimension ((i % kVph) * kLpt + j) * kEpv +
+  // e of head h + i / kVph; the heads of a group are adjacent in both queries and pools.
   float qv[L::kDpl];
   {
     const float* qrow = a.queries + t * a.q_stride + static_cast<int64_t>(h) * D;
@@ -284,8 +306,13 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
     }
   }
 
-  float m = -INFINITY;
-  float l = 0.f;
+  float m[HPW];
+  float l[HPW];
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    m[hh] = -INFINITY;
+    l[hh] = 0.f;
+  }
   float acc[L::kDpl];
 #pragma unroll
   for (int d = 0; d < L::kDpl; ++d) acc[d] = 0.f;
@@ -330,80 +357,94 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
       }
     }
 
-    // Scores of this lane group's rows (base-2 units), reduced over the kLpt lanes of a row.
-    float s[L::kRounds];
+    // Scores of this lane group's rows (base-2 units) for each head, reduced over the kLpt lanes
+    // of a row.
+    float s[L::kRounds][HPW];
 #pragma unroll
     for (int rr = 0; rr < L::kRounds; ++rr) {
-      float dot = 0.f;
 #pragma unroll
-      for (int i = 0; i < L::kVpl; ++i) {
-        float kf[L::kEpv];
-        widen(kraw[rr][i], kf, KVT{});
+      for (int hh = 0; hh < HPW; ++hh) {
+        float dot = 0.f;
 #pragma unroll
-        for (int e = 0; e < L::kEpv; ++e) dot = fmaf(qv[i * L::kEpv + e], kf[e], dot);
+        for (int i = hh * L::kVph; i < (hh + 1) * L::kVph; ++i) {
+          float kf[L::kEpv];
+          widen(kraw[rr][i], kf, KVT{});
+#pragma unroll
+          for (int e = 0; e < L::kEpv; ++e) dot = fmaf(qv[i * L::kEpv + e], kf[e], dot);
+        }
+        dot = group_sum<L::kLpt>(dot);
+        s[rr][hh] = valid[rr] ? dot : -INFINITY;
       }
-      dot = group_sum<L::kLpt>(dot);
-      s[rr] = valid[rr] ? dot : -INFINITY;
     }
 
-    // Online softmax update.
-    float mx = m;
+    // Online softmax update, per head.
+    float pr[L::kRounds][HPW];
+    float alpha[HPW];
 #pragma unroll
-    for (int rr = 0; rr < L::kRounds; ++rr) mx = fmaxf(mx, s[rr]);
-    const float shift = mx == -INFINITY ? 0.f : mx;
-    const float alpha = fast_exp2(m - shift);
-    float pr[L::kRounds];
-    float psum = 0.f;
+    for (int hh = 0; hh < HPW; ++hh) {
+      float mx = m[hh];
 #pragma unroll
-    for (int rr = 0; rr < L::kRounds; ++rr) {
-      pr[rr] = fast_exp2(s[rr] - shift);
-      psum += pr[rr];
+      for (int rr = 0; rr < L::kRounds; ++rr) mx = fmaxf(mx, s[rr][hh]);
+      const float shift = mx == -INFINITY ? 0.f : mx;
+      alpha[hh] = fast_exp2(m[hh] - shift);
+      float psum = 0.f;
+#pragma unroll
+      for (int rr = 0; rr < L::kRounds; ++rr) {
+        pr[rr][hh] = fast_exp2(s[rr][hh] - shift);
+        psum += pr[rr][hh];
+      }
+      l[hh] = fmaf(l[hh], alpha[hh], psum);
+      m[hh] = mx;
     }
-    l = fmaf(l, alpha, psum);
 #pragma unroll
-    for (int d = 0; d < L::kDpl; ++d) acc[d] *= alpha;
+    for (int d = 0; d < L::kDpl; ++d) acc[d] *= alpha[d / L::kDph];
 #pragma unroll
     for (int rr = 0; rr < L::kRounds; ++rr) {
 #pragma unroll
       for (int i = 0; i < L::kVpl; ++i) {
         float vf[L::kEpv];
         widen(vraw[rr][i], vf, KVT{});
+        const float w = pr[rr][i / L::kVph];
 #pragma unroll
         for (int e = 0; e < L::kEpv; ++e) {
-          acc[i * L::kEpv + e] = fmaf(pr[rr], vf[e], acc[i * L::kEpv + e]);
+          acc[i * L::kEpv + e] = fmaf(w, vf[e], acc[i * L::kEpv + e]);
         }
       }
     }
-    m = mx;
   }
 
-  // Merge the kGroups partial states of the workgroup.
+  // Merge the kGroups partial states of the workgroup, head by head.
   const int grp = wave * L::kTpr + g;
   if (j == 0) {
-    s_m[grp] = m;
-    s_l[grp] = l;
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      s_m[grp * HPW + hh] = m[hh];
+      s_l[grp * HPW + hh] = l[hh];
+    }
   }
 #pragma unroll
   for (int i = 0; i < L::kVpl; ++i) {
 #pragma unroll
     for (int e = 0; e < L::kEpv; ++e) {
-      s_acc[grp * D + (i * L::kLpt + j) * L::kEpv + e] = acc[i * L::kEpv + e];
+      s_acc[grp * kSlice + (i * L::kLpt + j) * L::kEpv + e] = acc[i * L::kEpv + e];
     }
   }
   __syncthreads();
 
-  for (int d = threadIdx.x; d < D; d += kThreads) {
+  for (int x = threadIdx.x; x < kSlice; x += kThreads) {
+    const int hh = x / D;
+    const int d = x - hh * D;
     float big = -INFINITY;
-    for (int k = 0; k < L::kGroups; ++k) big = fmaxf(big, s_m[k]);
+    for (int k = 0; k < L::kGroups; ++k) big = fmaxf(big, s_m[k * HPW + hh]);
     const float shift = big == -INFINITY ? 0.f : big;
     float lsum = 0.f;
     float sum_acc = 0.f;
     for (int k = 0; k < L::kGroups; ++k) {
-      const float w = fast_exp2(s_m[k] - shift);
-      lsum = fmaf(s_l[k], w, lsum);
-      sum_acc = fmaf(s_acc[k * D + d], w, sum_acc);
+      const float w = fast_exp2(s_m[k * HPW + hh] - shift);
+      lsum = fmaf(s_l[k * HPW + hh], w, lsum);
+      sum_acc = fmaf(s_acc[k * kSlice + x], w, sum_acc);
     }
-    store_result(a, t, h, p, nparts, d, D, sum_acc, big, lsum, d == 0);
+    store_result(a, t, h + hh, p, nparts, d, D, sum_acc, big, lsum, d == 0);
   }
 }
 
@@ -762,7 +803,6 @@ template <typename KVT, int D>
 int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t num_tiles,
                bool stream_kv, int device, hipStream_t stream) {
   const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
-  const int64_t per_row = static_cast<int64_t>(a.max_parts) * a.num_heads;
   std::unique_lock<std::mutex> overlap_lock(g_overlap_mutex, std::defer_lock);
   Overlap* overlap = nullptr;
   if (PKV_ATTN_OVERLAP && num_tiles > 0 && num_rows > 0) {
@@ -770,21 +810,28 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     overlap = overlap_locked(device);
     if (overlap == nullptr) overlap_lock.unlock();
   }
-  auto launch_rows = [&]() -> int {
-    if (num_rows == 0) return PKV_OK;
-    const int64_t groups = num_rows * per_row;
+  auto launch_rows_hpw = [&](auto hpw_tag) -> int {
+    constexpr int HPW = decltype(hpw_tag)::value;
+    const int64_t groups = num_rows * static_cast<int64_t>(a.max_parts) * (a.num_heads / HPW);
     if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
     const dim3 grid(static_cast<uint32_t>(groups));
     if (pow2 && stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, true, true>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true>), grid, dim3(kThreads), 0, stream, a);
     } else if (pow2) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, true, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false>), grid, dim3(kThreads), 0, stream, a);
     } else if (stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, false, true>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, true>), grid, dim3(kThreads), 0, stream, a);
     } else {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, false, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, false>), grid, dim3(kThreads), 0, stream, a);
     }
     return check_launch();
+  };
+  auto launch_rows = [&]() -> int {
+    if (num_rows == 0) return PKV_OK;
+    if constexpr (kPairHeads<KVT, D>) {
+      if (a.num_heads % 2 == 0) return launch_rows_hpw(std::integral_constant<int, 2>{});
+    }
+    return launch_rows_hpw(std::integral_constant<int, 1>{});
   };
   if (PKV_ATTN_ROWS_FIRST || overlap == nullptr) {
     // Without overlap the order does not matter; with it, rows first takes the CUs first.

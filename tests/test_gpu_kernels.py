@@ -345,6 +345,28 @@ def test_bfloat16_kv_matches_the_oracle_on_rounded_inputs(device, dim) -> None:
     assert np.max(np.abs(got - dense)) < FP32_TOL
 
 
+@pytest.mark.parametrize("heads", [1, 3, 4, 6])
+@pytest.mark.parametrize("dim", [8, 32, 64, 128, 256])
+@pytest.mark.parametrize("kv", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_row_pass_head_pairs_match_the_oracle(device, kv, dim, heads) -> None:
+    """The row pass reads two adjacent heads per workgroup when a head row is at most 256 bytes
+    and the head count is even, one otherwise: both layouts, every head of the batch."""
+    say("row pass heads", kv, dim, heads)
+    rng = np.random.default_rng(1000 * heads + dim)
+    kc, vc, tables, contexts, positions, seq_of, q = _ragged_case(
+        rng, heads=heads, dim=dim, block=16, pool=160, seqs=5, max_ctx=600, prefill=True, max_rows=4
+    )
+    scale = dim**-0.5
+    if kv == torch.bfloat16:
+        kc, vc = bf16_round(kc), bf16_round(vc)
+    want, dense = _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale)
+    for partition in (0, 64):
+        got = _run_kernel(device, kc, vc, tables, contexts, positions, seq_of, q, scale,
+                          partition=partition, dtype=kv)  # fmt: skip
+        assert np.max(np.abs(got - want)) < FP32_TOL, partition
+        assert np.max(np.abs(got - dense)) < FP32_TOL, partition
+
+
 def test_poisoned_slots_and_padding_are_never_read(device) -> None:
     say("poison")
     rng = np.random.default_rng(9)
