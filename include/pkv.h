@@ -42,6 +42,9 @@ typedef enum pkv_dtype {
                                 prefix): load K/V rows through the caches instead of streaming
                                 them past, so the other readers hit L2 / the Infinity Cache */
 
+/* pkv_paged_attention tile record: end partition of a tile computed whole by one workgroup. */
+#define PKV_TILE_WHOLE (-1)
+
 #define PKV_OK 0
 #define PKV_EINVAL (-1)       /* a size, stride, pointer or enum argument is out of range */
 #define PKV_EUNSUPPORTED (-2) /* a valid but unimplemented shape (e.g. head_dim 96) */
@@ -165,14 +168,24 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *   tiles, num_tiles : the plan's tile list, int32 [num_tiles, 4] = (first row, row count <= 64,
  *                      first partition, end partition; end <= first means through the last):
  *                      runs of consecutive rows computed by the fp32 MFMA tile pass over those
- *                      partitions. Keys are read through the table of the tile's first row, so
- *                      the rows are either one sequence's (a prefill chunk) or rows of several
- *                      sequences whose tables hold the same block ids over the tile's
- *                      partitions (a shared prefix; those rows then also appear in the row list
- *                      with the first partition after the tile's). Needs
- *                      pkv_tile_head_dim_supported(head_dim).
+ *                      partitions, one workgroup per (tile, head, partition). Keys are read
+ *                      through the table of the tile's first row, so the rows are either one
+ *                      sequence's (a prefill chunk) or rows of several sequences whose tables
+ *                      hold the same block ids over the tile's partitions (a shared prefix;
+ *                      those rows then also appear in the row list with the first partition
+ *                      after the tile's). End partition PKV_TILE_WHOLE: one workgroup per
+ *                      (tile, head) covers every visible key of the tile's rows and writes
+ *                      their final outputs (the first partition is then ignored; such rows must
+ *                      not be in the merge list). Needs pkv_tile_head_dim_supported(head_dim).
  *                      Every (query row, partition) must be covered exactly once. With rows and
  *                      tiles both NULL, every row goes through the row-streaming pass.
+ *   merge_rows,
+ *   num_merge_rows   : int32 [num_merge_rows], the query rows whose per-partition results the
+ *                      reduce pass merges: every row whose visible context spans more than one
+ *                      partition and that no whole tile covers (listing a row that fits one
+ *                      partition is harmless; merge_rows may be NULL when the count is 0).
+ *                      num_merge_rows = -1: every row of the batch, which is only correct
+ *                      without whole tiles.
  *   key_cache,
  *   value_cache      : the layer's pools, [num_blocks, block_size, num_heads, head_dim], kv_dtype,
  *                      16-byte aligned.
@@ -194,7 +207,8 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
 int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,
                         const int32_t* query_positions, const int32_t* query_seq,
                         int64_t num_queries, const int32_t* rows, int64_t num_rows,
-                        const int32_t* tiles, int64_t num_tiles, const void* key_cache,
+                        const int32_t* tiles, int64_t num_tiles, const int32_t* merge_rows,
+                        int64_t num_merge_rows, const void* key_cache,
                         const void* value_cache, pkv_dtype kv_dtype, int64_t num_blocks,
                         int32_t block_size, const int32_t* block_tables,
                         int32_t block_table_stride, const int32_t* context_lens,

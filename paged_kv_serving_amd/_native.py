@@ -60,6 +60,7 @@ HIPCC_FLAGS = (
 PKV_F32 = 0
 PKV_BF16 = 1
 PKV_ATTN_SHARED_KV = 1
+PKV_TILE_WHOLE = -1
 
 PKV_OK = 0
 
@@ -167,6 +168,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         _ptr, _ptr, _i64,  # out, queries, query_token_stride
         _ptr, _ptr, _i64,  # query_positions, query_seq, num_queries
         _ptr, _i64, _ptr, _i64,  # rows, num_rows, tiles, num_tiles
+        _ptr, _i64,  # merge_rows, num_merge_rows
         _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size
         _ptr, _i32, _ptr, _i32,  # block_tables, block_table_stride, context_lens, num_seqs
         _i32, _i32, ctypes.c_float,  # num_heads, head_dim, scale

@@ -76,6 +76,8 @@ constexpr int kDefaultPartition = 512;
 constexpr int kTableSlots = kMaxPartition + 4;  // ceil(P / B) + 1 entries at most
 constexpr int kTileRows = 64;           // query rows per tile_partial workgroup (4 x 16)
 constexpr int kTileThreads = 256;
+constexpr int kTileWhole = PKV_TILE_WHOLE;  // tile end partition: every key in one workgroup
+constexpr int kReduceThreads = 256;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -101,7 +103,10 @@ struct Params {
   const int32_t* q_seq;    // [T]
   const int32_t* rows;     // row_partial: [R, 2] = (query row, first partition); null: identity
   const int32_t* tiles;    // tile_partial: [n, 4] = (first row, row count <= 64, first
-                           // partition, end partition; end <= first: through the last)
+                           // partition, end partition; end <= first: through the last;
+                           // kTileWhole: one workgroup covers every key and writes final rows)
+  const int32_t* merge_rows;  // reduce: the query rows whose partials are merged
+  int64_t num_merge;       // entries of merge_rows; negative: every query row instead
   const void* kcache;      // [N, B, H, D]
   const void* vcache;
   int64_t num_queries;
@@ -525,7 +530,9 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
   const int32_t* entry = a.tiles + 4 * tile;
   const int64_t t0 = entry[0];
   if (t0 < 0 || t0 >= a.num_queries) return;  // a tile outside the batch is skipped
-  if (p < entry[2] || (entry[3] > entry[2] && p >= entry[3])) return;  // outside its partitions
+  // A whole tile is computed by its partition-0 workgroup alone, over every visible key.
+  const bool whole = entry[3] == kTileWhole;
+  if (whole ? p != 0 : (p < entry[2] || (entry[3] > entry[2] && p >= entry[3]))) return;
   const int nrows = static_cast<int>(min<int64_t>(min(entry[1], kTileRows), a.num_queries - t0));
   const int seq = a.q_seq[t0];
 
@@ -540,12 +547,18 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
 #pragma unroll
   for (int mask = 32; mask > 0; mask >>= 1) tile_vis = max(tile_vis, __shfl_xor(tile_vis, mask));
   const int nparts = parts_of(tile_vis, a.part_size);
-  if (p >= nparts) return;
-  const int kbeg = p * a.part_size;
-  const int kend = min(kbeg + a.part_size, tile_vis);
-  const int b0 = block_of<kPow2Block>(kbeg, a);
-  const int nb = kend > kbeg ? block_of<kPow2Block>(kend - 1, a) - b0 + 1 : 0;
-  if (nb > 0) stage_table(s_table, a, seq, b0, nb, kTileThreads);
+  if (!whole && p >= nparts) return;
+  const int kbeg = whole ? 0 : p * a.part_size;
+  const int kend = whole ? tile_vis : min(kbeg + a.part_size, tile_vis);
+  // The table entries of blocks [b0, b0 + kTableSlots) are staged in LDS. A partition always
+  // fits; a whole tile moves the window forward when the next key tile would leave it.
+  const int last_block = kend > kbeg ? block_of<kPow2Block>(kend - 1, a) : -1;
+  int b0 = block_of<kPow2Block>(kbeg, a);
+  auto stage_window = [&]() {
+    const int nb = min(last_block - b0 + 1, kTableSlots);
+    if (nb > 0) stage_table(s_table, a, seq, b0, nb, kTileThreads);
+  };
+  stage_window();
 
   const int c = lane >> 4;
   const int n = lane & 15;
@@ -612,6 +625,13 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
 
   const int lim = min(my_vis, kend);
   for (int k0 = kbeg; k0 < kend; k0 += kKeys) {
+    // Every read of s_table by the last prefetch happened before the previous barrier, so the
+    // window can move here; the barrier below publishes it before the next prefetch reads it.
+    const int next = k0 + kKeys;
+    if (next < kend && block_of<kPow2Block>(min(next + kKeys, kend) - 1, a) >= b0 + kTableSlots) {
+      b0 = block_of<kPow2Block>(next, a);
+      stage_window();
+    }
     // Widen the prefetched tile (zeros past kend) into LDS as float32.
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
@@ -697,7 +717,8 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
   // Epilogue: register r of tile b is O[query n][16b + 4c + r].
   const float l = column_sum(l_part);
   if (!q_ok) return;
-  const int row_parts = parts_of(my_vis, a.part_size);
+  // A whole tile covered every visible key of its rows: their outputs are final.
+  const int row_parts = whole ? 1 : parts_of(my_vis, a.part_size);
   if (p >= row_parts) return;
   const int64_t qh = (t0 + qi) * a.num_heads + h;
   if (row_parts == 1) {
@@ -723,29 +744,57 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
 }
 
 // ---------------------------------------------------------------------------------------------
-// Pass 3: reduce. One workgroup per (query row, head); thread d owns output dimension d.
+// Pass 3: reduce. Item i = (entry i / H of the merge list, or query row i / H without one; head
+// i % H). D / 4 threads per item, four output dimensions each, so a workgroup of kReduceThreads
+// merges several (row, head) items; kVec selects 16-byte accesses (out and workspace aligned).
 // ---------------------------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(D < kWave ? kWave : D) void reduce_kernel(const Params a) {
-  const int64_t qh = blockIdx.x;
-  const int64_t t = qh / a.num_heads;
+template <int D, bool kVec>
+__global__ __launch_bounds__(kReduceThreads) void reduce_kernel(const Params a, int64_t num_items) {
+  static_assert(D % 4 == 0 && D / 4 <= kReduceThreads, "four dimensions per thread");
+  constexpr int kTpi = D / 4;                       // threads per item
+  constexpr int kItems = kReduceThreads / kTpi;     // items per workgroup
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kItems + threadIdx.x / kTpi;
+  if (item >= num_items) return;
+  const int h = static_cast<int>(item % a.num_heads);
+  const int64_t idx = item / a.num_heads;
+  const int64_t t = a.num_merge >= 0 ? a.merge_rows[idx] : idx;
+  if (t < 0 || t >= a.num_queries) return;  // a row outside the batch is skipped
   const int nparts = parts_of(row_visible(a, t), a.part_size);
   if (nparts == 1) return;  // written by the partial pass
-  const int d = threadIdx.x;
-  if (d >= D) return;
+  const int d = (static_cast<int>(threadIdx.x) % kTpi) * 4;
+  const int64_t qh = t * a.num_heads + h;
   const float* ml = a.ws_ml + 2 * qh * a.max_parts;
   float big = -INFINITY;
   for (int k = 0; k < nparts; ++k) big = fmaxf(big, ml[2 * k]);
   const float shift = big == -INFINITY ? 0.f : big;
   float lsum = 0.f;
-  float acc = 0.f;
-  const float* part = a.ws_acc + qh * a.max_parts * D;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const float* part = a.ws_acc + qh * a.max_parts * D + d;
   for (int k = 0; k < nparts; ++k) {
     const float w = fast_exp2(ml[2 * k] - shift);
     lsum = fmaf(ml[2 * k + 1], w, lsum);
-    acc = fmaf(part[static_cast<int64_t>(k) * D + d], w, acc);
+    float v[4];
+    if constexpr (kVec) {
+      const float4 x = *reinterpret_cast<const float4*>(part + static_cast<int64_t>(k) * D);
+      v[0] = x.x;
+      v[1] = x.y;
+      v[2] = x.z;
+      v[3] = x.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = part[static_cast<int64_t>(k) * D + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] = fmaf(v[e], w, acc[e]);
   }
-  a.out[qh * D + d] = acc / (lsum > 0.f ? lsum : 1.f);
+  const float sum = lsum > 0.f ? lsum : 1.f;
+  float* dst = a.out + qh * D + d;
+  if constexpr (kVec) {
+    *reinterpret_cast<float4*>(dst) = make_float4(acc[0] / sum, acc[1] / sum, acc[2] / sum, acc[3] / sum);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = acc[e] / sum;
+  }
 }
 
 // A second stream per device, with fork/join events, so the compute-bound tile pass runs beside
@@ -862,11 +911,18 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     if (hipStreamWaitEvent(stream, overlap->join, 0) != hipSuccess) return PKV_EHIP;
     overlap_lock.unlock();
   }
-  if (a.max_parts > 1) {
-    const int64_t groups = num_queries * a.num_heads;
+  const int64_t merge = a.num_merge >= 0 ? a.num_merge : num_queries;
+  if (a.max_parts > 1 && merge > 0) {
+    constexpr int kItems = kReduceThreads / (D / 4);
+    const int64_t items = merge * a.num_heads;
+    const int64_t groups = (items + kItems - 1) / kItems;
     if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
-    hipLaunchKernelGGL((reduce_kernel<D>), dim3(static_cast<uint32_t>(groups)),
-                       dim3(D < kWave ? kWave : D), 0, stream, a);
+    const dim3 grid(static_cast<uint32_t>(groups));
+    if (aligned16(a.out) && aligned16(a.ws_acc)) {
+      hipLaunchKernelGGL((reduce_kernel<D, true>), grid, dim3(kReduceThreads), 0, stream, a, items);
+    } else {
+      hipLaunchKernelGGL((reduce_kernel<D, false>), grid, dim3(kReduceThreads), 0, stream, a, items);
+    }
     if (check_launch() != PKV_OK) return PKV_EHIP;
   }
   return PKV_OK;
@@ -928,8 +984,10 @@ extern "C" int pkv_tile_head_dim_supported(int32_t head_dim) {
 extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,
                                    const int32_t* query_positions, const int32_t* query_seq,
                                    int64_t num_queries, const int32_t* rows, int64_t num_rows,
-                                   const int32_t* tiles, int64_t num_tiles, const void* key_cache,
-                                   const void* value_cache, pkv_dtype kv_dtype, int64_t num_blocks,
+                                   const int32_t* tiles, int64_t num_tiles,
+                                   const int32_t* merge_rows, int64_t num_merge_rows,
+                                   const void* key_cache, const void* value_cache,
+                                   pkv_dtype kv_dtype, int64_t num_blocks,
                                    int32_t block_size, const int32_t* block_tables,
                                    int32_t block_table_stride, const int32_t* context_lens,
                                    int32_t num_seqs, int32_t num_heads, int32_t head_dim,
@@ -941,7 +999,8 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   if (part < 0) return PKV_EINVAL;
   if (flags & ~PKV_ATTN_SHARED_KV) return PKV_EINVAL;
   const bool stream_kv = (flags & PKV_ATTN_SHARED_KV) == 0;
-  if (num_queries < 0 || num_rows < 0 || num_tiles < 0 || num_blocks < 1 || block_size < 1 ||
+  if (num_queries < 0 || num_rows < 0 || num_tiles < 0 || num_merge_rows < -1 || num_blocks < 1 ||
+      block_size < 1 ||
       block_table_stride < 0 || num_seqs < 0 || num_heads < 1 || head_dim < 1 ||
       max_context_len < 0) {
     return PKV_EINVAL;
@@ -962,7 +1021,8 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
     num_rows = num_queries;
     num_tiles = 0;
   }
-  if ((num_rows > 0 && !rows && num_rows != num_queries) || (num_tiles > 0 && !tiles)) {
+  if ((num_rows > 0 && !rows && num_rows != num_queries) || (num_tiles > 0 && !tiles) ||
+      (num_merge_rows > 0 && !merge_rows)) {
     return PKV_EINVAL;
   }
   if (num_tiles > 0 && !pkv_tile_head_dim_supported(head_dim)) return PKV_EUNSUPPORTED;
@@ -994,6 +1054,8 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   a.q_seq = query_seq;
   a.rows = rows;
   a.tiles = tiles;
+  a.merge_rows = merge_rows;
+  a.num_merge = num_merge_rows;
   a.kcache = key_cache;
   a.vcache = value_cache;
   a.num_queries = num_queries;

@@ -266,16 +266,19 @@ class AttentionPlan:
 
     ``rows``: ``[R, 2]`` = (query row, first partition) for the row-streaming pass. ``tiles``:
     ``[n, 4]`` = (first row, row count, first partition, end partition; end <= first: through
-    the last) for the MFMA tile pass: a run of consecutive rows of one sequence, or decode rows
-    of several sequences over the partitions of a prefix whose blocks they share. Every (row,
-    partition) is covered exactly once. ``partition_size`` (0: library default) and
-    ``shared_kv`` choose the launch.
+    the last; ``TILE_WHOLE``: one workgroup per head over every visible key) for the MFMA tile
+    pass: a run of consecutive rows of one sequence, or decode rows of several sequences over
+    the partitions of a prefix whose blocks they share. Every (row, partition) is covered
+    exactly once. ``merge``: int32 ``[M]``, the rows whose partition results the reduce pass
+    merges (None: every row, which is only correct without whole tiles). ``partition_size``
+    (0: library default) and ``shared_kv`` choose the launch.
     """
 
     rows: torch.Tensor
     tiles: torch.Tensor
     partition_size: int = 0
     shared_kv: bool = False
+    merge: torch.Tensor | None = None
 
     @property
     def num_rows(self) -> int:
@@ -334,6 +337,12 @@ MIN_SHARED_ROWS = 16
 #: smallest partition it will choose for them.
 TARGET_PREFIX_GROUPS = 512
 MIN_PREFIX_PARTITION = 256
+#: Prefill tiles are computed whole (one workgroup per tile and head over every visible key,
+#: final rows written directly, nothing for the reduce) once the call has at least this many
+#: (tile, head) workgroups: four per CU of 256 keeps the chip full without splitting contexts.
+WHOLE_TILE_GROUPS = 1024
+#: Tile record end partition of a whole tile (include/pkv.h PKV_TILE_WHOLE).
+TILE_WHOLE = -1
 
 
 def _wide_partition(contexts: np.ndarray, num_heads: int, rows_per_seq: int) -> int:
@@ -381,13 +390,14 @@ def batch_hints(
 
 @dataclass(frozen=True)
 class BatchPlan:
-    """A host plan: ``rows [R, 2]``, ``tiles [n, 4]`` (int32, the :class:`AttentionPlan` layout),
-    the partition size and the load hint."""
+    """A host plan: ``rows [R, 2]``, ``tiles [n, 4]`` and ``merge [M]`` (int32, the
+    :class:`AttentionPlan` layout), the partition size and the load hint."""
 
     rows: np.ndarray
     tiles: np.ndarray
     partition_size: int
     shared_kv: bool
+    merge: np.ndarray | None = None
 
 
 def _common_prefix(a: np.ndarray, b: np.ndarray) -> int:
@@ -449,24 +459,68 @@ def _prefix_partition(shared_tokens: int, tiles: int, num_heads: int) -> int:
     return best
 
 
+def _visible(seq: np.ndarray, contexts: np.ndarray, positions: np.ndarray | None) -> np.ndarray:
+    """Visible key count of every query row, min(context, position + 1) (the context when the
+    positions are not known: an upper bound)."""
+    ctx = contexts[seq]
+    if positions is None:
+        return ctx
+    pos = np.asarray(positions, dtype=np.int64)
+    return np.where(pos < 0, 0, np.minimum(ctx, pos + 1))
+
+
+def _whole_tiles(tiles: np.ndarray, visible: np.ndarray, num_heads: int) -> np.ndarray:
+    """Prefill tiles as whole tiles, longest first (the grid runs them in record order, so the
+    longest workgroups start first), when there are enough of them to fill the GPU."""
+    if tiles.shape[0] == 0 or tiles.shape[0] * num_heads < WHOLE_TILE_GROUPS:
+        return tiles
+    longest = np.fromiter(
+        (visible[f : f + c].max() for f, c in zip(tiles[:, 0].tolist(), tiles[:, 1].tolist())),
+        dtype=np.int64, count=tiles.shape[0],
+    )  # fmt: skip
+    whole = tiles[np.argsort(-longest, kind="stable")].copy()
+    whole[:, 2] = 0
+    whole[:, 3] = TILE_WHOLE
+    return whole
+
+
+def merge_rows_for(
+    num_queries: int, tiles: np.ndarray, visible: np.ndarray | None = None, partition_size: int = 0
+) -> np.ndarray:
+    """The rows the reduce pass merges: every row no whole tile covers, and of those only the
+    ones whose visible length spans more than one partition when ``visible`` is known."""
+    keep = np.ones(num_queries, dtype=bool)
+    for first, count, _, end in np.asarray(tiles, dtype=np.int64).reshape(-1, 4).tolist():
+        if end == TILE_WHOLE:
+            keep[first : first + count] = False
+    if visible is not None and partition_size > 0:
+        keep &= np.asarray(visible) > partition_size
+    return np.flatnonzero(keep).astype(np.int32)
+
+
 def plan_batch(
     query_seq: np.ndarray, head_dim: int, num_heads: int, tables, context_lens: np.ndarray,
     block_size: int, *, partition_size: int = 0, min_tile_rows: int = MIN_TILE_ROWS,
+    query_positions: np.ndarray | None = None,
 ) -> BatchPlan:  # fmt: skip
     """The full host plan of a ragged call: the row/tile split of :func:`plan_rows`, shared-prefix
-    tiles, the partition size and the load hint.
+    tiles, whole prefill tiles, the reduce's merge list, the partition size and the load hint.
 
     ``tables[s]`` / ``context_lens[s]``: block table (any int sequence) and context length of
     the sequence index ``s`` used in ``query_seq``. Row-pass rows of consecutive queries whose
     sequences share at least MIN_SHARED_TOKENS of leading blocks, MIN_SHARED_ROWS or more of
     them, read that prefix once per head as MFMA tiles over its whole partitions, and start the
-    row pass at the first partition after it. A nonzero ``partition_size`` is kept as given.
+    row pass at the first partition after it. Prefill tiles become whole tiles when there are at
+    least WHOLE_TILE_GROUPS (tile, head) pairs. ``query_positions`` (optional) narrows the merge
+    list to rows that span several partitions. A nonzero ``partition_size`` is kept as given.
     """
     seq = np.asarray(query_seq, dtype=np.int64)
     contexts = np.asarray(context_lens, dtype=np.int64)
     rows, tiles = plan_rows(seq, head_dim, min_tile_rows=min_tile_rows)
     if seq.size == 0:
-        return BatchPlan(rows, tiles, partition_size or 0, False)
+        return BatchPlan(rows, tiles, partition_size or 0, False, np.zeros(0, np.int32))
+    visible = _visible(seq, contexts, query_positions)
+    tiles = _whole_tiles(tiles, visible, num_heads)
     used_blocks = -(-contexts // block_size)
     groups = []
     if rows.shape[0] >= MIN_SHARED_ROWS and tiles_supported(head_dim):
@@ -503,26 +557,37 @@ def plan_batch(
         seen.add((s, f))
         parts.append(np.asarray(tables[s][f : used_blocks[s]]))
     ids = np.concatenate(parts) if parts else np.zeros(0, np.int64)
-    return BatchPlan(rows, tiles, int(partition), _repeated_fraction_reached(ids))
+    merge = merge_rows_for(seq.size, tiles, visible, int(partition))
+    return BatchPlan(rows, tiles, int(partition), _repeated_fraction_reached(ids), merge)
 
 
 def upload_plan(
     rows: np.ndarray, tiles: np.ndarray, device: torch.device, *, partition_size: int = 0,
-    shared_kv: bool = False,
+    shared_kv: bool = False, merge: np.ndarray | None = None,
 ) -> AttentionPlan:
-    """Copy a host plan (``rows [R, 2]``, ``tiles [n, 4]``) to the device in one transfer."""
+    """Copy a host plan (``rows [R, 2]``, ``tiles [n, 4]``, ``merge [M]``) to the device in one
+    transfer. Without a merge list, one is derived when a tile is whole (every row no whole tile
+    covers), since the reduce must not touch the rows those tiles finish."""
     rows = np.asarray(rows, dtype=np.int32).reshape(-1, 2)
     tiles = np.asarray(tiles, dtype=np.int32).reshape(-1, 4)
-    packed = np.concatenate([rows.ravel(), tiles.ravel()])
+    if merge is None and tiles.size and np.any(tiles[:, 3] == TILE_WHOLE):
+        num_queries = max(int(rows[:, 0].max()) + 1 if rows.size else 0,
+                          int((tiles[:, 0] + tiles[:, 1]).max()))  # fmt: skip
+        merge = merge_rows_for(num_queries, tiles)
+    merge_arr = np.zeros(0, np.int32) if merge is None else np.asarray(merge, dtype=np.int32).ravel()
+    packed = np.concatenate([rows.ravel(), tiles.ravel(), merge_arr])
     data = torch.from_numpy(packed).to(device)
+    end_tiles = rows.size + tiles.size
     return AttentionPlan(
-        rows=data[: rows.size].view(-1, 2), tiles=data[rows.size :].view(-1, 4),
+        rows=data[: rows.size].view(-1, 2), tiles=data[rows.size : end_tiles].view(-1, 4),
         partition_size=partition_size, shared_kv=shared_kv,
+        merge=None if merge is None else data[end_tiles:],
     )  # fmt: skip
 
 
 def upload_batch_plan(plan: BatchPlan, device: torch.device) -> AttentionPlan:
-    return upload_plan(plan.rows, plan.tiles, device, partition_size=plan.partition_size, shared_kv=plan.shared_kv)
+    return upload_plan(plan.rows, plan.tiles, device, partition_size=plan.partition_size,
+                       shared_kv=plan.shared_kv, merge=plan.merge)  # fmt: skip
 
 
 def attention_workspace_bytes(
@@ -613,8 +678,9 @@ def paged_attention_ragged(
         workspace = torch.empty(need // 4, dtype=torch.float32, device=queries.device)
     ws_ptr = workspace.data_ptr() if need else None
     ws_bytes = workspace.numel() * workspace.element_size() if need else 0
-    rows_ptr = tiles_ptr = None
+    rows_ptr = tiles_ptr = merge_ptr = None
     num_rows = num_tiles = 0
+    num_merge = -1  # every row
     if plan is not None:
         for name, tensor in (("rows", plan.rows), ("tiles", plan.tiles)):
             if tensor.dtype != torch.int32 or tensor.device != queries.device:
@@ -630,10 +696,18 @@ def paged_attention_ragged(
         tiles_ptr = plan.tiles.data_ptr() if num_tiles else None
         if num_rows == 0 and num_tiles == 0:
             return out
+        if plan.merge is not None:
+            merge = plan.merge
+            if merge.dtype != torch.int32 or merge.device != queries.device or merge.dim() != 1:
+                raise ValueError("plan.merge must be a 1-D int32 tensor on the queries' device")
+            if not merge.is_contiguous():
+                raise ValueError("plan.merge must be contiguous")
+            num_merge = int(merge.shape[0])
+            merge_ptr = merge.data_ptr() if num_merge else None
     rc = _native.library().pkv_paged_attention(
         out.data_ptr(), queries.data_ptr(), stride,
         query_positions.data_ptr(), query_seq.data_ptr(), num_queries,
-        rows_ptr, num_rows, tiles_ptr, num_tiles,
+        rows_ptr, num_rows, tiles_ptr, num_tiles, merge_ptr, num_merge,
         key_cache.data_ptr(), value_cache.data_ptr(), kv_dtype_code(key_cache.dtype),
         key_cache.shape[0], key_cache.shape[1],
         block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(), num_seqs,

@@ -328,17 +328,17 @@ class ModelRunner:
         query_seq = np.repeat(update.rows, per_entry)
         host_plan = ops.plan_batch(
             query_seq, config.head_dim, config.n_heads, self._tables.host, contexts_by_row,
-            self.block_size, partition_size=self.partition_size,
+            self.block_size, partition_size=self.partition_size, query_positions=positions,
         )  # fmt: skip
         self.last_plan = host_plan
         partition = host_plan.partition_size
-        plan_rows, plan_tiles = host_plan.rows, host_plan.tiles
+        plan_rows, plan_tiles, plan_merge = host_plan.rows, host_plan.tiles, host_plan.merge
         changed = update.index.size
         meta64 = torch.from_numpy(np.concatenate([tokens, positions, slots, update.index])).to(self.device)
         meta32 = torch.from_numpy(
             np.concatenate([
                 positions.astype(np.int32), query_seq, contexts_by_row, update.values,
-                plan_rows.ravel(), plan_tiles.ravel(),
+                plan_rows.ravel(), plan_tiles.ravel(), plan_merge,
             ])  # fmt: skip
         ).to(self.device)
         tokens_d, positions_d = meta64[:total], meta64[total : 2 * total]
@@ -349,11 +349,14 @@ class ModelRunner:
         end_values = 2 * total + arena_rows + changed
         self._tables.apply(meta64[3 * total :], meta32[2 * total + arena_rows : end_values])
         tables_d = self._tables.tables
+        end_rows = end_values + plan_rows.size
+        end_tiles = end_rows + plan_tiles.size
         plan = ops.AttentionPlan(
-            rows=meta32[end_values : end_values + plan_rows.size].view(-1, 2),
-            tiles=meta32[end_values + plan_rows.size :].view(-1, 4),
+            rows=meta32[end_values:end_rows].view(-1, 2),
+            tiles=meta32[end_rows:end_tiles].view(-1, 4),
             partition_size=partition,
             shared_kv=host_plan.shared_kv,
+            merge=meta32[end_tiles:],
         )
         max_context = int(context.max())
 

@@ -63,7 +63,7 @@ class AttentionBatch:
         heads, dim = self.key_cache.shape[2], self.key_cache.shape[3]
         host = ops.plan_batch(
             self.host_seq, dim, heads, self.host_tables, self.host_context, self.key_cache.shape[1],
-            partition_size=partition_size,
+            partition_size=partition_size, query_positions=self.host_positions,
         )  # fmt: skip
         self.plan = ops.upload_batch_plan(host, self.queries.device)
 
@@ -149,7 +149,9 @@ def _assemble(
     padded = np.zeros((len(tables), width), dtype=np.int32)
     for i, table in enumerate(tables):
         padded[i, : len(table)] = table
-    plan = ops.upload_batch_plan(ops.plan_batch(seq, head_dim, heads, tables, context, block_size), device)
+    plan = ops.upload_batch_plan(
+        ops.plan_batch(seq, head_dim, heads, tables, context, block_size, query_positions=positions), device
+    )
     return AttentionBatch(
         key_cache=key_cache,
         value_cache=value_cache,
@@ -368,7 +370,9 @@ def prefix_sharing_step(
         context_lens=torch.from_numpy(contexts.astype(np.int32)).to(device),
         max_context_len=int(contexts.max()),
         scale=float(head_dim) ** -0.5,
-        plan=ops.upload_batch_plan(ops.plan_batch(seq, head_dim, heads, tables, contexts, block_size), device),
+        plan=ops.upload_batch_plan(
+            ops.plan_batch(seq, head_dim, heads, tables, contexts, block_size, query_positions=positions), device
+        ),
         host_tables=tables,
         host_context=contexts.astype(np.int64),
         host_positions=positions.astype(np.int64),

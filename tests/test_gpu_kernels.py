@@ -367,6 +367,57 @@ def test_row_pass_head_pairs_match_the_oracle(device, kv, dim, heads) -> None:
         assert np.max(np.abs(got - dense)) < FP32_TOL, partition
 
 
+def _whole_tile_plan(seq_of, positions, contexts, dim, partition, device, *, explicit_merge):
+    """Every run of >= 2 rows of one sequence as whole tiles; the rest in the row pass."""
+    rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)
+    tiles[:, 3] = ops.TILE_WHOLE
+    merge = None
+    if explicit_merge:
+        visible = np.minimum(contexts[seq_of], positions + 1)
+        merge = ops.merge_rows_for(seq_of.size, tiles, visible, partition or 512)
+    return ops.upload_plan(rows, tiles, device, partition_size=partition, merge=merge)
+
+
+@pytest.mark.parametrize("dim", [32, 64, 128, 256])
+@pytest.mark.parametrize("kv", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("block", [1, 16])
+def test_whole_tiles_match_the_oracle(device, dim, kv, block) -> None:
+    """Whole tiles: one workgroup per (tile, head) over every visible key, final rows written
+    directly, beside row-pass rows that the reduce merges. At block_size 1 the contexts exceed
+    the 1028 table entries a workgroup stages at once, so the staged window moves."""
+    say("whole tiles", dim, kv, block)
+    rng = np.random.default_rng(dim + block + (7 if kv == torch.bfloat16 else 0))
+    max_ctx = 1500 if block == 1 else 900
+    kc, vc, tables, contexts, positions, seq_of, q = _ragged_case(
+        rng, heads=2, dim=dim, block=block, pool=5 * max_ctx // block + 8, seqs=6, max_ctx=max_ctx,
+        prefill=True, max_rows=150,
+    )  # fmt: skip
+    scale = dim**-0.5
+    if kv == torch.bfloat16:
+        kc, vc = bf16_round(kc), bf16_round(vc)
+    want, dense = _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale)
+    width = max(len(t) for t in tables)
+    padded = np.full((len(tables), width), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    args = (
+        torch.from_numpy(q).to(device), torch.from_numpy(positions.astype(np.int32)).to(device),
+        torch.from_numpy(seq_of.astype(np.int32)).to(device),
+        torch.from_numpy(kc).to(device).to(kv), torch.from_numpy(vc).to(device).to(kv),
+        torch.from_numpy(padded).to(device), torch.from_numpy(contexts.astype(np.int32)).to(device),
+        scale,
+    )  # fmt: skip
+    for partition in (0, 64):
+        for explicit in (False, True):
+            plan = _whole_tile_plan(seq_of, positions, contexts, dim, partition, device,
+                                    explicit_merge=explicit)  # fmt: skip
+            got = ops.paged_attention_ragged(
+                *args, max_context_len=int(contexts.max()), plan=plan
+            ).cpu().numpy()  # fmt: skip
+            assert np.max(np.abs(got - want)) < FP32_TOL, (partition, explicit)
+            assert np.max(np.abs(got - dense)) < FP32_TOL, (partition, explicit)
+
+
 def test_poisoned_slots_and_padding_are_never_read(device) -> None:
     say("poison")
     rng = np.random.default_rng(9)

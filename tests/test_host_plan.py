@@ -165,3 +165,61 @@ def test_every_public_name_of_ops_exists_and_the_workspace_helper_answers() -> N
     assert not missing
     assert ops.attention_workspace_bytes(64, 32, 128, 4096, 512) == 64 * 32 * 8 * 130 * 4
     assert ops.attention_workspace_bytes(64, 32, 128, 512, 512) == 0
+
+
+# --- whole prefill tiles and the merge list ------------------------------------------------------
+
+
+def _mixed(rng, heads):
+    """The mixed workload's shape: 8 chunks of 512 rows at offsets U[0, 2048], then 120 decode
+    rows with contexts U[256, 4096]."""
+    offsets = rng.integers(0, 2049, 8)
+    decode = rng.integers(256, 4097, 120)
+    contexts = np.concatenate([offsets + 512, decode])
+    positions = np.concatenate([np.arange(o, o + 512) for o in offsets] + [decode - 1])
+    seq = np.concatenate([np.full(512, i) for i in range(8)] + [np.arange(8, 128)])
+    return seq, positions, contexts, _tables(contexts, 16, rng)
+
+
+def test_prefill_tiles_become_whole_when_they_fill_the_gpu() -> None:
+    rng = np.random.default_rng(7)
+    seq, positions, contexts, tables = _mixed(rng, 32)
+    plan = ops.plan_batch(seq, 128, 32, tables, contexts, 16, query_positions=positions)
+    assert plan.tiles.shape == (64, 4) and 64 * 32 >= ops.WHOLE_TILE_GROUPS
+    assert np.all(plan.tiles[:, 2] == 0) and np.all(plan.tiles[:, 3] == ops.TILE_WHOLE)
+    # longest tile first: a tile's longest row is its last one (consecutive positions)
+    longest = [int(positions[f + c - 1]) + 1 for f, c in plan.tiles[:, :2].tolist()]
+    assert longest == sorted(longest, reverse=True)
+    _covered(plan, seq, contexts, 16)
+    # only decode rows are merged, and only those spanning more than one partition
+    visible = np.minimum(contexts[seq], positions + 1)
+    want = [t for t in range(4096, 4216) if visible[t] > plan.partition_size]
+    assert plan.merge.tolist() == want
+    # with 8 heads the 64 tiles would leave the GPU half empty: they stay split by partition
+    plan8 = ops.plan_batch(seq, 128, 8, tables, contexts, 16, query_positions=positions)
+    assert np.all(plan8.tiles[:, 3] == 0)
+    assert set(range(4096)) <= set(plan8.merge.tolist()) | {
+        t for t in range(4096) if visible[t] <= plan8.partition_size
+    }
+
+
+def test_merge_list_without_positions_is_every_row_outside_whole_tiles() -> None:
+    tiles = np.array([[0, 64, 0, ops.TILE_WHOLE], [64, 10, 0, 0], [80, 3, 0, ops.TILE_WHOLE]])
+    assert ops.merge_rows_for(90, tiles).tolist() == [*range(64, 80), *range(83, 90)]
+    visible = np.arange(90) * 10
+    assert ops.merge_rows_for(90, tiles, visible, 700).tolist() == [*range(71, 80), *range(83, 90)]
+    assert ops.merge_rows_for(0, np.zeros((0, 4), np.int32)).tolist() == []
+
+
+def test_upload_derives_a_merge_list_for_whole_tiles() -> None:
+    import torch
+
+    rows = np.array([[5, 0], [6, 0]], np.int32)
+    tiles = np.array([[0, 5, 0, ops.TILE_WHOLE]], np.int32)
+    plan = ops.upload_plan(rows, tiles, torch.device("cpu"))
+    assert plan.merge.tolist() == [5, 6]
+    plan = ops.upload_plan(rows, np.array([[0, 5, 0, 0]], np.int32), torch.device("cpu"))
+    assert plan.merge is None, "without whole tiles every row may be merged"
+    plan = ops.upload_plan(rows, tiles, torch.device("cpu"), merge=np.array([6]))
+    assert plan.rows.tolist() == rows.tolist() and plan.tiles.tolist() == tiles.tolist()
+    assert plan.merge.tolist() == [6]

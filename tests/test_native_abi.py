@@ -81,14 +81,19 @@ def test_bad_arguments_are_refused_before_any_device_work(lib) -> None:
     assert lib.pkv_copy_blocks(null, null, 9, null, 1, 1, 4, 16, 0, null) == -1
     assert lib.pkv_copy_blocks(null, null, 0, null, 0, 1, 4, 16, 0, null) == 0
     # partition size not a multiple of 16
-    args = [null, null, 8, null, null, 1, null, 0, null, 0, null, null, 0, 4, 4, null, 1, null,
-            1, 1, 8, ctypes.c_float(0.5), 8, 17, 0, null, 0, 0, null]  # fmt: skip
+    args = [null, null, 8, null, null, 1, null, 0, null, 0, null, -1, null, null, 0, 4, 4, null, 1,
+            null, 1, 1, 8, ctypes.c_float(0.5), 8, 17, 0, null, 0, 0, null]  # fmt: skip
     assert lib.pkv_paged_attention(*args) == -1
-    args[23] = 16
-    args[24] = 2
+    args[25] = 16
+    args[26] = 2
     assert lib.pkv_paged_attention(*args) == -1  # unknown flag
-    args[24] = 1
+    args[26] = 1
     assert lib.pkv_paged_attention(*args) == -1  # null pointers
+    args[26] = 0
+    args[11] = -2
+    assert lib.pkv_paged_attention(*args) == -1  # a merge count below -1
+    args[11] = 3
+    assert lib.pkv_paged_attention(*args) == -1  # merge rows counted but not given
     assert lib.pkv_tile_head_dim_supported(128) == 1
     assert lib.pkv_tile_head_dim_supported(16) == 0
 
