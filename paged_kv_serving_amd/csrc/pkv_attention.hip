@@ -61,6 +61,10 @@ namespace {
 #ifndef PKV_ATTN_ROWS_FIRST
 #define PKV_ATTN_ROWS_FIRST 0
 #endif
+// Tile-pass workgroups per CU while the row pass runs beside it (0: one workgroup per item).
+#ifndef PKV_ATTN_TILE_GROUPS_PER_CU
+#define PKV_ATTN_TILE_GROUPS_PER_CU 1
+#endif
 // Workgroup order of the row pass: 0 = the hardware's round robin over the 8 XCDs (consecutive
 // workgroups, i.e. neighbouring heads of one token, on different XCDs); 1 = each XCD walks one
 // contiguous eighth of the grid. Measured on MI355X (64 x 4k decode): 0 reads at 6.79 TB/s,
@@ -107,6 +111,7 @@ struct Params {
                            // kTileWhole: one workgroup covers every key and writes final rows)
   const int32_t* merge_rows;  // reduce: the query rows whose partials are merged
   int64_t num_merge;       // entries of merge_rows; negative: every query row instead
+  int64_t num_tiles;       // entries of tiles
   const void* kcache;      // [N, B, H, D]
   const void* vcache;
   int64_t num_queries;
@@ -505,8 +510,13 @@ struct TileShape {
   static constexpr int kNb = D / 16;
 };
 
+// One work item of the tile pass: item `bid` = (partition, tile, head), heads fastest, partitions
+// slowest (a whole tile's work is all in partition 0, so those items come first). Every
+// thread of the workgroup calls it with the same item; it returns early (uniformly) for items
+// outside the tile's partitions.
 template <typename KVT, int D, bool kPow2Block>
-__global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params a) {
+__device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_table, float* s_k,
+                                          float* s_v, int* s_vis) {
   static_assert(D % 16 == 0 && D >= 32, "the MFMA tile needs whole 16-wide output tiles");
   using S = TileShape<D>;
   constexpr int kKeys = S::kKeys;
@@ -517,16 +527,11 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
   constexpr int kEsize = KVTraits<KVT>::kEsize;
   constexpr int kEpv = 16 / kEsize;  // elements per 16-byte vector
   constexpr int kVecPerRow = D / kEpv;
-  __shared__ int s_table[kTableSlots];
-  __shared__ float s_k[kKeys * kRow];
-  __shared__ float s_v[kKeys * kRow];
-  __shared__ int s_vis[kTileRows];
 
-  const uint32_t bid = blockIdx.x;
   const int h = static_cast<int>(bid % static_cast<uint32_t>(a.num_heads));
   const uint32_t rest = bid / static_cast<uint32_t>(a.num_heads);
-  const int p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
-  const int64_t tile = rest / static_cast<uint32_t>(a.max_parts);
+  const int64_t tile = rest % static_cast<uint32_t>(a.num_tiles);
+  const int p = static_cast<int>(rest / static_cast<uint32_t>(a.num_tiles));
   const int32_t* entry = a.tiles + 4 * tile;
   const int64_t t0 = entry[0];
   if (t0 < 0 || t0 >= a.num_queries) return;  // a tile outside the batch is skipped
@@ -743,6 +748,23 @@ __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params
   }
 }
 
+// The tile pass: workgroup w computes items w, w + gridDim.x, ... of the num_items (tile,
+// partition, head) items. With one item per workgroup the grid is the item count; beside the
+// row pass the host launches one workgroup per CU instead, so the tile pass holds one wave per
+// SIMD and leaves the rest of each CU to the memory-bound row pass.
+template <typename KVT, int D, bool kPow2Block>
+__global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params a, uint32_t num_items) {
+  using S = TileShape<D>;
+  __shared__ int s_table[kTableSlots];
+  __shared__ float s_k[S::kKeys * S::kRow];
+  __shared__ float s_v[S::kKeys * S::kRow];
+  __shared__ int s_vis[kTileRows];
+  for (uint32_t item = blockIdx.x; item < num_items; item += gridDim.x) {
+    __syncthreads();  // the previous item's reads of LDS are done
+    tile_item<KVT, D, kPow2Block>(a, item, s_table, s_k, s_v, s_vis);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Pass 3: reduce. Item i = (entry i / H of the merge list, or query row i / H without one; head
 // i % H). D / 4 threads per item, four output dimensions each, so a workgroup of kReduceThreads
@@ -807,6 +829,7 @@ struct Overlap {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr;
   hipEvent_t join = nullptr;
+  int64_t tile_groups = 0;  // tile-pass workgroups beside the row pass (0: one per item)
   bool failed = false;
 };
 
@@ -820,27 +843,32 @@ Overlap* overlap_locked(int device) {
   Overlap& o = g_overlap[device];
   if (o.failed) return nullptr;
   if (o.stream == nullptr) {
+    int cus = 0;
     if (hipStreamCreateWithFlags(&o.stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&o.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&o.join, hipEventDisableTiming) != hipSuccess) {
+        hipEventCreateWithFlags(&o.join, hipEventDisableTiming) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
       o.failed = true;
       (void)hipGetLastError();
       return nullptr;
     }
+    o.tile_groups = static_cast<int64_t>(cus) * PKV_ATTN_TILE_GROUPS_PER_CU;
   }
   return &o;
 }
 
 template <typename KVT, int D>
-int launch_tiles(const Params& a, int64_t num_tiles, hipStream_t stream) {
+int launch_tiles(const Params& a, int64_t num_tiles, int64_t max_groups, hipStream_t stream) {
   if constexpr (D % 16 == 0 && D >= 32) {
-    const int64_t groups = num_tiles * static_cast<int64_t>(a.max_parts) * a.num_heads;
-    if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
+    const int64_t items = num_tiles * static_cast<int64_t>(a.max_parts) * a.num_heads;
+    if (items > 0x7fffffff) return PKV_EUNSUPPORTED;
+    const int64_t groups = max_groups > 0 && max_groups < items ? max_groups : items;
     const dim3 grid(static_cast<uint32_t>(groups));
+    const auto n = static_cast<uint32_t>(items);
     if ((a.block_size & (a.block_size - 1)) == 0) {
-      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true>), grid, dim3(kTileThreads), 0, stream, a);
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true>), grid, dim3(kTileThreads), 0, stream, a, n);
     } else {
-      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false>), grid, dim3(kTileThreads), 0, stream, a);
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false>), grid, dim3(kTileThreads), 0, stream, a, n);
     }
     return check_launch();
   } else {
@@ -894,11 +922,11 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     if (overlap != nullptr) {
       // fork: the tile pass starts when the caller's stream reaches the fork point
       if (hipStreamWaitEvent(overlap->stream, overlap->fork, 0) != hipSuccess) return PKV_EHIP;
-      const int rc = launch_tiles<KVT, D>(a, num_tiles, overlap->stream);
+      const int rc = launch_tiles<KVT, D>(a, num_tiles, overlap->tile_groups, overlap->stream);
       if (rc != PKV_OK) return rc;
       if (hipEventRecord(overlap->join, overlap->stream) != hipSuccess) return PKV_EHIP;
     } else {
-      const int rc = launch_tiles<KVT, D>(a, num_tiles, stream);
+      const int rc = launch_tiles<KVT, D>(a, num_tiles, 0, stream);
       if (rc != PKV_OK) return rc;
     }
   }
@@ -1056,6 +1084,7 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   a.tiles = tiles;
   a.merge_rows = merge_rows;
   a.num_merge = num_merge_rows;
+  a.num_tiles = tiles ? num_tiles : 0;
   a.kcache = key_cache;
   a.vcache = value_cache;
   a.num_queries = num_queries;
