@@ -161,10 +161,11 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *   query_positions  : int32 [num_queries], absolute position of each query (the causal mask:
  *                      key position > query position is masked, attention.py:102-104).
  *   query_seq        : int32 [num_queries], index of the sequence each query belongs to.
- *   rows, num_rows   : the plan's row list, int32 [num_rows, 2] = (query row, first partition):
- *                      query rows computed by the row-streaming pass (one workgroup per row,
- *                      head and partition; the right pass for decode rows), from their first
- *                      partition on.
+ *   rows, num_rows   : the plan's row-pass work items, int32 [num_rows, 2] = (query row,
+ *                      partition): one workgroup per item and group of heads computes that
+ *                      partition of that row with the row-streaming pass (the right pass for
+ *                      decode rows). Items past a row's last partition are skipped, so listing
+ *                      partitions up to an upper bound of the row's visible length is safe.
  *   tiles, num_tiles : the plan's tile list, int32 [num_tiles, 4] = (first row, row count <= 64,
  *                      first partition, end partition; end <= first means through the last):
  *                      runs of consecutive rows computed by the fp32 MFMA tile pass over those
@@ -178,7 +179,8 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *                      their final outputs (the first partition is then ignored; such rows must
  *                      not be in the merge list). Needs pkv_tile_head_dim_supported(head_dim).
  *                      Every (query row, partition) must be covered exactly once. With rows and
- *                      tiles both NULL, every row goes through the row-streaming pass.
+ *                      tiles both NULL, every partition of every row goes through the
+ *                      row-streaming pass.
  *   merge_rows,
  *   num_merge_rows   : int32 [num_merge_rows], the query rows whose per-partition results the
  *                      reduce pass merges: every row whose visible context spans more than one

@@ -105,7 +105,8 @@ struct Params {
   int64_t q_stride;
   const int32_t* q_pos;    // [T]
   const int32_t* q_seq;    // [T]
-  const int32_t* rows;     // row_partial: [R, 2] = (query row, first partition); null: identity
+  const int32_t* rows;     // row_partial: [R, 2] = (query row, partition) items; null: every
+                           // partition of every query row
   const int32_t* tiles;    // tile_partial: [n, 4] = (first row, row count <= 64, first
                            // partition, end partition; end <= first: through the last;
                            // kTileWhole: one workgroup covers every key and writes final rows)
@@ -277,13 +278,18 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   const uint32_t head_groups = static_cast<uint32_t>(a.num_heads / HPW);
   const int h = static_cast<int>(bid % head_groups) * HPW;  // first head of the group
   const uint32_t rest = bid / head_groups;
-  const int p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
-  const int64_t r = rest / static_cast<uint32_t>(a.max_parts);
-  const int64_t t = a.rows ? a.rows[2 * r] : r;
-  if (t < 0 || t >= a.num_queries) return;  // a row outside the batch is skipped
-  // Partitions before the row's first one are computed by a tile (a prefix shared with the
-  // other rows of the tile).
-  if (a.rows && p < a.rows[2 * r + 1]) return;
+  // With a plan, work item `rest` names its (query row, partition); without one, every
+  // partition of every row.
+  int64_t t;
+  int p;
+  if (a.rows) {
+    t = a.rows[2 * static_cast<int64_t>(rest)];
+    p = a.rows[2 * static_cast<int64_t>(rest) + 1];
+  } else {
+    t = rest / static_cast<uint32_t>(a.max_parts);
+    p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
+  }
+  if (t < 0 || t >= a.num_queries || p < 0) return;  // an item outside the batch is skipped
 
   const int seq = a.q_seq[t];
   const int kv_len = row_visible(a, t);
@@ -889,7 +895,8 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
   }
   auto launch_rows_hpw = [&](auto hpw_tag) -> int {
     constexpr int HPW = decltype(hpw_tag)::value;
-    const int64_t groups = num_rows * static_cast<int64_t>(a.max_parts) * (a.num_heads / HPW);
+    const int64_t items = a.rows ? num_rows : num_rows * static_cast<int64_t>(a.max_parts);
+    const int64_t groups = items * (a.num_heads / HPW);
     if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
     const dim3 grid(static_cast<uint32_t>(groups));
     if (pow2 && stream_kv) {

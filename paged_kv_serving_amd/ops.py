@@ -22,6 +22,7 @@ __all__ = [
     "append_kv",
     "attention_workspace_bytes",
     "copy_blocks",
+    "expand_rows",
     "greedy_tokens",
     "independent_groups",
     "kv_dtype_code",
@@ -265,7 +266,8 @@ class AttentionPlan:
     """Which (query row, partition) goes to which attention pass, as int32 device tensors, plus
     the launch hints.
 
-    ``rows``: ``[R, 2]`` = (query row, first partition) for the row-streaming pass. ``tiles``:
+    ``rows``: ``[R, 2]`` = (query row, partition) work items of the row-streaming pass
+    (:func:`expand_rows` makes them from each row's first partition). ``tiles``:
     ``[n, 4]`` = (first row, row count, first partition, end partition; end <= first: through
     the last; ``TILE_WHOLE``: one workgroup per head over every visible key) for the MFMA tile
     pass: a run of consecutive rows of one sequence, or decode rows of several sequences over
@@ -504,6 +506,29 @@ def _whole_tiles(tiles: np.ndarray, seq: np.ndarray, visible: np.ndarray, num_he
     return whole
 
 
+def expand_rows(rows: np.ndarray, visible: np.ndarray, partition_size: int) -> np.ndarray:
+    """Row-pass work items ``[W, 2]`` = (query row, partition) from ``rows [R, 2]`` = (query
+    row, first partition): partitions first .. ceil(visible / partition_size) - 1 of each row
+    (at least its first). Full partitions come first in row order, then every row's shorter last
+    partition, longest first, so the grid ends on its shortest workgroups. ``partition_size`` 0
+    is the library default (512). ``visible`` may overstate a row (the kernel skips partitions
+    past the row's visible length), never understate it."""
+    rows = np.asarray(rows, dtype=np.int64).reshape(-1, 2)
+    if rows.shape[0] == 0:
+        return np.zeros((0, 2), np.int32)
+    part = partition_size or 512
+    vis = np.asarray(visible, dtype=np.int64)[rows[:, 0]]
+    nparts = np.maximum(1, -(-vis // part))
+    first = rows[:, 1]
+    count = np.maximum(nparts - first, 0)  # a row whose keys all lie in a prefix tile has none
+    row_of = np.repeat(rows[:, 0], count)
+    offsets = np.arange(count.sum()) - np.repeat(np.cumsum(count) - count, count)
+    p_of = np.repeat(first, count) + offsets
+    keys = np.minimum(part, np.repeat(vis, count) - p_of * part)  # keys in each item
+    order = np.lexsort((np.arange(keys.size), -keys))  # longest first, stable
+    return np.stack([row_of[order], p_of[order]], axis=1).astype(np.int32)
+
+
 def merge_rows_for(
     num_queries: int, tiles: np.ndarray, visible: np.ndarray | None = None, partition_size: int = 0
 ) -> np.ndarray:
@@ -578,7 +603,8 @@ def plan_batch(
         parts.append(np.asarray(tables[s][f : used_blocks[s]]))
     ids = np.concatenate(parts) if parts else np.zeros(0, np.int64)
     merge = merge_rows_for(seq.size, tiles, visible, int(partition))
-    return BatchPlan(rows, tiles, int(partition), _repeated_fraction_reached(ids), merge)
+    items = expand_rows(rows, visible, int(partition))
+    return BatchPlan(items, tiles, int(partition), _repeated_fraction_reached(ids), merge)
 
 
 def upload_plan(
@@ -709,8 +735,6 @@ def paged_attention_ragged(
             raise ValueError("plan.rows must be contiguous int32 of shape (R, 2)")
         if plan.tiles.dim() != 2 or plan.tiles.shape[1] != 4 or not plan.tiles.is_contiguous():
             raise ValueError("plan.tiles must be contiguous int32 of shape (n, 4)")
-        if plan.num_rows + 0 > num_queries:
-            raise ValueError("plan.rows lists more rows than the batch has")
         num_rows, num_tiles = plan.num_rows, plan.num_tiles
         rows_ptr = plan.rows.data_ptr() if num_rows else None
         tiles_ptr = plan.tiles.data_ptr() if num_tiles else None

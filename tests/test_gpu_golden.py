@@ -33,7 +33,9 @@ def test_attention_meets_the_golden_closed_form(device, tiles) -> None:
         to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
         plan = None
         if tiles:
-            plan = ops.upload_plan(*ops.plan_rows(case["seq"], case["queries"].shape[2], min_tile_rows=2), device)
+            rows, tiles_ = ops.plan_rows(case["seq"], case["queries"].shape[2], min_tile_rows=2)
+            visible = np.minimum(case["contexts"][case["seq"]], case["positions"] + 1)
+            plan = ops.upload_plan(ops.expand_rows(rows, visible, 0), tiles_, device)
         out = ops.paged_attention_ragged(
             to(case["queries"]), to(case["positions"]), to(case["seq"]), to(case["keys"]),
             to(case["values"]), to(case["tables"]), to(case["contexts"]), float(case["scale"]),

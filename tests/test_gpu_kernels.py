@@ -194,7 +194,9 @@ def _run_kernel(device, kc, vc, tables, contexts, positions, seq_of, q, scale, *
     dv = torch.from_numpy(vc).to(device).to(dtype)
     plan = None
     if tiles:  # runs of >= 2 rows of one sequence go to the MFMA tile pass
-        plan = ops.upload_plan(*ops.plan_rows(seq_of, q.shape[2], min_tile_rows=2), device)
+        rows, tile_list = ops.plan_rows(seq_of, q.shape[2], min_tile_rows=2)
+        visible = np.minimum(np.asarray(contexts)[seq_of], positions + 1)
+        plan = ops.upload_plan(ops.expand_rows(rows, visible, partition), tile_list, device)
     out = ops.paged_attention_ragged(
         torch.from_numpy(q).to(device),
         torch.from_numpy(positions.astype(np.int32)).to(device),
@@ -289,7 +291,10 @@ def test_shared_prefix_tiles_match_the_oracle(device, kv) -> None:
     seq_of = np.arange(40)
     q = rng.standard_normal((40, heads, dim)).astype(np.float32)
     plan = ops.plan_batch(seq_of, dim, heads, tables, contexts, block)
-    assert plan.tiles.shape[0] >= 2 and np.count_nonzero(plan.rows[:, 1]) == 40
+    # every row-pass item lies after the prefix partitions the tiles cover (a row whose context
+    # ends inside the prefix has no row-pass item at all)
+    assert plan.tiles.shape[0] >= 2 and np.all(plan.rows[:, 1] > 0)
+    assert len(set(plan.rows[:, 0].tolist())) >= 36
     want, dense = _oracle(kc, vc, tables, contexts, positions, seq_of, q, 0.09)
     width = max(len(t) for t in tables)
     padded = np.full((40, width), -7, dtype=np.int32)
@@ -371,11 +376,12 @@ def _whole_tile_plan(seq_of, positions, contexts, dim, partition, device, *, exp
     """Every run of >= 2 rows of one sequence as whole tiles; the rest in the row pass."""
     rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)
     tiles[:, 3] = ops.TILE_WHOLE
+    visible = np.minimum(contexts[seq_of], positions + 1)
     merge = None
     if explicit_merge:
-        visible = np.minimum(contexts[seq_of], positions + 1)
         merge = ops.merge_rows_for(seq_of.size, tiles, visible, partition or 512)
-    return ops.upload_plan(rows, tiles, device, partition_size=partition, merge=merge)
+    items = ops.expand_rows(rows, visible, partition)
+    return ops.upload_plan(items, tiles, device, partition_size=partition, merge=merge)
 
 
 @pytest.mark.parametrize("dim", [32, 64, 128, 256])
@@ -541,7 +547,8 @@ def test_config3_mixed_prefill_and_decode_matches_the_oracle(device) -> None:
 
     say("config 3: build")
     batch = mixed_batch(seed=0, device=device)
-    assert batch.plan.num_tiles == 64 and batch.plan.num_rows == 120
+    assert batch.plan.num_tiles == 64
+    assert set(batch.plan.rows[:, 0].tolist()) == set(range(4096, 4216)), "decode rows: row pass"
     say("config 3: run")
     out = _run_batch(batch)
     torch.cuda.synchronize()

@@ -98,10 +98,8 @@ def _covered(plan, seq, contexts, block_size):
             for p in range(pb, pe if pe > pb else parts):
                 if p < parts:
                     seen[(t, p)] = seen.get((t, p), 0) + 1
-    for t, f in plan.rows.tolist():
-        parts = max(1, -(-int(contexts[seq[t]]) // P))
-        for p in range(f, parts):
-            seen[(t, p)] = seen.get((t, p), 0) + 1
+    for t, p in plan.rows.tolist():  # row-pass work items
+        seen[(t, p)] = seen.get((t, p), 0) + 1
     want = {(t, p) for t in range(seq.size) for p in range(max(1, -(-int(contexts[seq[t]]) // P)))}
     assert set(seen) == want and all(v == 1 for v in seen.values())
 
@@ -116,7 +114,7 @@ def test_a_shared_prefix_becomes_tiles_over_whole_partitions() -> None:
     plan = ops.plan_batch(seq, 128, 32, tables, contexts, 16)
     assert plan.partition_size == 336
     assert plan.tiles.tolist() == [[64 * i, 64, 0, 3] for i in range(4)]
-    assert np.all(plan.rows[:, 1] == 3)
+    assert plan.rows.shape == (256, 2) and np.all(plan.rows[:, 1] == 3), "one suffix item per row"
     assert not plan.shared_kv, "what the row pass still reads is private"
     _covered(plan, seq, contexts, 16)
 
@@ -135,7 +133,8 @@ def test_prefix_groups_split_where_tables_diverge_and_skip_small_groups() -> Non
     assert {f for f, _, _, _ in groups} == {0, 50}
     assert all(pe * P <= 100 * 16 for f, _, _, pe in groups if f == 0)
     assert all(pe * P <= 40 * 16 for f, _, _, pe in groups if f == 50)
-    assert np.all(plan.rows[40:50, 1] == 0), "the small group stays in the row pass"
+    starts = {t for t, p in plan.rows.tolist() if p == 0}
+    assert set(range(40, 50)) <= starts, "the small group stays in the row pass"
     _covered(plan, seq, contexts, 16)
 
 
@@ -156,8 +155,9 @@ def test_no_sharing_keeps_the_plain_plan() -> None:
     contexts = rng.integers(512, 4097, 64)
     tables = _tables(contexts, 16, rng)
     plan = ops.plan_batch(np.arange(64), 128, 32, tables, contexts, 16)
-    assert plan.tiles.shape == (0, 4) and np.all(plan.rows[:, 1] == 0)
+    assert plan.tiles.shape == (0, 4)
     assert (plan.partition_size, plan.shared_kv) == ops.batch_hints(tables, contexts, 32, 16)
+    _covered(plan, np.arange(64), contexts, 16)
 
 
 def test_every_public_name_of_ops_exists_and_the_workspace_helper_answers() -> None:
@@ -228,3 +228,15 @@ def test_upload_derives_a_merge_list_for_whole_tiles() -> None:
     plan = ops.upload_plan(rows, tiles, torch.device("cpu"), merge=np.array([6]))
     assert plan.rows.tolist() == rows.tolist() and plan.tiles.tolist() == tiles.tolist()
     assert plan.merge.tolist() == [6]
+
+
+def test_row_items_list_each_partition_full_ones_first() -> None:
+    rows = np.array([[0, 0], [1, 0], [2, 2], [3, 0]], np.int32)
+    visible = np.array([1030, 512, 3000, 0])
+    items = ops.expand_rows(rows, visible, 512)
+    # full partitions in row order, then the partial last ones, longest first
+    assert items.tolist() == [[0, 0], [0, 1], [1, 0], [2, 2], [2, 3], [2, 4], [2, 5], [0, 2], [3, 0]]
+    assert ops.expand_rows(rows, visible, 0).tolist() == items.tolist(), "0 is the 512 default"
+    # a row whose first partition is past its visible keys has nothing left for the row pass
+    assert ops.expand_rows(np.array([[5, 3]]), np.full(6, 1000), 512).tolist() == []
+    assert ops.expand_rows(np.zeros((0, 2), np.int32), visible, 512).shape == (0, 2)
