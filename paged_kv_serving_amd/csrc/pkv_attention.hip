@@ -792,12 +792,15 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(const Params a, 
   const int d = (static_cast<int>(threadIdx.x) % kTpi) * 4;
   const int64_t qh = t * a.num_heads + h;
   const float* ml = a.ws_ml + 2 * qh * a.max_parts;
+  // Unrolled so that several partitions' loads are in flight at once (a long context has tens).
   float big = -INFINITY;
+#pragma unroll 8
   for (int k = 0; k < nparts; ++k) big = fmaxf(big, ml[2 * k]);
   const float shift = big == -INFINITY ? 0.f : big;
   float lsum = 0.f;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   const float* part = a.ws_acc + qh * a.max_parts * D + d;
+#pragma unroll 8
   for (int k = 0; k < nparts; ++k) {
     const float w = fast_exp2(ml[2 * k] - shift);
     lsum = fmaf(ml[2 * k + 1], w, lsum);
