@@ -42,6 +42,9 @@ typedef enum pkv_dtype {
                                 prefix): load K/V rows through the caches instead of streaming
                                 them past, so the other readers hit L2 / the Infinity Cache */
 
+#define PKV_ATTN_SHORT_ROWS 2 /* the row pass's items are short (a few hundred keys): launch a
+                                lighter workgroup so more of them are in flight at once */
+
 /* pkv_paged_attention tile record: end partition of a tile computed whole by one workgroup. */
 #define PKV_TILE_WHOLE (-1)
 
@@ -198,7 +201,8 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *                      >= max_context_len (checked).
  *   partition_size   : keys per split-context partition, a positive multiple of 16, <= 1024;
  *                      0 selects the library default (512).
- *   flags            : 0 or PKV_ATTN_SHARED_KV.
+ *   flags            : PKV_ATTN_SHARED_KV and/or PKV_ATTN_SHORT_ROWS, or 0. Both only choose
+ *                      how the kernels run; the results agree within float32 rounding.
  *   workspace        : float32 scratch of pkv_attention_workspace_bytes(...) bytes (may be
  *                      NULL when that is 0); 16-byte aligned when num_tiles > 0.
  * A query whose every key is masked gets a zero output (attention.py:120-121).

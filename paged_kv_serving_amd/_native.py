@@ -63,6 +63,7 @@ HIPCC_FLAGS = (
 PKV_F32 = 0
 PKV_BF16 = 1
 PKV_ATTN_SHARED_KV = 1
+PKV_ATTN_SHORT_ROWS = 2
 PKV_TILE_WHOLE = -1
 
 PKV_OK = 0

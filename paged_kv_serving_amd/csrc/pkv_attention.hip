@@ -113,6 +113,7 @@ struct Params {
   const int32_t* merge_rows;  // reduce: the query rows whose partials are merged
   int64_t num_merge;       // entries of merge_rows; negative: every query row instead
   int64_t num_tiles;       // entries of tiles
+  int32_t flags;           // PKV_ATTN_* launch hints
   const void* kcache;      // [N, B, H, D]
   const void* vcache;
   int64_t num_queries;
@@ -154,7 +155,7 @@ __device__ __forceinline__ uint32_t logical_block() {
 // and best overall. Slices of at least 512 contiguous bytes per token row stream faster than
 // 256-byte ones from a shuffled pool (a load-only probe of the bfloat16 head_dim-128 pattern:
 // 6.65 TB/s at one head per workgroup, 6.97 TB/s at two), which is what HPW = 2 is for.
-template <typename KVT, int D, int HPW>
+template <typename KVT, int D, int HPW, int kIterBytes = PKV_ATTN_ITER_BYTES>
 struct Layout {
   static constexpr int kEsize = KVTraits<KVT>::kEsize;
   static constexpr int kHeadBytes = D * kEsize;
@@ -171,8 +172,7 @@ struct Layout {
   static constexpr int kDph = kVph * kEpv;  // dimensions per lane per head
   static constexpr int kDpl = kVpl * kEpv;
   static constexpr int kTpr = kWave / kLpt;
-  static constexpr int kIterWanted =
-      PKV_ATTN_ITER_BYTES / kSliceBytes < 64 ? PKV_ATTN_ITER_BYTES / kSliceBytes : 64;
+  static constexpr int kIterWanted = kIterBytes / kSliceBytes < 64 ? kIterBytes / kSliceBytes : 64;
   static constexpr int kRounds = kTpr >= kIterWanted ? 1 : kIterWanted / kTpr;
   static constexpr int kIterTok = kTpr * kRounds;
   static constexpr int kGroups = kWaves * kTpr;  // lane groups per workgroup
@@ -264,9 +264,14 @@ __device__ __forceinline__ void store_result(const Params& a, int64_t t, int h, 
 // ---------------------------------------------------------------------------------------------
 // Pass 1: row_partial.
 // ---------------------------------------------------------------------------------------------
-template <typename KVT, int D, int HPW, bool kPow2Block, bool kStream>
+// kLean: half the bytes in flight per wavefront (112 instead of 176 VGPRs at float32 head_dim
+// 128), so twice as many workgroups fit on a CU; chosen for batches whose row-pass items are
+// short, where the workgroups' set-up and latency, not their streaming, dominate (measured: the
+// 256-sequence prefix-sharing step's attention 0.242 -> 0.228 ms; long items are unchanged or
+// slower beside the tile pass).
+template <typename KVT, int D, int HPW, bool kPow2Block, bool kStream, bool kLean>
 __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
-  using L = Layout<KVT, D, HPW>;
+  using L = Layout<KVT, D, HPW, kLean ? PKV_ATTN_ITER_BYTES / 2 : PKV_ATTN_ITER_BYTES>;
   constexpr int kSlice = HPW * D;  // elements of the token-row slice this workgroup reads
   __shared__ int s_table[kTableSlots];
   __shared__ float s_m[L::kGroups * HPW];
@@ -889,6 +894,7 @@ template <typename KVT, int D>
 int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t num_tiles,
                bool stream_kv, int device, hipStream_t stream) {
   const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
+  const bool short_rows = (a.flags & PKV_ATTN_SHORT_ROWS) != 0;
   std::unique_lock<std::mutex> overlap_lock(g_overlap_mutex, std::defer_lock);
   Overlap* overlap = nullptr;
   if (PKV_ATTN_OVERLAP && num_tiles > 0 && num_rows > 0) {
@@ -902,14 +908,19 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     const int64_t groups = items * (a.num_heads / HPW);
     if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
     const dim3 grid(static_cast<uint32_t>(groups));
-    if (pow2 && stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true>), grid, dim3(kThreads), 0, stream, a);
+    // The lean variant exists for power-of-two block sizes only (the others ignore the hint).
+    if (pow2 && short_rows && stream_kv) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, true>), grid, dim3(kThreads), 0, stream, a);
+    } else if (pow2 && short_rows) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, true>), grid, dim3(kThreads), 0, stream, a);
+    } else if (pow2 && stream_kv) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, false>), grid, dim3(kThreads), 0, stream, a);
     } else if (pow2) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, false>), grid, dim3(kThreads), 0, stream, a);
     } else if (stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, true>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, true, false>), grid, dim3(kThreads), 0, stream, a);
     } else {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, false, false>), grid, dim3(kThreads), 0, stream, a);
     }
     return check_launch();
   };
@@ -1035,7 +1046,7 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   using namespace pkv;
   const int part = resolve_partition(partition_size);
   if (part < 0) return PKV_EINVAL;
-  if (flags & ~PKV_ATTN_SHARED_KV) return PKV_EINVAL;
+  if (flags & ~(PKV_ATTN_SHARED_KV | PKV_ATTN_SHORT_ROWS)) return PKV_EINVAL;
   const bool stream_kv = (flags & PKV_ATTN_SHARED_KV) == 0;
   if (num_queries < 0 || num_rows < 0 || num_tiles < 0 || num_merge_rows < -1 || num_blocks < 1 ||
       block_size < 1 ||
@@ -1095,6 +1106,7 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   a.merge_rows = merge_rows;
   a.num_merge = num_merge_rows;
   a.num_tiles = tiles ? num_tiles : 0;
+  a.flags = flags;
   a.kcache = key_cache;
   a.vcache = value_cache;
   a.num_queries = num_queries;

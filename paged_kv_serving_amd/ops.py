@@ -274,7 +274,8 @@ class AttentionPlan:
     the partitions of a prefix whose blocks they share. Every (row, partition) is covered
     exactly once. ``merge``: int32 ``[M]``, the rows whose partition results the reduce pass
     merges (None: every row, which is only correct without whole tiles). ``partition_size``
-    (0: library default) and ``shared_kv`` choose the launch.
+    (0: library default), ``shared_kv`` and ``short_rows`` (the lighter row-pass workgroup for
+    short items) choose the launch.
     """
 
     rows: torch.Tensor
@@ -282,6 +283,7 @@ class AttentionPlan:
     partition_size: int = 0
     shared_kv: bool = False
     merge: torch.Tensor | None = None
+    short_rows: bool = False
 
     @property
     def num_rows(self) -> int:
@@ -346,6 +348,9 @@ MIN_PREFIX_PARTITION = 256
 WHOLE_TILE_GROUPS = 1024
 #: Tile record end partition of a whole tile (include/pkv.h PKV_TILE_WHOLE).
 TILE_WHOLE = -1
+#: Row-pass items shorter than this many keys on average launch the lighter row-pass workgroup
+#: (PKV_ATTN_SHORT_ROWS): with half the bytes in flight per wavefront, twice as many fit on a CU.
+SHORT_ROW_KEYS = 256
 
 
 def _wide_partition(contexts: np.ndarray, num_heads: int, rows_per_seq: int) -> int:
@@ -401,6 +406,7 @@ class BatchPlan:
     partition_size: int
     shared_kv: bool
     merge: np.ndarray | None = None
+    short_rows: bool = False
 
 
 def _common_prefix(a: np.ndarray, b: np.ndarray) -> int:
@@ -604,12 +610,16 @@ def plan_batch(
     ids = np.concatenate(parts) if parts else np.zeros(0, np.int64)
     merge = merge_rows_for(seq.size, tiles, visible, int(partition))
     items = expand_rows(rows, visible, int(partition))
-    return BatchPlan(items, tiles, int(partition), _repeated_fraction_reached(ids), merge)
+    short = False
+    if items.shape[0]:
+        keys = np.minimum(partition, visible[items[:, 0]] - items[:, 1].astype(np.int64) * partition)
+        short = bool(np.mean(np.maximum(keys, 0)) < SHORT_ROW_KEYS)
+    return BatchPlan(items, tiles, int(partition), _repeated_fraction_reached(ids), merge, short)
 
 
 def upload_plan(
     rows: np.ndarray, tiles: np.ndarray, device: torch.device, *, partition_size: int = 0,
-    shared_kv: bool = False, merge: np.ndarray | None = None,
+    shared_kv: bool = False, merge: np.ndarray | None = None, short_rows: bool = False,
 ) -> AttentionPlan:
     """Copy a host plan (``rows [R, 2]``, ``tiles [n, 4]``, ``merge [M]``) to the device in one
     transfer. Without a merge list, one is derived when a tile is whole (every row no whole tile
@@ -627,13 +637,13 @@ def upload_plan(
     return AttentionPlan(
         rows=data[: rows.size].view(-1, 2), tiles=data[rows.size : end_tiles].view(-1, 4),
         partition_size=partition_size, shared_kv=shared_kv,
-        merge=None if merge is None else data[end_tiles:],
+        merge=None if merge is None else data[end_tiles:], short_rows=short_rows,
     )  # fmt: skip
 
 
 def upload_batch_plan(plan: BatchPlan, device: torch.device) -> AttentionPlan:
     return upload_plan(plan.rows, plan.tiles, device, partition_size=plan.partition_size,
-                       shared_kv=plan.shared_kv, merge=plan.merge)  # fmt: skip
+                       shared_kv=plan.shared_kv, merge=plan.merge, short_rows=plan.short_rows)  # fmt: skip
 
 
 def attention_workspace_bytes(
@@ -756,7 +766,8 @@ def paged_attention_ragged(
         key_cache.shape[0], key_cache.shape[1],
         block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(), num_seqs,
         heads, dim, float(scale), max_context_len, partition_size,
-        _native.PKV_ATTN_SHARED_KV if shared_kv else 0,
+        (_native.PKV_ATTN_SHARED_KV if shared_kv else 0)
+        | (_native.PKV_ATTN_SHORT_ROWS if plan is not None and plan.short_rows else 0),
         ws_ptr, ws_bytes, device, _stream(device),
     )  # fmt: skip
     _native.check(rc, "pkv_paged_attention")

@@ -357,6 +357,7 @@ class ModelRunner:
             partition_size=partition,
             shared_kv=host_plan.shared_kv,
             merge=meta32[end_tiles:],
+            short_rows=host_plan.short_rows,
         )
         max_context = int(context.max())
 

@@ -372,6 +372,43 @@ def test_row_pass_head_pairs_match_the_oracle(device, kv, dim, heads) -> None:
         assert np.max(np.abs(got - dense)) < FP32_TOL, partition
 
 
+@pytest.mark.parametrize("dim", [64, 128, 256])
+@pytest.mark.parametrize("kv", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("block", [16, 5])
+def test_short_row_workgroups_match_the_oracle(device, dim, kv, block) -> None:
+    """PKV_ATTN_SHORT_ROWS launches the lighter row-pass workgroup (half the keys in flight per
+    wavefront); it must give the same rows as the default one (block 5: the hint is ignored)."""
+    say("short rows", dim, kv, block)
+    rng = np.random.default_rng(dim + block)
+    kc, vc, tables, contexts, positions, seq_of, q = _ragged_case(
+        rng, heads=4, dim=dim, block=block, pool=700, seqs=7, max_ctx=500, prefill=True, max_rows=3
+    )
+    scale = dim**-0.5
+    if kv == torch.bfloat16:
+        kc, vc = bf16_round(kc), bf16_round(vc)
+    want, dense = _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale)
+    width = max(len(t) for t in tables)
+    padded = np.full((len(tables), width), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    visible = np.minimum(contexts[seq_of], positions + 1)
+    rows = np.stack([np.arange(seq_of.size), np.zeros(seq_of.size, np.int64)], axis=1)
+    for partition in (64, 0):
+        items = ops.expand_rows(rows, visible, partition)
+        for short in (False, True):
+            plan = ops.upload_plan(items, np.zeros((0, 4), np.int32), device, partition_size=partition,
+                                   short_rows=short)  # fmt: skip
+            got = ops.paged_attention_ragged(
+                torch.from_numpy(q).to(device), torch.from_numpy(positions.astype(np.int32)).to(device),
+                torch.from_numpy(seq_of.astype(np.int32)).to(device),
+                torch.from_numpy(kc).to(device).to(kv), torch.from_numpy(vc).to(device).to(kv),
+                torch.from_numpy(padded).to(device), torch.from_numpy(contexts.astype(np.int32)).to(device),
+                scale, max_context_len=int(contexts.max()), plan=plan,
+            ).cpu().numpy()  # fmt: skip
+            assert np.max(np.abs(got - want)) < FP32_TOL, (partition, short)
+            assert np.max(np.abs(got - dense)) < FP32_TOL, (partition, short)
+
+
 def _whole_tile_plan(seq_of, positions, contexts, dim, partition, device, *, explicit_merge):
     """Every run of >= 2 rows of one sequence as whole tiles; the rest in the row pass."""
     rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)

@@ -115,6 +115,7 @@ def test_a_shared_prefix_becomes_tiles_over_whole_partitions() -> None:
     assert plan.partition_size == 336
     assert plan.tiles.tolist() == [[64 * i, 64, 0, 3] for i in range(4)]
     assert plan.rows.shape == (256, 2) and np.all(plan.rows[:, 1] == 3), "one suffix item per row"
+    assert plan.short_rows, "suffixes of 32-256 keys: the lighter row-pass workgroup"
     assert not plan.shared_kv, "what the row pass still reads is private"
     _covered(plan, seq, contexts, 16)
 
@@ -157,6 +158,7 @@ def test_no_sharing_keeps_the_plain_plan() -> None:
     plan = ops.plan_batch(np.arange(64), 128, 32, tables, contexts, 16)
     assert plan.tiles.shape == (0, 4)
     assert (plan.partition_size, plan.shared_kv) == ops.batch_hints(tables, contexts, 32, 16)
+    assert not plan.short_rows, "512-key partitions of 512-4096-key contexts are long items"
     _covered(plan, np.arange(64), contexts, 16)
 
 
