@@ -223,6 +223,36 @@ int pkv_paged_attention(float* out, const float* queries, int64_t query_token_st
                         float* workspace, int64_t workspace_bytes, int device, void* stream);
 
 /*
+ * A decode step's append and attention in one pass: pkv_append of every query row's own new key
+ * and value row followed by pkv_paged_attention, with the append done by the row-streaming pass
+ * itself. The workgroups whose partition holds a row's position take that row's key and value
+ * from new_keys / new_values, use them for that position and write them to slot_mapping[t], so
+ * the pools end exactly as after pkv_append and the outputs are those of the two calls.
+ *
+ * Replaces src/paged_kv_serving/engine/runner.py:195-196 (the append) and :198-212 (the
+ * per-entry attention loop, attention.py:42-121) for a batch of decode rows.
+ *
+ * Arguments are pkv_paged_attention's (without tiles: every query row goes through the row pass)
+ * plus new_keys / new_values ([num_queries, num_heads, head_dim] of new_dtype with token strides
+ * new_key_token_stride / new_value_token_stride, 16-byte aligned rows; bfloat16 only into a
+ * bfloat16 pool) and slot_mapping (int64 [num_queries]), as for pkv_append. Row t's new token
+ * sits at query_positions[t]. Preconditions, which the caller checks: each sequence has exactly
+ * one query row in the call, that row's position is below its context_len and below
+ * max_context_len, and slot_mapping[t] is the slot the block table gives that position (as in
+ * runner.py:149-159). A slot outside the pool is not written, as in pkv_append.
+ */
+int pkv_paged_attention_append(
+    float* out, const float* queries, int64_t query_token_stride, const int32_t* query_positions,
+    const int32_t* query_seq, int64_t num_queries, const int32_t* rows, int64_t num_rows,
+    const int32_t* merge_rows, int64_t num_merge_rows, void* key_cache, void* value_cache,
+    pkv_dtype kv_dtype, int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
+    int32_t block_table_stride, const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,
+    int32_t head_dim, float scale, int32_t max_context_len, int32_t partition_size, int32_t flags,
+    float* workspace, int64_t workspace_bytes, const void* new_keys, const void* new_values,
+    pkv_dtype new_dtype, int64_t new_key_token_stride, int64_t new_value_token_stride,
+    const int64_t* slot_mapping, int device, void* stream);
+
+/*
  * Greedy sampling: the argmax of each logits row, on the device.
  *
  * Replaces src/paged_kv_serving/engine/sampling.py:28-30 (greedy_token: int(np.argmax(logits)))

@@ -77,6 +77,7 @@ EXPORTED_SYMBOLS = (
     "pkv_attention_workspace_bytes",
     "pkv_tile_head_dim_supported",
     "pkv_paged_attention",
+    "pkv_paged_attention_append",
     "pkv_greedy_tokens",
 )
 
@@ -201,6 +202,20 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_int, _ptr,  # device, stream
     ]
     lib.pkv_paged_attention.restype = _c_int
+    lib.pkv_paged_attention_append.argtypes = [
+        _ptr, _ptr, _i64,  # out, queries, query_token_stride
+        _ptr, _ptr, _i64,  # query_positions, query_seq, num_queries
+        _ptr, _i64,  # rows, num_rows
+        _ptr, _i64,  # merge_rows, num_merge_rows
+        _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size
+        _ptr, _i32, _ptr, _i32,  # block_tables, block_table_stride, context_lens, num_seqs
+        _i32, _i32, ctypes.c_float,  # num_heads, head_dim, scale
+        _i32, _i32, _i32,  # max_context_len, partition_size, flags
+        _ptr, _i64,  # workspace, workspace_bytes
+        _ptr, _ptr, _c_int, _i64, _i64, _ptr,  # new_keys, new_values, new_dtype, strides, slot_mapping
+        _c_int, _ptr,  # device, stream
+    ]
+    lib.pkv_paged_attention_append.restype = _c_int
     lib.pkv_greedy_tokens.argtypes = [
         _ptr, _ptr, _i64, _i64, _i64,  # token_ids, logits, row_stride, num_rows, vocab_size
         _c_int, _ptr,  # device, stream

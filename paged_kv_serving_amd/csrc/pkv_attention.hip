@@ -129,6 +129,16 @@ struct Params {
   int32_t max_parts;
   int32_t max_ctx;
   float scale_log2;        // scale * log2(e)
+  // The decode append fused into the row pass (new_keys null: none). Query row t's own key and
+  // value row (token t of new_keys / new_values) is written to pool slot new_slots[t] by the
+  // row-pass workgroups whose partition holds position q_pos[t], which also use it as that key.
+  const void* new_keys;    // [T, H, D] of new_dtype, token t at t * new_key_stride elements
+  const void* new_values;
+  int64_t new_key_stride;
+  int64_t new_value_stride;
+  const int64_t* new_slots;  // [T]
+  int64_t num_slots;       // pool token rows (num_blocks * block_size)
+  int32_t new_dtype;       // PKV_F32 or PKV_BF16 (bfloat16 only into a bfloat16 pool)
 };
 
 constexpr uint32_t kXcds = 8;  // MI355X: workgroup i runs on XCD i % 8
@@ -215,6 +225,22 @@ __device__ __forceinline__ uint4 load_row(const uint4* p) {
   }
 }
 
+// One 16-byte pool vector (16 / sizeof(KVT) elements) of a new key or value row, from element
+// `elem` of the append source, in the pool's element type: equal types copy bits, float32 into a
+// bfloat16 pool rounds to nearest even, exactly what pkv_append stores.
+__device__ __forceinline__ uint4 new_row_vector(const Params& a, const void* src, int64_t elem, float) {
+  return *reinterpret_cast<const uint4*>(static_cast<const float*>(src) + elem);
+}
+__device__ __forceinline__ uint4 new_row_vector(const Params& a, const void* src, int64_t elem, uint16_t) {
+  if (a.new_dtype == PKV_BF16) return *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + elem);
+  const float4 x = reinterpret_cast<const float4*>(static_cast<const float*>(src) + elem)[0];
+  const float4 y = reinterpret_cast<const float4*>(static_cast<const float*>(src) + elem)[1];
+  return make_uint4(f32_to_bf16_bits(x.x) | (f32_to_bf16_bits(x.y) << 16),
+                    f32_to_bf16_bits(x.z) | (f32_to_bf16_bits(x.w) << 16),
+                    f32_to_bf16_bits(y.x) | (f32_to_bf16_bits(y.y) << 16),
+                    f32_to_bf16_bits(y.z) | (f32_to_bf16_bits(y.w) << 16));
+}
+
 // Visible key count of a query: keys at positions 0 .. min(context_len, position + 1) - 1.
 __device__ __forceinline__ int visible_len(int ctx, int pos) {
   if (pos < 0) return 0;
@@ -269,7 +295,9 @@ __device__ __forceinline__ void store_result(const Params& a, int64_t t, int h, 
 // short, where the workgroups' set-up and latency, not their streaming, dominate (measured: the
 // 256-sequence prefix-sharing step's attention 0.242 -> 0.228 ms; long items are unchanged or
 // slower beside the tile pass).
-template <typename KVT, int D, int HPW, bool kPow2Block, bool kStream, bool kLean>
+// kAppend: the decode append fused into the pass (pkv_paged_attention_append); a separate
+// instantiation, so the plain pass keeps its register budget.
+template <typename KVT, int D, int HPW, bool kPow2Block, bool kStream, bool kLean, bool kAppend>
 __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   using L = Layout<KVT, D, HPW, kLean ? PKV_ATTN_ITER_BYTES / 2 : PKV_ATTN_ITER_BYTES>;
   constexpr int kSlice = HPW * D;  // elements of the token-row slice this workgroup reads
@@ -343,6 +371,11 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   const int64_t head_off = static_cast<int64_t>(h) * D;
   const int64_t row_stride = static_cast<int64_t>(a.num_heads) * D;  // elements per token row
   const int n_iter = (kend - kbeg + L::kIterTok - 1) / L::kIterTok;
+  // With the fused append, the key position of this row's own new token (else none), and where
+  // its head group's key and value rows start in the append source.
+  const int own_pos = kAppend ? a.q_pos[t] : -1;
+  const int64_t own_key = t * a.new_key_stride + head_off;
+  const int64_t own_value = t * a.new_value_stride + head_off;
 
   for (int it = wave; it < n_iter; it += kWaves) {
     const int base = kbeg + it * L::kIterTok;
@@ -362,7 +395,33 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
         row = (static_cast<int64_t>(blk) * a.block_size + off) * row_stride + head_off;
       }
       valid[rr] = ok;
-      if (ok) {
+      if (kAppend && kpos == own_pos && kpos < kend) {
+        // This row's own new token: its key and value come from the append source and are
+        // written to the token's slot here (the workgroup of each head group writes its slice).
+#pragma unroll
+        for (int i = 0; i < L::kVpl; ++i) {
+          const int64_t e = static_cast<int64_t>(i * L::kLpt + j) * L::kEpv;
+          kraw[rr][i] = new_row_vector(a, a.new_keys, own_key + e, KVT{});
+          vraw[rr][i] = new_row_vector(a, a.new_values, own_value + e, KVT{});
+        }
+        const int64_t slot = a.new_slots[t];
+        if (slot >= 0 && slot < a.num_slots) {
+          uint4* kd = reinterpret_cast<uint4*>(const_cast<KVT*>(kcache) + slot * row_stride + head_off);
+          uint4* vd = reinterpret_cast<uint4*>(const_cast<KVT*>(vcache) + slot * row_stride + head_off);
+#pragma unroll
+          for (int i = 0; i < L::kVpl; ++i) {
+            kd[i * L::kLpt + j] = kraw[rr][i];
+            vd[i * L::kLpt + j] = vraw[rr][i];
+          }
+        }
+        if (!ok) {  // a block id outside the pool masks the key, as it would after pkv_append
+#pragma unroll
+          for (int i = 0; i < L::kVpl; ++i) {
+            kraw[rr][i] = make_uint4(0, 0, 0, 0);
+            vraw[rr][i] = make_uint4(0, 0, 0, 0);
+          }
+        }
+      } else if (ok) {
         const uint4* kp = reinterpret_cast<const uint4*>(kcache + row);
         const uint4* vp = reinterpret_cast<const uint4*>(vcache + row);
 #pragma unroll
@@ -895,6 +954,7 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
                bool stream_kv, int device, hipStream_t stream) {
   const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
   const bool short_rows = (a.flags & PKV_ATTN_SHORT_ROWS) != 0;
+  const bool append = a.new_keys != nullptr;
   std::unique_lock<std::mutex> overlap_lock(g_overlap_mutex, std::defer_lock);
   Overlap* overlap = nullptr;
   if (PKV_ATTN_OVERLAP && num_tiles > 0 && num_rows > 0) {
@@ -908,19 +968,24 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     const int64_t groups = items * (a.num_heads / HPW);
     if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
     const dim3 grid(static_cast<uint32_t>(groups));
-    // The lean variant exists for power-of-two block sizes only (the others ignore the hint).
-    if (pow2 && short_rows && stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, true>), grid, dim3(kThreads), 0, stream, a);
+    // The lean and the appending variants exist for power-of-two block sizes only (the others
+    // ignore the hint; attention_call appends separately for them).
+    if (pow2 && append && stream_kv) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, false, true>), grid, dim3(kThreads), 0, stream, a);
+    } else if (pow2 && append) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, false, true>), grid, dim3(kThreads), 0, stream, a);
+    } else if (pow2 && short_rows && stream_kv) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, true, false>), grid, dim3(kThreads), 0, stream, a);
     } else if (pow2 && short_rows) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, true>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, true, false>), grid, dim3(kThreads), 0, stream, a);
     } else if (pow2 && stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, false, false>), grid, dim3(kThreads), 0, stream, a);
     } else if (pow2) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, false, false>), grid, dim3(kThreads), 0, stream, a);
     } else if (stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, true, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, true, false, false>), grid, dim3(kThreads), 0, stream, a);
     } else {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, false, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, false, false, false>), grid, dim3(kThreads), 0, stream, a);
     }
     return check_launch();
   };
@@ -1030,20 +1095,29 @@ extern "C" int pkv_tile_head_dim_supported(int32_t head_dim) {
   return head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
 }
 
-extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,
-                                   const int32_t* query_positions, const int32_t* query_seq,
-                                   int64_t num_queries, const int32_t* rows, int64_t num_rows,
-                                   const int32_t* tiles, int64_t num_tiles,
-                                   const int32_t* merge_rows, int64_t num_merge_rows,
-                                   const void* key_cache, const void* value_cache,
-                                   pkv_dtype kv_dtype, int64_t num_blocks,
-                                   int32_t block_size, const int32_t* block_tables,
-                                   int32_t block_table_stride, const int32_t* context_lens,
-                                   int32_t num_seqs, int32_t num_heads, int32_t head_dim,
-                                   float scale, int32_t max_context_len, int32_t partition_size,
-                                   int32_t flags, float* workspace, int64_t workspace_bytes,
-                                   int device, void* stream) {
-  using namespace pkv;
+namespace pkv {
+namespace {
+
+// The source of a decode append fused into the row pass (pkv_paged_attention_append).
+struct AppendSource {
+  const void* keys;
+  const void* values;
+  pkv_dtype dtype;
+  int64_t key_stride;
+  int64_t value_stride;
+  const int64_t* slots;
+};
+
+int attention_call(float* out, const float* queries, int64_t query_token_stride,
+                   const int32_t* query_positions, const int32_t* query_seq, int64_t num_queries,
+                   const int32_t* rows, int64_t num_rows, const int32_t* tiles, int64_t num_tiles,
+                   const int32_t* merge_rows, int64_t num_merge_rows, const void* key_cache,
+                   const void* value_cache, pkv_dtype kv_dtype, int64_t num_blocks,
+                   int32_t block_size, const int32_t* block_tables, int32_t block_table_stride,
+                   const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,
+                   int32_t head_dim, float scale, int32_t max_context_len, int32_t partition_size,
+                   int32_t flags, float* workspace, int64_t workspace_bytes, int device,
+                   void* stream, const AppendSource* append) {
   const int part = resolve_partition(partition_size);
   if (part < 0) return PKV_EINVAL;
   if (flags & ~(PKV_ATTN_SHARED_KV | PKV_ATTN_SHORT_ROWS)) return PKV_EINVAL;
@@ -1088,6 +1162,22 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   }
   // The tile pass writes four dimensions of a row at a time.
   if (num_tiles > 0 && (!aligned16(out) || (ws_acc && !aligned16(ws_acc)))) return PKV_EINVAL;
+  if (append != nullptr) {
+    // Only the row pass appends, so a fused append takes a plan without tiles; the source rows
+    // are read as 16-byte vectors.
+    const int src_size = dtype_size(append->dtype);
+    if (num_tiles > 0 || src_size == 0 || !append->keys || !append->values || !append->slots) {
+      return PKV_EINVAL;
+    }
+    if (append->dtype == PKV_BF16 && kv_dtype == PKV_F32) return PKV_EUNSUPPORTED;
+    const int64_t row = static_cast<int64_t>(num_heads) * head_dim;
+    if (append->key_stride < row || append->value_stride < row) return PKV_EINVAL;
+    if (!aligned16(append->keys) || !aligned16(append->values) ||
+        (append->key_stride * src_size) % 16 != 0 || (append->value_stride * src_size) % 16 != 0 ||
+        (static_cast<int64_t>(head_dim) * src_size) % 16 != 0) {
+      return PKV_EUNSUPPORTED;
+    }
+  }
   DeviceGuard guard(device);
   if (!guard.ok()) return PKV_EHIP;
   (void)hipGetLastError();
@@ -1122,9 +1212,71 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
   a.max_parts = static_cast<int32_t>(parts);
   a.max_ctx = max_context_len;
   a.scale_log2 = static_cast<float>(static_cast<double>(scale) * 1.4426950408889634);
+  if (append != nullptr && (block_size & (block_size - 1)) != 0) {
+    // No fused instantiation for this block size: the same two steps as separate launches.
+    const int rc = pkv_append(const_cast<void*>(key_cache), const_cast<void*>(value_cache), kv_dtype, num_blocks * block_size,
+                              append->keys, append->values, append->dtype, append->key_stride,
+                              append->value_stride, append->slots, num_queries, num_heads,
+                              head_dim, device, stream);
+    if (rc != PKV_OK) return rc;
+    append = nullptr;
+  }
+  if (append != nullptr) {
+    a.new_keys = append->keys;
+    a.new_values = append->values;
+    a.new_key_stride = append->key_stride;
+    a.new_value_stride = append->value_stride;
+    a.new_slots = append->slots;
+    a.num_slots = num_blocks * block_size;
+    a.new_dtype = append->dtype;
+  }
   auto s = static_cast<hipStream_t>(stream);
   if (kv_dtype == PKV_F32) {
     return dispatch_head_dim<float>(head_dim, a, num_queries, num_rows, num_tiles, stream_kv, device, s);
   }
   return dispatch_head_dim<uint16_t>(head_dim, a, num_queries, num_rows, num_tiles, stream_kv, device, s);
+}
+
+}  // namespace
+}  // namespace pkv
+
+extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,
+                                   const int32_t* query_positions, const int32_t* query_seq,
+                                   int64_t num_queries, const int32_t* rows, int64_t num_rows,
+                                   const int32_t* tiles, int64_t num_tiles,
+                                   const int32_t* merge_rows, int64_t num_merge_rows,
+                                   const void* key_cache, const void* value_cache,
+                                   pkv_dtype kv_dtype, int64_t num_blocks,
+                                   int32_t block_size, const int32_t* block_tables,
+                                   int32_t block_table_stride, const int32_t* context_lens,
+                                   int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+                                   float scale, int32_t max_context_len, int32_t partition_size,
+                                   int32_t flags, float* workspace, int64_t workspace_bytes,
+                                   int device, void* stream) {
+  return pkv::attention_call(out, queries, query_token_stride, query_positions, query_seq,
+                             num_queries, rows, num_rows, tiles, num_tiles, merge_rows,
+                             num_merge_rows, key_cache, value_cache, kv_dtype, num_blocks,
+                             block_size, block_tables, block_table_stride, context_lens, num_seqs,
+                             num_heads, head_dim, scale, max_context_len, partition_size, flags,
+                             workspace, workspace_bytes, device, stream, nullptr);
+}
+
+extern "C" int pkv_paged_attention_append(
+    float* out, const float* queries, int64_t query_token_stride, const int32_t* query_positions,
+    const int32_t* query_seq, int64_t num_queries, const int32_t* rows, int64_t num_rows,
+    const int32_t* merge_rows, int64_t num_merge_rows, void* key_cache, void* value_cache,
+    pkv_dtype kv_dtype, int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
+    int32_t block_table_stride, const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,
+    int32_t head_dim, float scale, int32_t max_context_len, int32_t partition_size, int32_t flags,
+    float* workspace, int64_t workspace_bytes, const void* new_keys, const void* new_values,
+    pkv_dtype new_dtype, int64_t new_key_token_stride, int64_t new_value_token_stride,
+    const int64_t* slot_mapping, int device, void* stream) {
+  const pkv::AppendSource append{new_keys, new_values, new_dtype, new_key_token_stride,
+                                 new_value_token_stride, slot_mapping};
+  return pkv::attention_call(out, queries, query_token_stride, query_positions, query_seq,
+                             num_queries, rows, num_rows, nullptr, 0, merge_rows, num_merge_rows,
+                             key_cache, value_cache, kv_dtype, num_blocks, block_size,
+                             block_tables, block_table_stride, context_lens, num_seqs, num_heads,
+                             head_dim, scale, max_context_len, partition_size, flags, workspace,
+                             workspace_bytes, device, stream, &append);
 }

@@ -674,8 +674,17 @@ def paged_attention_ragged(
     workspace: torch.Tensor | None = None,
     plan: AttentionPlan | None = None,
     shared_kv: bool | None = None,
+    append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
 ) -> torch.Tensor:
     """Causal paged attention of every query row of a ragged batch, in one call.
+
+    ``append=(new_keys, new_values, slot_mapping)`` fuses a decode step's append into the call
+    (``pkv_paged_attention_append``): row t's own key and value row (``[T, H, D]`` float32, or
+    bfloat16 for a bfloat16 pool; token-strided views allowed) is written to slot
+    ``slot_mapping[t]`` (int64) by the row pass itself, exactly as :func:`append_kv` followed by
+    this call would. Every row then goes through the row pass (a plan must have no tiles), and the
+    caller guarantees the decode shape: one query row per sequence, at a position below its
+    context length, with the slot its block table gives (reference runner.py:149-159).
 
     ``queries``: float32 ``[T, H, D]`` (token-strided views allowed); ``query_positions`` and
     ``query_seq``: int32 ``[T]``; ``key_cache``/``value_cache``: one layer's pools
@@ -748,6 +757,8 @@ def paged_attention_ragged(
         num_rows, num_tiles = plan.num_rows, plan.num_tiles
         rows_ptr = plan.rows.data_ptr() if num_rows else None
         tiles_ptr = plan.tiles.data_ptr() if num_tiles else None
+        if append is not None and (num_tiles or not num_rows):
+            raise ValueError("a fused append needs a plan whose rows all go through the row pass")
         if num_rows == 0 and num_tiles == 0:
             return out
         if plan.merge is not None:
@@ -758,6 +769,34 @@ def paged_attention_ragged(
                 raise ValueError("plan.merge must be contiguous")
             num_merge = int(merge.shape[0])
             merge_ptr = merge.data_ptr() if num_merge else None
+    flags = (_native.PKV_ATTN_SHARED_KV if shared_kv else 0) | (
+        _native.PKV_ATTN_SHORT_ROWS if plan is not None and plan.short_rows else 0
+    )
+    if append is not None:
+        new_keys, new_values, slot_mapping = append
+        if _device_index(new_keys, new_values, slot_mapping) != device:
+            raise ValueError("the appended rows must be on the queries' device")
+        if new_keys.shape != (num_queries, heads, dim) or new_values.shape != new_keys.shape:
+            raise ValueError("new keys and values must be [num_queries, heads, head_dim]")
+        if new_keys.dtype != new_values.dtype:
+            raise ValueError("new keys and values must have the same dtype")
+        if slot_mapping.dtype != torch.int64 or slot_mapping.shape != (num_queries,):
+            raise ValueError("slot_mapping must be int64 with one slot per query row")
+        rc = _native.library().pkv_paged_attention_append(
+            out.data_ptr(), queries.data_ptr(), stride,
+            query_positions.data_ptr(), query_seq.data_ptr(), num_queries,
+            rows_ptr, num_rows, merge_ptr, num_merge,
+            key_cache.data_ptr(), value_cache.data_ptr(), kv_dtype_code(key_cache.dtype),
+            key_cache.shape[0], key_cache.shape[1],
+            block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(), num_seqs,
+            heads, dim, float(scale), max_context_len, partition_size, flags,
+            ws_ptr, ws_bytes, new_keys.data_ptr(), new_values.data_ptr(),
+            kv_dtype_code(new_keys.dtype), _rows_contiguous(new_keys, "new keys"),
+            _rows_contiguous(new_values, "new values"), slot_mapping.data_ptr(),
+            device, _stream(device),
+        )  # fmt: skip
+        _native.check(rc, "pkv_paged_attention_append")
+        return out
     rc = _native.library().pkv_paged_attention(
         out.data_ptr(), queries.data_ptr(), stride,
         query_positions.data_ptr(), query_seq.data_ptr(), num_queries,
@@ -765,9 +804,7 @@ def paged_attention_ragged(
         key_cache.data_ptr(), value_cache.data_ptr(), kv_dtype_code(key_cache.dtype),
         key_cache.shape[0], key_cache.shape[1],
         block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(), num_seqs,
-        heads, dim, float(scale), max_context_len, partition_size,
-        (_native.PKV_ATTN_SHARED_KV if shared_kv else 0)
-        | (_native.PKV_ATTN_SHORT_ROWS if plan is not None and plan.short_rows else 0),
+        heads, dim, float(scale), max_context_len, partition_size, flags,
         ws_ptr, ws_bytes, device, _stream(device),
     )  # fmt: skip
     _native.check(rc, "pkv_paged_attention")

@@ -71,6 +71,14 @@ class AttentionBatch:
     def num_seqs(self) -> int:
         return int(self.context_lens.shape[0])
 
+    def decode_rows_only(self) -> bool:
+        """One query row per sequence, each at its sequence's last position: the decode shape
+        whose append can ride in the attention call (pkv_paged_attention_append)."""
+        seq = self.host_seq
+        if seq is None or np.unique(seq).size != seq.size:
+            return False
+        return bool(np.all(self.host_positions == self.host_context[seq] - 1))
+
     def context_bytes(self) -> int:
         """Algorithmic K+V bytes: each query row's visible keys and values, read once."""
         heads, dim = self.key_cache.shape[2], self.key_cache.shape[3]

@@ -409,6 +409,64 @@ def test_short_row_workgroups_match_the_oracle(device, dim, kv, block) -> None:
             assert np.max(np.abs(got - dense)) < FP32_TOL, (partition, short)
 
 
+@pytest.mark.parametrize("heads", [3, 4])
+@pytest.mark.parametrize("block", [16, 5])
+@pytest.mark.parametrize("kinds", ["f32<-f32", "bf16<-f32", "bf16<-bf16"])
+def test_fused_decode_append_equals_append_then_attention(device, kinds, block, heads) -> None:
+    """pkv_paged_attention_append: the row pass writes each decode row's new key and value to its
+    slot and uses them as that position's key; the pools end bit for bit as after pkv_append and
+    the rows match the oracle on the appended pools (block 5 has no fused instantiation: the call
+    runs the append kernel first)."""
+    say("fused append", kinds, block, heads)
+    pool_dtype = torch.float32 if kinds.startswith("f32") else torch.bfloat16
+    src_dtype = torch.float32 if kinds.endswith("f32") else torch.bfloat16
+    rng = np.random.default_rng(block * 10 + heads)
+    dim, seqs = 128, 9
+    pool = seqs * -(-700 // block) + 8
+    contexts = rng.integers(1, 700, seqs)
+    perm = rng.permutation(pool)
+    tables, offset = [], 0
+    for c in contexts:
+        n = -(-int(c) // block)
+        tables.append(perm[offset : offset + n])
+        offset += n
+    width = max(len(t) for t in tables)
+    padded = np.full((seqs, width), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    positions = contexts - 1
+    slots = np.asarray([int(t[p // block]) * block + p % block for t, p in zip(tables, positions)])
+    g = torch.Generator(device=device)
+    g.manual_seed(block * 10 + heads)
+    kc = torch.randn((pool, block, heads, dim), generator=g, device=device).to(pool_dtype)
+    vc = torch.randn((pool, block, heads, dim), generator=g, device=device).to(pool_dtype)
+    q = torch.randn((seqs, heads, dim), generator=g, device=device)
+    new_k = torch.randn((seqs, heads, dim), generator=g, device=device).to(src_dtype)
+    new_v = torch.randn((seqs, heads, dim), generator=g, device=device).to(src_dtype)
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    args = (q, to(positions.astype(np.int32)), to(np.arange(seqs, dtype=np.int32)))
+    meta = (to(padded), to(contexts.astype(np.int32)), dim**-0.5)
+    slot_d = to(slots.astype(np.int64))
+    for partition in (0, 64):
+        k_sep, v_sep = kc.clone(), vc.clone()
+        ops.append_kv(k_sep, v_sep, new_k, new_v, slot_d)
+        want = ops.paged_attention_ragged(*args, k_sep, v_sep, *meta, max_context_len=int(contexts.max()),
+                                          partition_size=partition)  # fmt: skip
+        k_fus, v_fus = kc.clone(), vc.clone()
+        got = ops.paged_attention_ragged(*args, k_fus, v_fus, *meta, max_context_len=int(contexts.max()),
+                                         partition_size=partition, append=(new_k, new_v, slot_d))  # fmt: skip
+        assert torch.equal(k_fus.view(torch.int16) if pool_dtype == torch.bfloat16 else k_fus,
+                           k_sep.view(torch.int16) if pool_dtype == torch.bfloat16 else k_sep)  # fmt: skip
+        assert torch.equal(v_fus.view(torch.int16) if pool_dtype == torch.bfloat16 else v_fus,
+                           v_sep.view(torch.int16) if pool_dtype == torch.bfloat16 else v_sep)  # fmt: skip
+        assert float((got - want).abs().max()) < 1e-6, partition
+        kh, vh = k_sep.float().cpu().numpy(), v_sep.float().cpu().numpy()
+        qh = q.cpu().numpy()
+        oracle, dense = _oracle(kh, vh, tables, contexts, positions, np.arange(seqs), qh, dim**-0.5)
+        assert np.max(np.abs(got.cpu().numpy() - oracle)) < FP32_TOL, partition
+        assert np.max(np.abs(got.cpu().numpy() - dense)) < FP32_TOL, partition
+
+
 def _whole_tile_plan(seq_of, positions, contexts, dim, partition, device, *, explicit_merge):
     """Every run of >= 2 rows of one sequence as whole tiles; the rest in the row pass."""
     rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)

@@ -135,3 +135,24 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch) -> None:
     monkeypatch.setattr(_native, "_LIB", None)
     with pytest.raises(_native.NativeLibraryError, match="missing"):
         _native.library()
+
+
+def test_fused_append_arguments_are_refused_before_any_device_work(lib) -> None:
+    # Placeholder addresses: every call below returns before touching them or the device.
+    fake = [ctypes.c_void_p(4096 * (i + 1)) for i in range(12)]
+    out, q, qpos, qseq, kc, vc, tables, ctx, ws, nk, nv, slots = fake
+
+    def call(new_keys=nk, new_values=nv, new_dtype=0, key_stride=512, value_stride=512,
+             pool_dtype=0, slot_mapping=slots, head_dim=128):  # fmt: skip
+        return lib.pkv_paged_attention_append(
+            out, q, 4 * head_dim, qpos, qseq, 3, None, 0, None, -1, kc, vc, pool_dtype, 100, 16,
+            tables, 8, ctx, 3, 4, head_dim, ctypes.c_float(0.1), 100, 0, 0, ws, 1 << 20,
+            new_keys, new_values, new_dtype, key_stride, value_stride, slot_mapping, 0, None,
+        )  # fmt: skip
+
+    assert call(new_keys=None) == -1
+    assert call(slot_mapping=None) == -1
+    assert call(new_dtype=1, pool_dtype=0) == -2  # bfloat16 rows into a float32 pool
+    assert call(new_dtype=5) == -1
+    assert call(key_stride=100) == -1  # shorter than a token row (4 heads x 128)
+    assert call(key_stride=514) == -2  # rows not 16-byte aligned
