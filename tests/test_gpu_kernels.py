@@ -576,6 +576,15 @@ def _run_batch(batch, partition=0, plan=True):
     )  # fmt: skip
 
 
+def _run_fused(batch):
+    """The decode step as one pkv_paged_attention_append call (append done by the row pass)."""
+    return ops.paged_attention_ragged(
+        batch.queries, batch.query_positions, batch.query_seq, batch.key_cache, batch.value_cache,
+        batch.block_tables, batch.context_lens, batch.scale, max_context_len=batch.max_context_len,
+        plan=batch.plan, append=(batch.new_keys, batch.new_values, batch.slot_mapping),
+    )  # fmt: skip
+
+
 def _oracle_rows(batch, out, seqs, tol):
     """CPU oracle (reference algorithm, 128-key tiles) on every row of the chosen sequences."""
     got = out.cpu().numpy()
@@ -595,13 +604,16 @@ def test_config2_decode_64x4k_matches_the_oracle(device) -> None:
 
     say("config 2: build")
     batch = decode_batch(seed=0, device=device)
-    say("config 2: run")
-    out = _run_batch(batch)
+    say("config 2: fused append + attention (the bench's step)")
+    fused = _run_fused(batch)
     torch.cuda.synchronize()
     # appended rows landed, bit-exact
     slots = batch.slot_mapping
     assert torch.equal(batch.key_cache.view(-1, 32, 128)[slots], batch.new_keys)
     assert torch.equal(batch.value_cache.view(-1, 32, 128)[slots], batch.new_values)
+    say("config 2: run")
+    out = _run_batch(batch)  # appends the same rows again, then attends
+    assert float((fused - out).abs().max()) < 1e-6
     # every sequence against the float64 torch reference
     ref = _torch_dense(batch, range(batch.num_queries))
     worst = max(float((out[t] - ref[t]).abs().max()) for t in ref)
@@ -665,11 +677,15 @@ def test_config5_long_context_bf16_matches_the_oracle(device) -> None:
 
     say("config 5: build")
     batch = long_context_batch(seed=0, device=device)
-    out = _run_batch(batch)
+    fused = _run_fused(batch)
     torch.cuda.synchronize()
     slots = batch.slot_mapping
     want_bits = batch.new_keys.to(torch.bfloat16).view(torch.int16)
     assert torch.equal(batch.key_cache.view(-1, 32, 128)[slots].view(torch.int16), want_bits)
+    want_bits = batch.new_values.to(torch.bfloat16).view(torch.int16)
+    assert torch.equal(batch.value_cache.view(-1, 32, 128)[slots].view(torch.int16), want_bits)
+    out = _run_batch(batch)
+    assert float((fused - out).abs().max()) < 1e-6
     ref = _torch_dense(batch, range(batch.num_queries))  # on the stored (bf16) K/V, in float64
     worst = max(float((out[t] - ref[t]).abs().max()) for t in ref)
     say("config 5: worst vs float64 torch on bf16 K/V", worst)
