@@ -15,8 +15,10 @@
 //     workgroup per (tile of <= 64 rows, head, context partition). Keys are read through the
 //     table of the tile's first row, which the planner only allows where every row of the tile
 //     has the same blocks. Key and value tiles of 32 rows
-//     (16 at head_dim 256) are staged in padded LDS and shared by 4 wavefronts of 16 queries
-//     each; the scores are computed as S^T = K Q^T and the output as O = P V with
+//     (16 at head_dim 256) are staged in LDS and shared by 4 wavefronts of 16 queries each:
+//     through registers into padded rows, or, for float32 pools beside the row pass, straight
+//     from HBM into three swizzled LDS stages (global_load_lds_dwordx4, two tiles in flight);
+//     the scores are computed as S^T = K Q^T and the output as O = P V with
 //     v_mfma_f32_16x16x4f32, so every lane owns four scores of one query per 16 keys and the P
 //     operand of the second product is the lane's own registers.
 //  3. reduce: rows whose visible context spans several partitions merge the per-partition
@@ -72,6 +74,20 @@ namespace {
 #ifndef PKV_ATTN_XCD_REMAP
 #define PKV_ATTN_XCD_REMAP 0
 #endif
+// Tile pass beside the row pass, float32 pools: 1 = key and value tiles go from HBM straight into
+// LDS (global_load_lds_dwordx4) through PKV_TILE_STAGES buffers, all but one in flight while one
+// is multiplied; 0 = through registers, one tile ahead. A tile pass on its own (one workgroup per
+// item) and the bfloat16 path always go through registers: the 96 KiB of stages allow one
+// workgroup per CU, where the register path runs three (measured: 0.86 vs 0.68 ms for config 3's
+// tiles alone; beside its row pass the direct path takes the call 1.56 -> 1.53 ms).
+#ifndef PKV_TILE_DMA
+#define PKV_TILE_DMA 1
+#endif
+// Direct-to-LDS path: LDS stages (2..5; 32 KiB each at head_dim 128: three leave room for two
+// row-pass workgroups on the CU).
+#ifndef PKV_TILE_STAGES
+#define PKV_TILE_STAGES 3
+#endif
 
 constexpr int kWaves = PKV_ATTN_WAVES;  // wavefronts per row_partial workgroup
 constexpr int kThreads = kWaves * kWave;
@@ -80,6 +96,8 @@ constexpr int kDefaultPartition = 512;
 constexpr int kTableSlots = kMaxPartition + 4;  // ceil(P / B) + 1 entries at most
 constexpr int kTileRows = 64;           // query rows per tile_partial workgroup (4 x 16)
 constexpr int kTileThreads = 256;
+constexpr int kTileStages = PKV_TILE_STAGES;  // LDS key/value stages of the direct-to-LDS path
+static_assert(kTileStages >= 2 && kTileStages <= 5, "2..5 direct-to-LDS stages");
 constexpr int kTileWhole = PKV_TILE_WHOLE;  // tile end partition: every key in one workgroup
 constexpr int kReduceThreads = 256;
 
@@ -571,6 +589,36 @@ __device__ __forceinline__ float column_sum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// One 16-byte global load per lane written straight into LDS (global_load_lds_dwordx4): lane l
+// of the wavefront writes LDS bytes [lds + 16 l, lds + 16 l + 16). `lds` is the wavefront-uniform
+// LDS byte address, which the instruction takes in M0, set in the same statement (with the one
+// wait state GFX9 requires between an SALU write of M0 and an LDS DMA). The compiler does not
+// see these loads, so their completion is waited for explicitly (wait_vmcnt) before the barrier
+// that publishes the data.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void load_to_lds16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(N), leaving the other counters alone (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// A workgroup barrier that orders LDS accesses only: unlike __syncthreads it does not wait for
+// outstanding global loads, so loads into the other LDS stages stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <int D>
 struct TileShape {
   static constexpr int kKeys = D <= 128 ? 32 : 16;  // keys per LDS tile (registers bound D = 256)
@@ -578,13 +626,28 @@ struct TileShape {
   static constexpr int kRow = D + 4;                 // padded LDS row (floats): conflict-free reads
   static constexpr int kD4 = D / 4;
   static constexpr int kNb = D / 16;
+  // Direct-to-LDS stages: unpadded rows of D floats whose 16-byte chunks are XOR-swizzled by
+  // (row & 7): chunk q of key row r sits at chunk q ^ (r & 7). The S^T reads (16 rows, one
+  // chunk each) and the PV reads (4 rows x 16 columns) then spread over all LDS banks, as the
+  // padded rows do, while every 16-byte chunk stays whole for the DMA.
+  static constexpr int kChunks = kKeys * D / 4;            // 16-byte chunks of one K (or V) tile
+  static constexpr int kDmaPerLane = kChunks / 256;        // DMA loads per lane per K (or V) tile
+  static constexpr int kTileFloats = kKeys * D;
+  static constexpr int kStageFloats = 2 * kTileFloats;     // K tile then V tile
 };
+
+// LDS float offset of element `col` of key row `row` in a swizzled direct-to-LDS tile.
+template <int D>
+__device__ __forceinline__ int swz(int row, int col) {
+  return row * D + ((((col >> 2) ^ (row & 7))) << 2) + (col & 3);
+}
 
 // One work item of the tile pass: item `bid` = (partition, tile, head), heads fastest, partitions
 // slowest (a whole tile's work is all in partition 0, so those items come first). Every
 // thread of the workgroup calls it with the same item; it returns early (uniformly) for items
-// outside the tile's partitions.
-template <typename KVT, int D, bool kPow2Block>
+// outside the tile's partitions. On the direct-to-LDS path (kDma) s_k holds the kTileStages (key
+// tile, value tile) stages and s_v is unused.
+template <typename KVT, int D, bool kPow2Block, bool kDma>
 __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_table, float* s_k,
                                           float* s_v, int* s_vis) {
   static_assert(D % 16 == 0 && D >= 32, "the MFMA tile needs whole 16-wide output tiles");
@@ -612,7 +675,7 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   const int seq = a.q_seq[t0];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   if (threadIdx.x < kTileRows) {
     s_vis[threadIdx.x] = static_cast<int>(threadIdx.x) < nrows ? row_visible(a, t0 + threadIdx.x) : 0;
   }
@@ -621,6 +684,7 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   int tile_vis = s_vis[lane];
 #pragma unroll
   for (int mask = 32; mask > 0; mask >>= 1) tile_vis = max(tile_vis, __shfl_xor(tile_vis, mask));
+  tile_vis = __builtin_amdgcn_readfirstlane(tile_vis);  // the same in every lane: keep it scalar
   const int nparts = parts_of(tile_vis, a.part_size);
   if (!whole && p >= nparts) return;
   const int kbeg = whole ? 0 : p * a.part_size;
@@ -666,6 +730,191 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   const int64_t row_stride = static_cast<int64_t>(a.num_heads) * D;
   __syncthreads();  // s_table ready
 
+  const int lim = min(my_vis, kend);
+
+  // One key tile's scores st -> probabilities pr, updating the running reference and sum. A key
+  // counts when it is below the lane's limit and its bit in kmask is set.
+  auto softmax_step = [&](floatx4 (&st)[kSub], int k0, uint32_t kmask, float (&pr)[kSub][4]) {
+    float sc[kSub][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kk = 16 * j + 4 * c + r;
+        sc[j][r] = (k0 + kk) < lim && ((kmask >> kk) & 1u) ? st[j][r] : -INFINITY;
+        mx = fmaxf(mx, sc[j][r]);
+      }
+    }
+    mx = column_max(mx);
+    // Raise the reference only when a score passes it by more than kLazyLog2 (or it is unset).
+    const bool raise = mx > m_ref + kLazyLog2 || (m_ref == -INFINITY && mx > -INFINITY);
+    // The direct-to-LDS step rescales without a branch (alpha is exactly 1 in lanes that keep
+    // their reference), so the step stays one block of straight-line code the compiler can
+    // interleave; the register path skips the multiplies when no lane raises (fewer VGPRs).
+    if (kDma || __builtin_amdgcn_ballot_w64(raise) != 0) {
+      const float m_next = raise ? mx : m_ref;
+      const float alpha = raise ? fast_exp2(m_ref - m_next) : 1.f;  // exp2(-inf) = 0
+      l_part *= alpha;
+#pragma unroll
+      for (int b = 0; b < kNb; ++b) o[b] *= alpha;
+      m_ref = m_next;
+    }
+    const float shift = m_ref == -INFINITY ? 0.f : m_ref;
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[j][r] = fast_exp2(sc[j][r] - shift);
+        l_part += pr[j][r];
+      }
+    }
+  };
+
+  if constexpr (kDma) {
+    static_assert(std::is_same_v<KVT, float>, "the direct-to-LDS tiles are float32");
+    // Direct-to-LDS pipeline over kTileStages buffers: the key and value tiles of steps i + 1
+    // .. i + kTileStages - 1 are in flight while step i is multiplied. Step i waits for its own
+    // loads (vmcnt), then one barrier publishes every wavefront's share and also closes step
+    // i - 1, whose buffer the loads of step i + kTileStages - 1 then fill. Those are queued
+    // between the step's two products, in straight-line code the compiler can interleave with
+    // the matrix instructions. Every lane issues the same loads in every step, past the last
+    // step too: a lane whose key is past kend or in a block outside the pool loads row 0 of
+    // block 0 (always in the pool) instead, and the key's bit in the step's mask stays clear.
+    constexpr int kPer = S::kDmaPerLane;
+    static_assert(S::kChunks % kTileThreads == 0, "whole wavefront DMA loads per tile");
+    constexpr int kCpr = D / 4;  // chunks per key row
+    constexpr int kAhead = kTileStages - 1;
+    const uint32_t lds_kv = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_k));
+    // Branch-free address arithmetic (selects, no divergent branches). A block's elements and a
+    // token row's fit 32 bits (the host checks block_size * num_heads * head_dim < 2^31).
+    const uint64_t block_elems = static_cast<uint64_t>(a.block_size) * static_cast<uint64_t>(row_stride);
+    const uint32_t row_elems = static_cast<uint32_t>(row_stride);
+    const uint32_t pool_blocks = static_cast<uint32_t>(min<int64_t>(a.num_blocks, INT32_MAX));
+    // Table entry of key kpos (clamped into the window; callers discard it when kpos is out).
+    auto table_at = [&](int kpos) {
+      const int lb = min(max(block_of<kPow2Block>(kpos, a) - b0, 0), kTableSlots - 1);
+      return s_table[lb];
+    };
+    // Element offsets of this lane's kPer chunks of key tile k0, and the tile's key mask.
+    auto prepare = [&](int k0, int lane_v, int64_t (&off)[kPer]) -> uint32_t {
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int chunk = (wave * kPer + u) * kWave + lane_v;
+        const int row = chunk / kCpr;
+        const int col = ((chunk % kCpr) ^ (row & 7)) * 4;
+        const int kpos = k0 + row;
+        const int blk = table_at(kpos);
+        const bool ok = (kpos < kend) & (static_cast<uint32_t>(blk) < pool_blocks);
+        const uint32_t within = kPow2Block ? (kpos & (a.block_size - 1)) : kpos % a.block_size;
+        const uint32_t blk_u = ok ? static_cast<uint32_t>(blk) : 0u;
+        const uint32_t row_off = ok ? within * row_elems : 0u;
+        off[u] = static_cast<int64_t>(blk_u * block_elems) + static_cast<int64_t>(row_off) + head_off + col;
+      }
+      const int kpos = k0 + lane_v;
+      const bool ok = (lane_v < kKeys) & (kpos < kend) &
+                      (static_cast<uint32_t>(table_at(kpos)) < pool_blocks);
+      return static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(ok));
+    };
+    auto fire = [&](int buf, const int64_t (&off)[kPer]) {
+      const uint32_t dst = lds_kv + static_cast<uint32_t>(buf * S::kStageFloats * 4 + wave * kPer * 1024);
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        load_to_lds16(kcache + off[u], dst + u * 1024);
+        load_to_lds16(vcache + off[u], dst + u * 1024 + S::kTileFloats * 4);
+      }
+    };
+    const int nsteps = kend > kbeg ? (kend - kbeg + kKeys - 1) / kKeys : 0;
+    uint32_t kmask[kAhead];  // key masks of steps i .. i + kAhead - 1
+    wait_vmcnt<0>();  // the query loads above complete before the pipeline's loads are queued
+    if (nsteps > 0) {
+#pragma unroll
+      for (int st = 0; st < kAhead; ++st) {
+        int64_t off[kPer];
+        kmask[st] = prepare(kbeg + st * kKeys, lane, off);
+        fire(st, off);
+      }
+    }
+    int buf = 0;
+    for (int i = 0; i < nsteps; ++i) {
+      const int k0 = kbeg + i * kKeys;
+      wait_vmcnt<(kAhead - 1) * 2 * kPer>();  // this step's loads have landed
+      lds_barrier();
+      const int k_next = k0 + kAhead * kKeys;  // the tile whose loads this step queues
+      if (block_of<kPow2Block>(min(k_next + kKeys, kend) - 1, a) >= b0 + kTableSlots) {
+        // A whole tile moves its table window; no wavefront reads the table between the barrier
+        // above and the one below.
+        b0 = block_of<kPow2Block>(k_next, a);
+        stage_window();
+        lds_barrier();
+      }
+      // The swizzled LDS addresses are lane constants; they are recomputed from an opaque copy
+      // of the lane index each step (a few VALU operations) instead of being hoisted out of the
+      // loop, which would hold about 20 more VGPRs and cost the CU a row-pass workgroup.
+      int lane_o = lane;
+      asm volatile("" : "+v"(lane_o));
+      const int cl = lane_o >> 4;
+      const int nl = lane_o & 15;
+      const float* sk = s_k + buf * S::kStageFloats;
+      const float* sv = sk + S::kTileFloats;
+
+      // S^T blocks: register r of st[j] = S[query n][key k0 + 16j + 4c + r]. Lane (c, n) reads
+      // chunk c * kD4 / 4 + q of key row 16 j + n, swizzled by n & 7.
+      floatx4 st[kSub];
+#pragma unroll
+      for (int j = 0; j < kSub; ++j) st[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < kD4 / 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < kSub; ++j) {
+          const float4 kv = *reinterpret_cast<const float4*>(
+              sk + (16 * j + nl) * D + (((cl * (kD4 / 4) + q) ^ (nl & 7)) << 2));
+          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qreg[4 * q], st[j], 0, 0, 0);
+          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qreg[4 * q + 1], st[j], 0, 0, 0);
+          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qreg[4 * q + 2], st[j], 0, 0, 0);
+          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qreg[4 * q + 3], st[j], 0, 0, 0);
+        }
+      }
+      // Queue step i + kAhead's loads into the buffer step i - 1 used. Their address arithmetic
+      // is scheduled among the PV products below, not the S^T products above (which would keep
+      // more registers live across the S^T loop).
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t next_mask;
+      {
+        int64_t off[kPer];
+        next_mask = prepare(k_next, lane_o, off);
+        fire(buf == 0 ? kAhead : buf - 1, off);
+      }
+      float pr[kSub][4];
+      softmax_step(st, k0, kmask[0], pr);
+
+      // O^T += V^T P^T. Column 16 b + n of row 16 j + 4 c + step is chunk 4 b + n / 4, swizzled
+      // by (4 c + step) & 7: chunk 4 (b ^ (c & 1)) + ((n / 4) ^ step), so each (j, step) needs one
+      // lane base for even b and one for odd b, and b itself is an immediate offset. The
+      // products are accumulated in the register path's order (j, then step, then b), so both
+      // paths round identically.
+#pragma unroll
+      for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+        for (int step = 0; step < 4; ++step) {
+          const int lane_col = 4 * cl * D + 4 * ((nl >> 2) ^ step) + (nl & 3);
+          const float* v_even = sv + lane_col + 16 * (cl & 1);
+          const float* v_odd = sv + lane_col - 16 * (cl & 1);
+          const int row_off = (16 * j + step) * D;
+#pragma unroll
+          for (int b = 0; b < kNb; ++b) {
+            const float x = (b & 1) ? v_odd[row_off + 16 * b] : v_even[row_off + 16 * b];
+            o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, pr[j][step], o[b], 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int st = 0; st + 1 < kAhead; ++st) kmask[st] = kmask[st + 1];
+      kmask[kAhead - 1] = next_mask;
+      buf = buf == kTileStages - 1 ? 0 : buf + 1;
+    }
+    wait_vmcnt<0>();  // the loads queued past the last step land before the LDS is reused
+  } else {
   // Software pipeline: the raw vectors of key tile k0 + kKeys are loaded into registers while
   // tile k0 is being multiplied; at the top of each step they are widened into LDS.
   constexpr int kVecs = kKeys * kVecPerRow;  // 16-byte vectors per K (or V) tile
@@ -698,7 +947,6 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   };
   if (kbeg < kend) prefetch(kbeg);
 
-  const int lim = min(my_vis, kend);
   for (int k0 = kbeg; k0 < kend; k0 += kKeys) {
     // Every read of s_table by the last prefetch happened before the previous barrier, so the
     // window can move here; the barrier below publishes it before the next prefetch reads it.
@@ -742,37 +990,8 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
       }
     }
 
-    float sc[kSub][4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kSub; ++j) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sc[j][r] = (k0 + 16 * j + 4 * c + r) < lim ? st[j][r] : -INFINITY;
-        mx = fmaxf(mx, sc[j][r]);
-      }
-    }
-    mx = column_max(mx);
-    // Raise the reference only when a score passes it by more than kLazyLog2 (or it is unset).
-    const bool raise = mx > m_ref + kLazyLog2 || (m_ref == -INFINITY && mx > -INFINITY);
-    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-      const float m_next = raise ? mx : m_ref;
-      const float alpha = raise ? fast_exp2(m_ref - m_next) : 1.f;  // exp2(-inf) = 0
-      l_part *= alpha;
-#pragma unroll
-      for (int b = 0; b < kNb; ++b) o[b] *= alpha;
-      m_ref = m_next;
-    }
-    const float shift = m_ref == -INFINITY ? 0.f : m_ref;
     float pr[kSub][4];
-#pragma unroll
-    for (int j = 0; j < kSub; ++j) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pr[j][r] = fast_exp2(sc[j][r] - shift);
-        l_part += pr[j][r];
-      }
-    }
+    softmax_step(st, k0, ~0u, pr);
 
     // O^T += V^T P^T.
 #pragma unroll
@@ -787,6 +1006,7 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
       }
     }
     __syncthreads();
+  }
   }
 
   // Epilogue: register r of tile b is O[query n][16b + 4c + r].
@@ -822,16 +1042,24 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
 // partition, head) items. With one item per workgroup the grid is the item count; beside the
 // row pass the host launches one workgroup per CU instead, so the tile pass holds one wave per
 // SIMD and leaves the rest of each CU to the memory-bound row pass.
-template <typename KVT, int D, bool kPow2Block>
+template <typename KVT, int D, bool kPow2Block, bool kDma>
 __global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params a, uint32_t num_items) {
   using S = TileShape<D>;
   __shared__ int s_table[kTableSlots];
-  __shared__ float s_k[S::kKeys * S::kRow];
-  __shared__ float s_v[S::kKeys * S::kRow];
   __shared__ int s_vis[kTileRows];
-  for (uint32_t item = blockIdx.x; item < num_items; item += gridDim.x) {
-    __syncthreads();  // the previous item's reads of LDS are done
-    tile_item<KVT, D, kPow2Block>(a, item, s_table, s_k, s_v, s_vis);
+  if constexpr (kDma) {
+    __shared__ __align__(16) float s_kv[kTileStages * S::kStageFloats];
+    for (uint32_t item = blockIdx.x; item < num_items; item += gridDim.x) {
+      __syncthreads();  // the previous item's reads of LDS are done
+      tile_item<KVT, D, kPow2Block, true>(a, item, s_table, s_kv, nullptr, s_vis);
+    }
+  } else {
+    __shared__ float s_k[S::kKeys * S::kRow];
+    __shared__ float s_v[S::kKeys * S::kRow];
+    for (uint32_t item = blockIdx.x; item < num_items; item += gridDim.x) {
+      __syncthreads();  // the previous item's reads of LDS are done
+      tile_item<KVT, D, kPow2Block, false>(a, item, s_table, s_k, s_v, s_vis);
+    }
   }
 }
 
@@ -938,10 +1166,17 @@ int launch_tiles(const Params& a, int64_t num_tiles, int64_t max_groups, hipStre
     const int64_t groups = max_groups > 0 && max_groups < items ? max_groups : items;
     const dim3 grid(static_cast<uint32_t>(groups));
     const auto n = static_cast<uint32_t>(items);
-    if ((a.block_size & (a.block_size - 1)) == 0) {
-      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true>), grid, dim3(kTileThreads), 0, stream, a, n);
+    const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
+    // The direct-to-LDS tiles beside the row pass (a persistent grid), float32 pools only.
+    constexpr bool kDmaType = PKV_TILE_DMA && std::is_same_v<KVT, float>;
+    if (kDmaType && max_groups > 0 && pow2) {
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true, kDmaType>), grid, dim3(kTileThreads), 0, stream, a, n);
+    } else if (kDmaType && max_groups > 0) {
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false, kDmaType>), grid, dim3(kTileThreads), 0, stream, a, n);
+    } else if (pow2) {
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true, false>), grid, dim3(kTileThreads), 0, stream, a, n);
     } else {
-      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false>), grid, dim3(kTileThreads), 0, stream, a, n);
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false, false>), grid, dim3(kTileThreads), 0, stream, a, n);
     }
     return check_launch();
   } else {

@@ -519,6 +519,60 @@ def test_whole_tiles_match_the_oracle(device, dim, kv, block) -> None:
             assert np.max(np.abs(got - dense)) < FP32_TOL, (partition, explicit)
 
 
+@pytest.mark.parametrize("dim", [32, 64, 128, 256])
+@pytest.mark.parametrize("block", [1, 5, 16])
+@pytest.mark.parametrize("whole", [False, True], ids=["partitions", "whole"])
+def test_tiles_beside_rows_equal_tiles_alone(device, dim, block, whole) -> None:
+    """Beside row-pass rows the float32 tile pass is a persistent grid that loads key and value
+    tiles straight into LDS; on its own it runs one workgroup per item through registers. Both
+    form the same sums in the same order, so the tile rows come out bit-identical; and both
+    match the oracle. At block_size 1 whole tiles move their staged table window."""
+    say("tile paths", dim, block, whole)
+    rng = np.random.default_rng(dim * 7 + block + whole)
+    max_ctx = 1400 if block == 1 else 800
+    kc, vc, tables, contexts, positions, seq_of, q = _ragged_case(
+        rng, heads=2, dim=dim, block=block, pool=5 * max_ctx // block + 8, seqs=6, max_ctx=max_ctx,
+        prefill=True, max_rows=150,
+    )  # fmt: skip
+    # Two more decode sequences, so the batch surely has row-pass rows next to the tiles.
+    extra = [rng.permutation(kc.shape[0])[: -(-c // block)] for c in (max_ctx - 3, 37)]
+    tables = list(tables) + extra
+    contexts = np.concatenate([contexts, [max_ctx - 3, 37]])
+    positions = np.concatenate([positions, [max_ctx - 4, 36]])
+    seq_of = np.concatenate([seq_of, [len(tables) - 2, len(tables) - 1]])
+    q = np.concatenate([q, rng.standard_normal((2,) + q.shape[1:]).astype(np.float32)])
+    scale = dim**-0.5
+    want, _ = _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale)
+    width = max(len(t) for t in tables)
+    padded = np.full((len(tables), width), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    args = (
+        torch.from_numpy(q).to(device), torch.from_numpy(positions.astype(np.int32)).to(device),
+        torch.from_numpy(seq_of.astype(np.int32)).to(device),
+        torch.from_numpy(kc).to(device), torch.from_numpy(vc).to(device),
+        torch.from_numpy(padded).to(device), torch.from_numpy(contexts.astype(np.int32)).to(device),
+        scale,
+    )  # fmt: skip
+    rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)
+    assert rows.shape[0] >= 2 and tiles.shape[0] >= 2
+    if whole:
+        tiles[:, 3] = ops.TILE_WHOLE
+    tile_rows = np.concatenate([np.arange(t0, t0 + n) for t0, n, _, _ in tiles])
+    visible = np.minimum(contexts[seq_of], positions + 1)
+    for partition in (0, 64):
+        beside = ops.upload_plan(ops.expand_rows(rows, visible, partition), tiles, device,
+                                 partition_size=partition)  # fmt: skip
+        alone = ops.upload_plan(np.zeros((0, 2), np.int32), tiles, device, partition_size=partition,
+                                merge=ops.merge_rows_for(seq_of.size, tiles, visible, partition or 512)
+                                if whole else None)  # fmt: skip
+        mc = int(contexts.max())
+        got = ops.paged_attention_ragged(*args, max_context_len=mc, plan=beside).cpu().numpy()
+        solo = ops.paged_attention_ragged(*args, max_context_len=mc, plan=alone).cpu().numpy()
+        assert np.max(np.abs(got - want)) < FP32_TOL, partition
+        assert np.array_equal(got[tile_rows], solo[tile_rows]), partition
+
+
 def test_poisoned_slots_and_padding_are_never_read(device) -> None:
     say("poison")
     rng = np.random.default_rng(9)
