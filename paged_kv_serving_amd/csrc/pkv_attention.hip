@@ -1041,9 +1041,13 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
 // The tile pass: workgroup w computes items w, w + gridDim.x, ... of the num_items (tile,
 // partition, head) items. With one item per workgroup the grid is the item count; beside the
 // row pass the host launches one workgroup per CU instead, so the tile pass holds one wave per
-// SIMD and leaves the rest of each CU to the memory-bound row pass.
+// SIMD and leaves the rest of each CU to the memory-bound row pass. The register path at
+// head_dim 128 is held to 168 VGPRs (three waves per SIMD; it needs about 170 unconstrained,
+// which allows two); the other instantiations have no occupancy target.
 template <typename KVT, int D, bool kPow2Block, bool kDma>
-__global__ __launch_bounds__(kTileThreads) void tile_partial_kernel(const Params a, uint32_t num_items) {
+__global__ __launch_bounds__(kTileThreads)
+__attribute__((amdgpu_waves_per_eu(!kDma && D == 128 ? 3 : 1)))
+void tile_partial_kernel(const Params a, uint32_t num_items) {
   using S = TileShape<D>;
   __shared__ int s_table[kTableSlots];
   __shared__ int s_vis[kTileRows];
@@ -1158,8 +1162,13 @@ Overlap* overlap_locked(int device) {
   return &o;
 }
 
+// max_groups > 0: a persistent grid of that many workgroups beside the row pass, staged straight
+// into LDS for float32 pools unless the row pass runs its lean workgroups (those pack many per CU,
+// and the 100 KiB of stages would crowd them out: the prefix-sharing step's attention took
+// 0.30 instead of 0.23 ms).
 template <typename KVT, int D>
-int launch_tiles(const Params& a, int64_t num_tiles, int64_t max_groups, hipStream_t stream) {
+int launch_tiles(const Params& a, int64_t num_tiles, int64_t max_groups, bool lean_rows,
+                 hipStream_t stream) {
   if constexpr (D % 16 == 0 && D >= 32) {
     const int64_t items = num_tiles * static_cast<int64_t>(a.max_parts) * a.num_heads;
     if (items > 0x7fffffff) return PKV_EUNSUPPORTED;
@@ -1167,11 +1176,11 @@ int launch_tiles(const Params& a, int64_t num_tiles, int64_t max_groups, hipStre
     const dim3 grid(static_cast<uint32_t>(groups));
     const auto n = static_cast<uint32_t>(items);
     const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
-    // The direct-to-LDS tiles beside the row pass (a persistent grid), float32 pools only.
     constexpr bool kDmaType = PKV_TILE_DMA && std::is_same_v<KVT, float>;
-    if (kDmaType && max_groups > 0 && pow2) {
+    const bool dma = kDmaType && max_groups > 0 && !lean_rows;
+    if (dma && pow2) {
       hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true, kDmaType>), grid, dim3(kTileThreads), 0, stream, a, n);
-    } else if (kDmaType && max_groups > 0) {
+    } else if (dma) {
       hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false, kDmaType>), grid, dim3(kTileThreads), 0, stream, a, n);
     } else if (pow2) {
       hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true, false>), grid, dim3(kTileThreads), 0, stream, a, n);
@@ -1243,11 +1252,11 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     if (overlap != nullptr) {
       // fork: the tile pass starts when the caller's stream reaches the fork point
       if (hipStreamWaitEvent(overlap->stream, overlap->fork, 0) != hipSuccess) return PKV_EHIP;
-      const int rc = launch_tiles<KVT, D>(a, num_tiles, overlap->tile_groups, overlap->stream);
+      const int rc = launch_tiles<KVT, D>(a, num_tiles, overlap->tile_groups, short_rows, overlap->stream);
       if (rc != PKV_OK) return rc;
       if (hipEventRecord(overlap->join, overlap->stream) != hipSuccess) return PKV_EHIP;
     } else {
-      const int rc = launch_tiles<KVT, D>(a, num_tiles, 0, stream);
+      const int rc = launch_tiles<KVT, D>(a, num_tiles, 0, short_rows, stream);
       if (rc != PKV_OK) return rc;
     }
   }
