@@ -787,7 +787,8 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
     constexpr int kAhead = kTileStages - 1;
     const uint32_t lds_kv = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_k));
     // Branch-free address arithmetic (selects, no divergent branches). A block's elements and a
-    // token row's fit 32 bits (the host checks block_size * num_heads * head_dim < 2^31).
+    // token row's fit 31 bits (launch_tiles takes this path only when block_size * num_heads *
+    // head_dim does).
     const uint64_t block_elems = static_cast<uint64_t>(a.block_size) * static_cast<uint64_t>(row_stride);
     const uint32_t row_elems = static_cast<uint32_t>(row_stride);
     const uint32_t pool_blocks = static_cast<uint32_t>(min<int64_t>(a.num_blocks, INT32_MAX));
@@ -1177,7 +1178,8 @@ int launch_tiles(const Params& a, int64_t num_tiles, int64_t max_groups, bool le
     const auto n = static_cast<uint32_t>(items);
     const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
     constexpr bool kDmaType = PKV_TILE_DMA && std::is_same_v<KVT, float>;
-    const bool dma = kDmaType && max_groups > 0 && !lean_rows;
+    const bool block_fits = static_cast<int64_t>(a.block_size) * a.num_heads * D <= INT32_MAX;
+    const bool dma = kDmaType && max_groups > 0 && !lean_rows && block_fits;
     if (dma && pow2) {
       hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true, kDmaType>), grid, dim3(kTileThreads), 0, stream, a, n);
     } else if (dma) {
