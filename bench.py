@@ -3,10 +3,14 @@
 Workload ("config 2"): one decode step of one layer for 64 sequences
 with contexts uniform in [512, 4096], 32 heads x head_dim 128 (MHA), block_size 16, float32 K/V,
 block tables drawn from a shuffled 20,000-block pool; seeded N(0, 1) data resident in HBM.
-A step is the data path of that iteration:
+A step is the data path of that iteration, in one call:
 
-    pkv_append           the 64 new tokens' keys and values into their slots
-    pkv_paged_attention  64 decode queries over their block tables (partial + reduce passes)
+    pkv_paged_attention_append  the 64 new tokens' keys and values into their slots, appended by
+                                the row pass itself, and 64 decode queries over their block
+                                tables (row pass + reduce pass)
+
+The standalone pkv_append on the same tokens is timed outside the steps and reported as
+``append_us`` / ``append_gbps``.
 
 ``value`` is decode tokens per second (64 tokens per step). The roofline object is for the
 dominant kernel, the attention pass: achieved = algorithmic bytes per launch (each sequence's
@@ -41,6 +45,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
 METRIC = "paged-attn decode tokens/s & HBM GB/s (% of peak) at 64 seq x 4k ctx; append GB/s"
 
 
@@ -380,9 +385,18 @@ def config3(args) -> dict:
     prefill_flops = 4 * 32 * 128 * visible
 
     rope = rope_append_timing(args, batch)
+    tiles_ms = prefill_tiles_alone_ms(args, batch)
+    tflops = prefill_flops / (tiles_ms * 1e-3) / 1e12
 
     def extra(result, attention_ms):
-        return {"prefill_gflop": round(prefill_flops / 1e9, 2), **rope}
+        return {
+            "prefill_gflop": round(prefill_flops / 1e9, 2),
+            # The chunks' MFMA tiles as their own call (no decode rows beside them).
+            "prefill_tiles_alone_ms": round(tiles_ms, 4),
+            "prefill_tiles_alone_tflops": round(tflops, 1),
+            "prefill_tiles_alone_frac_of_fp32_mfma_peak": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4),
+            **rope,
+        }
 
     return run_attention_config(
         args, batch, dtype="f32", extra=extra,
@@ -391,6 +405,49 @@ def config3(args) -> dict:
         "rows ctx U[256,4096], 32x128 fp32, block 16, 40000-block shuffled pool; step = append "
         "4216 tokens + one ragged attention call (MFMA tiles for chunks, row pass for decode)",
     )  # fmt: skip
+
+
+def prefill_tiles_alone_ms(args, batch) -> float:
+    """Mean HIP-event time of the batch's prefill chunks as their own attention call: the plan's
+    whole tiles with no row-pass items, so the tile pass runs one workgroup per (tile, head) and
+    nothing beside it (the decode rows' outputs are left unwritten). This is the MFMA-bound part
+    of config 3 measured alone."""
+    import torch
+
+    from paged_kv_serving_amd import ops
+
+    device = batch.queries.device
+    heads, dim = batch.key_cache.shape[2], batch.key_cache.shape[3]
+    host = ops.plan_batch(
+        batch.host_seq, dim, heads, batch.host_tables, batch.host_context, batch.key_cache.shape[1],
+        partition_size=args.partition, query_positions=batch.host_positions,
+    )  # fmt: skip
+    plan = ops.upload_plan(np.zeros((0, 2), np.int32), host.tiles, device,
+                           partition_size=host.partition_size, merge=np.zeros(0, np.int32))  # fmt: skip
+    need = ops.attention_workspace_bytes(batch.num_queries, heads, dim, batch.max_context_len,
+                                         host.partition_size)  # fmt: skip
+    workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=device)
+    out = torch.empty_like(batch.queries)
+
+    def run() -> None:
+        ops.paged_attention_ragged(
+            batch.queries, batch.query_positions, batch.query_seq, batch.key_cache,
+            batch.value_cache, batch.block_tables, batch.context_lens, batch.scale,
+            max_context_len=batch.max_context_len, out=out, workspace=workspace, plan=plan,
+        )  # fmt: skip
+
+    for _ in range(max(args.warmup, 1)):
+        run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(device)
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(max(args.steps, 1))]  # fmt: skip
+    for e0, e1 in marks:
+        e0.record(stream)
+        run()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return float(np.mean([e0.elapsed_time(e1) for e0, e1 in marks]))
 
 
 def rope_append_timing(args, batch) -> dict:
