@@ -207,7 +207,9 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *                      NULL when that is 0); 16-byte aligned when num_tiles > 0.
  * A query whose every key is masked gets a zero output (attention.py:120-121).
  * Block ids are read only for positions below the query's visible length, so table entries
- * past a sequence's last used block may hold anything. Supported head_dim: 8, 16, 32, 64, 128,
+ * past a sequence's last used block may hold anything. A block id outside [0, num_blocks) at a
+ * visible position is not read either: its keys take no part in the softmax (the reference
+ * would raise on such a table; every pass here skips them alike). Supported head_dim: 8, 16, 32, 64, 128,
  * 256; any block_size >= 1; kv_dtype F32 or BF16 (accumulation is float32 either way).
  */
 int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,

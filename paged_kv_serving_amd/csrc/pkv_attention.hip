@@ -922,7 +922,17 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   constexpr int kPerThread = (kVecs + kTileThreads - 1) / kTileThreads;
   uint4 kraw[kPerThread];
   uint4 vraw[kPerThread];
+  // The prefetched tile's key mask (keys before kend in blocks inside the pool), a wavefront
+  // ballot kept in scalar registers until the tile's scores are masked.
+  uint32_t mask_next = 0u;
   auto prefetch = [&](int k0) {
+    {
+      const int kpos = k0 + lane;
+      const int lb = min(max(block_of<kPow2Block>(kpos, a) - b0, 0), kTableSlots - 1);
+      const int blk = s_table[lb];
+      const bool ok = lane < kKeys && kpos < kend && blk >= 0 && blk < a.num_blocks;
+      mask_next = static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(ok));
+    }
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
       const int v = threadIdx.x + u * kTileThreads;
@@ -949,6 +959,7 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   if (kbeg < kend) prefetch(kbeg);
 
   for (int k0 = kbeg; k0 < kend; k0 += kKeys) {
+    const uint32_t kmask = mask_next;  // this tile's, from its prefetch
     // Every read of s_table by the last prefetch happened before the previous barrier, so the
     // window can move here; the barrier below publishes it before the next prefetch reads it.
     const int next = k0 + kKeys;
@@ -992,7 +1003,7 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
     }
 
     float pr[kSub][4];
-    softmax_step(st, k0, ~0u, pr);
+    softmax_step(st, k0, kmask, pr);
 
     // O^T += V^T P^T.
 #pragma unroll

@@ -573,6 +573,78 @@ def test_tiles_beside_rows_equal_tiles_alone(device, dim, block, whole) -> None:
         assert np.array_equal(got[tile_rows], solo[tile_rows]), partition
 
 
+def _attention_skipping_bad_blocks(q, positions, seq_of, kc, vc, tables, contexts, scale):
+    """float64 attention in which keys whose block id lies outside the pool take no part (the
+    library's rule for such table entries; the reference would raise on them)."""
+    pool, block = kc.shape[0], kc.shape[1]
+    out = np.zeros(q.shape, dtype=np.float64)
+    for t in range(q.shape[0]):
+        s = int(seq_of[t])
+        visible = min(int(contexts[s]), int(positions[t]) + 1)
+        keep = [p for p in range(visible) if 0 <= tables[s][p // block] < pool]
+        if not keep:
+            continue
+        k = np.stack([kc[tables[s][p // block], p % block] for p in keep]).astype(np.float64)
+        v = np.stack([vc[tables[s][p // block], p % block] for p in keep]).astype(np.float64)
+        scores = np.einsum("hd,nhd->hn", q[t].astype(np.float64), k) * scale
+        w = np.exp(scores - scores.max(axis=1, keepdims=True))
+        w /= w.sum(axis=1, keepdims=True)
+        out[t] = np.einsum("hn,nhd->hd", w, v)
+    return out
+
+
+@pytest.mark.parametrize("block", [16, 5])
+@pytest.mark.parametrize("bad", [-1, 10**6], ids=["negative", "past-pool"])
+def test_blocks_outside_the_pool_are_skipped_by_every_pass(device, block, bad) -> None:
+    """A table entry outside [0, num_blocks) inside a visible context is never read: the row
+    pass, the tile pass beside it (direct-to-LDS stages) and the tile pass alone (registers)
+    all leave its keys out of the softmax."""
+    say("bad blocks", block, bad)
+    rng = np.random.default_rng(block + (bad > 0))
+    dim, heads = 128, 2
+    kc, vc, tables, contexts, positions, seq_of, q = _ragged_case(
+        rng, heads=heads, dim=dim, block=block, pool=2000, seqs=6, max_ctx=900, prefill=True,
+        max_rows=150,
+    )  # fmt: skip
+    extra = rng.permutation(kc.shape[0])[: -(-700 // block)]
+    tables = [np.asarray(t).copy() for t in tables] + [extra]
+    contexts = np.concatenate([contexts, [700]])
+    positions = np.concatenate([positions, [699]])
+    seq_of = np.concatenate([seq_of, [len(tables) - 1]])
+    q = np.concatenate([q, rng.standard_normal((1,) + q.shape[1:]).astype(np.float32)])
+    for t in tables:  # spoil about one in eight of each table's used entries
+        t[rng.random(t.size) < 0.125] = bad
+    scale = dim**-0.5
+    want = _attention_skipping_bad_blocks(q, positions, seq_of, kc, vc, tables, contexts, scale)
+    width = max(len(t) for t in tables)
+    padded = np.full((len(tables), width), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    args = (
+        torch.from_numpy(q).to(device), torch.from_numpy(positions.astype(np.int32)).to(device),
+        torch.from_numpy(seq_of.astype(np.int32)).to(device),
+        torch.from_numpy(kc).to(device), torch.from_numpy(vc).to(device),
+        torch.from_numpy(padded).to(device), torch.from_numpy(contexts.astype(np.int32)).to(device),
+        scale,
+    )  # fmt: skip
+    mc = int(contexts.max())
+    rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)
+    assert rows.shape[0] >= 1 and tiles.shape[0] >= 2
+    visible = np.minimum(contexts[seq_of], positions + 1)
+    tile_rows = np.concatenate([np.arange(t0, t0 + n) for t0, n, _, _ in tiles])
+    row_only = ops.paged_attention_ragged(*args, max_context_len=mc).cpu().numpy()
+    beside = ops.paged_attention_ragged(
+        *args, max_context_len=mc,
+        plan=ops.upload_plan(ops.expand_rows(rows, visible, 0), tiles, device),
+    ).cpu().numpy()  # fmt: skip
+    alone = ops.paged_attention_ragged(
+        *args, max_context_len=mc, plan=ops.upload_plan(np.zeros((0, 2), np.int32), tiles, device),
+    ).cpu().numpy()  # fmt: skip
+    assert np.max(np.abs(row_only - want)) < FP32_TOL
+    assert np.max(np.abs(beside - want)) < FP32_TOL
+    assert np.max(np.abs(alone[tile_rows] - want[tile_rows])) < FP32_TOL
+
+
 def test_poisoned_slots_and_padding_are_never_read(device) -> None:
     say("poison")
     rng = np.random.default_rng(9)
