@@ -127,6 +127,29 @@ def compute_slots(entries, block_size: int) -> np.ndarray:
     return out
 
 
+def shared_prefix_order(entries, block_size: int) -> list[int] | None:
+    """A row order that puts decode entries whose block tables share their leading blocks next
+    to each other, so ``ops.plan_batch`` can read a common prefix once per head as MFMA tiles
+    (it looks for runs of consecutive rows). Decode entries (one token) with at least
+    MIN_SHARED_TOKENS of table come first, stably sorted by those leading block ids; every other
+    entry follows in batch order. None when the batch order already has every such run together
+    or there are too few decode entries to form one."""
+    lead = -(-ops.MIN_SHARED_TOKENS // block_size)
+    decode = [i for i, e in enumerate(entries) if len(e.token_ids) == 1 and len(e.block_table) >= lead]
+    if len(decode) < ops.MIN_SHARED_ROWS:
+        return None
+    keys = {i: tuple(entries[i].block_table[:lead]) for i in decode}
+    grouped = sorted(decode, key=lambda i: keys[i])
+    # Nothing to gain when no two decode entries share their leading blocks, or when the
+    # entries that do are already adjacent in the batch.
+    shared = sum(keys[a] == keys[b] for a, b in zip(grouped, grouped[1:]))
+    adjacent = sum(keys[a] == keys[b] for a, b in zip(decode, decode[1:]) if b == a + 1)
+    if shared == 0 or shared == adjacent:
+        return None
+    rest = [i for i in range(len(entries)) if i not in keys]
+    return grouped + rest
+
+
 def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return x / torch.sqrt(torch.mean(x * x, dim=-1, keepdim=True) + eps) * weight
 
@@ -316,6 +339,20 @@ class ModelRunner:
         slots = compute_slots(entries, self.block_size)
         if slots.size and (slots.min() < 0 or slots.max() >= self.capacity_tokens):
             raise IndexError("a block table names a block outside the pool")
+        # Rows in the order the planner can use (validation above ran in batch order, so errors
+        # name the same entry as the reference's); logits come back in batch order below.
+        order = shared_prefix_order(entries, self.block_size)
+        lengths = np.fromiter((len(e.token_ids) for e in entries), dtype=np.int64, count=len(entries))
+        batch_starts = np.cumsum(lengths) - lengths
+        if order is not None:
+            token_order = np.concatenate([np.arange(batch_starts[i], batch_starts[i] + lengths[i]) for i in order])
+            tokens, positions, slots = tokens[token_order], positions[token_order], slots[token_order]
+            moved = np.cumsum(lengths[order]) - lengths[order]
+            starts = np.empty_like(batch_starts)
+            starts[order] = moved
+            entries = [entries[i] for i in order]
+        else:
+            starts = batch_starts
 
         num_seqs = len(entries)
         # Block tables live in a device arena between calls; only changed entries travel.
@@ -389,12 +426,11 @@ class ModelRunner:
             normed = _rms_norm(hidden, ffn_norm, eps)
             hidden = hidden + (_silu(normed @ gate) * (normed @ up)) @ down
 
-        wanted, names, offset = [], [], 0
-        for entry in entries:
+        wanted, names = [], []
+        for start, entry in zip(starts.tolist(), batch.entries):
             if entry.logits_index is not None:
-                wanted.append(offset + entry.logits_index)
+                wanted.append(start + entry.logits_index)
                 names.append(entry.seq_id)
-            offset += len(entry.token_ids)
         if not wanted:
             return [], None
         rows = torch.tensor(wanted, dtype=torch.int64).to(self.device)

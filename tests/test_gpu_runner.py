@@ -189,6 +189,53 @@ def test_a_shared_prompt_decodes_through_prefix_tiles(device) -> None:
         assert float(np.max(np.abs(got[name] - want[name]))) < TOLERANCE, name
 
 
+def test_interleaved_sharers_are_grouped_into_prefix_tiles(device) -> None:
+    """The same 20 sharing sequences, interleaved in the batch with 8 unrelated ones: the runner
+    orders the sharers next to each other, so their prompt is still read as prefix tiles, and
+    every logits row (returned in batch order) matches the NumPy runner."""
+    config = ModelConfig(vocab_size=64, d_model=64, n_layers=1, n_heads=2, d_ff=64, max_seq_len=1024)
+    weights = random_weights(config, seed=5)
+    model, oracle = LanguageModel(config, weights), OracleModel(config, weights)
+    block = 16
+    gpu = ModelRunner(model, num_blocks=160, block_size=block, device=device)
+    cpu = OracleRunner(oracle, num_blocks=160, block_size=block)
+    rng = np.random.default_rng(12)
+    prompt = [int(t) for t in rng.integers(0, 64, 544)]
+    shared = tuple(range(34))
+    suffixes = [int(n) for n in rng.integers(3, 20, 20)]
+    tables = [shared + (34 + 2 * i, 35 + 2 * i) for i in range(20)]
+    others = [(f"o{i}", tuple(range(80 + 3 * i, 83 + 3 * i)), int(rng.integers(10, 40))) for i in range(8)]
+    setup = [ExecutionBatch((BatchEntry("p", tuple(prompt), tuple(range(544)), shared, None),)),
+             ExecutionBatch(tuple(
+                 BatchEntry(f"c{i}", tuple(int(t) for t in rng.integers(0, 64, n)),
+                            tuple(range(544, 544 + n)), tables[i], n - 1)
+                 for i, n in enumerate(suffixes))),
+             ExecutionBatch(tuple(
+                 BatchEntry(name, tuple(int(t) for t in rng.integers(0, 64, n)), tuple(range(n)), table,
+                            n - 1)
+                 for name, table, n in others))]  # fmt: skip
+    for batch in setup:
+        gpu.execute(batch)
+        cpu.execute(batch)
+    children = [BatchEntry(f"c{i}", (int(rng.integers(0, 64)),), (544 + n,), tables[i], 0)
+                for i, n in enumerate(suffixes)]  # fmt: skip
+    strangers = [BatchEntry(name, (int(rng.integers(0, 64)),), (n,), table, 0) for name, table, n in others]
+    mixed = []
+    for i, child in enumerate(children):
+        mixed.append(child)
+        if i % 3 == 1 and strangers:
+            mixed.append(strangers.pop())
+    mixed += strangers
+    decode = ExecutionBatch(tuple(mixed))
+    got = gpu.execute(decode)
+    plan = gpu.last_plan
+    assert plan.tiles.shape[0] == 1 and plan.tiles[0, 1] == 20 and plan.tiles[0, 3] >= 1
+    assert list(got) == [e.seq_id for e in mixed]  # batch order
+    want = cpu.execute(decode)
+    for name in want:
+        assert float(np.max(np.abs(got[name] - want[name]))) < TOLERANCE, name
+
+
 def test_sharing_a_prefix_block_does_not_change_either_continuation(device, models) -> None:
     model, oracle = models
     rng = np.random.default_rng(12)

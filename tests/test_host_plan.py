@@ -242,3 +242,30 @@ def test_row_items_list_each_partition_full_ones_first() -> None:
     # a row whose first partition is past its visible keys has nothing left for the row pass
     assert ops.expand_rows(np.array([[5, 3]]), np.full(6, 1000), 512).tolist() == []
     assert ops.expand_rows(np.zeros((0, 2), np.int32), visible, 512).shape == (0, 2)
+
+
+def _entry(seq_id, table, tokens=1):
+    from paged_kv_serving_amd.runner import BatchEntry
+
+    start = len(table) * 16 - tokens
+    return BatchEntry(seq_id, tuple([1] * tokens), tuple(range(start, start + tokens)), tuple(table), tokens - 1)
+
+
+def test_shared_prefix_order_groups_decode_rows_that_share_leading_blocks() -> None:
+    from paged_kv_serving_amd.runner import shared_prefix_order
+
+    prefix = list(range(40))  # 640 tokens at block size 16: past the 512-token threshold
+    children = [_entry(f"c{i}", prefix + [100 + i]) for i in range(20)]
+    strangers = [_entry(f"s{i}", list(range(200 + 50 * i, 241 + 50 * i))) for i in range(20)]
+    prefill = _entry("p", list(range(2000, 2050)), tokens=30)
+    interleaved = [e for pair in zip(children, strangers) for e in pair] + [prefill]
+    order = shared_prefix_order(interleaved, 16)
+    assert order is not None and sorted(order) == list(range(len(interleaved)))
+    names = [interleaved[i].seq_id for i in order]
+    first = names.index("c0")
+    assert names[first : first + 20] == [f"c{i}" for i in range(20)]  # stable within the group
+    assert names[-1] == "p"  # non-decode entries keep their place after the decode rows
+    # Already grouped, no sharing, or too few decode rows: the batch order is kept.
+    assert shared_prefix_order(children + strangers + [prefill], 16) is None
+    assert shared_prefix_order(strangers, 16) is None
+    assert shared_prefix_order(interleaved[:10], 16) is None
