@@ -409,12 +409,17 @@ class BatchPlan:
     short_rows: bool = False
 
 
-def _common_prefix(a: np.ndarray, b: np.ndarray) -> int:
-    n = min(a.size, b.size)
-    if n == 0:
-        return 0
-    differ = np.flatnonzero(a[:n] != b[:n])
-    return int(differ[0]) if differ.size else n
+def _padded_tables(tables, sid: np.ndarray, used: np.ndarray, width: int) -> np.ndarray:
+    """``[len(sid), width]`` int64 matrix of the used table entries of sequences ``sid``, -1 past
+    each one's used length. A 2-D table array (the runner's arena) is gathered in one step."""
+    if isinstance(tables, np.ndarray) and tables.ndim == 2 and tables.shape[1] >= width:
+        out = tables[sid, :width].astype(np.int64)
+    else:
+        out = np.full((sid.size, width), -1, dtype=np.int64)
+        for r, (s, n) in enumerate(zip(sid.tolist(), used.tolist())):
+            out[r, :n] = np.asarray(tables[s][:n])
+    out[np.arange(width)[None, :] >= used[:, None]] = -1
+    return out
 
 
 def _prefix_groups(
@@ -423,32 +428,56 @@ def _prefix_groups(
     """Runs of consecutive row-pass rows whose sequences' used tables agree over a common
     prefix of at least ``min_blocks`` blocks. Returns
     ``[(first index into rows, row count, common blocks)]``; a member whose whole used table is
-    a prefix of the first row's constrains nothing (its visible keys end inside the prefix)."""
-    groups = []
+    a prefix of the first row's constrains nothing (its visible keys end inside the prefix).
+
+    Vectorised: one comparison of every row with the one before finds where a run can start;
+    from each such start the rows that follow are compared with it a chunk at a time until one
+    fails, so a batch without sharing costs one pass over its tables."""
     count = rows.shape[0]
-    i = 0
-    while i < count:
-        t0 = int(rows[i, 0])
-        s0 = int(seq[t0])
-        first = np.asarray(tables[s0][: used_blocks[s0]])
-        common = int(used_blocks[s0])
-        j = i + 1
-        while j < count and int(rows[j, 0]) == int(rows[j - 1, 0]) + 1:
-            sj = int(seq[int(rows[j, 0])])
-            if used_blocks[sj] and first.size and tables[sj][0] != first[0]:
-                break  # nothing shared (the common case, without an array comparison)
-            mine = np.asarray(tables[sj][: used_blocks[sj]])
-            shared = _common_prefix(first, mine)
-            limit = common if shared == mine.size else min(common, shared)
-            if limit < min_blocks:
+    if count < MIN_SHARED_ROWS:
+        return []
+    qrow = np.asarray(rows[:, 0], dtype=np.int64)
+    sid = np.asarray(seq, dtype=np.int64)[qrow]
+    used = np.asarray(used_blocks, dtype=np.int64)[sid]
+    width = int(used.max())
+    if width < min_blocks:
+        return []
+    table = _padded_tables(tables, sid, used, width)
+    col = np.arange(width)
+    consecutive = qrow[1:] == qrow[:-1] + 1  # row k + 1 continues row k
+    both = np.minimum(used[1:], used[:-1])
+    same = (table[1:] == table[:-1]) & (col[None, :] < both[:, None])
+    lead_prev = np.where(same.all(axis=1), both, same.argmin(axis=1))
+    # A run can start at k only if row k + 1 joins it: it shares enough, or its whole table is
+    # a prefix of row k's.
+    starts = np.flatnonzero(consecutive & ((lead_prev >= min_blocks) | (lead_prev == used[1:])))
+    stops = np.flatnonzero(~consecutive)  # row k + 1 does not continue row k
+    groups = []
+    free = 0  # rows before this index already belong to a group
+    chunk = 32
+    for k in starts.tolist():
+        if k < free:
+            continue
+        after = stops[np.searchsorted(stops, k)] + 1 if stops.size and stops[-1] >= k else count
+        first = table[k]
+        common = int(used[k])
+        joined = 0
+        for lo in range(k + 1, after, chunk):
+            hi = min(lo + chunk, after)
+            eq = (table[lo:hi] == first) & (col[None, :] < used[k])
+            lead = np.where(eq.all(axis=1), width, eq.argmin(axis=1))
+            limit = np.where(lead >= used[lo:hi], common, lead)  # a whole-prefix member: no limit
+            running = np.minimum.accumulate(np.minimum(limit, common))
+            bad = np.flatnonzero(running < min_blocks)
+            take = int(bad[0]) if bad.size else hi - lo
+            if take:
+                common = int(running[take - 1])
+            joined += take
+            if bad.size:
                 break
-            common = limit
-            j += 1
-        if j - i >= MIN_SHARED_ROWS and common >= min_blocks:
-            groups.append((i, j - i, common))
-            i = j
-        else:
-            i += 1
+        if joined + 1 >= MIN_SHARED_ROWS and common >= min_blocks:
+            groups.append((k, joined + 1, common))
+            free = k + joined + 1
     return groups
 
 
@@ -564,6 +593,9 @@ def plan_batch(
     row pass at the first partition after it. Prefill tiles become whole tiles when there are at
     least WHOLE_TILE_GROUPS (tile, head) pairs. ``query_positions`` (optional) narrows the merge
     list to rows that span several partitions. A nonzero ``partition_size`` is kept as given.
+    Shared-prefix groups and the load hint are only searched for when two row-pass sequences
+    start with the same block; tables that repeat ids only past their first block get the
+    streaming hint (the hint chooses a load path, never a result).
     """
     seq = np.asarray(query_seq, dtype=np.int64)
     contexts = np.asarray(context_lens, dtype=np.int64)
@@ -573,8 +605,21 @@ def plan_batch(
     visible = _visible(seq, contexts, query_positions)
     tiles = _whole_tiles(tiles, seq, visible, num_heads)
     used_blocks = -(-contexts // block_size)
+    # Prefix sharing gives sequences the same first block (a shared block's whole prefix is
+    # shared), so when the row pass's sequences all start in different blocks there is neither a
+    # shared-prefix group nor a repeated block to look for: the common decode step skips both.
+    row_seqs = np.unique(seq[rows[:, 0]]) if rows.size else np.zeros(0, np.int64)
+    starting = row_seqs[used_blocks[row_seqs] > 0]
+    if starting.size == 0:
+        first_blocks = np.zeros(0, np.int64)
+    elif isinstance(tables, np.ndarray) and tables.ndim == 2:
+        first_blocks = tables[starting, 0]
+    else:
+        first_blocks = np.fromiter((tables[s][0] for s in starting.tolist()), dtype=np.int64,
+                                   count=starting.size)  # fmt: skip
+    may_share = np.unique(first_blocks).size < first_blocks.size
     groups = []
-    if rows.shape[0] >= MIN_SHARED_ROWS and tiles_supported(head_dim):
+    if may_share and rows.shape[0] >= MIN_SHARED_ROWS and tiles_supported(head_dim):
         groups = _prefix_groups(rows, seq, tables, used_blocks, -(-MIN_SHARED_TOKENS // block_size))
     present = np.unique(seq)
     partition = partition_size
@@ -598,16 +643,18 @@ def plan_batch(
         tiles = np.concatenate([tiles, np.asarray(prefix_tiles, dtype=np.int32)])
     # The load hint looks at what the row pass still reads: each row-pass sequence's blocks from
     # its first partition on (tiles read their keys once per 64 rows either way).
-    row_seqs = seq[rows[:, 0]] if rows.size else np.zeros(0, np.int64)
-    firsts = rows[:, 1].astype(np.int64) * partition // block_size
-    seen = set()
-    parts = []
-    for s, f in zip(row_seqs.tolist(), firsts.tolist()):
-        if (s, f) in seen:
-            continue
-        seen.add((s, f))
-        parts.append(np.asarray(tables[s][f : used_blocks[s]]))
-    ids = np.concatenate(parts) if parts else np.zeros(0, np.int64)
+    ids = np.zeros(0, np.int64)
+    if rows.size and may_share:
+        firsts = rows[:, 1].astype(np.int64) * partition // block_size
+        span = int(firsts.max()) + 1
+        pair = np.unique(seq[rows[:, 0]] * span + firsts)  # distinct (sequence, first block)
+        pair_seq, pair_first = pair // span, pair % span
+        reads = used_blocks[pair_seq]
+        width = int(reads.max())
+        if width > 0:
+            table = _padded_tables(tables, pair_seq, reads, width)
+            col = np.arange(width)[None, :]
+            ids = table[(col >= pair_first[:, None]) & (col < reads[:, None])]
     merge = merge_rows_for(seq.size, tiles, visible, int(partition))
     items = expand_rows(rows, visible, int(partition))
     short = False

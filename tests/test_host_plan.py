@@ -162,6 +162,29 @@ def test_no_sharing_keeps_the_plain_plan() -> None:
     _covered(plan, np.arange(64), contexts, 16)
 
 
+def test_plan_hint_sees_shared_blocks_in_list_and_arena_tables() -> None:
+    """A batch of forks (every sequence reads the same 40 blocks, then 5 of its own) keeps the
+    cached-load hint in both table forms; distinct first blocks, zero contexts and an empty
+    arena give the streaming hint and no prefix tiles."""
+    rng = np.random.default_rng(8)
+    contexts = np.full(24, 45 * 16)
+    tables = _tables(contexts, 16, rng, shared_prefix=40)
+    arena = np.zeros((24, 50), np.int32)
+    for i, t in enumerate(tables):
+        arena[i, : len(t)] = t
+    for form in (tables, arena):
+        plan = ops.plan_batch(np.arange(24), 128, 8, form, contexts, 16, partition_size=1024)
+        assert plan.tiles.shape == (0, 4), "a 640-key prefix fills no 1024-key partition"
+        assert plan.shared_kv == ops.batch_hints(tables, contexts, 8, 16)[1] is True
+    private = _tables(contexts, 16, rng)
+    plan = ops.plan_batch(np.arange(24), 128, 8, private, contexts, 16)
+    assert not plan.shared_kv and plan.tiles.shape == (0, 4)
+    zero = np.zeros(24, np.int64)
+    for form in (private, np.zeros((24, 0), np.int32)):
+        plan = ops.plan_batch(np.arange(24), 128, 8, form, zero, 16)
+        assert not plan.shared_kv and plan.tiles.shape == (0, 4)
+
+
 def test_every_public_name_of_ops_exists_and_the_workspace_helper_answers() -> None:
     missing = [name for name in ops.__all__ if not hasattr(ops, name)]
     assert not missing
@@ -269,3 +292,71 @@ def test_shared_prefix_order_groups_decode_rows_that_share_leading_blocks() -> N
     assert shared_prefix_order(children + strangers + [prefill], 16) is None
     assert shared_prefix_order(strangers, 16) is None
     assert shared_prefix_order(interleaved[:10], 16) is None
+
+
+def _groups_scalar(rows, seq, tables, used_blocks, min_blocks):
+    """Row-by-row restatement of the shared-prefix run search (the vectorised planner must
+    find exactly these runs)."""
+    def common(a, b):
+        n = min(len(a), len(b))
+        for k in range(n):
+            if a[k] != b[k]:
+                return k
+        return n
+
+    groups, count, i = [], rows.shape[0], 0
+    while i < count:
+        s0 = int(seq[int(rows[i, 0])])
+        first = list(tables[s0][: used_blocks[s0]])
+        shared_len, j = len(first), i + 1
+        while j < count and int(rows[j, 0]) == int(rows[j - 1, 0]) + 1:
+            sj = int(seq[int(rows[j, 0])])
+            mine = list(tables[sj][: used_blocks[sj]])
+            c = common(first, mine)
+            limit = shared_len if c == len(mine) else min(shared_len, c)
+            if limit < min_blocks:
+                break
+            shared_len = limit
+            j += 1
+        if j - i >= ops.MIN_SHARED_ROWS and shared_len >= min_blocks:
+            groups.append((i, j - i, shared_len))
+            i = j
+        else:
+            i += 1
+    return groups
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_vectorised_prefix_groups_match_the_row_by_row_search(seed) -> None:
+    rng = np.random.default_rng(seed)
+    min_blocks = int(rng.integers(2, 12))
+    trunks = [list(rng.integers(0, 10**6, 40)) for _ in range(3)]
+    tables = []
+    while len(tables) < 40 + seed * 3:  # runs of rows that branch off one trunk, or private rows
+        length = int(rng.integers(1, 30))
+        trunk = trunks[int(rng.integers(0, len(trunks)))] if rng.random() < 0.7 else None
+        for _ in range(length):
+            if trunk is None:
+                t = list(rng.integers(2 * 10**6, 3 * 10**6, int(rng.integers(0, 50))))
+            else:
+                r = rng.random()  # mostly long branches; some end inside the trunk or diverge early
+                keep = int(rng.integers(min_blocks, 41)) if r < 0.8 else int(rng.integers(0, min_blocks + 2))
+                tail = 0 if r > 0.9 else int(rng.integers(0, 20))
+                t = trunk[:keep] + list(rng.integers(10**6, 2 * 10**6, tail))
+            tables.append(np.asarray(t, dtype=np.int64))
+    n = len(tables)
+    used = np.asarray([t.size for t in tables])
+    seq = np.arange(n)
+    rows = np.zeros((n, 2), np.int32)
+    gaps = np.cumsum(rng.random(n) < 0.05)  # now and then a query row the row pass does not hold
+    rows[:, 0] = np.arange(n) + gaps
+    seq_full = np.zeros(int(rows[:, 0].max()) + 1, dtype=np.int64)
+    seq_full[rows[:, 0]] = seq
+    want = _groups_scalar(rows, seq_full, tables, used, min_blocks)
+    assert ops._prefix_groups(rows, seq_full, tables, used, min_blocks) == want
+    # the 2-D arena form of the same tables gives the same runs
+    width = max(1, int(used.max()))
+    arena = np.full((n, width + 3), -5, dtype=np.int64)
+    for s, t in enumerate(tables):
+        arena[s, : t.size] = t
+    assert ops._prefix_groups(rows, seq_full, arena, used, min_blocks) == want
