@@ -423,7 +423,8 @@ def _padded_tables(tables, sid: np.ndarray, used: np.ndarray, width: int) -> np.
 
 
 def _prefix_groups(
-    rows: np.ndarray, seq: np.ndarray, tables, used_blocks: np.ndarray, min_blocks: int
+    rows: np.ndarray, seq: np.ndarray, tables, used_blocks: np.ndarray, min_blocks: int,
+    padded: tuple | None = None,
 ) -> list:
     """Runs of consecutive row-pass rows whose sequences' used tables agree over a common
     prefix of at least ``min_blocks`` blocks. Returns
@@ -432,7 +433,8 @@ def _prefix_groups(
 
     Vectorised: one comparison of every row with the one before finds where a run can start;
     from each such start the rows that follow are compared with it a chunk at a time until one
-    fails, so a batch without sharing costs one pass over its tables."""
+    fails, so a batch without sharing costs one pass over its tables. ``padded`` (sorted
+    sequence ids, their :func:`_padded_tables` matrix) reuses tables the caller already padded."""
     count = rows.shape[0]
     if count < MIN_SHARED_ROWS:
         return []
@@ -442,7 +444,10 @@ def _prefix_groups(
     width = int(used.max())
     if width < min_blocks:
         return []
-    table = _padded_tables(tables, sid, used, width)
+    if padded is None:
+        table = _padded_tables(tables, sid, used, width)
+    else:
+        table = padded[1][np.searchsorted(padded[0], sid), :width]
     col = np.arange(width)
     consecutive = qrow[1:] == qrow[:-1] + 1  # row k + 1 continues row k
     both = np.minimum(used[1:], used[:-1])
@@ -618,9 +623,14 @@ def plan_batch(
         first_blocks = np.fromiter((tables[s][0] for s in starting.tolist()), dtype=np.int64,
                                    count=starting.size)  # fmt: skip
     may_share = np.unique(first_blocks).size < first_blocks.size
+    padded = None  # the row pass's sequences' used tables, padded once for both searches below
+    if may_share:
+        held = used_blocks[row_seqs]
+        padded = (row_seqs, _padded_tables(tables, row_seqs, held, int(held.max())))
     groups = []
     if may_share and rows.shape[0] >= MIN_SHARED_ROWS and tiles_supported(head_dim):
-        groups = _prefix_groups(rows, seq, tables, used_blocks, -(-MIN_SHARED_TOKENS // block_size))
+        groups = _prefix_groups(rows, seq, tables, used_blocks, -(-MIN_SHARED_TOKENS // block_size),
+                                padded)  # fmt: skip
     present = np.unique(seq)
     partition = partition_size
     if partition == 0:
@@ -650,11 +660,9 @@ def plan_batch(
         pair = np.unique(seq[rows[:, 0]] * span + firsts)  # distinct (sequence, first block)
         pair_seq, pair_first = pair // span, pair % span
         reads = used_blocks[pair_seq]
-        width = int(reads.max())
-        if width > 0:
-            table = _padded_tables(tables, pair_seq, reads, width)
-            col = np.arange(width)[None, :]
-            ids = table[(col >= pair_first[:, None]) & (col < reads[:, None])]
+        table = padded[1][np.searchsorted(padded[0], pair_seq)]
+        col = np.arange(table.shape[1])[None, :]
+        ids = table[(col >= pair_first[:, None]) & (col < reads[:, None])]
     merge = merge_rows_for(seq.size, tiles, visible, int(partition))
     items = expand_rows(rows, visible, int(partition))
     short = False
