@@ -10,7 +10,10 @@ A step is the data path of that iteration, in one call:
                                 tables (row pass + reduce pass)
 
 The standalone pkv_append on the same tokens is timed outside the steps and reported as
-``append_us`` / ``append_gbps``.
+``append_us`` / ``append_gbps`` (4.2 MB: launch-bound), beside the attention call without the
+fused append (``fused_append_cost_us`` is the difference). ``append_bulk`` times pkv_append of
+every context token of the 64 sequences (the append of a 64 x 4k-context prefill, 9.8 GB) for
+the append's HBM rate at that scale.
 
 ``value`` is decode tokens per second (64 tokens per step). The roofline object is for the
 dominant kernel, the attention pass: achieved = algorithmic bytes per launch (each sequence's
@@ -291,15 +294,19 @@ def run_attention_config(args, batch, *, metric: str, workload: str, dtype: str,
         # The standalone append kernel on the same tokens, outside the timed steps, for the
         # record (it rewrites the same rows with the same values). Each one is queued behind an
         # attention call, so the GPU does not wait for the host to submit it.
+        # The same attention without the fused append is timed between them, so the fused
+        # append's own cost is the difference of the two attention times.
         plain = attention_call(batch, args, out, workspace)
-        standalone = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
-        for e0, e1 in standalone:
+        standalone = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+        for p0, e0, e1 in standalone:
+            p0.record(stream)
             plain()
             e0.record(stream)
             append()
             e1.record(stream)
         torch.cuda.synchronize()
-        append_ms = float(np.mean([e0.elapsed_time(e1) for e0, e1 in standalone]))
+        plain_ms = float(np.mean([p0.elapsed_time(e0) for p0, e0, _ in standalone]))
+        append_ms = float(np.mean([e0.elapsed_time(e1) for _, e0, e1 in standalone]))
     else:
         append_ms = float(np.mean([events[0].elapsed_time(events[1]) for events in marks]))
     tokens = batch.num_queries
@@ -334,6 +341,8 @@ def run_attention_config(args, batch, *, metric: str, workload: str, dtype: str,
         "attention_frac_of_peak": round(achieved / HBM_PEAK_GBPS, 4),
         "attention_tokens_per_s": round(tokens / (attention_ms * 1e-3), 1),
         "append_fused_into_attention": fused,
+        **({"attention_without_append_ms": round(plain_ms, 4),
+            "fused_append_cost_us": round((attention_ms - plain_ms) * 1e3, 2)} if fused else {}),
         "append_us": round(append_ms * 1e3, 2),
         "append_gbps": round(append_bytes / (append_ms * 1e-3) / 1e9, 1),
         "roofline": {
@@ -365,6 +374,7 @@ def config2(args) -> dict:
         "paged attention in one call (append fused into the row pass)",
     )  # fmt: skip
     result["unit"] = "decode tokens/s"
+    result.update(bulk_append_timing(args, batch))
     result["roofline"]["traffic"] = traffic_from_profiles()
     result["roofline"]["kernel"] = (
         "row_partial_kernel<float,128> (append fused) + reduce_kernel<128>"
@@ -448,6 +458,48 @@ def prefill_tiles_alone_ms(args, batch) -> float:
         e1.record(stream)
     torch.cuda.synchronize()
     return float(np.mean([e0.elapsed_time(e1) for e0, e1 in marks]))
+
+
+def bulk_append_timing(args, batch) -> dict:
+    """``pkv_append`` of every context token of the batch, into the batch's own slots: the append
+    a prefill of all its sequences makes (149,713 tokens for config 2, 9.8 GB moved). Timed with
+    HIP events on the launching stream after the attention steps; it overwrites the pool rows
+    with fresh values, which nothing timed afterwards reads for its result."""
+    import torch
+
+    from paged_kv_serving_amd import ops
+
+    device = batch.queries.device
+    _, block_size, heads, dim = batch.key_cache.shape
+    slots = np.concatenate([
+        np.asarray(table, dtype=np.int64)[np.arange(c) // block_size] * block_size + np.arange(c) % block_size
+        for table, c in zip(batch.host_tables, batch.host_context.tolist())
+    ])  # fmt: skip
+    tokens = slots.size
+    gen = torch.Generator(device=device)
+    gen.manual_seed(args.seed + 1)
+    keys = torch.randn((tokens, heads, dim), generator=gen, device=device)
+    values = torch.randn((tokens, heads, dim), generator=gen, device=device)
+    slot_mapping = torch.from_numpy(slots).to(device)
+
+    def run() -> None:
+        ops.append_kv(batch.key_cache, batch.value_cache, keys, values, slot_mapping)
+
+    for _ in range(max(args.warmup, 1)):
+        run()
+    torch.cuda.synchronize()
+    ms = timed(run, max(5, min(args.steps, 20)), torch.cuda.current_stream(device))
+    moved = 2 * tokens * heads * dim * (4 + batch.key_cache.element_size()) + tokens * 8
+    del keys, values, slot_mapping
+    gbps = moved / (ms * 1e-3) / 1e9
+    return {
+        "append_bulk": {
+            "tokens": tokens, "us": round(ms * 1e3, 1), "gbps": round(gbps, 1),
+            "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4), "bytes": moved,
+            "what": "pkv_append of all context tokens of the 64 sequences (a 64 x 4k-context "
+            "prefill's append), read k, v + write k, v + slots",
+        }
+    }  # fmt: skip
 
 
 def rope_append_timing(args, batch) -> dict:
