@@ -31,6 +31,7 @@ attention pass with that ceiling on the same GPU (boxes differ by a few percent)
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--partition P] [--no-cpu]
                        [--no-ceiling]
        python bench.py --config {1,3,4,5}   (the other BASELINE.json configurations)
+       python bench.py --micro              (the reference's published micro-benchmarks)
 """
 
 from __future__ import annotations
@@ -64,6 +65,8 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--cpu-seqs", type=int, default=64, help="sequences in the CPU sample")
     parser.add_argument("--cpu-repeats", type=int, default=5, help="timed CPU steps (median)")
+    parser.add_argument("--micro", action="store_true",
+                        help="the reference's published micro-benchmarks of the path instead")
     parser.add_argument("--no-ceiling", action="store_true",
                         help="skip the read_ceiling child process (configs 2 and 5)")
     return parser.parse_args()
@@ -662,6 +665,170 @@ def config1(args) -> dict:
     }
 
 
+def _host_timed(function, runs: int, warmup: int = 5) -> dict:
+    """p50/p95 microseconds of host wall time per call, ``perf_counter_ns`` around each call
+    after ``warmup`` calls: the reference's timing method (bench/bench_baseline.py:70-83)."""
+    for _ in range(warmup):
+        function()
+    samples = []
+    for _ in range(runs):
+        start = time.perf_counter_ns()
+        function()
+        samples.append(time.perf_counter_ns() - start)
+    micros = np.asarray(samples, dtype=np.float64) / 1e3
+    return {"runs": runs, "p50_us": round(float(np.percentile(micros, 50)), 1),
+            "p95_us": round(float(np.percentile(micros, 95)), 1)}  # fmt: skip
+
+
+def micro(args) -> dict:
+    """The reference's published micro-benchmarks of this path, at their own shapes and with
+    their own timing method, run on this build (bench/bench_baseline.py:86-186; the published
+    figures are bench/results/latest.json on an i5-8500, 1 BLAS thread). Calls that return a
+    result the caller can read include the synchronisation that makes it readable."""
+    import torch
+
+    from paged_kv_serving_amd import ops
+    from paged_kv_serving_amd.attention import paged_attention
+    from paged_kv_serving_amd.blocks import BlockManager, RecordingBlockStore
+    from paged_kv_serving_amd.config import EngineConfig, ModelConfig
+    from paged_kv_serving_amd.engine import Engine
+    from paged_kv_serving_amd.model import LanguageModel, random_weights
+    from paged_kv_serving_amd.runner import BatchEntry, ExecutionBatch, ModelRunner
+    from paged_kv_serving_amd.sequence import Request, SamplingParams
+
+    device = torch.device("cuda", 0)
+    out: dict = {}
+
+    # paged_attention_decode_256ctx (bench_baseline.py:122-136): 1 query, 4 heads x 32, 16 blocks.
+    rng = np.random.default_rng(0)
+    heads, dim, block_size, blocks = 4, 32, 16, 16
+    keys = rng.standard_normal((blocks, block_size, heads, dim)).astype(np.float32)
+    values = rng.standard_normal((blocks, block_size, heads, dim)).astype(np.float32)
+    query = rng.standard_normal((1, heads, dim)).astype(np.float32)
+    positions = np.asarray([blocks * block_size - 1], dtype=np.int64)
+    table = np.arange(blocks, dtype=np.int64)
+    context, scale = blocks * block_size, dim**-0.5
+    host_call = lambda: paged_attention(query, positions, keys, values, table, context, scale)  # noqa: E731
+    d_keys, d_values, d_query, d_pos, d_table = (
+        torch.from_numpy(a).to(device) for a in (keys, values, query, positions, table)
+    )
+
+    def resident_call():
+        paged_attention(d_query, d_pos, d_keys, d_values, d_table, context, scale)
+        torch.cuda.synchronize(device)
+
+    q32, seq32 = d_query.contiguous(), torch.zeros(1, dtype=torch.int32, device=device)
+    pos32, table32 = d_pos.to(torch.int32), d_table.to(torch.int32).reshape(1, -1).contiguous()
+    ctx32 = torch.tensor([context], dtype=torch.int32, device=device)
+    result_buffer = torch.empty_like(q32)
+    kernel_call = lambda: ops.paged_attention_ragged(  # noqa: E731
+        q32, pos32, seq32, d_keys, d_values, table32, ctx32, scale, max_context_len=context,
+        out=result_buffer)  # fmt: skip
+    for _ in range(10):
+        kernel_call()
+    torch.cuda.synchronize(device)
+    out["paged_attention_decode_256ctx"] = {
+        "reference_p50_us": 129.4, "reference_p95_us": 171.9,
+        "host_arrays": _host_timed(host_call, 2000),
+        "device_resident": _host_timed(resident_call, 2000),
+        "gpu_us_per_call": round(timed(kernel_call, 200, torch.cuda.current_stream(device)) * 1e3, 2),
+        "what": "host_arrays: the drop-in call on NumPy arrays (K/V copied in, output copied "
+        "back); device_resident: device tensors in and out, synchronised; gpu_us_per_call: HIP "
+        "events around back-to-back ragged calls",
+    }  # fmt: skip
+
+    # block_allocate_free_16 and copy_on_write_block (bench_baseline.py:86-110): host bookkeeping.
+    manager = BlockManager(num_blocks=4096, block_size=16, store=RecordingBlockStore())
+
+    def alloc_cycle():
+        manager.free_many(manager.allocate_many(16))
+
+    def cow_cycle(blocks_manager):
+        block = blocks_manager.allocate()
+        blocks_manager.incref(block)
+        blocks_manager.incref(block)
+        private = blocks_manager.prepare_for_write(block)
+        blocks_manager.free(private)
+        blocks_manager.free(block)
+        blocks_manager.free(block)
+
+    out["block_allocate_free_16"] = {"reference_p50_us": 5.4, "reference_p95_us": 5.5,
+                                     **_host_timed(alloc_cycle, 5000)}  # fmt: skip
+    out["copy_on_write_block"] = {"reference_p50_us": 1.8, "reference_p95_us": 2.0,
+                                  **_host_timed(lambda: cow_cycle(manager), 5000)}  # fmt: skip
+
+    # The same COW cycle with the bytes moved: the block store is a ModelRunner (4 layers,
+    # 4 heads x 32, block 16: 32 KiB per block and layer for K+V), flushed and synchronised.
+    config = ModelConfig(vocab_size=512, d_model=128, n_layers=4, n_heads=4, d_ff=320, max_seq_len=1024)
+    model = LanguageModel(config, random_weights(config, seed=0))
+    store = ModelRunner(model, num_blocks=4096, block_size=16, device=device)
+    moving = BlockManager(num_blocks=4096, block_size=16, store=store)
+
+    def cow_with_copy():
+        cow_cycle(moving)
+        store.flush_copies()
+        torch.cuda.synchronize(device)
+
+    out["copy_on_write_block"]["with_device_copy"] = _host_timed(cow_with_copy, 2000)
+
+    # engine_iteration_128_tokens (bench_baseline.py:163-186): 16 decode rows + a 112-token
+    # prefill through a 4-layer d_model-128 model (the reference's random checkpoint shape).
+    runner = ModelRunner(model, num_blocks=256, block_size=16, device=device)
+    entries = [BatchEntry(seq_id=f"decode-{i}", token_ids=(1,), positions=(63,),
+                          block_table=tuple(range(i * 4, i * 4 + 4)), logits_index=0)
+               for i in range(16)]  # fmt: skip
+    entries.append(BatchEntry(seq_id="prefill", token_ids=tuple(range(1, 113)),
+                              positions=tuple(range(112)), block_table=tuple(range(128, 135)),
+                              logits_index=111))  # fmt: skip
+    batch = ExecutionBatch(tuple(entries))
+    out["engine_iteration_128_tokens"] = {"reference_p50_us": 12330.9, "reference_p95_us": 13426.5,
+                                          **_host_timed(lambda: runner.execute(batch), 20, warmup=3)}  # fmt: skip
+
+    # engine_throughput_24_requests (bench_baseline.py:189-214): 24 requests of 48 prompt tokens,
+    # 12 greedy tokens each, under the reference's bench engine limits.
+    limits = EngineConfig(block_size=16, num_blocks=192, max_batched_tokens=128, max_running_seqs=12,
+                          max_prompt_tokens=192, max_new_tokens=24, max_context_tokens=256)  # fmt: skip
+
+    def requests():
+        draw = np.random.default_rng(4)
+        return [Request(f"bench-{i}", tuple(int(v) for v in draw.integers(1, 256, 48)),
+                        SamplingParams(max_new_tokens=12, seed=i)) for i in range(24)]  # fmt: skip
+
+    Engine(model, limits).generate(requests())  # warm the kernels and the allocator
+    torch.cuda.synchronize(device)
+    engine = Engine(model, limits)
+    start = time.perf_counter()
+    outputs = engine.generate(requests())
+    torch.cuda.synchronize(device)
+    elapsed = time.perf_counter() - start
+    generated = sum(len(s) for samples in outputs.values() for s in samples)
+    out["engine_throughput_24_requests"] = {
+        "reference_tokens_per_second": 1453.36, "tokens_per_second": round(generated / elapsed, 1),
+        "output_tokens": generated, "seconds": round(elapsed, 4), "iterations": engine.iterations,
+    }  # fmt: skip
+
+    latency = out["paged_attention_decode_256ctx"]["device_resident"]["p50_us"]
+    return {
+        "metric": "reference micro-benchmarks of the path (bench/bench_baseline.py) at their own "
+        "shapes: paged_attention_decode_256ctx p50 latency, device-resident",
+        "value": latency,
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": 2000,
+        "warmup": 5,
+        "ms_per_step": round(latency / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(latency / 129.4, 4),  # the published p50 of the same benchmark
+        "dtype": "f32",
+        "data": "synthetic: the reference benchmarks' own seeded inputs and random-init weights",
+        "config": {"workload": "reference micro-benchmarks: decode 256 ctx (1 query, 4 heads x "
+                   "32, 16 blocks), allocate/free 16, COW cycle, 128-token iteration and 24-request "
+                   "engine run on a 4-layer d_model-128 vocab-512 model"},  # fmt: skip
+        "micro": out,
+    }
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -674,6 +841,10 @@ def main() -> int:
         return 2
     import torch
 
+    if args.micro:
+        torch.cuda.set_device(0)
+        print(json.dumps(micro(args)), flush=True)
+        return 0
     # The ceiling runs first, in its own process, before this one allocates its pools.
     ceiling = read_ceiling() if args.config in (2, 5) and not args.no_ceiling else None
     torch.cuda.set_device(0)

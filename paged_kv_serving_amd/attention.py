@@ -75,7 +75,7 @@ def paged_attention(
     query_seq = torch.zeros(num_queries, dtype=torch.int32, device=device)
     used = -(-context_len // block_size)
     table = _to_device(block_table, torch.int32, device)[:used].reshape(1, used).contiguous()
-    context = torch.tensor([context_len], dtype=torch.int32).to(device)
+    context = torch.full((1,), int(context_len), dtype=torch.int32, device=device)  # no host copy
     out = ops.paged_attention_ragged(
         q, positions, query_seq, keys, values, table, context, scale,
         max_context_len=int(context_len),
