@@ -9,9 +9,35 @@ namespace {
 
 constexpr int kCopyThreads = 256;
 
+// 16-byte unit of the byte-moving kernels, as a vector type the non-temporal builtins accept.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+#ifndef PKV_APPEND_UNROLL
+#define PKV_APPEND_UNROLL 1
+#endif
+#ifndef PKV_APPEND_NT
+#define PKV_APPEND_NT 0  // bit 0: non-temporal loads of the new rows; bit 1: of the pool stores
+#endif
+constexpr int kAppendUnroll = PKV_APPEND_UNROLL;
+
+__device__ __forceinline__ u32x4 append_load(const void* p) {
+  const auto* q = static_cast<const u32x4*>(p);
+  if constexpr ((PKV_APPEND_NT & 1) != 0) return __builtin_nontemporal_load(q);
+  return *q;
+}
+__device__ __forceinline__ void append_store(void* p, u32x4 v) {
+  auto* q = static_cast<u32x4*>(p);
+  if constexpr ((PKV_APPEND_NT & 2) != 0) {
+    __builtin_nontemporal_store(v, q);
+  } else {
+    *q = v;
+  }
+}
+
 // --------------------------------------------------------------------------------------------
 // Append. grid = (tokens * chunks of a token row, 2); y selects keys (0) or values (1).
-// Each thread converts/copies VEC consecutive elements of one token's [heads * head_dim] row.
+// Each thread moves kAppendUnroll vectors of VEC consecutive elements of one token's
+// [heads * head_dim] row, all loads issued before the stores.
 // --------------------------------------------------------------------------------------------
 template <typename SrcT, typename DstT>
 struct Mover;
@@ -20,33 +46,40 @@ struct Mover;
 template <>
 struct Mover<float, float> {
   static constexpr int kVec = 4;
-  __device__ static void move(float* dst, const float* src) {
-    *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
-  }
+  struct In {
+    u32x4 v;
+  };
+  __device__ static In load(const float* src) { return {append_load(src)}; }
+  __device__ static void store(float* dst, In in) { append_store(dst, in.v); }
 };
 
 // bfloat16 -> bfloat16, 8 elements (16 bytes); bits are copied unchanged.
 template <>
 struct Mover<uint16_t, uint16_t> {
   static constexpr int kVec = 8;
-  __device__ static void move(uint16_t* dst, const uint16_t* src) {
-    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
-  }
+  struct In {
+    u32x4 v;
+  };
+  __device__ static In load(const uint16_t* src) { return {append_load(src)}; }
+  __device__ static void store(uint16_t* dst, In in) { append_store(dst, in.v); }
 };
 
 // float32 -> bfloat16, 8 elements (32 bytes in, 16 bytes out), round to nearest even.
 template <>
 struct Mover<float, uint16_t> {
   static constexpr int kVec = 8;
-  __device__ static void move(uint16_t* dst, const float* src) {
-    const float4 a = reinterpret_cast<const float4*>(src)[0];
-    const float4 b = reinterpret_cast<const float4*>(src)[1];
-    uint4 o;
-    o.x = f32_to_bf16_bits(a.x) | (f32_to_bf16_bits(a.y) << 16);
-    o.y = f32_to_bf16_bits(a.z) | (f32_to_bf16_bits(a.w) << 16);
-    o.z = f32_to_bf16_bits(b.x) | (f32_to_bf16_bits(b.y) << 16);
-    o.w = f32_to_bf16_bits(b.z) | (f32_to_bf16_bits(b.w) << 16);
-    *reinterpret_cast<uint4*>(dst) = o;
+  struct In {
+    u32x4 a, b;
+  };
+  __device__ static In load(const float* src) { return {append_load(src), append_load(src + 4)}; }
+  __device__ static void store(uint16_t* dst, In in) {
+    const auto bits = [](unsigned int x) { return f32_to_bf16_bits(__uint_as_float(x)); };
+    u32x4 o;
+    o.x = bits(in.a.x) | (bits(in.a.y) << 16);
+    o.y = bits(in.a.z) | (bits(in.a.w) << 16);
+    o.z = bits(in.b.x) | (bits(in.b.y) << 16);
+    o.w = bits(in.b.z) | (bits(in.b.w) << 16);
+    append_store(dst, o);
   }
 };
 
@@ -68,13 +101,24 @@ __global__ __launch_bounds__(kCopyThreads) void append_kernel(
   const bool is_value = blockIdx.y != 0;
   const SrcT* src = is_value ? new_values + token * value_stride : new_keys + token * key_stride;
   DstT* dst = (is_value ? value_pool : key_pool) + slot * row_elems;
-  constexpr int kVec = kVectorized ? Mover<SrcT, DstT>::kVec : 1;
-  const int64_t e = (chunk * kCopyThreads + threadIdx.x) * kVec;
-  if (e >= row_elems) return;
   if constexpr (kVectorized) {
-    Mover<SrcT, DstT>::move(dst + e, src + e);
+    using M = Mover<SrcT, DstT>;
+    constexpr int64_t kStep = static_cast<int64_t>(kCopyThreads) * M::kVec;
+    const int64_t first = chunk * kStep * kAppendUnroll + threadIdx.x * M::kVec;
+    typename M::In buf[kAppendUnroll];
+#pragma unroll
+    for (int u = 0; u < kAppendUnroll; ++u) {
+      const int64_t e = first + u * kStep;
+      if (e < row_elems) buf[u] = M::load(src + e);
+    }
+#pragma unroll
+    for (int u = 0; u < kAppendUnroll; ++u) {
+      const int64_t e = first + u * kStep;
+      if (e < row_elems) M::store(dst + e, buf[u]);
+    }
   } else {
-    move_one(dst + e, src + e);
+    const int64_t e = chunk * kCopyThreads + threadIdx.x;
+    if (e < row_elems) move_one(dst + e, src + e);
   }
 }
 
@@ -88,7 +132,7 @@ int launch_append(void* key_pool, void* value_pool, int64_t num_slots, const voi
                           value_stride % kVec == 0 &&
                           aligned16(key_pool) && aligned16(value_pool) && aligned16(new_keys) &&
                           aligned16(new_values);
-  const int64_t per_block = static_cast<int64_t>(kCopyThreads) * (vectorized ? kVec : 1);
+  const int64_t per_block = static_cast<int64_t>(kCopyThreads) * (vectorized ? kVec * kAppendUnroll : 1);
   const int64_t chunks = (row_elems + per_block - 1) / per_block;
   if (chunks * num_tokens > 0x7fffffff) return PKV_EUNSUPPORTED;
   const dim3 grid(static_cast<uint32_t>(chunks * num_tokens), 2);
@@ -120,9 +164,6 @@ int launch_append(void* key_pool, void* value_pool, int64_t num_slots, const voi
 #ifndef PKV_COPY_UNROLL
 #define PKV_COPY_UNROLL 4
 #endif
-
-// 16-byte unit of the block copy, as a vector type the non-temporal builtins accept.
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // The source block is read once, so it is loaded non-temporally; the destination is read again
 // by the same step's attention, so by default it is stored normally and may stay in the caches.
