@@ -863,3 +863,29 @@ def test_config4_prefix_sharing_cow_then_decode(device) -> None:
     # a plan's partition indices belong to its partition size
     with pytest.raises(ValueError, match="partition"):
         ops.paged_attention_ragged(*common, max_context_len=d.max_context_len, plan=plan, partition_size=512)
+
+
+def test_empty_inputs_leave_the_pools_alone(device) -> None:
+    """Zero tokens, zero copy pairs, zero query rows and zero logits rows are no-ops: every entry
+    point returns before launching, and the pools keep their bits."""
+    say("empty inputs")
+    heads, dim, block = 2, 32, 4
+    keys = torch.randn((1, 6, block, heads, dim), device=device)
+    values = torch.randn_like(keys)
+    before = (keys.clone(), values.clone())
+    none = torch.zeros((0, heads, dim), device=device)
+    no_slots = torch.zeros(0, dtype=torch.int64, device=device)
+    ops.append_kv(keys[0], values[0], none, none, no_slots)
+    ops.copy_blocks(keys, values, torch.zeros((0, 2), dtype=torch.int64, device=device))
+    cos = torch.ones((8, dim // 2), device=device)
+    rotated = ops.rope_append(keys[0], values[0], none, none, none, no_slots, cos, torch.zeros_like(cos), no_slots)
+    assert rotated.shape == (0, heads, dim)
+    out = ops.paged_attention_ragged(
+        none, torch.zeros(0, dtype=torch.int32, device=device), torch.zeros(0, dtype=torch.int32, device=device),
+        keys[0], values[0], torch.zeros((1, 2), dtype=torch.int32, device=device),
+        torch.ones(1, dtype=torch.int32, device=device), dim**-0.5, max_context_len=1,
+    )  # fmt: skip
+    assert out.shape == (0, heads, dim)
+    assert ops.greedy_tokens(torch.zeros((0, 16), device=device)).shape == (0,)
+    torch.cuda.synchronize()
+    assert torch.equal(keys, before[0]) and torch.equal(values, before[1])
