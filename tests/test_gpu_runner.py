@@ -323,3 +323,48 @@ def test_reference_error_messages(device, models) -> None:
     with pytest.raises(ValueError, match="onto itself"):
         runner.copy_block(1, 1)
     assert runner.execute(ExecutionBatch(())) == {}
+
+
+def test_steps_from_changing_worker_threads_match_one_thread(device, models) -> None:
+    """The reference's service calls execute() from asyncio.to_thread workers that change between
+    steps (service.py:265-296). The same steps, each run on a fresh thread, give the same logits
+    bit for bit as on the calling thread, and leave the same pool bytes."""
+    import threading
+
+    model, _ = models
+    rng = np.random.default_rng(21)
+    prompts = [[int(t) for t in rng.integers(0, 64, n)] for n in (23, 9, 17)]
+    tables = [(0, 1, 2, 3), (4, 5), (6, 7, 8)]
+
+    def steps():
+        """A chunked prefill of three prompts, then four decode steps of all three."""
+        out = [ExecutionBatch(tuple(
+            BatchEntry(f"s{i}", tuple(p[:8]), tuple(range(8)), tables[i], 7) for i, p in enumerate(prompts)))]  # fmt: skip
+        out.append(ExecutionBatch(tuple(
+            BatchEntry(f"s{i}", tuple(p[8:]), tuple(range(8, len(p))), tables[i], len(p) - 9)
+            for i, p in enumerate(prompts) if len(p) > 8)))  # fmt: skip
+        for step in range(4):
+            out.append(ExecutionBatch(tuple(
+                BatchEntry(f"s{i}", (step + i,), (len(p) + step,), tables[i], 0) for i, p in enumerate(prompts))))  # fmt: skip
+        return out
+
+    def run(on_threads: bool):
+        runner = ModelRunner(model, num_blocks=10, block_size=BLOCK_SIZE, device=device)
+        results = []
+        for batch in steps():
+            if on_threads:
+                box = {}
+                worker = threading.Thread(target=lambda b=batch: box.update(r=runner.execute(b)))
+                worker.start()
+                worker.join()
+                results.append(box["r"])
+            else:
+                results.append(runner.execute(batch))
+        return results, [runner.block_fingerprint(b) for b in range(10)]
+
+    main, main_prints = run(False)
+    threaded, thread_prints = run(True)
+    assert main_prints == thread_prints
+    for a, b in zip(main, threaded):
+        assert a.keys() == b.keys()
+        assert all(np.array_equal(a[k], b[k]) for k in a)
