@@ -12,6 +12,8 @@ hand-built plans of the other kernel tests.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -23,7 +25,7 @@ from paged_kv_serving_amd import ops
 pytestmark = pytest.mark.gpu
 
 FP32_TOL = 1e-5
-CASES = 48
+CASES = int(os.environ.get("PKV_RANDOM_CASES", "48"))  # seeds 0 .. CASES - 1
 
 
 def _random_batch(rng):
