@@ -368,3 +368,36 @@ def test_steps_from_changing_worker_threads_match_one_thread(device, models) -> 
     for a, b in zip(main, threaded):
         assert a.keys() == b.keys()
         assert all(np.array_equal(a[k], b[k]) for k in a)
+
+
+def test_a_bfloat16_pool_matches_the_numpy_runner_on_rounded_kv(device, models, monkeypatch) -> None:
+    """ModelRunner with bfloat16 K/V storage through chunked prefill and decode steps, against
+    the NumPy runner whose append stores each key and value rounded to bfloat16 (nearest even):
+    the north star's bar for bfloat16 KV, at the reference's logits tolerance."""
+    import oracle.runner as oracle_runner
+    from oracle.bf16 import bf16_round
+
+    model, oracle = models
+    plain_append = oracle_runner.append
+
+    def rounded_append(key_pool, value_pool, slots, keys, values):
+        plain_append(key_pool, value_pool, slots, bf16_round(np.asarray(keys, dtype=np.float32)),
+                     bf16_round(np.asarray(values, dtype=np.float32)))  # fmt: skip
+
+    monkeypatch.setattr(oracle_runner, "append", rounded_append)
+    rng = np.random.default_rng(33)
+    prompts = [[int(t) for t in rng.integers(0, 64, n)] for n in (29, 13)]
+    tables = [(0, 1, 2, 3, 4), (5, 6, 7)]
+    gpu = ModelRunner(model, num_blocks=8, block_size=BLOCK_SIZE, kv_dtype=torch.bfloat16, device=device)
+    cpu = OracleRunner(oracle, num_blocks=8, block_size=BLOCK_SIZE)
+    batches = [ExecutionBatch(tuple(BatchEntry(f"s{i}", tuple(p), tuple(range(len(p))), tables[i], len(p) - 1)
+                                    for i, p in enumerate(prompts)))]  # fmt: skip
+    for step in range(6):
+        batches.append(ExecutionBatch(tuple(
+            BatchEntry(f"s{i}", (step * 3 + i,), (len(p) + step,), tables[i], 0) for i, p in enumerate(prompts))))  # fmt: skip
+    for batch in batches:
+        want, got = cpu.execute(batch), gpu.execute(batch)
+        assert want.keys() == got.keys()
+        for name in want:
+            assert float(np.max(np.abs(got[name] - want[name]))) < TOLERANCE, name
+    assert gpu.kv_dtype == torch.bfloat16
