@@ -23,13 +23,7 @@ oracle's NumPy restatement of the reference path (reference attention.py:42-121 
 tile_blocks 8, plus the runner.py:195-196 append) on a bounded sample of the same workload,
 single-threaded BLAS as the reference pins it.
 
-For configs 2 and 5 the run first starts paged_kv_serving_amd/read_ceiling in a child process: a
-load-only kernel that reads the same amount of K/V in the row pass's exact pattern with no
-arithmetic, next to contiguous streams. ``attention_frac_of_read_ceiling`` compares the
-attention pass with that ceiling on the same GPU (boxes differ by a few percent).
-
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--partition P] [--no-cpu]
-                       [--no-ceiling]
        python bench.py --config {1,3,4,5}   (the other BASELINE.json configurations)
        python bench.py --micro              (the reference's published micro-benchmarks)
 """
@@ -67,8 +61,6 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--cpu-repeats", type=int, default=5, help="timed CPU steps (median)")
     parser.add_argument("--micro", action="store_true",
                         help="the reference's published micro-benchmarks of the path instead")
-    parser.add_argument("--no-ceiling", action="store_true",
-                        help="skip the read_ceiling child process (configs 2 and 5)")
     return parser.parse_args()
 
 
@@ -81,27 +73,6 @@ def traffic_from_profiles() -> float | None:
         return float(json.loads(path.read_text())["bytes_per_launch"])
     except (KeyError, ValueError, json.JSONDecodeError):
         return None
-
-
-def read_ceiling() -> dict | None:
-    """The load-only read rates of this GPU (paged_kv_serving_amd/read_ceiling, a child process
-    built by __graft_entry__.build()): contiguous streams and the row pass's exact read pattern
-    without its arithmetic. None when the executable is missing or fails."""
-    import subprocess
-
-    from paged_kv_serving_amd import _native
-
-    if not _native.READ_CEILING_PATH.exists():
-        return None
-    try:
-        done = subprocess.run([str(_native.READ_CEILING_PATH)], capture_output=True, text=True,
-                              timeout=300, check=False)  # fmt: skip
-    except subprocess.TimeoutExpired:
-        return None
-    lines = [line for line in done.stdout.splitlines() if line.startswith("{")]
-    if done.returncode != 0 or not lines:
-        return None
-    return json.loads(lines[-1])
 
 
 def copy_peak(device) -> dict:
@@ -845,19 +816,13 @@ def main() -> int:
         torch.cuda.set_device(0)
         print(json.dumps(micro(args)), flush=True)
         return 0
-    # The ceiling runs first, in its own process, before this one allocates its pools.
-    ceiling = read_ceiling() if args.config in (2, 5) and not args.no_ceiling else None
     torch.cuda.set_device(0)
     runners = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
     result = runners[args.config](args)
-    if ceiling is not None:
-        key = "paged_f32_head_slice_gbps" if args.config == 2 else "paged_bf16_two_heads_gbps"
-        result["read_ceiling"] = ceiling
-        result["attention_frac_of_read_ceiling"] = round(result["roofline"]["achieved"] / ceiling[key], 4)
     if args.config == 2:
+        # The known-size dispatch that calibrates the rocprofv3 FETCH_SIZE/WRITE_SIZE counters.
         peak = copy_peak(torch.device("cuda", 0))
         result["copy_peak_gbps"] = peak["copy_peak_gbps"]
-        result["attention_frac_of_copy_peak"] = round(result["roofline"]["achieved"] / peak["copy_peak_gbps"], 4)
         if not args.no_cpu:
             result["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(result), flush=True)

@@ -34,9 +34,6 @@ REPO_ROOT = PACKAGE_DIR.parent
 CSRC = PACKAGE_DIR / "csrc"
 INCLUDE = REPO_ROOT / "include"
 LIB_PATH = PACKAGE_DIR / "libpkv.so"
-# A standalone load-only benchmark of the row pass's read pattern (not part of the library).
-READ_CEILING_SOURCE = CSRC / "read_ceiling.hip"
-READ_CEILING_PATH = PACKAGE_DIR / "read_ceiling"
 SOURCES = (
     CSRC / "pkv_copy.hip", CSRC / "pkv_rope.hip", CSRC / "pkv_attention.hip", CSRC / "pkv_sample.hip"
 )
@@ -125,26 +122,6 @@ def build(*, verbose: bool = False) -> Path:
     with _LOCK:
         _LIB = None  # reload on next use
     return LIB_PATH
-
-
-def build_read_ceiling(*, verbose: bool = False) -> Path:
-    """Compile the ``read_ceiling`` benchmark executable next to this file. Always recompiles."""
-    flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
-    with tempfile.NamedTemporaryFile(dir=PACKAGE_DIR, prefix=".read_ceiling.", suffix=".tmp", delete=False) as handle:
-        tmp = Path(handle.name)
-    try:
-        command = [_hipcc(), *flags, "-o", str(tmp), str(READ_CEILING_SOURCE)]
-        result = subprocess.run(command, capture_output=True, text=True, check=False)
-        lines = [line for line in result.stderr.splitlines() if "packed-fp32-ops" not in line]
-        if (verbose or result.returncode != 0) and lines:
-            print("\n".join(lines))
-        if result.returncode != 0:
-            raise NativeLibraryError(f"hipcc failed with exit code {result.returncode}")
-        os.replace(tmp, READ_CEILING_PATH)
-    finally:
-        if tmp.exists():
-            tmp.unlink()
-    return READ_CEILING_PATH
 
 
 _LOCK = threading.Lock()

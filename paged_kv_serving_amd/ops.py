@@ -645,6 +645,15 @@ def plan_batch(
         parts = common * block_size // partition
         if parts < 1:
             continue
+        # A tile reads its keys through its first row's table, so every 64-row tile must start at
+        # a row whose table covers the parts * partition prefix keys. A member whose whole table
+        # ends inside the prefix may sit inside a tile, never at its start: the group ends before
+        # such a row, and the rows from there on stay in the row pass from partition 0.
+        need = -(-parts * partition // block_size)
+        for offset in range(TILE_ROWS, count, TILE_ROWS):
+            if used_blocks[seq[rows[start + offset, 0]]] < need:
+                count = offset
+                break
         rows[start : start + count, 1] = parts
         first_row = int(rows[start, 0])
         for offset in range(0, count, TILE_ROWS):

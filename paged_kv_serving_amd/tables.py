@@ -48,6 +48,9 @@ class BlockTableArena:
         self._held: list[tuple[int, ...]] = [()] * rows
         self._last_use = np.zeros(rows, dtype=np.int64)
         self._step = 0
+        # Rows whose recorded content an update changed and no apply() has written to the device
+        # yet. If the caller fails between the two, the next update forgets what they hold.
+        self._unapplied: list[int] = []
 
     @property
     def num_rows(self) -> int:
@@ -64,7 +67,12 @@ class BlockTableArena:
     def update(self, entries) -> TableUpdate:
         """Assign a row to every entry (by ``seq_id``) and record the table entries that differ
         from what the row holds. The host mirror is updated at once; the device rows change when
-        the returned indices and values are applied with :meth:`apply`."""
+        the returned indices and values are applied with :meth:`apply`. If the previous update
+        was never applied (its caller raised in between), the rows it changed are treated as
+        holding nothing, so their whole tables are uploaded again."""
+        for row in self._unapplied:
+            self._held[row] = ()
+        self._unapplied = []
         self._step += 1
         step = self._step
         count = len(entries)
@@ -98,6 +106,7 @@ class BlockTableArena:
                 index_parts.append(np.arange(row * width + start, row * width + len(new), dtype=np.int64))
                 value_parts.append(segment)
             self._held[row] = new
+            self._unapplied.append(row)
         if index_parts:
             index = np.concatenate(index_parts)
             values = np.fromiter((v for part in value_parts for v in part), dtype=np.int32, count=index.size)
@@ -110,6 +119,7 @@ class BlockTableArena:
         """Write an update's values (device int32) at its flat indices (device int64)."""
         if index.numel():
             self.tables.view(-1).index_copy_(0, index, values)
+        self._unapplied = []
 
     def used_blocks(self, rows: np.ndarray, block_counts: np.ndarray) -> np.ndarray:
         """The first ``block_counts[i]`` table entries of arena row ``rows[i]``, concatenated."""

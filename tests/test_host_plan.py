@@ -151,6 +151,25 @@ def test_a_member_whose_table_ends_inside_the_prefix_still_joins() -> None:
     _covered(plan, seq, contexts, 16)
 
 
+def test_no_tile_starts_at_a_member_whose_table_ends_inside_the_prefix() -> None:
+    """80 decode rows share 39 blocks, but row 64 holds only block 0 (context 16). A tile reads
+    keys through its first row's table, so row 64 must not start the second 64-row tile: every
+    tile's first row has to cover the tile's parts * partition keys."""
+    rng = np.random.default_rng(8)
+    contexts = np.full(80, 39 * 16 + 40)
+    tables = _tables(contexts, 16, rng, shared_prefix=39)
+    contexts[64] = 16
+    tables[64] = tables[64][:1]
+    seq = np.arange(80)
+    plan = ops.plan_batch(seq, 128, 32, tables, contexts, 16)
+    P = plan.partition_size
+    assert plan.tiles.shape[0] >= 1
+    for first, count, _, end in plan.tiles.tolist():
+        assert end != ops.TILE_WHOLE
+        assert len(tables[first]) * 16 >= end * P, f"tile at row {first} reads past its table"
+    _covered(plan, seq, contexts, 16)
+
+
 def test_no_sharing_keeps_the_plain_plan() -> None:
     rng = np.random.default_rng(6)
     contexts = rng.integers(512, 4097, 64)

@@ -49,6 +49,17 @@ def test_only_changed_entries_travel() -> None:
     assert shrunk.index.size == 0
 
 
+def test_an_update_never_applied_is_sent_again() -> None:
+    """A caller that raises between update() and apply() leaves the device rows stale; the next
+    update must not trust what the host mirror recorded for them."""
+    arena = BlockTableArena("cpu", rows=4, width=8)
+    step(arena, [Entry("a", (5, 6, 7))])
+    arena.update([Entry("a", (5, 6, 7, 8)), Entry("b", (1, 2))])  # never applied
+    again = step(arena, [Entry("a", (5, 6, 7, 8)), Entry("b", (1, 2))])
+    assert again.values.tolist() == [5, 6, 7, 8, 1, 2], "both rows travel whole"
+    assert step(arena, [Entry("a", (5, 6, 7, 8))]).index.size == 0
+
+
 def test_least_recently_used_rows_are_reclaimed_and_refilled() -> None:
     arena = BlockTableArena("cpu", rows=2, width=4)
     rows_a = step(arena, [Entry("a", (1, 2))]).rows
