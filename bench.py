@@ -575,54 +575,57 @@ def config4(args) -> dict:
     return result
 
 
+TRACES = ROOT / "tests" / "golden" / "traces"
+
+
 def config1(args) -> dict:
-    """The whole engine (config 1): continuous batching + chunked prefill over the GPU runner."""
+    """Config 1 end to end: the reference engine's recorded run (scheduler decisions, KV-cache
+    calls, batches; tests/golden/traces/config1.json) replayed through this package's
+    KVCacheManager and the GPU ModelRunner, sampling greedily on the device. The timed run is
+    the whole replay: allocator calls, 42 iterations of the 2-layer model, one int32 per sampled
+    row back to the host."""
     import torch
 
-    from paged_kv_serving_amd.config import EngineConfig, ModelConfig
-    from paged_kv_serving_amd.engine import Engine
-    from paged_kv_serving_amd.model import LanguageModel, random_weights
-    from paged_kv_serving_amd.sequence import Request, SamplingParams
+    from paged_kv_serving_amd.replay import Trace, TraceReplay
+    from paged_kv_serving_amd.runner import ModelRunner
 
-    config = ModelConfig(vocab_size=256, d_model=128, n_layers=2, n_heads=4, d_ff=320, max_seq_len=1024)
-    model = LanguageModel(config, random_weights(config, seed=0))
+    trace = Trace.load(TRACES / "config1.json")
+    model = trace.language_model()
+    device = torch.device("cuda", 0)
 
-    def requests():
-        rng = np.random.default_rng(args.seed)
-        out = []
-        for i in range(32):
-            length = int(rng.integers(16, 129))
-            tokens = tuple(int(t) for t in rng.integers(0, 256, length))
-            out.append(Request(f"req{i}", tokens, SamplingParams(max_new_tokens=32, seed=i)))
-        return out
+    def one_run(check: bool):
+        runner = ModelRunner(model, num_blocks=trace.engine["num_blocks"], block_size=trace.engine["block_size"],
+                             device=device)  # fmt: skip
+        result = TraceReplay(trace, runner, check=check, greedy=True).run()
+        torch.cuda.synchronize(device)
+        return result
 
-    for _ in range(max(1, args.warmup // 5)):
-        Engine(model, EngineConfig()).generate(requests())
-    torch.cuda.synchronize()
+    checked = one_run(True)  # bit-exact tables, slots and allocator state; warms the kernels
+    for _ in range(max(0, args.warmup // 5 - 1)):
+        one_run(False)
     runs = max(1, args.steps // 10)
-    seconds, iterations, generated = [], 0, 0
+    seconds = []
     for _ in range(runs):
-        engine = Engine(model, EngineConfig())
         start = time.perf_counter()
-        outputs = engine.generate(requests())
-        torch.cuda.synchronize()
+        result = one_run(False)
         seconds.append(time.perf_counter() - start)
-        iterations = engine.iterations
-        generated = sum(len(s) for samples in outputs.values() for s in samples)
     elapsed = float(np.median(seconds))
+    generated = len(result.greedy)
+    agree = sum(int(tok == trace.tokens[sid][ctx]) for tok, (sid, ctx) in zip(checked.greedy, checked.row_seqs))
     return {
         "metric": "engine output tokens/s, continuous batching + chunked prefill (config 1)",
         "value": round(generated / elapsed, 1),
         "unit": "output tokens/s",
         "n_gpus": 1,
-        "steps": iterations,
+        "steps": result.iterations,
         "warmup": max(1, args.warmup // 5),
-        "ms_per_step": round(elapsed * 1e3 / iterations, 4),
+        "ms_per_step": round(elapsed * 1e3 / result.iterations, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: random_weights(seed 0), 32 prompts U[16,128] random tokens (seed 0)",
+        "data": "synthetic: random_weights(seed 0), 32 prompts U[16,128] random tokens (seed 0), "
+        "the reference engine's recorded schedule",
         "config": {
             "workload": "config1: fp32 decoder vocab 256, d_model 128, 2 layers, 4 heads x 32, d_ff "
             "320; 32 requests, 32 greedy tokens each; EngineConfig defaults (block 16, 512 blocks, "
@@ -631,6 +634,7 @@ def config1(args) -> dict:
         },
         "seconds_per_run": round(elapsed, 4),
         "generated_tokens": generated,
+        "greedy_tokens_equal_reference": f"{agree}/{len(checked.greedy)}",
         "reference_published": "1453.36 output tok/s (engine_throughput_24_requests, i5-8500, "
         "bench/results/latest.json:46-53; a different workload, for orientation only)",
     }
@@ -652,20 +656,19 @@ def _host_timed(function, runs: int, warmup: int = 5) -> dict:
 
 
 def micro(args) -> dict:
-    """The reference's published micro-benchmarks of this path, at their own shapes and with
-    their own timing method, run on this build (bench/bench_baseline.py:86-186; the published
-    figures are bench/results/latest.json on an i5-8500, 1 BLAS thread). Calls that return a
-    result the caller can read include the synchronisation that makes it readable."""
+    """The reference's published benchmarks of this path (bench/bench_baseline.py: the paged
+    decode, the copy-on-write cycle, the two correctness gaps, and the 128-token iteration of the
+    runner), at their own shapes and with their own timing method, run on this build. The
+    published figures are bench/results/latest.json (an i5-8500, 1 BLAS thread). Calls that
+    return a result the caller can read include the synchronisation that makes it readable."""
     import torch
 
     from paged_kv_serving_amd import ops
     from paged_kv_serving_amd.attention import paged_attention
     from paged_kv_serving_amd.blocks import BlockManager, RecordingBlockStore
-    from paged_kv_serving_amd.config import EngineConfig, ModelConfig
-    from paged_kv_serving_amd.engine import Engine
-    from paged_kv_serving_amd.model import LanguageModel, random_weights
+    from paged_kv_serving_amd.equivalence import max_logit_gap, rows_logit_gap
+    from paged_kv_serving_amd.replay import Trace, TraceReplay
     from paged_kv_serving_amd.runner import BatchEntry, ExecutionBatch, ModelRunner
-    from paged_kv_serving_amd.sequence import Request, SamplingParams
 
     device = torch.device("cuda", 0)
     out: dict = {}
@@ -708,11 +711,8 @@ def micro(args) -> dict:
         "events around back-to-back ragged calls",
     }  # fmt: skip
 
-    # block_allocate_free_16 and copy_on_write_block (bench_baseline.py:86-110): host bookkeeping.
+    # copy_on_write_block (bench_baseline.py:97-110): host bookkeeping of one COW cycle.
     manager = BlockManager(num_blocks=4096, block_size=16, store=RecordingBlockStore())
-
-    def alloc_cycle():
-        manager.free_many(manager.allocate_many(16))
 
     def cow_cycle(blocks_manager):
         block = blocks_manager.allocate()
@@ -723,15 +723,17 @@ def micro(args) -> dict:
         blocks_manager.free(block)
         blocks_manager.free(block)
 
-    out["block_allocate_free_16"] = {"reference_p50_us": 5.4, "reference_p95_us": 5.5,
-                                     **_host_timed(alloc_cycle, 5000)}  # fmt: skip
     out["copy_on_write_block"] = {"reference_p50_us": 1.8, "reference_p95_us": 2.0,
                                   **_host_timed(lambda: cow_cycle(manager), 5000)}  # fmt: skip
 
+    # The reference benchmarks' model: build_random_checkpoint(seed 3, max_seq_len 512), i.e.
+    # random_weights(seed 3) of a 4-layer d_model-128 vocab-512 decoder; the engine-equivalence
+    # trace holds the SHA-256 of the reference's weights, which language_model() checks.
+    trace = Trace.load(TRACES / "engine_equivalence.json")
+    model = trace.language_model()
+
     # The same COW cycle with the bytes moved: the block store is a ModelRunner (4 layers,
     # 4 heads x 32, block 16: 32 KiB per block and layer for K+V), flushed and synchronised.
-    config = ModelConfig(vocab_size=512, d_model=128, n_layers=4, n_heads=4, d_ff=320, max_seq_len=1024)
-    model = LanguageModel(config, random_weights(config, seed=0))
     store = ModelRunner(model, num_blocks=4096, block_size=16, device=device)
     moving = BlockManager(num_blocks=4096, block_size=16, store=store)
 
@@ -743,7 +745,7 @@ def micro(args) -> dict:
     out["copy_on_write_block"]["with_device_copy"] = _host_timed(cow_with_copy, 2000)
 
     # engine_iteration_128_tokens (bench_baseline.py:163-186): 16 decode rows + a 112-token
-    # prefill through a 4-layer d_model-128 model (the reference's random checkpoint shape).
+    # prefill through the 4-layer model: one ModelRunner.execute, logits back on the host.
     runner = ModelRunner(model, num_blocks=256, block_size=16, device=device)
     entries = [BatchEntry(seq_id=f"decode-{i}", token_ids=(1,), positions=(63,),
                           block_table=tuple(range(i * 4, i * 4 + 4)), logits_index=0)
@@ -755,27 +757,37 @@ def micro(args) -> dict:
     out["engine_iteration_128_tokens"] = {"reference_p50_us": 12330.9, "reference_p95_us": 13426.5,
                                           **_host_timed(lambda: runner.execute(batch), 20, warmup=3)}  # fmt: skip
 
-    # engine_throughput_24_requests (bench_baseline.py:189-214): 24 requests of 48 prompt tokens,
-    # 12 greedy tokens each, under the reference's bench engine limits.
-    limits = EngineConfig(block_size=16, num_blocks=192, max_batched_tokens=128, max_running_seqs=12,
-                          max_prompt_tokens=192, max_new_tokens=24, max_context_tokens=256)  # fmt: skip
+    # paged_vs_reference_equivalence (bench_baseline.py:217-238): 4 prompts from default_rng(5),
+    # each through the paged runner whole, token by token, in 7/5/13/rest chunks and over a
+    # reversed block table, against one dense pass (float32 torch on the device).
+    draw = np.random.default_rng(5)
+    vocab = min(model.config.vocab_size, 256)
+    worst = 0.0
+    for _ in range(4):
+        length = int(draw.integers(20, 120))
+        tokens = [int(v) for v in draw.integers(1, vocab, length)]
+        for chunks in ([length], [1] * length, [7, 5, 13, length - 25]):
+            if any(size < 1 for size in chunks):
+                continue
+            worst = max(worst, max_logit_gap(model, tokens, device=device, block_size=16, chunks=chunks))
+        blocks_needed = -(-length // 16)
+        worst = max(worst, max_logit_gap(model, tokens, device=device, block_size=16,
+                                         block_order=list(reversed(range(blocks_needed)))))  # fmt: skip
+    out["paged_vs_reference_equivalence"] = {"runs": 4, "max_abs_logit_gap": float(f"{worst:.4g}"),
+                                             "reference_max_abs_logit_gap": 2.444e-06}  # fmt: skip
 
-    def requests():
-        draw = np.random.default_rng(4)
-        return [Request(f"bench-{i}", tuple(int(v) for v in draw.integers(1, 256, 48)),
-                        SamplingParams(max_new_tokens=12, seed=i)) for i in range(24)]  # fmt: skip
-
-    Engine(model, limits).generate(requests())  # warm the kernels and the allocator
-    torch.cuda.synchronize(device)
-    engine = Engine(model, limits)
-    start = time.perf_counter()
-    outputs = engine.generate(requests())
-    torch.cuda.synchronize(device)
-    elapsed = time.perf_counter() - start
-    generated = sum(len(s) for samples in outputs.values() for s in samples)
-    out["engine_throughput_24_requests"] = {
-        "reference_tokens_per_second": 1453.36, "tokens_per_second": round(generated / elapsed, 1),
-        "output_tokens": generated, "seconds": round(elapsed, 4), "iterations": engine.iterations,
+    # engine_vs_reference_equivalence (bench_baseline.py:241-284): the reference engine's run
+    # over a 20-block pool (preemption, prefix hits, forked samples), replayed through this
+    # package's KV-cache manager and the GPU runner; every sampled row against the dense pass.
+    replay_runner = ModelRunner(model, num_blocks=trace.engine["num_blocks"], block_size=16, device=device)
+    replayed = TraceReplay(trace, replay_runner).run()
+    gap, rows_checked = rows_logit_gap(model, replayed.rows, replayed.row_seqs, trace.tokens, device)
+    out["engine_vs_reference_equivalence"] = {
+        "runs": 1, "max_abs_logit_gap": float(f"{gap:.4g}"), "rows_checked": float(rows_checked),
+        "preemptions": float(trace.summary["preemptions"]), "prefix_hit_blocks": float(trace.summary["prefix_hit_blocks"]),
+        "cow_copies": replayed.copies,
+        "max_abs_gap_to_reference_rows": float(f"{float(np.max(np.abs(np.stack(replayed.rows) - trace.logits))):.4g}"),
+        "reference_max_abs_logit_gap": 3.248e-06,
     }  # fmt: skip
 
     latency = out["paged_attention_decode_256ctx"]["device_resident"]["p50_us"]
@@ -793,9 +805,9 @@ def micro(args) -> dict:
         "vs_baseline": round(latency / 129.4, 4),  # the published p50 of the same benchmark
         "dtype": "f32",
         "data": "synthetic: the reference benchmarks' own seeded inputs and random-init weights",
-        "config": {"workload": "reference micro-benchmarks: decode 256 ctx (1 query, 4 heads x "
-                   "32, 16 blocks), allocate/free 16, COW cycle, 128-token iteration and 24-request "
-                   "engine run on a 4-layer d_model-128 vocab-512 model"},  # fmt: skip
+        "config": {"workload": "reference benchmarks of the path: decode 256 ctx (1 query, 4 heads "
+                   "x 32, 16 blocks), COW cycle, 128-token iteration, paged-vs-dense and "
+                   "engine-vs-dense logit gaps on a 4-layer d_model-128 vocab-512 model"},  # fmt: skip
         "micro": out,
     }
 

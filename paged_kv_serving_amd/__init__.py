@@ -11,6 +11,8 @@ reference's Python API:
     kvcache       KVCacheManager                            (reference engine/kvcache.py)
     prefix_cache  PrefixCache and the block hash chain      (reference engine/prefix_cache.py)
     attention     paged_attention                           (reference engine/attention.py)
+    equivalence   paged vs cache-free logits on the device  (reference engine/equivalence.py)
+    replay        a recorded reference serving run driven through the KV-cache manager and runner
     ops           tensor-level calls into libpkv.so
     workloads     seeded synthetic batches of the benchmark configurations
 

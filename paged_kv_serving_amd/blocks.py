@@ -1,21 +1,33 @@
-"""Reference-counted block allocator with copy-on-write, with the reference's API and semantics.
+"""The block pool behind every block table: owner counts, a FIFO ring of free ids, copy-on-write.
 
-Mirrors src/paged_kv_serving/engine/blocks.py:35-192. Block ids are handed out FIFO from a free
-list that starts as ``0, 1, ..., num_blocks - 1`` and receives a block back at its tail when the
-last owner frees it, so the sequence of ids (and therefore every block table built on top) is
-identical to the reference's for the same sequence of calls. ``prepare_for_write`` of a shared
-block allocates the destination, asks the store to copy, then drops the caller's reference on
-the source -- the exact order of blocks.py:156-165, which fixes which ids copies land in.
+Interface (kept so the reference's scheduler and tests run unchanged): ``BlockManager`` with
+``allocate / allocate_many / incref / free / free_many / prepare_for_write / ref_count /
+check_invariants / snapshot``, the ``BlockStore`` protocol, ``RecordingBlockStore`` and the two
+error types, with the reference's messages (src/paged_kv_serving/engine/blocks.py:35-192).
 
-The store behind copy-on-write is any object with ``copy_block(source, destination)``; the GPU
-:class:`~paged_kv_serving_amd.runner.ModelRunner` is one.
+Observable order (kept so block tables are bit-exact with the reference): ids start free in the
+order ``0 .. N-1``; allocation takes the oldest free id; a block whose last owner leaves goes
+behind every other free id; a write to a shared block allocates the destination, asks the store
+for the copy, then drops the writer's ownership of the source (blocks.py:148-165).
+
+Representation. The pool is two int32 arrays of ``num_blocks`` entries:
+
+* ``_owners[b]`` -- how many block tables (and prefix-cache entries) hold block ``b``; 0 = free;
+* ``_ring`` -- the free ids as a circular FIFO: the ``_nfree`` ids starting at ``_head``.
+
+A run of ``k`` ids leaves the ring as at most two slices, and a table's worth of blocks returns
+with one gather of their counts, so the per-iteration work of a large batch (hundreds of tables,
+thousands of blocks) is a few array operations instead of a Python loop per block. The same
+arrays answer the questions the KV-cache manager asks of whole tables at once ("which blocks of
+this write range are shared?", "which cached blocks does only the cache hold?") in one gather.
 """
 
 from __future__ import annotations
 
-from collections import deque
 from collections.abc import Iterable
 from typing import Protocol, runtime_checkable
+
+import numpy as np
 
 __all__ = [
     "BlockAllocationError",
@@ -25,25 +37,29 @@ __all__ = [
     "RecordingBlockStore",
 ]
 
+# Below this many ids a batch call runs the scalar path: a handful of NumPy calls costs more
+# than a short Python loop.
+_VECTOR_MIN = 8
+
 
 class BlockAllocationError(RuntimeError):
-    """No free block is available (blocks.py:35-36)."""
+    """The pool cannot supply the blocks asked for (reference blocks.py:35-36)."""
 
 
 class InvariantError(AssertionError):
-    """An allocator invariant is broken (blocks.py:39-40)."""
+    """The pool's bookkeeping is inconsistent, or a call would make it so (blocks.py:39-40)."""
 
 
 @runtime_checkable
 class BlockStore(Protocol):
-    """The bytes behind block ids (blocks.py:43-48)."""
+    """Whatever holds the bytes of the blocks (blocks.py:43-48): the GPU ModelRunner here."""
 
     def copy_block(self, source: int, destination: int) -> None:
         """Copy every byte of block ``source`` over block ``destination``."""
 
 
 class RecordingBlockStore:
-    """Records copies instead of moving bytes (blocks.py:51-60)."""
+    """A store that keeps the list of requested copies and moves no bytes (blocks.py:51-60)."""
 
     def __init__(self) -> None:
         self.copies: list[tuple[int, int]] = []
@@ -55,87 +71,162 @@ class RecordingBlockStore:
 
 
 class BlockManager:
-    """FIFO, reference-counted allocator over a fixed pool of KV blocks (blocks.py:63-192)."""
+    """Owner-counted pool of ``num_blocks`` KV blocks with FIFO reuse; see the module docstring."""
 
     def __init__(self, *, num_blocks: int, block_size: int, store: BlockStore) -> None:
         if num_blocks < 1:
             raise ValueError("num_blocks must be >= 1")
         if block_size < 1:
             raise ValueError("block_size must be >= 1")
-        self._num_blocks = num_blocks
         self.block_size = block_size
+        self._size = num_blocks
         self._store = store
-        self._refs = [0] * num_blocks
-        self._free: deque[int] = deque(range(num_blocks))
+        self._owners = np.zeros(num_blocks, dtype=np.int32)
+        self._ring = np.arange(num_blocks, dtype=np.int32)
+        self._head = 0
+        self._nfree = num_blocks
+
+    # --- sizes ---------------------------------------------------------------------------
 
     @property
     def num_blocks(self) -> int:
-        return self._num_blocks
+        return self._size
 
     @property
     def num_free_blocks(self) -> int:
-        return len(self._free)
+        return self._nfree
 
     @property
     def num_used_blocks(self) -> int:
-        return self._num_blocks - len(self._free)
+        return self._size - self._nfree
 
     @property
     def utilization(self) -> float:
-        return self.num_used_blocks / self._num_blocks
+        """Share of the pool held by at least one owner."""
+        return (self._size - self._nfree) / self._size
 
-    def _id(self, block_id: int) -> int:
-        if block_id < 0 or block_id >= self._num_blocks:
+    # --- queries -------------------------------------------------------------------------
+
+    def _in_pool(self, block_id: int) -> int:
+        if block_id < 0 or block_id >= self._size:
             raise InvariantError(f"block id {block_id} is outside the pool")
         return block_id
 
     def ref_count(self, block_id: int) -> int:
-        return self._refs[self._id(block_id)]
+        return int(self._owners[self._in_pool(block_id)])
+
+    def counts_of(self, block_ids) -> np.ndarray:
+        """Owner counts of many blocks in one gather (int32, same order as ``block_ids``)."""
+        ids = np.asarray(block_ids, dtype=np.int64)
+        if ids.size and (ids.min() < 0 or ids.max() >= self._size):
+            bad = int(ids[(ids < 0) | (ids >= self._size)][0])
+            raise InvariantError(f"block id {bad} is outside the pool")
+        return self._owners[ids]
+
+    def free_order(self) -> list[int]:
+        """The free ids, oldest first: the order in which they will be allocated."""
+        return self._take_view(self._nfree).tolist()
+
+    def snapshot(self) -> tuple[int, ...]:
+        """Owner count of every block."""
+        return tuple(self._owners.tolist())
+
+    # --- the ring ------------------------------------------------------------------------
+
+    def _take_view(self, count: int) -> np.ndarray:
+        """The ``count`` oldest free ids (a copy), without removing them."""
+        end = self._head + count
+        if end <= self._size:
+            return self._ring[self._head : end].copy()
+        return np.concatenate((self._ring[self._head :], self._ring[: end - self._size]))
+
+    def _push(self, block_id: int) -> None:
+        tail = self._head + self._nfree
+        self._ring[tail - self._size if tail >= self._size else tail] = block_id
+        self._nfree += 1
+
+    def _push_many(self, ids: np.ndarray) -> None:
+        slots = (self._head + self._nfree + np.arange(ids.size)) % self._size
+        self._ring[slots] = ids
+        self._nfree += int(ids.size)
+
+    # --- ownership -----------------------------------------------------------------------
 
     def allocate(self) -> int:
-        """Pop the oldest free block; it starts with one reference."""
-        if not self._free:
+        """The oldest free block, now with one owner."""
+        if self._nfree == 0:
             raise BlockAllocationError("the KV block pool is exhausted")
-        block_id = self._free.popleft()
-        self._refs[block_id] = 1
+        block_id = int(self._ring[self._head])
+        self._head = self._head + 1 if self._head + 1 < self._size else 0
+        self._nfree -= 1
+        self._owners[block_id] = 1
         return block_id
 
     def allocate_many(self, count: int) -> list[int]:
-        """``count`` blocks, or none if the pool cannot cover all of them."""
+        """The ``count`` oldest free blocks, each with one owner; nothing if they do not all fit."""
         if count < 0:
             raise ValueError("count must be >= 0")
-        available = len(self._free)
-        if count > available:
+        if count > self._nfree:
             raise BlockAllocationError(
-                f"need {count} blocks, {available} free in a pool of {self._num_blocks}"
+                f"need {count} blocks, {self._nfree} free in a pool of {self._size}"
             )
-        return [self.allocate() for _ in range(count)]
+        if count < _VECTOR_MIN:
+            return [self.allocate() for _ in range(count)]
+        ids = self._take_view(count)
+        self._head = (self._head + count) % self._size
+        self._nfree -= count
+        self._owners[ids] = 1
+        return ids.tolist()
 
     def incref(self, block_id: int) -> int:
-        block_id = self._id(block_id)
-        if self._refs[block_id] == 0:
+        """One more owner of a held block; returns its new count."""
+        owners = self._owners[self._in_pool(block_id)]
+        if owners == 0:
             raise InvariantError(f"block {block_id} is free and cannot gain a reference")
-        self._refs[block_id] += 1
-        return self._refs[block_id]
+        self._owners[block_id] = owners + 1
+        return int(owners) + 1
 
     def free(self, block_id: int) -> int:
-        """Drop one owner; the last one returns the block to the tail of the free list."""
-        block_id = self._id(block_id)
-        if self._refs[block_id] == 0:
+        """One owner fewer; the block rejoins the ring, behind every free id, when none is left.
+        Returns the remaining count."""
+        owners = int(self._owners[self._in_pool(block_id)])
+        if owners == 0:
             raise InvariantError(f"block {block_id} was freed twice")
-        self._refs[block_id] -= 1
-        if self._refs[block_id] == 0:
-            self._free.append(block_id)
-        return self._refs[block_id]
+        owners -= 1
+        self._owners[block_id] = owners
+        if owners == 0:
+            self._push(block_id)
+        return owners
 
     def free_many(self, block_ids: Iterable[int]) -> None:
-        for block_id in block_ids:
-            self.free(block_id)
+        """:meth:`free` of each id, in order. A table of distinct, held ids is released with one
+        gather and one scatter; anything else (repeats, a free or foreign id) takes the one-by-one
+        path, so an error is raised at the same id, after the same earlier releases."""
+        ids = block_ids if isinstance(block_ids, (list, tuple)) else list(block_ids)
+        if len(ids) < _VECTOR_MIN:
+            for block_id in ids:
+                self.free(block_id)
+            return
+        arr = np.asarray(ids, dtype=np.int64)
+        if (
+            arr.min() < 0
+            or arr.max() >= self._size
+            or np.unique(arr).size != arr.size
+            or not np.all(self._owners[arr] > 0)
+        ):
+            for block_id in ids:
+                self.free(block_id)
+            return
+        left = self._owners[arr] - 1
+        self._owners[arr] = left
+        released = arr[left == 0]
+        if released.size:
+            self._push_many(released.astype(np.int32))
 
     def prepare_for_write(self, block_id: int) -> int:
-        """The block the caller may write: itself if unshared, else a fresh private copy."""
-        block_id = self._id(block_id)
-        owners = self._refs[block_id]
+        """The block the caller may write: ``block_id`` itself when the caller is its only owner,
+        otherwise a fresh block that receives a copy of it (the caller's ownership moves there)."""
+        owners = self._owners[self._in_pool(block_id)]
         if owners == 0:
             raise InvariantError(f"block {block_id} is free and cannot be written")
         if owners == 1:
@@ -145,25 +236,23 @@ class BlockManager:
         self.free(block_id)
         return private
 
-    def check_invariants(self) -> None:
-        """Raise :class:`InvariantError` on a leak, double free or corrupted free list."""
-        on_free_list = set(self._free)
-        if len(on_free_list) != len(self._free):
-            raise InvariantError("the free list contains duplicate block ids")
-        for block_id, count in enumerate(self._refs):
-            if count < 0:
-                raise InvariantError(f"block {block_id} has a negative reference count")
-            listed = block_id in on_free_list
-            if (count == 0) != listed:
-                raise InvariantError(
-                    f"block {block_id} has count {count} but "
-                    f"{'is' if listed else 'is not'} on the free list"
-                )
-        referenced = sum(1 for count in self._refs if count > 0)
-        if referenced + len(self._free) != self._num_blocks:
-            raise InvariantError(
-                f"{referenced} referenced + {len(self._free)} free != {self._num_blocks} blocks"
-            )
+    # --- consistency ---------------------------------------------------------------------
 
-    def snapshot(self) -> tuple[int, ...]:
-        return tuple(self._refs)
+    def check_invariants(self) -> None:
+        """Raise :class:`InvariantError` unless the ring holds exactly the ownerless blocks,
+        each once, and no count is negative."""
+        free = self._take_view(self._nfree).astype(np.int64)
+        listed = np.zeros(self._size, dtype=np.int64)
+        np.add.at(listed, free, 1)
+        if np.any(listed > 1):
+            raise InvariantError(f"block {int(np.flatnonzero(listed > 1)[0])} is on the free ring twice")
+        if np.any(self._owners < 0):
+            raise InvariantError(f"block {int(np.flatnonzero(self._owners < 0)[0])} has a negative owner count")
+        wrong = np.flatnonzero((self._owners == 0) != (listed == 1))
+        if wrong.size:
+            block = int(wrong[0])
+            where = "is" if listed[block] else "is not"
+            raise InvariantError(f"block {block} has {int(self._owners[block])} owners but {where} on the free ring")
+        held = int(np.count_nonzero(self._owners))
+        if held + self._nfree != self._size:
+            raise InvariantError(f"{held} held + {self._nfree} free != {self._size} blocks")

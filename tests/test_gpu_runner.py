@@ -266,7 +266,7 @@ def test_copy_on_write_moves_real_bytes_and_keeps_the_original(device, models) -
     cache.fork(parent, child)
     shared = parent.block_table[1]
     before = runner.block_fingerprint(shared)
-    child.append_token(9)
+    child.token_ids.append(9)
     cache.reserve(child, 7)  # copy-on-write of the partial block, queued in the runner
     private = child.block_table[1]
     assert private != shared

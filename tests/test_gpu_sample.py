@@ -1,7 +1,7 @@
 """Greedy sampling on the device (pkv_greedy_tokens) against NumPy's argmax, which is the
 reference's greedy_token (sampling.py:28-30): bit-exact token ids, including ties (lowest id),
-NaN (first NaN wins), -inf rows, signed zeros, odd vocabulary sizes and strided rows; and the
-engine's device-sampled run against its host-sampled run."""
+NaN (first NaN wins), -inf rows, signed zeros, odd vocabulary sizes and strided rows. The
+whole config-1 run sampled on the device is in test_gpu_replay.py."""
 
 from __future__ import annotations
 
@@ -58,28 +58,3 @@ def test_strided_and_misaligned_rows(device) -> None:
     assert np.array_equal(got, _argmax_rows(big[:, 1:258].cpu().numpy()))
     aligned = big[::2, :256]  # stride 600, aligned: the vector path
     assert np.array_equal(ops.greedy_tokens(aligned).cpu().numpy(), _argmax_rows(aligned.cpu().numpy()))
-
-
-def test_engine_samples_the_same_tokens_on_the_device(device) -> None:
-    """Config 1's engine with device sampling (the default executor) and with host sampling of
-    the recorded logits rows produce the same tokens."""
-    from paged_kv_serving_amd.config import EngineConfig, ModelConfig
-    from paged_kv_serving_amd.engine import Engine, RecordingExecutor
-    from paged_kv_serving_amd.model import LanguageModel, random_weights
-    from paged_kv_serving_amd.sequence import Request, SamplingParams
-
-    config = ModelConfig(vocab_size=256, d_model=128, n_layers=2, n_heads=4, d_ff=320, max_seq_len=1024)
-    model = LanguageModel(config, random_weights(config, seed=0))
-    rng = np.random.default_rng(4)
-    requests = [
-        Request(f"r{i}", tuple(int(t) for t in rng.integers(0, 256, int(rng.integers(16, 129)))),
-                SamplingParams(max_new_tokens=12), n=2 if i % 5 == 0 else 1)
-        for i in range(12)
-    ]  # fmt: skip
-    device_run = Engine(model, EngineConfig(), device=device)
-    assert hasattr(device_run.executor, "execute_greedy")
-    on_device = device_run.generate(requests)
-    host_run = Engine(model, EngineConfig(), device=device)
-    host_run.executor = RecordingExecutor(host_run.runner)
-    on_host = host_run.generate(requests)
-    assert on_device == on_host

@@ -25,7 +25,7 @@ from paged_kv_serving_amd.prefix_cache import (
     chain_seed,
     next_block_hash,
 )
-from paged_kv_serving_amd.sequence import Request, SamplingParams, Sequence
+from paged_kv_serving_amd.sequence import Request, Sequence
 
 # --- BlockManager (reference tests/unit/test_blocks.py) -------------------------------------
 
@@ -114,9 +114,41 @@ def test_double_free_and_out_of_range_ids_are_refused() -> None:
 def test_invariant_check_detects_a_corrupted_free_list() -> None:
     blocks, _ = manager(num_blocks=4)
     block = blocks.allocate()
-    blocks._free.append(block)
-    with pytest.raises(InvariantError):
+    blocks._push(block)  # a held block back on the free ring
+    with pytest.raises(InvariantError, match="owners but is on the free ring"):
         blocks.check_invariants()
+
+
+def test_runs_of_blocks_take_the_vector_path_with_the_same_order() -> None:
+    """allocate_many / free_many of many ids (one slice of the ring, one gather) hand out and
+    take back ids in exactly the order one-at-a-time calls would, across the ring's wrap."""
+    one, _ = manager(num_blocks=40)
+    many, _ = manager(num_blocks=40)
+    rng = __import__("numpy").random.default_rng(0)
+    held_one, held_many = [], []
+    for _ in range(30):
+        take = int(rng.integers(0, 12))
+        if take <= one.num_free_blocks:
+            held_one.append([one.allocate() for _ in range(take)])
+            held_many.append(many.allocate_many(take))
+            assert held_one[-1] == held_many[-1]
+        if held_one and rng.random() < 0.5:
+            k = int(rng.integers(0, len(held_one)))
+            for block in held_one.pop(k):
+                one.free(block)
+            many.free_many(held_many.pop(k))
+        assert one.free_order() == many.free_order() and one.snapshot() == many.snapshot()
+    many.check_invariants()
+
+
+def test_free_many_fails_at_the_same_id_as_one_by_one() -> None:
+    blocks, _ = manager(num_blocks=16)
+    held = blocks.allocate_many(10)
+    blocks.free(held[6])
+    with pytest.raises(InvariantError, match=f"block {held[6]} was freed twice"):
+        blocks.free_many(held)
+    assert [blocks.ref_count(b) for b in held] == [0] * 7 + [1] * 3, "released up to the bad id"
+    assert blocks.free_order()[-7:] == [held[6], *held[:6]]
 
 
 def test_utilisation_and_snapshot() -> None:
@@ -153,8 +185,7 @@ def build(num_blocks: int = 16, *, prefix_cache: bool = True):
 
 
 def sequence(tokens, *, key: str = "tenant-a", index: int = 0) -> Sequence:
-    request = Request(f"r{index}", tuple(tokens), SamplingParams(max_new_tokens=4, seed=index), key_id=key)
-    return Sequence.from_request(request, 0)
+    return Sequence.from_request(Request(f"r{index}", tuple(tokens), key_id=key), 0)
 
 
 def compute(cache: KVCacheManager, seq: Sequence, chunk: int) -> None:
@@ -230,7 +261,7 @@ def test_fork_shares_blocks_and_the_first_write_copies_only_the_partial_block() 
     cache.fork(parent, child)
     assert child.block_table == parent.block_table
     assert cache.blocks.ref_count(partial) == 2 and store.copies == []
-    child.append_token(99)
+    child.token_ids.append(99)
     compute(cache, child, 1)
     assert child.block_table[1] != partial
     assert store.copies == [(partial, child.block_table[1])]

@@ -1,0 +1,109 @@
+"""Recorded reference serving runs replayed through this package's KV-cache manager, on the CPU.
+
+Each trace under tests/golden/traces/ is a run of the reference engine (scheduler, KV-cache
+manager, prefix cache, NumPy runner) recorded by tests/golden/make_reference_traces.py: config 1,
+the reference's own bench_engine_equivalence shape, and three small-pool runs with prefix
+sharing, n-way forks, copy-on-write, preemption and eviction. The replay issues the same
+KVCacheManager calls to this package's BlockManager / KVCacheManager / PrefixCache and checks,
+bit for bit: every return value, block table, copy-on-write pair and prefix-hash chain; every
+batch's entries and slot mapping; and after every iteration the pool's owner counts, free-list
+order, cached block ids (LRU order) and cache counters. The batches then run on the NumPy
+oracle runner, whose logits rows must be within 1e-4 of the reference's recorded rows and of the
+cache-free recompute (the reference's bar, tests/property/test_equivalence.py:34).
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle.model import OracleModel
+from oracle.runner import OracleRunner
+from paged_kv_serving_amd.replay import ReplayMismatch, Trace, TraceReplay, weights_sha256
+
+TRACES = Path(__file__).resolve().parent / "golden" / "traces"
+NAMES = ("config1", "engine_equivalence", "sharing_b8", "sharing_b4", "sharing_b16")
+
+
+def load(name: str) -> Trace:
+    return Trace.load(TRACES / f"{name}.json")
+
+
+def recompute_gap(model, result, tokens) -> float:
+    """Largest |logits - reference_forward(full tokens)[context - 1]| over the replayed rows."""
+    dense: dict[str, np.ndarray] = {}
+    worst = 0.0
+    for row, (seq_id, context) in zip(result.rows, result.row_seqs):
+        if seq_id not in dense:
+            dense[seq_id] = model.reference_forward(tokens[seq_id])
+        worst = max(worst, float(np.max(np.abs(dense[seq_id][context - 1] - row))))
+    return worst
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_the_reference_run_replays_bit_exactly_on_the_numpy_runner(name) -> None:
+    trace = load(name)
+    model = trace.language_model()  # also checks random_weights against the reference's SHA-256
+    oracle = OracleModel(model.config, model.weights)
+    runner = OracleRunner(oracle, num_blocks=trace.engine["num_blocks"], block_size=trace.engine["block_size"])
+    result = TraceReplay(trace, runner).run()
+    assert result.iterations == trace.summary["iterations"]
+    assert result.copies == trace.summary["copies"]
+    rows = np.stack(result.rows)
+    assert rows.shape == trace.logits.shape
+    assert float(np.max(np.abs(rows - trace.logits))) < 1e-4
+    assert recompute_gap(oracle, result, trace.tokens) < 1e-4
+
+
+def test_the_traces_cover_what_they_are_for() -> None:
+    """Between them the traces exercise preemption, forks with copy-on-write, prefix hits and
+    eviction; config 1 and bench_engine_equivalence keep the reference's published shapes."""
+    summaries = {name: load(name).summary for name in NAMES}
+    assert summaries["config1"]["logits_rows"] == 32 * 32
+    eq = summaries["engine_equivalence"]
+    assert (eq["rows_checked"], eq["preemptions"], eq["prefix_hit_blocks"]) == (264, 7, 30)
+    assert sum(s["preemptions"] for s in summaries.values()) > 0
+    assert sum(s["copies"] for s in summaries.values()) > 0
+    events = {e[0] for name in NAMES for e in load(name).events}
+    assert {"attach", "detach", "record", "reserve", "fork", "free", "publish"} <= events
+    assert any(e[0] == "reserve" and not e[5] for name in NAMES for e in load(name).events), "a refused reserve"
+
+
+def test_random_weights_follow_the_reference_draw_order() -> None:
+    """The weights SHA-256 each trace recorded from the reference's random_weights is met by both
+    this package's and the oracle's restatement, and a swapped draw order is not."""
+    from oracle.model import random_weights as oracle_weights
+    from paged_kv_serving_amd.model import random_weights
+
+    for name in NAMES:
+        trace = load(name)
+        config = trace.model_config()
+        want = trace.model["weights_sha256"]
+        assert weights_sha256(random_weights(config, seed=trace.model["seed"])) == want
+        assert weights_sha256(oracle_weights(config, seed=trace.model["seed"])) == want
+    # planted mistake: gate and up drawn in the other order
+    trace = load("config1")
+    config = trace.model_config()
+    weights = random_weights(config, seed=0)
+    swapped = [
+        type(layer)(layer.attn_norm, layer.qkv_proj, layer.out_proj, layer.ffn_norm, layer.up_proj,
+                    layer.gate_proj, layer.down_proj)  # fmt: skip
+        for layer in weights.layers
+    ]
+    planted = type(weights)(weights.token_embedding, tuple(swapped), weights.final_norm)
+    assert weights_sha256(planted) != trace.model["weights_sha256"]
+
+
+def test_a_different_allocation_order_is_caught() -> None:
+    """A pool that hands out blocks LIFO instead of FIFO produces other tables: the replay must
+    say so at the first call that differs."""
+    trace = load("sharing_b4")
+    model = trace.language_model()
+    oracle = OracleModel(model.config, model.weights)
+    runner = OracleRunner(oracle, num_blocks=trace.engine["num_blocks"], block_size=trace.engine["block_size"])
+    replay = TraceReplay(trace, runner)
+    replay.blocks._ring[:] = replay.blocks._ring[::-1].copy()  # the same free set, other order
+    with pytest.raises(ReplayMismatch, match="table of"):
+        replay.run()
