@@ -10,20 +10,24 @@ order ``0 .. N-1``; allocation takes the oldest free id; a block whose last owne
 behind every other free id; a write to a shared block allocates the destination, asks the store
 for the copy, then drops the writer's ownership of the source (blocks.py:148-165).
 
-Representation. The pool is two int32 arrays of ``num_blocks`` entries:
+Representation. The pool is two int32 buffers of ``num_blocks`` entries:
 
 * ``_owners[b]`` -- how many block tables (and prefix-cache entries) hold block ``b``; 0 = free;
 * ``_ring`` -- the free ids as a circular FIFO: the ``_nfree`` ids starting at ``_head``.
 
-A run of ``k`` ids leaves the ring as at most two slices, and a table's worth of blocks returns
+Each buffer is a ``array('i')`` with a NumPy view of the same memory (``_owners_v``,
+``_ring_v``). Single-block calls (one allocate, one copy-on-write) index the array directly,
+which costs about half what a NumPy scalar access does; calls over many blocks use the views:
+a run of ``k`` ids leaves the ring as at most two slices, and a table's worth of blocks returns
 with one gather of their counts, so the per-iteration work of a large batch (hundreds of tables,
-thousands of blocks) is a few array operations instead of a Python loop per block. The same
-arrays answer the questions the KV-cache manager asks of whole tables at once ("which blocks of
-this write range are shared?", "which cached blocks does only the cache hold?") in one gather.
+thousands of blocks) is a few array operations instead of a Python loop per block. The views
+also answer what the KV-cache manager asks of whole tables at once ("which blocks of this write
+range are shared?", "which cached blocks does only the cache hold?") in one gather.
 """
 
 from __future__ import annotations
 
+from array import array
 from collections.abc import Iterable
 from typing import Protocol, runtime_checkable
 
@@ -37,9 +41,9 @@ __all__ = [
     "RecordingBlockStore",
 ]
 
-# Below this many ids a batch call runs the scalar path: a handful of NumPy calls costs more
-# than a short Python loop.
-_VECTOR_MIN = 8
+# Below this many ids a batch call runs the scalar path: a handful of NumPy calls (about a
+# microsecond each) costs more than a short Python loop (measured crossover: 40-60 ids).
+_VECTOR_MIN = 64
 
 
 class BlockAllocationError(RuntimeError):
@@ -81,8 +85,12 @@ class BlockManager:
         self.block_size = block_size
         self._size = num_blocks
         self._store = store
-        self._owners = np.zeros(num_blocks, dtype=np.int32)
-        self._ring = np.arange(num_blocks, dtype=np.int32)
+        self._owners = array("i", bytes(4 * num_blocks))
+        self._ring = array("i", range(num_blocks))
+        if self._owners.itemsize != 4:  # pragma: no cover - every supported platform has 4-byte int
+            raise RuntimeError("the block pool needs a 4-byte C int")
+        self._owners_v = np.frombuffer(self._owners, dtype=np.int32)
+        self._ring_v = np.frombuffer(self._ring, dtype=np.int32)
         self._head = 0
         self._nfree = num_blocks
 
@@ -107,13 +115,10 @@ class BlockManager:
 
     # --- queries -------------------------------------------------------------------------
 
-    def _in_pool(self, block_id: int) -> int:
-        if block_id < 0 or block_id >= self._size:
-            raise InvariantError(f"block id {block_id} is outside the pool")
-        return block_id
-
     def ref_count(self, block_id: int) -> int:
-        return int(self._owners[self._in_pool(block_id)])
+        if not 0 <= block_id < self._size:
+            raise InvariantError(f"block id {block_id} is outside the pool")
+        return self._owners[block_id]
 
     def counts_of(self, block_ids) -> np.ndarray:
         """Owner counts of many blocks in one gather (int32, same order as ``block_ids``)."""
@@ -121,7 +126,7 @@ class BlockManager:
         if ids.size and (ids.min() < 0 or ids.max() >= self._size):
             bad = int(ids[(ids < 0) | (ids >= self._size)][0])
             raise InvariantError(f"block id {bad} is outside the pool")
-        return self._owners[ids]
+        return self._owners_v[ids]
 
     def free_order(self) -> list[int]:
         """The free ids, oldest first: the order in which they will be allocated."""
@@ -129,7 +134,7 @@ class BlockManager:
 
     def snapshot(self) -> tuple[int, ...]:
         """Owner count of every block."""
-        return tuple(self._owners.tolist())
+        return tuple(self._owners)
 
     # --- the ring ------------------------------------------------------------------------
 
@@ -137,8 +142,8 @@ class BlockManager:
         """The ``count`` oldest free ids (a copy), without removing them."""
         end = self._head + count
         if end <= self._size:
-            return self._ring[self._head : end].copy()
-        return np.concatenate((self._ring[self._head :], self._ring[: end - self._size]))
+            return self._ring_v[self._head : end].copy()
+        return np.concatenate((self._ring_v[self._head :], self._ring_v[: end - self._size]))
 
     def _push(self, block_id: int) -> None:
         tail = self._head + self._nfree
@@ -147,7 +152,7 @@ class BlockManager:
 
     def _push_many(self, ids: np.ndarray) -> None:
         slots = (self._head + self._nfree + np.arange(ids.size)) % self._size
-        self._ring[slots] = ids
+        self._ring_v[slots] = ids
         self._nfree += int(ids.size)
 
     # --- ownership -----------------------------------------------------------------------
@@ -156,7 +161,7 @@ class BlockManager:
         """The oldest free block, now with one owner."""
         if self._nfree == 0:
             raise BlockAllocationError("the KV block pool is exhausted")
-        block_id = int(self._ring[self._head])
+        block_id = self._ring[self._head]
         self._head = self._head + 1 if self._head + 1 < self._size else 0
         self._nfree -= 1
         self._owners[block_id] = 1
@@ -170,26 +175,38 @@ class BlockManager:
             raise BlockAllocationError(
                 f"need {count} blocks, {self._nfree} free in a pool of {self._size}"
             )
-        if count < _VECTOR_MIN:
-            return [self.allocate() for _ in range(count)]
-        ids = self._take_view(count)
-        self._head = (self._head + count) % self._size
+        head, size = self._head, self._size
+        end = head + count
+        self._head = end - size if end >= size else end
         self._nfree -= count
-        self._owners[ids] = 1
-        return ids.tolist()
+        if count >= _VECTOR_MIN:
+            ids = self._ring_v[head:end].copy() if end <= size else np.concatenate(
+                (self._ring_v[head:], self._ring_v[: end - size]))  # fmt: skip
+            self._owners_v[ids] = 1
+            return ids.tolist()
+        ring = self._ring
+        ids = ring[head:end].tolist() if end <= size else ring[head:].tolist() + ring[: end - size].tolist()
+        owners = self._owners
+        for block_id in ids:
+            owners[block_id] = 1
+        return ids
 
     def incref(self, block_id: int) -> int:
         """One more owner of a held block; returns its new count."""
-        owners = self._owners[self._in_pool(block_id)]
+        if not 0 <= block_id < self._size:
+            raise InvariantError(f"block id {block_id} is outside the pool")
+        owners = self._owners[block_id]
         if owners == 0:
             raise InvariantError(f"block {block_id} is free and cannot gain a reference")
         self._owners[block_id] = owners + 1
-        return int(owners) + 1
+        return owners + 1
 
     def free(self, block_id: int) -> int:
         """One owner fewer; the block rejoins the ring, behind every free id, when none is left.
         Returns the remaining count."""
-        owners = int(self._owners[self._in_pool(block_id)])
+        if not 0 <= block_id < self._size:
+            raise InvariantError(f"block id {block_id} is outside the pool")
+        owners = self._owners[block_id]
         if owners == 0:
             raise InvariantError(f"block {block_id} was freed twice")
         owners -= 1
@@ -204,21 +221,31 @@ class BlockManager:
         path, so an error is raised at the same id, after the same earlier releases."""
         ids = block_ids if isinstance(block_ids, (list, tuple)) else list(block_ids)
         if len(ids) < _VECTOR_MIN:
+            owners, ring, size = self._owners, self._ring, self._size
             for block_id in ids:
-                self.free(block_id)
+                if not 0 <= block_id < size:
+                    raise InvariantError(f"block id {block_id} is outside the pool")
+                left = owners[block_id] - 1
+                if left < 0:
+                    raise InvariantError(f"block {block_id} was freed twice")
+                owners[block_id] = left
+                if left == 0:
+                    tail = self._head + self._nfree
+                    ring[tail - size if tail >= size else tail] = block_id
+                    self._nfree += 1
             return
         arr = np.asarray(ids, dtype=np.int64)
         if (
             arr.min() < 0
             or arr.max() >= self._size
             or np.unique(arr).size != arr.size
-            or not np.all(self._owners[arr] > 0)
+            or not np.all(self._owners_v[arr] > 0)
         ):
             for block_id in ids:
                 self.free(block_id)
             return
-        left = self._owners[arr] - 1
-        self._owners[arr] = left
+        left = self._owners_v[arr] - 1
+        self._owners_v[arr] = left
         released = arr[left == 0]
         if released.size:
             self._push_many(released.astype(np.int32))
@@ -226,7 +253,9 @@ class BlockManager:
     def prepare_for_write(self, block_id: int) -> int:
         """The block the caller may write: ``block_id`` itself when the caller is its only owner,
         otherwise a fresh block that receives a copy of it (the caller's ownership moves there)."""
-        owners = self._owners[self._in_pool(block_id)]
+        if not 0 <= block_id < self._size:
+            raise InvariantError(f"block id {block_id} is outside the pool")
+        owners = self._owners[block_id]
         if owners == 0:
             raise InvariantError(f"block {block_id} is free and cannot be written")
         if owners == 1:
@@ -246,13 +275,14 @@ class BlockManager:
         np.add.at(listed, free, 1)
         if np.any(listed > 1):
             raise InvariantError(f"block {int(np.flatnonzero(listed > 1)[0])} is on the free ring twice")
-        if np.any(self._owners < 0):
-            raise InvariantError(f"block {int(np.flatnonzero(self._owners < 0)[0])} has a negative owner count")
-        wrong = np.flatnonzero((self._owners == 0) != (listed == 1))
+        owners = self._owners_v
+        if np.any(owners < 0):
+            raise InvariantError(f"block {int(np.flatnonzero(owners < 0)[0])} has a negative owner count")
+        wrong = np.flatnonzero((owners == 0) != (listed == 1))
         if wrong.size:
             block = int(wrong[0])
             where = "is" if listed[block] else "is not"
-            raise InvariantError(f"block {block} has {int(self._owners[block])} owners but {where} on the free ring")
-        held = int(np.count_nonzero(self._owners))
+            raise InvariantError(f"block {block} has {int(owners[block])} owners but {where} on the free ring")
+        held = int(np.count_nonzero(owners))
         if held + self._nfree != self._size:
             raise InvariantError(f"{held} held + {self._nfree} free != {self._size} blocks")

@@ -104,6 +104,6 @@ def test_a_different_allocation_order_is_caught() -> None:
     oracle = OracleModel(model.config, model.weights)
     runner = OracleRunner(oracle, num_blocks=trace.engine["num_blocks"], block_size=trace.engine["block_size"])
     replay = TraceReplay(trace, runner)
-    replay.blocks._ring[:] = replay.blocks._ring[::-1].copy()  # the same free set, other order
+    replay.blocks._ring_v[:] = replay.blocks._ring_v[::-1].copy()  # the same free set, other order
     with pytest.raises(ReplayMismatch, match="table of"):
         replay.run()
