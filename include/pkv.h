@@ -8,10 +8,13 @@
  *
  * Conventions shared by every entry point:
  *   - Pointers are device pointers (HIP global memory) unless stated otherwise. The caller owns
- *     every buffer, including the attention workspace; the library never allocates.
+ *     every buffer, including the attention workspace. No compute entry point allocates memory
+ *     or creates a stream or event: the only resources the library makes are the per-device
+ *     ones pkv_init creates, once, when the caller asks for them.
  *   - `device` is the HIP device ordinal the pointers live on. The library makes it current for
  *     the duration of the call and restores the caller's device afterwards, so calls may come
- *     from any host thread (the library keeps no per-thread state).
+ *     from any host thread (the library keeps no per-thread state; per-device state is guarded
+ *     by a per-device mutex).
  *   - `stream` is a hipStream_t passed as void*; NULL means the default stream. All work is
  *     enqueued on it, asynchronously; nothing synchronises the host.
  *   - Return value: PKV_OK (0) on success, a negative PKV_E* code otherwise. pkv_error_string()
@@ -52,6 +55,18 @@ typedef enum pkv_dtype {
 #define PKV_EINVAL (-1)       /* a size, stride, pointer or enum argument is out of range */
 #define PKV_EUNSUPPORTED (-2) /* a valid but unimplemented shape (e.g. head_dim 96) */
 #define PKV_EHIP (-3)         /* the HIP runtime reported an error while enqueueing */
+
+/*
+ * Creates the library's resources on `device`: a second stream (default priority, non-blocking)
+ * and two events, used by pkv_paged_attention to run the MFMA tile pass of a call beside its
+ * row-streaming pass. Idempotent and thread-safe; the resources live until the process ends.
+ * Call it once per device before the first attention call that should overlap its passes, and
+ * before capturing attention calls into a HIP graph. Without it, calls run both passes one
+ * after the other on the caller's stream (same results).
+ *
+ * No counterpart in the reference (it has no device); the resources replace nothing there.
+ */
+int pkv_init(int device);
 
 /* Version string of the library ("pkv <major>.<minor>"). Host-only, never fails. */
 const char* pkv_version(void);

@@ -66,6 +66,7 @@ PKV_TILE_WHOLE = -1
 PKV_OK = 0
 
 EXPORTED_SYMBOLS = (
+    "pkv_init",
     "pkv_version",
     "pkv_error_string",
     "pkv_append",
@@ -134,6 +135,8 @@ _ptr = ctypes.c_void_p
 
 
 def _declare(lib: ctypes.CDLL) -> None:
+    lib.pkv_init.argtypes = [_c_int]
+    lib.pkv_init.restype = _c_int
     lib.pkv_version.argtypes = []
     lib.pkv_version.restype = ctypes.c_char_p
     lib.pkv_error_string.argtypes = [_c_int]
@@ -217,6 +220,21 @@ def library() -> ctypes.CDLL:
             _declare(lib)
             _LIB = lib
         return _LIB
+
+
+_READY: set[int] = set()
+
+
+def init_device(device: int) -> None:
+    """``pkv_init(device)`` once per device: the library's second stream and events, which let a
+    call's tile pass run beside its row pass. Later calls are a set lookup."""
+    if device in _READY:
+        return
+    lib = library()
+    with _LOCK:
+        if device not in _READY:
+            check(lib.pkv_init(device), f"pkv_init({device})")
+            _READY.add(device)
 
 
 def check(code: int, what: str) -> None:

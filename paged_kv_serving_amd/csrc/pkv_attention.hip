@@ -33,6 +33,7 @@
 // visible block are never read.
 #include <math.h>
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -1136,42 +1137,30 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(const Params a, 
   }
 }
 
-// A second stream per device, with fork/join events, so the compute-bound tile pass runs beside
-// the memory-bound row pass of the same call. Created once per device (default priority,
-// non-blocking) and kept for the life of the process; the enqueue sequence that uses the events
-// runs under one mutex, so calls from several host threads cannot interleave their records.
+// The library's per-device resources, created by pkv_init and kept for the life of the process:
+// a second stream (default priority, non-blocking) with fork and join events, so the
+// compute-bound tile pass of a call runs beside its memory-bound row pass. The compute entry
+// points never create anything; on a device pkv_init has not set up, they run both passes on the
+// caller's stream. Each device has its own mutex: it serialises the fork/join enqueue sequence
+// of calls from several host threads on that device (calls on other devices do not wait).
 constexpr int kMaxDevices = 64;
 
-struct Overlap {
+struct DeviceResources {
+  std::mutex mu;
+  std::atomic<bool> ready{false};  // stream and events exist
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr;
   hipEvent_t join = nullptr;
   int64_t tile_groups = 0;  // tile-pass workgroups beside the row pass (0: one per item)
-  bool failed = false;
 };
 
-std::mutex g_overlap_mutex;
-Overlap g_overlap[kMaxDevices];
+DeviceResources g_devices[kMaxDevices];
 
-// The current device's overlap stream and events (created on first use), or null when they
-// cannot be created; callers then run both passes on their own stream. Caller holds the mutex.
-Overlap* overlap_locked(int device) {
+// The device's overlap resources, or null when pkv_init has not created them.
+DeviceResources* overlap_for(int device) {
   if (device < 0 || device >= kMaxDevices) return nullptr;
-  Overlap& o = g_overlap[device];
-  if (o.failed) return nullptr;
-  if (o.stream == nullptr) {
-    int cus = 0;
-    if (hipStreamCreateWithFlags(&o.stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&o.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&o.join, hipEventDisableTiming) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
-      o.failed = true;
-      (void)hipGetLastError();
-      return nullptr;
-    }
-    o.tile_groups = static_cast<int64_t>(cus) * PKV_ATTN_TILE_GROUPS_PER_CU;
-  }
-  return &o;
+  DeviceResources& r = g_devices[device];
+  return r.ready.load(std::memory_order_acquire) ? &r : nullptr;
 }
 
 // max_groups > 0: a persistent grid of that many workgroups beside the row pass, staged straight
@@ -1212,12 +1201,11 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
   const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
   const bool short_rows = (a.flags & PKV_ATTN_SHORT_ROWS) != 0;
   const bool append = a.new_keys != nullptr;
-  std::unique_lock<std::mutex> overlap_lock(g_overlap_mutex, std::defer_lock);
-  Overlap* overlap = nullptr;
+  std::unique_lock<std::mutex> overlap_lock;
+  DeviceResources* overlap = nullptr;
   if (PKV_ATTN_OVERLAP && num_tiles > 0 && num_rows > 0) {
-    overlap_lock.lock();
-    overlap = overlap_locked(device);
-    if (overlap == nullptr) overlap_lock.unlock();
+    overlap = overlap_for(device);
+    if (overlap != nullptr) overlap_lock = std::unique_lock<std::mutex>(overlap->mu);
   }
   auto launch_rows_hpw = [&](auto hpw_tag) -> int {
     constexpr int HPW = decltype(hpw_tag)::value;
@@ -1350,6 +1338,36 @@ extern "C" int64_t pkv_attention_workspace_bytes(int64_t num_queries, int32_t nu
 
 extern "C" int pkv_tile_head_dim_supported(int32_t head_dim) {
   return head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
+}
+
+extern "C" int pkv_init(int device) {
+  using namespace pkv;
+  if (device < 0 || device >= kMaxDevices) return PKV_EINVAL;
+  DeviceResources& r = g_devices[device];
+  std::lock_guard<std::mutex> lock(r.mu);
+  if (r.ready.load(std::memory_order_relaxed)) return PKV_OK;
+  DeviceGuard guard(device);
+  if (!guard.ok()) return PKV_EHIP;
+  int cus = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t join = nullptr;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess) {
+    if (join != nullptr) (void)hipEventDestroy(join);
+    if (fork != nullptr) (void)hipEventDestroy(fork);
+    if (stream != nullptr) (void)hipStreamDestroy(stream);
+    (void)hipGetLastError();
+    return PKV_EHIP;
+  }
+  r.stream = stream;
+  r.fork = fork;
+  r.join = join;
+  r.tile_groups = static_cast<int64_t>(cus) * PKV_ATTN_TILE_GROUPS_PER_CU;
+  r.ready.store(true, std::memory_order_release);
+  return PKV_OK;
 }
 
 namespace pkv {

@@ -763,6 +763,7 @@ def paged_attention_ragged(
     device = _device_index(
         queries, query_positions, query_seq, key_cache, value_cache, block_tables, context_lens
     )
+    _native.init_device(device)  # once per device: the stream the tile pass overlaps on
     if queries.dtype != torch.float32:
         raise ValueError("queries must be float32")
     stride = _rows_contiguous(queries, "queries")

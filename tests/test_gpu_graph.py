@@ -24,7 +24,7 @@ def _replays_equal_eager(device, call) -> None:
     stream = torch.cuda.Stream(device=device)
     stream.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(stream):
-        call()  # warm the allocator and the library's per-device state outside the capture
+        call()  # warm torch's allocator outside the capture (pkv_init ran at the first call)
     torch.cuda.current_stream(device).wait_stream(stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()

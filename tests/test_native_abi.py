@@ -156,3 +156,16 @@ def test_fused_append_arguments_are_refused_before_any_device_work(lib) -> None:
     assert call(new_dtype=5) == -1
     assert call(key_stride=100) == -1  # shorter than a token row (4 heads x 128)
     assert call(key_stride=514) == -2  # rows not 16-byte aligned
+
+
+def test_init_refuses_device_ordinals_out_of_range(lib) -> None:
+    einval = -1  # PKV_EINVAL
+    assert lib.pkv_init(-1) == einval
+    assert lib.pkv_init(64) == einval
+
+
+@pytest.mark.gpu
+def test_init_is_idempotent_on_a_device(device) -> None:
+    lib = _native.library()
+    assert lib.pkv_init(device.index) == 0
+    assert lib.pkv_init(device.index) == 0
