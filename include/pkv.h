@@ -55,6 +55,10 @@ typedef enum pkv_dtype {
 #define PKV_EINVAL (-1)       /* a size, stride, pointer or enum argument is out of range */
 #define PKV_EUNSUPPORTED (-2) /* a valid but unimplemented shape (e.g. head_dim 96) */
 #define PKV_EHIP (-3)         /* the HIP runtime reported an error while enqueueing */
+#define PKV_ETOOBIG (-4)      /* the call needs more scratch than PKV_STATIC_SCRATCH_BYTES */
+
+/* Size of the library's static per-device scratch (pkv_paged_attention_noalloc). */
+#define PKV_STATIC_SCRATCH_BYTES (64LL << 20)
 
 /*
  * Creates the library's resources on `device`: a second stream (default priority, non-blocking)
@@ -238,6 +242,33 @@ int pkv_paged_attention(float* out, const float* queries, int64_t query_token_st
                         int32_t num_seqs, int32_t num_heads, int32_t head_dim, float scale,
                         int32_t max_context_len, int32_t partition_size, int32_t flags,
                         float* workspace, int64_t workspace_bytes, int device, void* stream);
+
+/*
+ * pkv_paged_attention without a workspace argument, for callers that cannot allocate: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ *
+ * No counterpart in the reference. Arguments, plan, results and errors are pkv_paged_attention's;
+ * the split-context workspace is instead a static device array of PKV_STATIC_SCRATCH_BYTES
+ * (64 MiB) in the library, one copy per GPU, held until the process ends. The call allocates
+ * nothing and creates nothing: on a device's first use it only looks up that device's copy of
+ * the array (pkv_init does the same). A batch whose workspace
+ * (pkv_attention_workspace_bytes) exceeds the buffer is refused with PKV_ETOOBIG before anything
+ * is enqueued. Nothing in the buffer needs to start at zero: every entry a call reads, the same
+ * call has written before. Every call on one GPU shares that GPU's buffer, so two calls whose
+ * execution overlaps on one GPU (on different streams, without ordering between them) race;
+ * calls on one stream, or ordered by events, do not.
+ */
+int pkv_paged_attention_noalloc(float* out, const float* queries, int64_t query_token_stride,
+                                const int32_t* query_positions, const int32_t* query_seq,
+                                int64_t num_queries, const int32_t* rows, int64_t num_rows,
+                                const int32_t* tiles, int64_t num_tiles,
+                                const int32_t* merge_rows, int64_t num_merge_rows,
+                                const void* key_cache, const void* value_cache,
+                                pkv_dtype kv_dtype, int64_t num_blocks, int32_t block_size,
+                                const int32_t* block_tables, int32_t block_table_stride,
+                                const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,
+                                int32_t head_dim, float scale, int32_t max_context_len,
+                                int32_t partition_size, int32_t flags, int device, void* stream);
 
 /*
  * A decode step's append and attention in one pass: pkv_append of every query row's own new key

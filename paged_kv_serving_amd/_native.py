@@ -64,6 +64,10 @@ PKV_ATTN_SHORT_ROWS = 2
 PKV_TILE_WHOLE = -1
 
 PKV_OK = 0
+PKV_EINVAL = -1
+PKV_ETOOBIG = -4
+#: Bytes of the library's static per-device scratch (pkv_paged_attention_noalloc).
+STATIC_SCRATCH_BYTES = 64 << 20
 
 EXPORTED_SYMBOLS = (
     "pkv_init",
@@ -76,6 +80,7 @@ EXPORTED_SYMBOLS = (
     "pkv_tile_head_dim_supported",
     "pkv_paged_attention",
     "pkv_paged_attention_append",
+    "pkv_paged_attention_noalloc",
     "pkv_greedy_tokens",
 )
 
@@ -182,6 +187,18 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_int, _ptr,  # device, stream
     ]
     lib.pkv_paged_attention.restype = _c_int
+    lib.pkv_paged_attention_noalloc.argtypes = [
+        _ptr, _ptr, _i64,  # out, queries, query_token_stride
+        _ptr, _ptr, _i64,  # query_positions, query_seq, num_queries
+        _ptr, _i64, _ptr, _i64,  # rows, num_rows, tiles, num_tiles
+        _ptr, _i64,  # merge_rows, num_merge_rows
+        _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size
+        _ptr, _i32, _ptr, _i32,  # block_tables, block_table_stride, context_lens, num_seqs
+        _i32, _i32, ctypes.c_float,  # num_heads, head_dim, scale
+        _i32, _i32, _i32,  # max_context_len, partition_size, flags
+        _c_int, _ptr,  # device, stream
+    ]
+    lib.pkv_paged_attention_noalloc.restype = _c_int
     lib.pkv_paged_attention_append.argtypes = [
         _ptr, _ptr, _i64,  # out, queries, query_token_stride
         _ptr, _ptr, _i64,  # query_positions, query_seq, num_queries

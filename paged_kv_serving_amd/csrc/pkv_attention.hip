@@ -39,6 +39,11 @@
 
 #include "pkv_common.h"
 
+// The split-context workspace of pkv_paged_attention_noalloc: a file-scope device array, one copy
+// per GPU (each device's address is looked up with hipGetSymbolAddress, with that device current,
+// and kept per device; host code never passes the array's own name to a kernel).
+static __device__ __align__(256) float scratch[PKV_STATIC_SCRATCH_BYTES / sizeof(float)];
+
 namespace pkv {
 namespace {
 
@@ -1147,7 +1152,8 @@ constexpr int kMaxDevices = 64;
 
 struct DeviceResources {
   std::mutex mu;
-  std::atomic<bool> ready{false};  // stream and events exist
+  std::atomic<bool> ready{false};            // stream and events exist
+  std::atomic<float*> scratch_ptr{nullptr};  // this device's copy of `scratch`
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr;
   hipEvent_t join = nullptr;
@@ -1155,6 +1161,19 @@ struct DeviceResources {
 };
 
 DeviceResources g_devices[kMaxDevices];
+
+// Looks up the current device's copy of `scratch` into r.scratch_ptr. Caller holds r.mu and has
+// made the device current.
+int resolve_scratch_locked(DeviceResources& r) {
+  if (r.scratch_ptr.load(std::memory_order_relaxed) != nullptr) return PKV_OK;
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    return PKV_EHIP;
+  }
+  r.scratch_ptr.store(static_cast<float*>(ptr), std::memory_order_release);
+  return PKV_OK;
+}
 
 // The device's overlap resources, or null when pkv_init has not created them.
 DeviceResources* overlap_for(int device) {
@@ -1348,6 +1367,8 @@ extern "C" int pkv_init(int device) {
   if (r.ready.load(std::memory_order_relaxed)) return PKV_OK;
   DeviceGuard guard(device);
   if (!guard.ok()) return PKV_EHIP;
+  const int found = resolve_scratch_locked(r);
+  if (found != PKV_OK) return found;
   int cus = 0;
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr;
@@ -1534,6 +1555,43 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
                              block_size, block_tables, block_table_stride, context_lens, num_seqs,
                              num_heads, head_dim, scale, max_context_len, partition_size, flags,
                              workspace, workspace_bytes, device, stream, nullptr);
+}
+
+extern "C" int pkv_paged_attention_noalloc(
+    float* out, const float* queries, int64_t query_token_stride, const int32_t* query_positions,
+    const int32_t* query_seq, int64_t num_queries, const int32_t* rows, int64_t num_rows,
+    const int32_t* tiles, int64_t num_tiles, const int32_t* merge_rows, int64_t num_merge_rows,
+    const void* key_cache, const void* value_cache, pkv_dtype kv_dtype, int64_t num_blocks,
+    int32_t block_size, const int32_t* block_tables, int32_t block_table_stride,
+    const int32_t* context_lens, int32_t num_seqs, int32_t num_heads, int32_t head_dim,
+    float scale, int32_t max_context_len, int32_t partition_size, int32_t flags, int device,
+    void* stream) {
+  using namespace pkv;
+  if (device < 0 || device >= kMaxDevices) return PKV_EINVAL;
+  const int64_t need = pkv_attention_workspace_bytes(num_queries, num_heads, head_dim,
+                                                     max_context_len, partition_size);
+  if (need < 0) return PKV_EINVAL;
+  if (need > PKV_STATIC_SCRATCH_BYTES) return PKV_ETOOBIG;
+  float* workspace = nullptr;
+  if (need > 0) {
+    DeviceResources& r = g_devices[device];
+    workspace = r.scratch_ptr.load(std::memory_order_acquire);
+    if (workspace == nullptr) {  // the device's first use: find its copy of the array
+      std::lock_guard<std::mutex> lock(r.mu);
+      DeviceGuard guard(device);
+      if (!guard.ok()) return PKV_EHIP;
+      const int rc = resolve_scratch_locked(r);
+      if (rc != PKV_OK) return rc;
+      workspace = r.scratch_ptr.load(std::memory_order_relaxed);
+    }
+  }
+  return pkv::attention_call(out, queries, query_token_stride, query_positions, query_seq,
+                             num_queries, rows, num_rows, tiles, num_tiles, merge_rows,
+                             num_merge_rows, key_cache, value_cache, kv_dtype, num_blocks,
+                             block_size, block_tables, block_table_stride, context_lens, num_seqs,
+                             num_heads, head_dim, scale, max_context_len, partition_size, flags,
+                             workspace, need > 0 ? PKV_STATIC_SCRATCH_BYTES : 0, device, stream,
+                             nullptr);
 }
 
 extern "C" int pkv_paged_attention_append(

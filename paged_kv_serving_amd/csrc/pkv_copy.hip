@@ -244,6 +244,8 @@ extern "C" const char* pkv_error_string(int code) {
       return "unsupported shape or dtype";
     case PKV_EHIP:
       return "HIP runtime error while enqueueing";
+    case PKV_ETOOBIG:
+      return "the batch needs more split-context scratch than the library's static buffer holds";
     default:
       return "unknown error code";
   }
