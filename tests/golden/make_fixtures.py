@@ -21,7 +21,7 @@ HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parents[1]))
 
 from oracle.attention import dense_attention, gather_context  # noqa: E402
-from oracle.model import apply_rope, rope_tables  # noqa: E402
+from oracle.model import rope_tables  # noqa: E402
 
 # (heads, head_dim, block_size, pool blocks, sequences, max context, prefill rows)
 ATTENTION_SHAPES = [
@@ -75,6 +75,25 @@ def attention_cases() -> dict[str, np.ndarray]:
     return out
 
 
+def rotate_elementwise(x: np.ndarray, positions: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """The rotation of model.py:77-81 evaluated one element at a time in float32 scalars, each
+    product and sum rounded on its own: out[i] = x[i] cos - x[i + D/2] sin and
+    out[i + D/2] = x[i + D/2] cos + x[i] sin, with (cos, sin) = table[position][i]. Written
+    independently of the vectorised oracle.apply_rope, so the fixture pins it."""
+    tokens, heads, dim = x.shape
+    half = dim // 2
+    out = np.empty_like(x)
+    for t in range(tokens):
+        p = int(positions[t])
+        for h in range(heads):
+            for i in range(half):
+                c, s = np.float32(cos[p, i]), np.float32(sin[p, i])
+                lo, hi = np.float32(x[t, h, i]), np.float32(x[t, h, i + half])
+                out[t, h, i] = np.float32(np.float32(lo * c) - np.float32(hi * s))
+                out[t, h, i + half] = np.float32(np.float32(hi * c) + np.float32(lo * s))
+    return out
+
+
 def rope_cases() -> dict[str, np.ndarray]:
     rng = np.random.default_rng(7)
     out: dict[str, np.ndarray] = {}
@@ -87,8 +106,8 @@ def rope_cases() -> dict[str, np.ndarray]:
         out.update({
             prefix + "fused": fused, prefix + "positions": positions,
             prefix + "cos": cos, prefix + "sin": sin,
-            prefix + "q": apply_rope(fused[:, 0], positions, cos, sin),
-            prefix + "k": apply_rope(fused[:, 1], positions, cos, sin),
+            prefix + "q": rotate_elementwise(fused[:, 0], positions, cos, sin),
+            prefix + "k": rotate_elementwise(fused[:, 1], positions, cos, sin),
         })  # fmt: skip
     out["count"] = np.int64(3)
     return out

@@ -50,3 +50,16 @@ def test_the_oracle_meets_the_closed_form_on_every_case() -> None:
             got[rows] = paged_attention(case["queries"][rows], case["positions"][rows], case["keys"],
                                         case["values"], table, ctx, float(case["scale"]))  # fmt: skip
         assert np.max(np.abs(got - case["expected"])) < 1e-5, i
+
+
+def test_the_oracle_rotation_equals_the_elementwise_fixture() -> None:
+    """The RoPE expectations are evaluated one element at a time in float32 scalars (not by the
+    oracle); the vectorised oracle must give the same bits."""
+    from oracle.model import apply_rope
+
+    data = _load("rope_cases.npz")
+    for i in range(int(data["count"])):
+        case = {k[len(f"r{i}_"):]: v for k, v in data.items() if k.startswith(f"r{i}_")}
+        for which, index in (("q", 0), ("k", 1)):
+            got = apply_rope(case["fused"][:, index], case["positions"], case["cos"], case["sin"])
+            assert np.array_equal(got, case[which]), (i, which)

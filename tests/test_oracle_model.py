@@ -10,6 +10,8 @@ order of model.py:173-203 independently).
 
 from __future__ import annotations
 
+from types import SimpleNamespace
+
 import numpy as np
 import pytest
 
@@ -157,3 +159,101 @@ def test_the_paged_runner_fails_when_the_table_is_wrong(model) -> None:
     runner.execute(ExecutionBatch((BatchEntry("s", tuple(tokens[:29]), tuple(range(29)), (0, 1, 2, 3)),)))
     wrong = runner.execute(ExecutionBatch((BatchEntry("s", (tokens[29],), (29,), (0, 5, 2, 3), 0),)))
     assert float(np.max(np.abs(wrong["s"] - model.reference_forward(tokens)[-1]))) > 1e-3
+
+
+# --- closed forms that a plausible slip (sign, swapped roles, transposed operand) would fail --
+
+
+def test_silu_is_the_clipped_logistic_closed_form() -> None:
+    """silu(x) = x / (1 + e^-clip(x, -60, 60)) (model.py:49-51) over a grid that crosses both
+    clips, against float64; and the exact identity silu(x) - silu(-x) = x, which a sign slip in
+    the exponent breaks."""
+    x = np.linspace(-80.0, 80.0, 3201).astype(np.float32)
+    x64 = x.astype(np.float64)
+    want = x64 / (1.0 + np.exp(-np.clip(x64, -60.0, 60.0)))
+    got = silu(x).astype(np.float64)
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 1e-30)) < 2e-6
+    assert np.isclose(float(silu(np.float32([1.0]))[0]), 0.7310585786300049, rtol=1e-6)
+    assert np.isclose(float(silu(np.float32([-1.0]))[0]), -0.2689414213699951, rtol=1e-6)
+    inner = np.linspace(-20.0, 20.0, 401).astype(np.float32)
+    assert np.max(np.abs((silu(inner) - silu(-inner)) - inner)) < 1e-5
+    assert np.isclose(float(silu(np.float32([-80.0]))[0]), -80.0 / (1.0 + np.exp(60.0)), rtol=1e-6, atol=0)
+
+
+def test_swiglu_gates_with_gate_and_scales_with_up() -> None:
+    """feed_forward = (silu(n @ gate) * (n @ up)) @ down with n = rms_norm(h) (model.py:256-259).
+    Hand-set 2 x 2 weights where swapping gate and up changes the answer."""
+    config = ModelConfig(vocab_size=4, d_model=2, n_layers=1, n_heads=1, d_ff=2, max_seq_len=4)
+    layer = SimpleNamespace(
+        ffn_norm=np.ones(2, np.float32),
+        gate_proj=np.asarray([[2.0, 0.0], [0.0, -1.0]], np.float32),
+        up_proj=np.asarray([[0.5, 0.0], [0.0, 3.0]], np.float32),
+        down_proj=np.asarray([[1.0, 0.0], [0.0, 1.0]], np.float32),
+    )
+    model = OracleModel(config, SimpleNamespace(token_embedding=np.zeros((4, 2), np.float32), layers=(),
+                                                final_norm=np.ones(2, np.float32)))  # fmt: skip
+    h = np.asarray([[3.0, 4.0]], np.float32)
+    n = np.asarray([3.0, 4.0]) / np.sqrt(12.5 + 1e-5)
+
+    def sig(v):
+        return 1.0 / (1.0 + np.exp(-v))
+
+    gate, up = n * np.asarray([2.0, -1.0]), n * np.asarray([0.5, 3.0])
+    want = gate * sig(gate) * up
+    swapped = up * sig(up) * gate
+    got = model.feed_forward(h, layer)[0].astype(np.float64)
+    assert np.max(np.abs(got - want)) < 1e-6
+    assert np.max(np.abs(got - swapped)) > 1e-2
+
+
+def test_logits_are_dot_products_with_the_tied_embedding() -> None:
+    """logits[r, v] = sum_j rms_norm(h)[r, j] * E[v, j] (model.py:261-264), each checked by an
+    explicit float64 loop; E is 5 x 4, so a missing transpose cannot even broadcast."""
+    rng = np.random.default_rng(21)
+    embedding = rng.standard_normal((5, 4)).astype(np.float32)
+    final = np.asarray([1.0, 0.5, 2.0, -1.0], np.float32)
+    config = ModelConfig(vocab_size=5, d_model=4, n_layers=1, n_heads=1, d_ff=2, max_seq_len=4)
+    model = OracleModel(config, SimpleNamespace(token_embedding=embedding, layers=(), final_norm=final))
+    hidden = rng.standard_normal((2, 4)).astype(np.float32)
+    got = model.logits_from_hidden(hidden)
+    assert got.shape == (2, 5)
+    for r in range(2):
+        h = hidden[r].astype(np.float64)
+        normed = h / np.sqrt(np.mean(h * h) + config.norm_eps) * final
+        for v in range(5):
+            want = sum(normed[j] * float(embedding[v, j]) for j in range(4))
+            assert abs(float(got[r, v]) - want) < 1e-5
+
+
+def test_project_qkv_splits_the_fused_output_as_tokens_x_3_x_heads_x_dim() -> None:
+    """qkv_proj = [I | 2I | 3I] makes q, k and v known multiples of the normed input: at
+    position 0 (rotation = identity) q = n, k = 2n, v = 3n per head; at any position k = 2q and
+    v = 3n. A (T, H, 3, D) split or a role swap fails."""
+    d, heads = 8, 2
+    config = ModelConfig(vocab_size=4, d_model=d, n_layers=1, n_heads=heads, d_ff=4, max_seq_len=16)
+    eye = np.eye(d, dtype=np.float32)
+    layer = SimpleNamespace(attn_norm=np.ones(d, np.float32), qkv_proj=np.concatenate([eye, 2 * eye, 3 * eye], axis=1))
+    model = OracleModel(config, SimpleNamespace(token_embedding=np.zeros((4, d), np.float32), layers=(),
+                                                final_norm=np.ones(d, np.float32)))  # fmt: skip
+    hidden = np.random.default_rng(22).standard_normal((3, d)).astype(np.float32)
+    normed = rms_norm(hidden, layer.attn_norm, config.norm_eps).reshape(3, heads, d // heads)
+    q, k, v = model.project_qkv(hidden, layer, np.zeros(3, np.int64))
+    assert np.allclose(q, normed, atol=1e-6) and np.allclose(k, 2 * normed, atol=1e-6)
+    assert np.allclose(v, 3 * normed, atol=1e-6)
+    q, k, v = model.project_qkv(hidden, layer, np.asarray([1, 5, 9]))
+    assert np.allclose(k, 2 * q, atol=1e-5) and np.allclose(v, 3 * normed, atol=1e-6)
+
+
+def test_rope_rotates_counter_clockwise_by_the_position_angle() -> None:
+    """At head_dim 2 the angle is the position itself (theta^0 = 1): [1, 0] at position p becomes
+    [cos p, sin p] and [0, 1] becomes [-sin p, cos p] (model.py:77-81). A rotation by -p gives
+    [cos p, -sin p] and fails."""
+    positions = np.arange(7)
+    cos, sin = rope_tables(7, 2, 10_000.0)
+    unit_x = np.tile(np.asarray([[[1.0, 0.0]]], np.float32), (7, 1, 1))
+    unit_y = np.tile(np.asarray([[[0.0, 1.0]]], np.float32), (7, 1, 1))
+    p = positions.astype(np.float64)
+    rx = apply_rope(unit_x, positions, cos, sin)[:, 0].astype(np.float64)
+    ry = apply_rope(unit_y, positions, cos, sin)[:, 0].astype(np.float64)
+    assert np.max(np.abs(rx - np.stack([np.cos(p), np.sin(p)], axis=1))) < 1e-7
+    assert np.max(np.abs(ry - np.stack([-np.sin(p), np.cos(p)], axis=1))) < 1e-7
