@@ -349,12 +349,61 @@ def config2(args) -> dict:
     )  # fmt: skip
     result["unit"] = "decode tokens/s"
     result.update(bulk_append_timing(args, batch))
+    result.update(runner_step_timing(args, batch))
+    result["runner_step_over_kernel"] = round(result["runner_step_ms"] / result["attention_ms"], 4)
     result["roofline"]["traffic"] = traffic_from_profiles()
     result["roofline"]["kernel"] = (
         "row_partial_kernel<float,128> (append fused) + reduce_kernel<128>"
         if result["append_fused_into_attention"] else "row_partial_kernel<float,128> + reduce_kernel<128>"
     )
     return result
+
+
+def runner_step_timing(args, batch, *, cow_pairs=None) -> dict:
+    """The same step through ``ModelRunner.attend``, as a serving loop runs it: reference-style
+    BatchEntry objects (block tables as tuples), host validation and slots, the block-table arena
+    update, the host plan (pkv_plan_batch), one metadata copy from pinned memory, the queued
+    copy-on-write flush (config 4), the append + attention call, and the synchronisation that
+    ends a step. Wall time per step, median; the runner has its own pool of the batch's size and
+    a model object with only the attention shape (attend reads no weights)."""
+    from types import SimpleNamespace
+
+    import torch
+
+    from paged_kv_serving_amd.config import ModelConfig
+    from paged_kv_serving_amd.runner import BatchEntry, ExecutionBatch, ModelRunner
+
+    device = batch.queries.device
+    num_blocks, block = batch.key_cache.shape[0], batch.key_cache.shape[1]
+    heads, dim = batch.key_cache.shape[2], batch.key_cache.shape[3]
+    config = ModelConfig(vocab_size=2, d_model=heads * dim, n_layers=1, n_heads=heads, d_ff=1,
+                         max_seq_len=int(batch.max_context_len) + 1)  # fmt: skip
+    model = SimpleNamespace(config=config, weights=None, rope=None, attention_scale=float(batch.scale))
+    runner = ModelRunner(model, num_blocks=num_blocks, block_size=block, device=device)
+    entries = []
+    for t in range(batch.num_queries):
+        s = int(batch.host_seq[t])
+        entries.append(BatchEntry(f"s{s}", (0,), (int(batch.host_positions[t]),),
+                                  tuple(int(b) for b in batch.host_tables[s]), 0))  # fmt: skip
+    step_batch = ExecutionBatch(tuple(entries))
+
+    def step() -> None:
+        for source, destination in cow_pairs or ():
+            runner.copy_block(source, destination)
+        runner.attend(step_batch, batch.queries, batch.new_keys, batch.new_values)
+        torch.cuda.synchronize(device)
+
+    for _ in range(max(args.warmup, 3)):
+        step()
+    seconds = []
+    for _ in range(max(args.steps, 5)):
+        start = time.perf_counter()
+        step()
+        seconds.append(time.perf_counter() - start)
+    ms = float(np.median(seconds)) * 1e3
+    del runner
+    torch.cuda.empty_cache()
+    return {"runner_step_ms": round(ms, 4)}
 
 
 def config3(args) -> dict:
@@ -478,7 +527,8 @@ def bulk_append_timing(args, batch) -> dict:
 
 def rope_append_timing(args, batch) -> dict:
     """The fused RoPE + append kernel on the batch's tokens (a [T, 3, H, D] projection output),
-    timed on its own: it is what ModelRunner.execute runs in place of the append."""
+    timed on its own as ModelRunner.execute runs it: the rotated queries overwrite the query
+    slice of the projection output in place, the rotated keys and the values go to the pool."""
     import torch
 
     from paged_kv_serving_amd import ops
@@ -491,12 +541,11 @@ def rope_append_timing(args, batch) -> dict:
     fused = torch.randn((tokens, 3, heads, dim), generator=gen, device=device)
     cos, sin = (torch.from_numpy(t).to(device) for t in rope_tables(4096, dim, 10_000.0))
     positions = batch.slot_mapping.remainder(4096)
-    out = torch.empty((tokens, heads, dim), device=device)
 
     def run() -> None:
         ops.rope_append(
             batch.key_cache, batch.value_cache, fused[:, 0], fused[:, 1], fused[:, 2],
-            positions, cos, sin, batch.slot_mapping, out=out,
+            positions, cos, sin, batch.slot_mapping, out=fused[:, 0],
         )  # fmt: skip
 
     for _ in range(max(args.warmup, 1)):
@@ -552,6 +601,8 @@ def config4(args) -> dict:
         workload="config4 prefix sharing: 256 seqs fork a 1016-token prefix (63 full + 1 partial "
         "block), suffixes U[32,256]; 256 COW copies of the partial block, then one decode step",
     )  # fmt: skip
+    result.update(runner_step_timing(args, batch, cow_pairs=step.host_pairs))
+    result["runner_step_over_kernel"] = round(result["runner_step_ms"] / (result["attention_ms"] + cow_ms), 4)
     unique = step.unique_context_bytes()
     # The roofline counts each distinct block once: the shared prefix is one HBM read, and the
     # logical rate (prefix counted per sequence) exceeds the HBM peak through cache hits.
@@ -562,6 +613,26 @@ def config4(args) -> dict:
         "algorithmic_bytes_per_launch": unique,
         "bytes_counted": "distinct K+V blocks read once",
     })  # fmt: skip
+    # The 256 COW pairs all copy the same partial block (every sequence forked it), so after its
+    # first read the caches serve the source: cow_gbps is not an HBM rate. The same launch over
+    # 256 distinct random sources (HBM-bound) gives the copy's HBM rate; run last, it overwrites
+    # pool blocks the decode step used.
+    rng = np.random.default_rng(args.seed + 1)
+    picks = rng.permutation(step.key_cache.shape[1])[:512]
+    distinct = torch.from_numpy(np.stack([picks[:256], picks[256:]], axis=1).astype(np.int64)).to(device)
+
+    def cow_distinct() -> None:
+        ops.copy_blocks(step.key_cache, step.value_cache, distinct)
+
+    for _ in range(args.warmup):
+        cow_distinct()
+    torch.cuda.synchronize()
+    distinct_ms = timed(cow_distinct, args.steps, stream)
+    result.update({
+        "cow_distinct_sources_us": round(distinct_ms * 1e3, 2),
+        "cow_distinct_sources_gbps": round(step.cow_bytes() / (distinct_ms * 1e-3) / 1e9, 1),
+        "cow_distinct_sources_frac_of_peak": round(step.cow_bytes() / (distinct_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+    })  # fmt: skip
     result.update({
         "cow_pairs": len(step.host_pairs),
         "cow_us": round(cow_ms * 1e3, 2),
@@ -570,7 +641,8 @@ def config4(args) -> dict:
         "unique_context_bytes": unique,
         "attention_unique_gbps": round(unique / (result["attention_ms"] * 1e-3) / 1e9, 1),
         "note": "attention_gbps counts the shared prefix once per sequence (logical bytes); "
-        "attention_unique_gbps counts distinct blocks",
+        "attention_unique_gbps counts distinct blocks; cow_gbps re-reads one cached source block "
+        "256 times, cow_distinct_sources_gbps is the HBM-bound copy rate",
     })  # fmt: skip
     return result
 

@@ -301,6 +301,38 @@ int pkv_paged_attention_append(
     const int64_t* slot_mapping, int device, void* stream);
 
 /*
+ * The host plan of one pkv_paged_attention call (host-only: reads and writes host memory, never
+ * touches a device).
+ *
+ * Replaces nothing in the reference, whose runner loops over sequences
+ * (src/paged_kv_serving/engine/runner.py:198-212); it decides how this library's one ragged call
+ * covers them: rows (the row pass's (query row, partition) items), tiles (runs of rows for the
+ * MFMA tile pass, including whole prefill tiles and shared-prefix tiles), the merge list, the
+ * partition size and the flags. Results never depend on the plan, only the launch does.
+ *
+ *   query_seq, query_positions : int32 [num_queries] (positions may be NULL: every row then
+ *                                sees its whole context), host memory.
+ *   block_tables               : int32 [num_seqs, block_table_stride], host; every sequence a
+ *                                query names must hold ceil(context / block_size) entries.
+ *   context_lens               : int32 [num_seqs], host.
+ *   partition_size             : 0 lets the planner choose; a positive value is kept.
+ *   min_tile_rows              : the shortest run of one sequence's rows made into tiles (8).
+ *   rows_out [rows_capacity, 2], tiles_out [tiles_capacity, 4], merge_out [merge_capacity] :
+ *                                int32 outputs in pkv_paged_attention's layout.
+ *   counts_out                 : int64 [3] = rows, tiles, merge rows written (or needed).
+ *   launch_out                 : int32 [2] = partition size, flags for pkv_paged_attention.
+ * Returns PKV_ETOOBIG, with counts_out holding the sizes needed and nothing else written, when a
+ * capacity is too small.
+ */
+int pkv_plan_batch(const int32_t* query_seq, const int32_t* query_positions, int64_t num_queries,
+                   const int32_t* block_tables, int32_t block_table_stride,
+                   const int32_t* context_lens, int32_t num_seqs, int32_t block_size,
+                   int32_t num_heads, int32_t head_dim, int32_t partition_size,
+                   int32_t min_tile_rows, int32_t* rows_out, int64_t rows_capacity,
+                   int32_t* tiles_out, int64_t tiles_capacity, int32_t* merge_out,
+                   int64_t merge_capacity, int64_t* counts_out, int32_t* launch_out);
+
+/*
  * Greedy sampling: the argmax of each logits row, on the device.
  *
  * Replaces src/paged_kv_serving/engine/sampling.py:28-30 (greedy_token: int(np.argmax(logits)))

@@ -9,9 +9,11 @@ exercised on a machine without a GPU (symbols resolve; no kernel is launched).
 from __future__ import annotations
 
 import ctypes
+import importlib
 import os
 import shutil
 import subprocess
+import sysconfig
 import tempfile
 import threading
 from pathlib import Path
@@ -35,7 +37,8 @@ CSRC = PACKAGE_DIR / "csrc"
 INCLUDE = REPO_ROOT / "include"
 LIB_PATH = PACKAGE_DIR / "libpkv.so"
 SOURCES = (
-    CSRC / "pkv_copy.hip", CSRC / "pkv_rope.hip", CSRC / "pkv_attention.hip", CSRC / "pkv_sample.hip"
+    CSRC / "pkv_copy.hip", CSRC / "pkv_rope.hip", CSRC / "pkv_attention.hip", CSRC / "pkv_sample.hip",
+    CSRC / "pkv_plan.hip",
 )
 
 # gfx950 only. Packed-FP32 VALU instructions are disabled: the code relies on scalar fp32 FMA.
@@ -82,6 +85,7 @@ EXPORTED_SYMBOLS = (
     "pkv_paged_attention_append",
     "pkv_paged_attention_noalloc",
     "pkv_greedy_tokens",
+    "pkv_plan_batch",
 )
 
 
@@ -128,6 +132,42 @@ def build(*, verbose: bool = False) -> Path:
     with _LOCK:
         _LIB = None  # reload on next use
     return LIB_PATH
+
+
+#: The host helper extension (csrc/pkv_host.cpp): per-entry batch work in C++, no device code.
+HOST_SOURCE = CSRC / "pkv_host.cpp"
+HOST_PATH = PACKAGE_DIR / f"_pkvhost{sysconfig.get_config_var('EXT_SUFFIX')}"
+
+
+def build_host(*, verbose: bool = False) -> Path:
+    """Compile the ``_pkvhost`` CPython extension next to this file with the host C++ compiler.
+    Always recompiles; written to a temporary file and renamed into place."""
+    compiler = shutil.which("g++") or shutil.which("c++")
+    if compiler is None:
+        raise NativeLibraryError("no host C++ compiler: the _pkvhost extension cannot be built")
+    with tempfile.NamedTemporaryFile(dir=PACKAGE_DIR, prefix="._pkvhost.", suffix=".so.tmp", delete=False) as handle:
+        tmp = Path(handle.name)
+    try:
+        command = [compiler, "-O3", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-missing-field-initializers",
+                   "-I", sysconfig.get_paths()["include"], "-o", str(tmp), str(HOST_SOURCE)]  # fmt: skip
+        result = subprocess.run(command, capture_output=True, text=True, check=False)
+        if verbose or result.returncode != 0:
+            if result.stderr.strip():
+                print(result.stderr)
+        if result.returncode != 0:
+            raise NativeLibraryError(f"building _pkvhost failed with exit code {result.returncode}")
+        os.replace(tmp, HOST_PATH)
+    finally:
+        if tmp.exists():
+            tmp.unlink()
+    return HOST_PATH
+
+
+def host():
+    """The ``_pkvhost`` extension module. Raises :class:`NativeLibraryError` if it is not built."""
+    if not HOST_PATH.exists():
+        raise NativeLibraryError(f"{HOST_PATH} is missing: build it with __graft_entry__.build()")
+    return importlib.import_module("paged_kv_serving_amd._pkvhost")
 
 
 _LOCK = threading.Lock()
@@ -218,6 +258,14 @@ def _declare(lib: ctypes.CDLL) -> None:
         _c_int, _ptr,  # device, stream
     ]
     lib.pkv_greedy_tokens.restype = _c_int
+    lib.pkv_plan_batch.argtypes = [
+        _ptr, _ptr, _i64,  # query_seq, query_positions, num_queries
+        _ptr, _i32, _ptr, _i32,  # block_tables, stride, context_lens, num_seqs
+        _i32, _i32, _i32, _i32, _i32,  # block_size, num_heads, head_dim, partition_size, min_tile_rows
+        _ptr, _i64, _ptr, _i64, _ptr, _i64,  # rows, capacity, tiles, capacity, merge, capacity
+        _ptr, _ptr,  # counts_out, launch_out
+    ]
+    lib.pkv_plan_batch.restype = _c_int
 
 
 def library() -> ctypes.CDLL:

@@ -10,10 +10,26 @@
 // bit-identical to the same expressions evaluated elementwise in float32.
 #include "pkv_common.h"
 
+// Tuning switches (config 3's 4,216 tokens, 32 heads x 128, float32 pool, MI355X):
+//   PKV_ROPE_NT    bit 0: non-temporal loads of q, k, v (they are read once); bit 1: of the pool
+//                  stores; bit 2: of the rotated-query store. Default 1: 64.2 us = 6.49 TB/s in
+//                  place (the runner's use), 65.1 us with a separate output; with cached loads
+//                  64.9 and 80.2 us. Bit 1 costs 3-9%; bit 2 gains under 1%, and the attention
+//                  call that follows reads the rotated queries, so they stay cacheable.
+//   PKV_ROPE_ITEMS (token, fragment) items per thread, all loads issued before any store.
+//                  Default 1: 2 and 4 items per thread took 65.7 and 70.6 us.
+#ifndef PKV_ROPE_NT
+#define PKV_ROPE_NT 1
+#endif
+#ifndef PKV_ROPE_ITEMS
+#define PKV_ROPE_ITEMS 1
+#endif
+
 namespace pkv {
 namespace {
 
 constexpr int kRopeThreads = 256;
+constexpr int kRopeItems = PKV_ROPE_ITEMS;
 
 // float32 row fragments are stored unchanged; into a bfloat16 pool they are rounded to nearest
 // even. kVec elements at a time (4: one 16-byte float load, 8-byte bf16 store; 1: scalar).
@@ -22,39 +38,64 @@ struct Frag {
   float v[kVec];
 };
 
-template <int kVec>
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+template <int kVec, bool kNt = false>
 __device__ __forceinline__ Frag<kVec> load_frag(const float* p) {
   Frag<kVec> f;
   if constexpr (kVec == 4) {
-    const float4 x = *reinterpret_cast<const float4*>(p);
+    f32x4 x;
+    if constexpr (kNt) {
+      x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    } else {
+      x = *reinterpret_cast<const f32x4*>(p);
+    }
     f.v[0] = x.x;
     f.v[1] = x.y;
     f.v[2] = x.z;
     f.v[3] = x.w;
+  } else if constexpr (kNt) {
+    f.v[0] = __builtin_nontemporal_load(p);
   } else {
     f.v[0] = *p;
   }
   return f;
 }
 
-template <int kVec>
+template <int kVec, bool kNt = false>
 __device__ __forceinline__ void store_frag(float* p, const Frag<kVec>& f) {
   if constexpr (kVec == 4) {
-    *reinterpret_cast<float4*>(p) = make_float4(f.v[0], f.v[1], f.v[2], f.v[3]);
+    const f32x4 x = {f.v[0], f.v[1], f.v[2], f.v[3]};
+    if constexpr (kNt) {
+      __builtin_nontemporal_store(x, reinterpret_cast<f32x4*>(p));
+    } else {
+      *reinterpret_cast<f32x4*>(p) = x;
+    }
+  } else if constexpr (kNt) {
+    __builtin_nontemporal_store(f.v[0], p);
   } else {
     *p = f.v[0];
   }
 }
 
-template <int kVec>
+template <int kVec, bool kNt = false>
 __device__ __forceinline__ void store_frag(uint16_t* p, const Frag<kVec>& f) {
   if constexpr (kVec == 4) {
-    uint2 o;
-    o.x = f32_to_bf16_bits(f.v[0]) | (f32_to_bf16_bits(f.v[1]) << 16);
-    o.y = f32_to_bf16_bits(f.v[2]) | (f32_to_bf16_bits(f.v[3]) << 16);
-    *reinterpret_cast<uint2*>(p) = o;
+    const u32x2 o = {f32_to_bf16_bits(f.v[0]) | (f32_to_bf16_bits(f.v[1]) << 16),
+                     f32_to_bf16_bits(f.v[2]) | (f32_to_bf16_bits(f.v[3]) << 16)};
+    if constexpr (kNt) {
+      __builtin_nontemporal_store(o, reinterpret_cast<u32x2*>(p));
+    } else {
+      *reinterpret_cast<u32x2*>(p) = o;
+    }
   } else {
-    *p = static_cast<uint16_t>(f32_to_bf16_bits(f.v[0]));
+    const auto bits = static_cast<uint16_t>(f32_to_bf16_bits(f.v[0]));
+    if constexpr (kNt) {
+      __builtin_nontemporal_store(bits, p);
+    } else {
+      *p = bits;
+    }
   }
 }
 
@@ -76,9 +117,10 @@ __device__ __forceinline__ void rotate(Frag<kVec>& lo, Frag<kVec>& hi, const Fra
   }
 }
 
-// One thread per (token, head, fragment of kVec elements of the lower half); the thread also
-// owns the matching fragment of the upper half. Flattened 1-D grid, fragment index fastest, so a
-// wavefront reads contiguous stretches of each head row.
+// One work item per (token, head, fragment of kVec elements of the lower half); its thread also
+// owns the matching fragment of the upper half. Flattened 1-D item space, fragment index fastest,
+// so a wavefront reads contiguous stretches of each head row. A thread takes kRopeItems items a
+// grid apart and issues all their loads before any store.
 template <typename PoolT, int kVec>
 __global__ __launch_bounds__(kRopeThreads) void rope_append_kernel(
     float* rotated, int64_t rotated_stride, const float* queries, const float* keys,
@@ -87,41 +129,60 @@ __global__ __launch_bounds__(kRopeThreads) void rope_append_kernel(
     const float* __restrict__ sin_table, int64_t table_rows, PoolT* __restrict__ key_pool,
     PoolT* __restrict__ value_pool, int64_t num_slots, const int64_t* __restrict__ slots,
     int64_t num_tokens, int num_heads, int head_dim) {
+  constexpr bool kNtLoad = (PKV_ROPE_NT & 1) != 0;
+  constexpr bool kNtPool = (PKV_ROPE_NT & 2) != 0;
+  constexpr bool kNtRot = (PKV_ROPE_NT & 4) != 0;
   const int half = head_dim / 2;
   const int frags = half / kVec;
-  const int64_t item = static_cast<int64_t>(blockIdx.x) * kRopeThreads + threadIdx.x;
   const int64_t per_token = static_cast<int64_t>(num_heads) * frags;
-  const int64_t token = item / per_token;
-  if (token >= num_tokens) return;
-  const int64_t rest = item - token * per_token;
-  const int h = static_cast<int>(rest / frags);
-  const int i = static_cast<int>(rest - static_cast<int64_t>(h) * frags) * kVec;
-  const int64_t pos = positions[token];
-  if (pos < 0 || pos >= table_rows) return;  // the host validates positions first
+  const int64_t total = num_tokens * per_token;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kRopeThreads + threadIdx.x;
+  const int64_t step = static_cast<int64_t>(gridDim.x) * kRopeThreads;
 
-  const Frag<kVec> c = load_frag<kVec>(cos_table + pos * half + i);
-  const Frag<kVec> s = load_frag<kVec>(sin_table + pos * half + i);
-  const int64_t head = static_cast<int64_t>(h) * head_dim + i;
-
-  Frag<kVec> qlo = load_frag<kVec>(queries + token * q_stride + head);
-  Frag<kVec> qhi = load_frag<kVec>(queries + token * q_stride + head + half);
-  Frag<kVec> klo = load_frag<kVec>(keys + token * k_stride + head);
-  Frag<kVec> khi = load_frag<kVec>(keys + token * k_stride + head + half);
-  const Frag<kVec> vlo = load_frag<kVec>(values + token * v_stride + head);
-  const Frag<kVec> vhi = load_frag<kVec>(values + token * v_stride + head + half);
-  rotate(qlo, qhi, c, s);
-  rotate(klo, khi, c, s);
-  // The rotated queries may overwrite the queries in place: this thread read its fragments above.
-  store_frag(rotated + token * rotated_stride + head, qlo);
-  store_frag(rotated + token * rotated_stride + head + half, qhi);
-
-  const int64_t slot = slots[token];
-  if (slot < 0 || slot >= num_slots) return;  // as pkv_append: a bad slot is skipped
-  const int64_t row = slot * num_heads * static_cast<int64_t>(head_dim) + head;
-  store_frag(key_pool + row, klo);
-  store_frag(key_pool + row + half, khi);
-  store_frag(value_pool + row, vlo);
-  store_frag(value_pool + row + half, vhi);
+  int64_t token[kRopeItems], head[kRopeItems];
+  bool live[kRopeItems];
+  Frag<kVec> qlo[kRopeItems], qhi[kRopeItems], klo[kRopeItems], khi[kRopeItems];
+  Frag<kVec> vlo[kRopeItems], vhi[kRopeItems], c[kRopeItems], s[kRopeItems];
+#pragma unroll
+  for (int k = 0; k < kRopeItems; ++k) {
+    const int64_t item = first + k * step;
+    token[k] = item / per_token;
+    live[k] = item < total;
+    if (!live[k]) continue;
+    const int64_t rest = item - token[k] * per_token;
+    const int h = static_cast<int>(rest / frags);
+    const int i = static_cast<int>(rest - static_cast<int64_t>(h) * frags) * kVec;
+    const int64_t pos = positions[token[k]];
+    live[k] = pos >= 0 && pos < table_rows;  // the host validates positions first
+    if (!live[k]) continue;
+    head[k] = static_cast<int64_t>(h) * head_dim + i;
+    c[k] = load_frag<kVec>(cos_table + pos * half + i);
+    s[k] = load_frag<kVec>(sin_table + pos * half + i);
+    const int64_t t = token[k];
+    qlo[k] = load_frag<kVec, kNtLoad>(queries + t * q_stride + head[k]);
+    qhi[k] = load_frag<kVec, kNtLoad>(queries + t * q_stride + head[k] + half);
+    klo[k] = load_frag<kVec, kNtLoad>(keys + t * k_stride + head[k]);
+    khi[k] = load_frag<kVec, kNtLoad>(keys + t * k_stride + head[k] + half);
+    vlo[k] = load_frag<kVec, kNtLoad>(values + t * v_stride + head[k]);
+    vhi[k] = load_frag<kVec, kNtLoad>(values + t * v_stride + head[k] + half);
+  }
+#pragma unroll
+  for (int k = 0; k < kRopeItems; ++k) {
+    if (!live[k]) continue;
+    const int64_t t = token[k];
+    rotate(qlo[k], qhi[k], c[k], s[k]);
+    rotate(klo[k], khi[k], c[k], s[k]);
+    // The rotated queries may overwrite the queries in place: this thread read them above.
+    store_frag<kVec, kNtRot>(rotated + t * rotated_stride + head[k], qlo[k]);
+    store_frag<kVec, kNtRot>(rotated + t * rotated_stride + head[k] + half, qhi[k]);
+    const int64_t slot = slots[t];
+    if (slot < 0 || slot >= num_slots) continue;  // as pkv_append: a bad slot is skipped
+    const int64_t row = slot * num_heads * static_cast<int64_t>(head_dim) + head[k];
+    store_frag<kVec, kNtPool>(key_pool + row, klo[k]);
+    store_frag<kVec, kNtPool>(key_pool + row + half, khi[k]);
+    store_frag<kVec, kNtPool>(value_pool + row, vlo[k]);
+    store_frag<kVec, kNtPool>(value_pool + row + half, vhi[k]);
+  }
 }
 
 template <typename PoolT>
@@ -140,7 +201,8 @@ int launch_rope_append(float* rotated, int64_t rotated_stride, const float* quer
                           aligned16(value_pool);
   const int vec = vectorized ? 4 : 1;
   const int64_t items = num_tokens * num_heads * (half / vec);
-  const int64_t groups = (items + kRopeThreads - 1) / kRopeThreads;
+  const int64_t threads = (items + kRopeItems - 1) / kRopeItems;
+  const int64_t groups = (threads + kRopeThreads - 1) / kRopeThreads;
   if (groups > 0x7fffffff) return PKV_EUNSUPPORTED;
   const dim3 grid(static_cast<uint32_t>(groups));
   auto* kp = static_cast<PoolT*>(key_pool);

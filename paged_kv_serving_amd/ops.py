@@ -30,7 +30,9 @@ __all__ = [
     "paged_attention_ragged",
     "BatchPlan",
     "batch_hints",
+    "NativePlanner",
     "plan_batch",
+    "plan_batch_native",
     "plan_rows",
     "tiles_supported",
     "upload_batch_plan",
@@ -248,6 +250,13 @@ def independent_groups(pairs: list[tuple[int, int]]) -> list[list[tuple[int, int
     time in list order: a copy starts a new group when it reads a block an earlier copy of the
     group writes, or writes a block an earlier copy of the group reads or writes.
     """
+    if not pairs:
+        return []
+    # The common case -- every destination distinct and none of them also a source (a batch of
+    # forks copying shared blocks into fresh ones) -- is one group.
+    destinations = {dst for _, dst in pairs}
+    if len(destinations) == len(pairs) and destinations.isdisjoint(src for src, _ in pairs):
+        return [list(pairs)]
     groups: list[list[tuple[int, int]]] = []
     reads: set[int] = set()
     writes: set[int] = set()
@@ -679,6 +688,112 @@ def plan_batch(
         keys = np.minimum(partition, visible[items[:, 0]] - items[:, 1].astype(np.int64) * partition)
         short = bool(np.mean(np.maximum(keys, 0)) < SHORT_ROW_KEYS)
     return BatchPlan(items, tiles, int(partition), _repeated_fraction_reached(ids), merge, short)
+
+
+class NativePlanner:
+    """:func:`plan_batch` computed by the library's host planner (``pkv_plan_batch``), with
+    output buffers kept between calls. The same plan, bit for bit (tests/test_host_plan_native.py),
+    at a few microseconds per decode batch instead of a hundred. One instance per caller: the
+    buffers are reused."""
+
+    def __init__(self) -> None:
+        self._rows = np.zeros((4096, 2), np.int32)
+        self._tiles = np.zeros((256, 4), np.int32)
+        self._merge = np.zeros(1024, np.int32)
+        self._counts = np.zeros(3, np.int64)
+        self._launch = np.zeros(2, np.int32)
+
+    def plan(
+        self, query_seq: np.ndarray, head_dim: int, num_heads: int, tables: np.ndarray,
+        context_lens: np.ndarray, block_size: int, *, partition_size: int = 0,
+        min_tile_rows: int = MIN_TILE_ROWS, query_positions: np.ndarray | None = None,
+    ) -> BatchPlan:  # fmt: skip
+        """Arguments as :func:`plan_batch`, except that ``tables`` is a 2-D int32 array (one
+        padded row per sequence index, as the runner's block-table arena holds them)."""
+        seq = np.ascontiguousarray(query_seq, dtype=np.int32)
+        table = np.ascontiguousarray(tables, dtype=np.int32)
+        if table.ndim != 2:
+            raise ValueError("tables must be a 2-D int32 array")
+        contexts = np.ascontiguousarray(context_lens, dtype=np.int32)
+        positions = None if query_positions is None else np.ascontiguousarray(query_positions, dtype=np.int32)
+        lib = _native.library()
+        while True:
+            rc = lib.pkv_plan_batch(
+                seq.ctypes.data, None if positions is None else positions.ctypes.data, seq.size,
+                table.ctypes.data, table.shape[1], contexts.ctypes.data, contexts.size,
+                block_size, num_heads, head_dim, partition_size, min_tile_rows,
+                self._rows.ctypes.data, self._rows.shape[0], self._tiles.ctypes.data, self._tiles.shape[0],
+                self._merge.ctypes.data, self._merge.size, self._counts.ctypes.data, self._launch.ctypes.data,
+            )  # fmt: skip
+            if rc != _native.PKV_ETOOBIG:
+                break
+            rows, tiles, merge = (int(c) for c in self._counts)
+            self._rows = np.zeros((max(rows, 2 * self._rows.shape[0]), 2), np.int32)
+            self._tiles = np.zeros((max(tiles, 2 * self._tiles.shape[0]), 4), np.int32)
+            self._merge = np.zeros(max(merge, 2 * self._merge.size), np.int32)
+        _native.check(rc, "pkv_plan_batch")
+        rows, tiles, merge = (int(c) for c in self._counts)
+        partition, flags = (int(v) for v in self._launch)
+        return BatchPlan(
+            self._rows[:rows].copy(), self._tiles[:tiles].copy(), partition,
+            bool(flags & _native.PKV_ATTN_SHARED_KV), self._merge[:merge].copy(),
+            bool(flags & _native.PKV_ATTN_SHORT_ROWS),
+        )  # fmt: skip
+
+
+def plan_batch_native(query_seq, head_dim, num_heads, tables, context_lens, block_size, **kwargs) -> BatchPlan:
+    """:meth:`NativePlanner.plan` with a fresh planner; ``tables`` may also be a list of
+    per-sequence tables (padded here)."""
+    if not (isinstance(tables, np.ndarray) and tables.ndim == 2):
+        width = max((len(t) for t in tables), default=0)
+        padded = np.zeros((len(tables), max(width, 1)), np.int32)
+        for i, t in enumerate(tables):
+            padded[i, : len(t)] = np.asarray(t)
+        tables = padded
+    return NativePlanner().plan(query_seq, head_dim, num_heads, tables, context_lens, block_size, **kwargs)
+
+
+def launch_paged_attention(
+    out: torch.Tensor, queries: torch.Tensor, query_positions: torch.Tensor, query_seq: torch.Tensor,
+    key_cache: torch.Tensor, value_cache: torch.Tensor, block_tables: torch.Tensor,
+    context_lens: torch.Tensor, scale: float, max_context_len: int, plan: AttentionPlan,
+    workspace: torch.Tensor, device: int, append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+) -> None:  # fmt: skip
+    """:func:`paged_attention_ragged` for callers that built every argument themselves (the
+    runner): the same C call without re-validating shapes and dtypes on the host. Preconditions
+    are the checked function's: contiguous float32 ``out`` ``[T, H, D]``; queries with
+    contiguous rows; int32 positions, sequence indices, tables, contexts and plan tensors on the
+    pools' device; a workspace of ``attention_workspace_bytes`` bytes; for ``append``, the decode
+    shape. The library still validates sizes and pointers before enqueueing anything."""
+    num_queries, heads, dim = out.shape
+    flags = (_native.PKV_ATTN_SHARED_KV if plan.shared_kv else 0) | (_native.PKV_ATTN_SHORT_ROWS if plan.short_rows else 0)
+    merge = plan.merge
+    num_merge = -1 if merge is None else int(merge.shape[0])
+    num_rows, num_tiles = int(plan.rows.shape[0]), int(plan.tiles.shape[0])
+    if num_queries == 0 or (num_rows == 0 and num_tiles == 0):
+        return
+    lib = _native.library()
+    common = (
+        out.data_ptr(), queries.data_ptr(), queries.stride(0), query_positions.data_ptr(), query_seq.data_ptr(),
+        num_queries, plan.rows.data_ptr() if num_rows else None, num_rows,
+    )  # fmt: skip
+    tail = (
+        merge.data_ptr() if num_merge > 0 else None, num_merge, key_cache.data_ptr(), value_cache.data_ptr(),
+        kv_dtype_code(key_cache.dtype), key_cache.shape[0], key_cache.shape[1], block_tables.data_ptr(),
+        block_tables.shape[1], context_lens.data_ptr(), block_tables.shape[0], heads, dim, float(scale),
+        max_context_len, plan.partition_size, flags, workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+    )  # fmt: skip
+    if append is None:
+        rc = lib.pkv_paged_attention(*common, plan.tiles.data_ptr() if num_tiles else None, num_tiles, *tail,
+                                     device, _stream(device))  # fmt: skip
+        _native.check(rc, "pkv_paged_attention")
+        return
+    new_keys, new_values, slot_mapping = append
+    rc = lib.pkv_paged_attention_append(
+        *common, *tail, new_keys.data_ptr(), new_values.data_ptr(), kv_dtype_code(new_keys.dtype),
+        new_keys.stride(0), new_values.stride(0), slot_mapping.data_ptr(), device, _stream(device),
+    )  # fmt: skip
+    _native.check(rc, "pkv_paged_attention_append")
 
 
 def upload_plan(

@@ -31,7 +31,7 @@ from dataclasses import dataclass
 import numpy as np
 import torch
 
-from paged_kv_serving_amd import ops
+from paged_kv_serving_amd import _native, ops
 from paged_kv_serving_amd.tables import BlockTableArena
 
 __all__ = ["DEFAULT_TILE_BLOCKS", "BatchEntry", "ExecutionBatch", "ModelRunner", "compute_slots"]
@@ -138,6 +138,10 @@ def shared_prefix_order(entries, block_size: int) -> list[int] | None:
     decode = [i for i, e in enumerate(entries) if len(e.token_ids) == 1 and len(e.block_table) >= lead]
     if len(decode) < ops.MIN_SHARED_ROWS:
         return None
+    # Sharers have the same first block: when every decode entry starts elsewhere (the common
+    # case of private sequences), there is nothing to group.
+    if len({entries[i].block_table[0] for i in decode}) == len(decode):
+        return None
     keys = {i: tuple(entries[i].block_table[:lead]) for i in decode}
     grouped = sorted(decode, key=lambda i: keys[i])
     # Nothing to gain when no two decode entries share their leading blocks, or when the
@@ -156,6 +160,69 @@ def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor
 
 def _silu(x: torch.Tensor) -> torch.Tensor:
     return x * (1.0 / (1.0 + torch.exp(-torch.clamp(x, -60.0, 60.0))))
+
+
+class _Staging:
+    """One call's integer metadata, sent in one asynchronous copy from pinned host memory.
+
+    The sections (int64 first, then int32, each 8-byte aligned) are written into a pinned host
+    buffer and copied to a device buffer of the same layout on the runner's stream; the host does
+    not wait for the copy. Before a later call rewrites the host buffer it waits for the copy that
+    last read it (an event), which has normally long finished."""
+
+    def __init__(self, device: torch.device) -> None:
+        self.device = device
+        self.host: torch.Tensor | None = None
+        self.dev: torch.Tensor | None = None
+        self.done = torch.cuda.Event()
+        self.pending = False
+
+    def send(self, parts64: list[np.ndarray], parts32: list[np.ndarray]) -> tuple[list[torch.Tensor], list[torch.Tensor]]:
+        """Device int64 and int32 tensors holding ``parts64`` and ``parts32``, in order."""
+        n64 = sum(p.size for p in parts64)
+        n32 = sum(p.size for p in parts32)
+        nbytes = 8 * n64 + 4 * n32 + 8
+        if self.pending:
+            self.done.synchronize()
+        if self.host is None or self.host.numel() < nbytes:
+            size = max(nbytes, 2 * (0 if self.host is None else self.host.numel()), 1 << 16)
+            self.host = torch.empty(size, dtype=torch.uint8, pin_memory=True)
+            self.dev = torch.empty(size, dtype=torch.uint8, device=self.device)
+        host = self.host.numpy()
+        off32 = 8 * n64
+        if parts64:
+            np.concatenate(parts64, out=host[:off32].view(np.int64), casting="same_kind")
+        if parts32:
+            np.concatenate(parts32, out=host[off32 : off32 + 4 * n32].view(np.int32), casting="same_kind")
+        with torch.cuda.device(self.device):
+            self.dev[: off32 + 4 * n32].copy_(self.host[: off32 + 4 * n32], non_blocking=True)
+            self.done.record(torch.cuda.current_stream(self.device))
+        self.pending = True
+        dev64 = self.dev[:off32].view(torch.int64)
+        dev32 = self.dev[off32 : off32 + 4 * n32].view(torch.int32)
+        return dev64.split([p.size for p in parts64]), dev32.split([p.size for p in parts32])
+
+
+@dataclass
+class _Step:
+    """One iteration's device-side metadata (from :meth:`ModelRunner._prepare`), in the planner's
+    row order; ``token_order`` maps it back to batch order (None: the same)."""
+
+    total: int
+    tokens: torch.Tensor
+    rope_positions: torch.Tensor
+    slots: torch.Tensor
+    query_positions: torch.Tensor
+    query_seq: torch.Tensor
+    contexts: torch.Tensor
+    tables: torch.Tensor
+    plan: ops.AttentionPlan
+    max_context: int
+    token_order: np.ndarray | None
+    names: list[str]
+    logits_rows: torch.Tensor
+    decode_only: bool
+    workspace: torch.Tensor | None = None
 
 
 class _DeviceWeights:
@@ -221,6 +288,13 @@ class ModelRunner:
         self._pending: list[tuple[int, int]] = []
         self._weights: _DeviceWeights | None = None
         self._tables = BlockTableArena(self.device)
+        self._planner = ops.NativePlanner()
+        self._staging = _Staging(self.device)
+        self._host = _native.host()
+        self._device_index = self.device.index
+        _native.init_device(self._device_index)  # the library's overlap stream on this device
+        self._per_token = (np.zeros(1024, np.int64), np.zeros(1024, np.int64), np.zeros(1024, np.int64))
+        self._per_entry = (np.zeros(256, np.int64), np.zeros(256, np.int32), np.zeros(256, np.int64))
         #: The host plan of the last ``execute`` (rows, tiles, partition size, load hint).
         self.last_plan: ops.BatchPlan | None = None
 
@@ -261,9 +335,9 @@ class ModelRunner:
         """
         if source == destination:
             raise ValueError("copy-on-write must not copy a block onto itself")
-        for block_id in (source, destination):
-            if not 0 <= block_id < self.num_blocks:
-                raise IndexError(f"block id {block_id} is outside the pool")
+        n = self.num_blocks
+        if not (0 <= source < n and 0 <= destination < n):
+            raise IndexError(f"block id {source if not 0 <= source < n else destination} is outside the pool")
         self._pending.append((int(source), int(destination)))
 
     def flush_copies(self) -> int:
@@ -320,91 +394,183 @@ class ModelRunner:
         tokens = ops.greedy_tokens(logits).cpu().numpy()
         return {name: int(tokens[i]) for i, name in enumerate(names)}
 
-    def _forward(self, batch: ExecutionBatch) -> tuple[list[str], torch.Tensor | None]:
-        """The forward pass of one iteration: (seq ids, device logits [rows, vocab]) of the
-        entries that ask for logits, in batch order."""
+    def _gather(self, entries):
+        """One C++ walk over the entries (``_pkvhost.gather``): token ids, positions and slots
+        (batch order, int64), per-entry lengths, context lengths (int32) and flat logits rows (-1:
+        none), and the first slot problem (0 none, 1 past the table, 2 before its start) with its
+        entry index and position."""
+        count = len(entries)
+        if self._per_entry[0].size < count:
+            n = max(count, 2 * self._per_entry[0].size)
+            self._per_entry = (np.zeros(n, np.int64), np.zeros(n, np.int32), np.zeros(n, np.int64))
+        lengths, contexts, logits = self._per_entry
+        while True:
+            tokens, positions, slots = self._per_token
+            total, problem, entry, position = self._host.gather(
+                entries, self.block_size, tokens, positions, slots, lengths, contexts, logits
+            )
+            if total >= 0:
+                break
+            n = max(-total, 2 * tokens.size)
+            self._per_token = (np.zeros(n, np.int64), np.zeros(n, np.int64), np.zeros(n, np.int64))
+        return (tokens[:total].copy(), positions[:total].copy(), slots[:total].copy(), lengths[:count].copy(),
+                contexts[:count].copy(), logits[:count].copy(), (problem, entry, position))  # fmt: skip
+
+    def _prepare(self, batch: ExecutionBatch) -> _Step | None:
+        """Everything one iteration needs on the device before its first kernel: validation in
+        the reference's order and with its messages, slots, the block-table arena update, the
+        attention plan, and one asynchronous copy of all of it (None for an empty batch)."""
         entries = batch.entries
         if not entries:
-            return [], None
+            return None
         config = self.model.config
-        total = sum(len(entry.token_ids) for entry in entries)
-        tokens = np.fromiter((t for e in entries for t in e.token_ids), dtype=np.int64, count=total)
+        tokens, positions, slots, lengths, context, logits_rows, (problem, bad, position) = self._gather(entries)
+        total = tokens.size
+        # The reference checks token ids, then positions, then forms the slots (runner.py:174-187).
         if np.any(tokens < 0) or np.any(tokens >= config.vocab_size):
             raise ValueError("token id outside the vocabulary")
-        positions = np.fromiter((p for e in entries for p in e.positions), dtype=np.int64, count=total)
         if np.any(positions >= config.max_seq_len):
             raise ValueError("position beyond max_seq_len")
-        if np.any(positions < 0):
-            raise ValueError("positions must be >= 0")
-        slots = compute_slots(entries, self.block_size)
+        if problem == 1:
+            raise ValueError(f"sequence {entries[bad].seq_id}: position {position} has no block in the table")
+        if problem == 2:
+            raise IndexError("tuple index out of range")
         if slots.size and (slots.min() < 0 or slots.max() >= self.capacity_tokens):
             raise IndexError("a block table names a block outside the pool")
-        # Rows in the order the planner can use (validation above ran in batch order, so errors
-        # name the same entry as the reference's); logits come back in batch order below.
-        order = shared_prefix_order(entries, self.block_size)
-        lengths = np.fromiter((len(e.token_ids) for e in entries), dtype=np.int64, count=len(entries))
-        batch_starts = np.cumsum(lengths) - lengths
+        # Negative positions run as in the reference: their slot comes from the end of the table
+        # (a Python index, runner.py:158), their rotary angle from the end of the tables (a NumPy
+        # index, model.py:77-78), and every key is masked for them (a zero attention row,
+        # attention.py:102-104, 120-121). An entry ending at one has context_len < 1, which the
+        # reference's attention refuses (attention.py:76-77).
+        rope_positions = positions
+        if positions.size and positions.min() < 0:
+            if positions.min() < -config.max_seq_len:
+                raise IndexError("position outside the rotary tables")
+            if context.min() < 1:
+                raise ValueError("context_len must be >= 1")
+            rope_positions = np.where(positions < 0, positions + config.max_seq_len, positions)
+        # Logits rows, in batch order of the entries that ask for them.
+        wanted = logits_rows[logits_rows >= 0]
+        names = [e.seq_id for e in entries if e.logits_index is not None] if wanted.size else []
+        # Rows in the order the planner can use: decode entries sharing leading blocks together
+        # (validation above ran in batch order, so errors name the reference's entry).
+        order = self._host.prefix_order(entries, -(-ops.MIN_SHARED_TOKENS // self.block_size), ops.MIN_SHARED_ROWS)
+        token_order = None
         if order is not None:
+            order = np.asarray(order, dtype=np.int64)
+            batch_starts = np.cumsum(lengths) - lengths
             token_order = np.concatenate([np.arange(batch_starts[i], batch_starts[i] + lengths[i]) for i in order])
             tokens, positions, slots = tokens[token_order], positions[token_order], slots[token_order]
-            moved = np.cumsum(lengths[order]) - lengths[order]
-            starts = np.empty_like(batch_starts)
-            starts[order] = moved
-            entries = [entries[i] for i in order]
-        else:
-            starts = batch_starts
+            rope_positions = rope_positions[token_order]
+            planner_row = np.empty(total, dtype=np.int64)  # batch token index -> planner token index
+            planner_row[token_order] = np.arange(total)
+            wanted = planner_row[wanted]
+            entries = [entries[i] for i in order.tolist()]
+            lengths, context = lengths[order], context[order]
 
-        num_seqs = len(entries)
         # Block tables live in a device arena between calls; only changed entries travel.
         update = self._tables.update(entries)
-        arena_rows = self._tables.num_rows
-        context = np.fromiter((e.positions[-1] + 1 for e in entries), dtype=np.int32, count=num_seqs)
-        contexts_by_row = np.zeros(arena_rows, dtype=np.int32)
+        contexts_by_row = np.zeros(self._tables.num_rows, dtype=np.int32)
         contexts_by_row[update.rows] = context
-        per_entry = np.fromiter((len(e.token_ids) for e in entries), dtype=np.int64, count=num_seqs)
-        query_seq = np.repeat(update.rows, per_entry)
-        host_plan = ops.plan_batch(
+        query_seq = np.repeat(update.rows, lengths)
+        host_plan = self._planner.plan(
             query_seq, config.head_dim, config.n_heads, self._tables.host, contexts_by_row,
             self.block_size, partition_size=self.partition_size, query_positions=positions,
         )  # fmt: skip
         self.last_plan = host_plan
-        partition = host_plan.partition_size
-        plan_rows, plan_tiles, plan_merge = host_plan.rows, host_plan.tiles, host_plan.merge
-        changed = update.index.size
-        meta64 = torch.from_numpy(np.concatenate([tokens, positions, slots, update.index])).to(self.device)
-        meta32 = torch.from_numpy(
-            np.concatenate([
-                positions.astype(np.int32), query_seq, contexts_by_row, update.values,
-                plan_rows.ravel(), plan_tiles.ravel(), plan_merge,
-            ])  # fmt: skip
-        ).to(self.device)
-        tokens_d, positions_d = meta64[:total], meta64[total : 2 * total]
-        slots_d = meta64[2 * total : 3 * total]
-        qpos_d = meta32[:total]
-        qseq_d = meta32[total : 2 * total]
-        context_d = meta32[2 * total : 2 * total + arena_rows]
-        end_values = 2 * total + arena_rows + changed
-        self._tables.apply(meta64[3 * total :], meta32[2 * total + arena_rows : end_values])
-        tables_d = self._tables.tables
-        end_rows = end_values + plan_rows.size
-        end_tiles = end_rows + plan_tiles.size
+        # Queued copy-on-write pairs travel in the same copy and run before this step's kernels.
+        groups = ops.independent_groups(self._pending) if self._pending else []
+        self._pending = []
+        pairs = [np.asarray(group, dtype=np.int64).ravel() for group in groups]
+        parts64, parts32 = self._staging.send(
+            [tokens, rope_positions, slots, update.index, wanted, *pairs],
+            [positions, query_seq, contexts_by_row, update.values, host_plan.rows.ravel(),
+             host_plan.tiles.ravel(), host_plan.merge],
+        )  # fmt: skip
+        tokens_d, rope_d, slots_d, index_d, rows_d = parts64[:5]
+        qpos_d, qseq_d, context_d, values_d, plan_rows_d, plan_tiles_d, merge_d = parts32
+        for pair_d in parts64[5:]:
+            ops.copy_blocks(self._keys, self._values, pair_d.view(-1, 2))
+        self._tables.apply(index_d, values_d)
         plan = ops.AttentionPlan(
-            rows=meta32[end_values:end_rows].view(-1, 2),
-            tiles=meta32[end_rows:end_tiles].view(-1, 4),
-            partition_size=partition,
-            shared_kv=host_plan.shared_kv,
-            merge=meta32[end_tiles:],
+            rows=plan_rows_d.view(-1, 2), tiles=plan_tiles_d.view(-1, 4),
+            partition_size=host_plan.partition_size, shared_kv=host_plan.shared_kv, merge=merge_d,
             short_rows=host_plan.short_rows,
-        )
-        max_context = int(context.max())
+        )  # fmt: skip
+        decode_only = bool(host_plan.tiles.size == 0 and len(entries) == total and
+                           np.array_equal(positions, context.astype(np.int64) - 1))  # fmt: skip
+        return _Step(
+            total=total, tokens=tokens_d, rope_positions=rope_d, slots=slots_d, query_positions=qpos_d,
+            query_seq=qseq_d, contexts=context_d, tables=self._tables.tables, plan=plan,
+            max_context=int(context.max()), token_order=token_order, names=names, logits_rows=rows_d,
+            decode_only=decode_only,
+        )  # fmt: skip
 
-        self.flush_copies()
+    def _attention(self, step: _Step, layer: int, queries: torch.Tensor, out: torch.Tensor, append=None) -> None:
+        """Paged attention of one layer's rotated queries over the pools (and the decode append
+        fused into it when ``append`` = (keys, values) rows is given)."""
+        config = self.model.config
+        need = ops.attention_workspace_bytes(step.total, config.n_heads, config.head_dim, step.max_context,
+                                             step.plan.partition_size)  # fmt: skip
+        if step.workspace is None or step.workspace.numel() * 4 < need:
+            step.workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=self.device)
+        ops.launch_paged_attention(
+            out, queries, step.query_positions, step.query_seq, self._keys[layer], self._values[layer],
+            step.tables, step.contexts, self.model.attention_scale, step.max_context, step.plan,
+            step.workspace, self._device_index, None if append is None else (append[0], append[1], step.slots),
+        )  # fmt: skip
+
+    def attend(
+        self, batch: ExecutionBatch, queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
+        *, layer: int = 0, out: torch.Tensor | None = None,
+    ) -> torch.Tensor:  # fmt: skip
+        """The KV data path of one layer for caller-computed projections: the batch's keys and
+        values (float32 ``[T, heads, head_dim]``, rotated already, in batch token order) are
+        written at its slots and every query attends over its entry's block table
+        (reference runner.py:184-212 for one layer). Returns float32 ``[T, heads, head_dim]`` in
+        batch order, on the device (asynchronous). A decode batch (one token per entry, at its
+        last position) appends inside the attention call."""
+        step = self._prepare(batch)
+        config = self.model.config
+        total = 0 if step is None else step.total
+        shape = (total, config.n_heads, config.head_dim)
+        if out is None:
+            out = torch.empty(shape, dtype=torch.float32, device=self.device)
+        if step is None:
+            return out
+        for name, tensor in (("queries", queries), ("keys", keys), ("values", values), ("out", out)):
+            if tuple(tensor.shape) != shape or tensor.dtype != torch.float32 or tensor.device != self.device:
+                raise ValueError(f"{name} must be float32 {list(shape)} on the runner's device")
+        if not out.is_contiguous():
+            raise ValueError("out must be contiguous")
+        queries, keys, values = (t if t.is_contiguous() else t.contiguous() for t in (queries, keys, values))
+        if step.token_order is not None:  # the planner's row order
+            index = torch.from_numpy(step.token_order).to(self.device)
+            queries, keys, values = queries[index], keys[index], values[index]
+            result = torch.empty_like(out)
+        else:
+            result = out
+        if step.decode_only:
+            self._attention(step, layer, queries, result, append=(keys, values))
+        else:
+            ops.append_kv(self._keys[layer], self._values[layer], keys, values, step.slots)
+            self._attention(step, layer, queries, result)
+        if step.token_order is not None:
+            out[index] = result
+        return out
+
+    def _forward(self, batch: ExecutionBatch) -> tuple[list[str], torch.Tensor | None]:
+        """The forward pass of one iteration: (seq ids, device logits [rows, vocab]) of the
+        entries that ask for logits, in batch order."""
+        step = self._prepare(batch)
+        if step is None:
+            return [], None
+        config = self.model.config
+        total = step.total
         w = self._device_weights()
         heads, dim, d_model = config.n_heads, config.head_dim, config.d_model
         eps = config.norm_eps
-        scale = self.model.attention_scale
-        hidden = w.embedding[tokens_d]
-        workspace = None
+        hidden = w.embedding[step.tokens]
         attended = torch.empty((total, heads, dim), dtype=torch.float32, device=self.device)
         for index, (attn_norm, qkv, out_proj, ffn_norm, gate, up, down) in enumerate(w.layers):
             fused = (_rms_norm(hidden, attn_norm, eps) @ qkv).view(total, 3, heads, dim)
@@ -412,26 +578,13 @@ class ModelRunner:
             # (reference model.py:251-252 then runner.py:195-196).
             queries = ops.rope_append(
                 self._keys[index], self._values[index], fused[:, 0], fused[:, 1], fused[:, 2],
-                positions_d, w.cos, w.sin, slots_d, out=fused[:, 0],
+                step.rope_positions, w.cos, w.sin, step.slots, out=fused[:, 0],
             )  # fmt: skip
-            if workspace is None:
-                need = ops.attention_workspace_bytes(total, heads, dim, max_context, partition)
-                workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=self.device)
-            ops.paged_attention_ragged(
-                queries, qpos_d, qseq_d, self._keys[index], self._values[index], tables_d,
-                context_d, scale, max_context_len=max_context,
-                partition_size=partition, out=attended, workspace=workspace, plan=plan,
-            )  # fmt: skip
+            self._attention(step, index, queries, attended)
             hidden = hidden + attended.view(total, d_model) @ out_proj
             normed = _rms_norm(hidden, ffn_norm, eps)
             hidden = hidden + (_silu(normed @ gate) * (normed @ up)) @ down
 
-        wanted, names = [], []
-        for start, entry in zip(starts.tolist(), batch.entries):
-            if entry.logits_index is not None:
-                wanted.append(start + entry.logits_index)
-                names.append(entry.seq_id)
-        if not wanted:
+        if not step.names:
             return [], None
-        rows = torch.tensor(wanted, dtype=torch.int64).to(self.device)
-        return names, _rms_norm(hidden[rows], w.final_norm, eps) @ w.embedding.T
+        return step.names, _rms_norm(hidden[step.logits_rows], w.final_norm, eps) @ w.embedding.T

@@ -19,6 +19,8 @@ from __future__ import annotations
 import numpy as np
 import torch
 
+from paged_kv_serving_amd import _native
+
 __all__ = ["BlockTableArena", "TableUpdate"]
 
 
@@ -45,12 +47,19 @@ class BlockTableArena:
         self.tables = torch.zeros((rows, width), dtype=torch.int32, device=self.device)
         self._row_of: dict[object, int] = {}
         self._key_of: list[object | None] = [None] * rows
-        self._held: list[tuple[int, ...]] = [()] * rows
+        # How many leading entries of each host row the device row is known to hold, and the
+        # tuple each row was last filled from (None: compare by value).
+        self._held_len = np.zeros(rows, dtype=np.int32)
+        self._held_obj: list[object] = [None] * rows
         self._last_use = np.zeros(rows, dtype=np.int64)
         self._step = 0
-        # Rows whose recorded content an update changed and no apply() has written to the device
-        # yet. If the caller fails between the two, the next update forgets what they hold.
-        self._unapplied: list[int] = []
+        # Rows an update touched whose device copy no apply() has written yet. If the caller
+        # fails between the two, the next update forgets what they hold.
+        self._unapplied = np.zeros(0, dtype=np.int32)
+        self._index = np.zeros(1024, dtype=np.int64)
+        self._values = np.zeros(1024, dtype=np.int32)
+        self._rows = np.zeros(64, dtype=np.int32)
+        self._host_ext = _native.host()
 
     @property
     def num_rows(self) -> int:
@@ -62,64 +71,49 @@ class BlockTableArena:
 
     def held(self, row: int) -> tuple[int, ...]:
         """The table arena row ``row`` currently holds."""
-        return self._held[row]
+        return tuple(self.host[row, : self._held_len[row]].tolist())
 
     def update(self, entries) -> TableUpdate:
         """Assign a row to every entry (by ``seq_id``) and record the table entries that differ
         from what the row holds. The host mirror is updated at once; the device rows change when
         the returned indices and values are applied with :meth:`apply`. If the previous update
-        was never applied (its caller raised in between), the rows it changed are treated as
-        holding nothing, so their whole tables are uploaded again."""
-        for row in self._unapplied:
-            self._held[row] = ()
-        self._unapplied = []
+        was never applied (its caller raised in between), the rows it touched are treated as
+        holding nothing, so their whole tables are uploaded again.
+
+        The walk over the entries runs in C++ (``_pkvhost.arena_update``): a sequence not seen
+        before claims the least recently used row not used in this iteration, the same sequence
+        twice in one batch gets a row per occurrence, and only the entries from the first one
+        that differs from the row's content travel."""
+        if self._unapplied.size:
+            self._held_len[self._unapplied] = 0
+            for row in self._unapplied.tolist():
+                self._held_obj[row] = None
+            self._unapplied = np.zeros(0, dtype=np.int32)
         self._step += 1
-        step = self._step
         count = len(entries)
-        longest = max((len(e.block_table) for e in entries), default=0)
-        if count > self.num_rows or longest > self.width:
-            self._grow(max(count, self.num_rows), longest)
-        rows = np.empty(count, dtype=np.int32)
-        index_parts: list[np.ndarray] = []
-        value_parts: list[tuple[int, ...]] = []
-        seen: dict[object, int] = {}
-        width = self.width
-        for i, entry in enumerate(entries):
-            key: object = entry.seq_id
-            repeat = seen.get(key, 0)
-            seen[key] = repeat + 1
-            if repeat:  # the same sequence twice in one batch gets a row per occurrence
-                key = (entry.seq_id, repeat)
-            row = self._row_of.get(key)
-            if row is None:
-                row = self._claim(key, step)
-            self._last_use[row] = step
-            rows[i] = row
-            new = tuple(entry.block_table)
-            old = self._held[row]
-            if new == old:
-                continue
-            start = _common_prefix(old, new)
-            if start < len(new):
-                segment = new[start:]
-                self.host[row, start : len(new)] = segment
-                index_parts.append(np.arange(row * width + start, row * width + len(new), dtype=np.int64))
-                value_parts.append(segment)
-            self._held[row] = new
-            self._unapplied.append(row)
-        if index_parts:
-            index = np.concatenate(index_parts)
-            values = np.fromiter((v for part in value_parts for v in part), dtype=np.int32, count=index.size)
-        else:
-            index = np.zeros(0, dtype=np.int64)
-            values = np.zeros(0, dtype=np.int32)
-        return TableUpdate(rows, index, values)
+        if self._rows.size < count:
+            self._rows = np.zeros(max(count, 2 * self._rows.size), dtype=np.int32)
+        while True:
+            changed, extra = self._host_ext.arena_update(
+                entries, self._row_of, self._key_of, self._held_len, self._held_obj, self._last_use, self.host,
+                self._step, self._rows, self._index, self._values,
+            )  # fmt: skip
+            if changed == -1:  # more rows or a wider table than the arena has
+                self._grow(max(count, self.num_rows), extra)
+            elif changed == -2:  # the index/values buffers may be too small
+                self._index = np.zeros(max(extra, 2 * self._index.size), dtype=np.int64)
+                self._values = np.zeros(max(extra, 2 * self._values.size), dtype=np.int32)
+            else:
+                break
+        rows = self._rows[:count].copy()
+        self._unapplied = rows
+        return TableUpdate(rows, self._index[:changed].copy(), self._values[:changed].copy())
 
     def apply(self, index: torch.Tensor, values: torch.Tensor) -> None:
         """Write an update's values (device int32) at its flat indices (device int64)."""
         if index.numel():
             self.tables.view(-1).index_copy_(0, index, values)
-        self._unapplied = []
+        self._unapplied = np.zeros(0, dtype=np.int32)
 
     def used_blocks(self, rows: np.ndarray, block_counts: np.ndarray) -> np.ndarray:
         """The first ``block_counts[i]`` table entries of arena row ``rows[i]``, concatenated."""
@@ -130,21 +124,6 @@ class BlockTableArena:
         return self.host[rows][mask]
 
     # --- rows ----------------------------------------------------------------------------
-
-    def _claim(self, key: object, step: int) -> int:
-        """A free row, or the least recently used row not used in this iteration."""
-        candidates = np.flatnonzero(self._last_use < step)
-        if candidates.size == 0:  # every row is in use by this iteration: add rows
-            self._grow(self.num_rows + 1, self.width)
-            candidates = np.flatnonzero(self._last_use < step)
-        row = int(candidates[np.argmin(self._last_use[candidates])])
-        previous = self._key_of[row]
-        if previous is not None:
-            del self._row_of[previous]
-        self._key_of[row] = key
-        self._row_of[key] = row
-        self._held[row] = ()  # nothing the row holds may be trusted for the new key
-        return row
 
     def _grow(self, rows: int, width: int) -> None:
         new_rows = max(rows, self.num_rows)
@@ -159,23 +138,8 @@ class BlockTableArena:
         tables[: self.num_rows, : self.width] = self.tables
         extra = new_rows - self.num_rows
         self._key_of.extend([None] * extra)
-        self._held.extend([()] * extra)
+        self._held_len = np.concatenate([self._held_len, np.zeros(extra, dtype=np.int32)])
+        self._held_obj.extend([None] * extra)
         self._last_use = np.concatenate([self._last_use, np.zeros(extra, dtype=np.int64)])
         self.host = host
         self.tables = tables
-
-
-def _common_prefix(old: tuple[int, ...], new: tuple[int, ...]) -> int:
-    """Length of the longest common prefix of two tables."""
-    n = min(len(old), len(new))
-    if old[:n] == new[:n]:
-        return n
-    # Usually only the last block or two differ (copy-on-write of the block being written).
-    lo, hi = 0, n
-    while hi - lo > 1:  # invariant: old[:lo] == new[:lo], old[:hi] != new[:hi]
-        mid = (lo + hi) // 2
-        if old[:mid] == new[:mid]:
-            lo = mid
-        else:
-            hi = mid
-    return lo

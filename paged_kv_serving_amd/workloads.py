@@ -61,7 +61,7 @@ class AttentionBatch:
     def replan(self, partition_size: int) -> None:
         """Rebuild the plan for a given partition size (0: the planner's choice)."""
         heads, dim = self.key_cache.shape[2], self.key_cache.shape[3]
-        host = ops.plan_batch(
+        host = ops.plan_batch_native(
             self.host_seq, dim, heads, self.host_tables, self.host_context, self.key_cache.shape[1],
             partition_size=partition_size, query_positions=self.host_positions,
         )  # fmt: skip
@@ -158,7 +158,7 @@ def _assemble(
     for i, table in enumerate(tables):
         padded[i, : len(table)] = table
     plan = ops.upload_batch_plan(
-        ops.plan_batch(seq, head_dim, heads, tables, context, block_size, query_positions=positions), device
+        ops.plan_batch_native(seq, head_dim, heads, tables, context, block_size, query_positions=positions), device
     )
     return AttentionBatch(
         key_cache=key_cache,
@@ -379,7 +379,7 @@ def prefix_sharing_step(
         max_context_len=int(contexts.max()),
         scale=float(head_dim) ** -0.5,
         plan=ops.upload_batch_plan(
-            ops.plan_batch(seq, head_dim, heads, tables, contexts, block_size, query_positions=positions), device
+            ops.plan_batch_native(seq, head_dim, heads, tables, contexts, block_size, query_positions=positions), device
         ),
         host_tables=tables,
         host_context=contexts.astype(np.int64),

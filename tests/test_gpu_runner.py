@@ -323,6 +323,25 @@ def test_reference_error_messages(device, models) -> None:
     with pytest.raises(ValueError, match="onto itself"):
         runner.copy_block(1, 1)
     assert runner.execute(ExecutionBatch(())) == {}
+    # an entry ending at a negative position has context_len < 1 (attention.py:76-77)
+    with pytest.raises(ValueError, match="context_len must be >= 1"):
+        runner.execute(ExecutionBatch((BatchEntry("s", (1, 2), (-2, -1), (0, 1)),)))
+
+
+def test_negative_positions_run_as_in_the_reference(device, models) -> None:
+    """A chunk whose first positions are negative: their slots come from the end of the table,
+    their rotary angle from the end of the tables, and all their keys are masked. The GPU runner
+    must agree with the NumPy runner, which follows the reference's indexing."""
+    model, oracle = models
+    runner = ModelRunner(model, num_blocks=6, block_size=BLOCK_SIZE, device=device)
+    cpu = OracleRunner(oracle, num_blocks=6, block_size=BLOCK_SIZE)
+    table = (3, 0, 5)
+    batch = ExecutionBatch((BatchEntry("s", (5, 9, 11, 2, 7), (-3, -2, -1, 0, 1), table, 4),))
+    got, want = runner.execute(batch), cpu.execute(batch)
+    assert float(np.max(np.abs(got["s"] - want["s"]))) < TOLERANCE
+    later = ExecutionBatch((BatchEntry("s", (3,), (2,), table, 0),))
+    got, want = runner.execute(later), cpu.execute(later)
+    assert float(np.max(np.abs(got["s"] - want["s"]))) < TOLERANCE
 
 
 def test_steps_from_changing_worker_threads_match_one_thread(device, models) -> None:
@@ -401,3 +420,65 @@ def test_a_bfloat16_pool_matches_the_numpy_runner_on_rounded_kv(device, models, 
         for name in want:
             assert float(np.max(np.abs(got[name] - want[name]))) < TOLERANCE, name
     assert gpu.kv_dtype == torch.bfloat16
+
+
+def _attend_case(seed: int, *, sharers: int = 0, prefill: bool = True):
+    """A batch over a random pool: decode entries (``sharers`` of them interleaved with the rest
+    share 40 leading blocks), optionally one prefill chunk, with random q/k/v."""
+    rng = np.random.default_rng(seed)
+    config = ModelConfig(vocab_size=16, d_model=256, n_layers=2, n_heads=4, d_ff=32, max_seq_len=2048)
+    model = LanguageModel(config, random_weights(config, seed=seed))
+    block, num_blocks = 16, 4000
+    perm = [int(b) for b in rng.permutation(num_blocks)]
+    shared = perm[:40]
+    used = 40
+    entries = []
+    for i in range(40):
+        if sharers and i % 2 == 0 and i // 2 < sharers:
+            ctx = 40 * block + int(rng.integers(1, 60))
+            table = shared + perm[used : used + (-(-ctx // block)) - 40]
+        else:
+            ctx = int(rng.integers(1, 900))
+            table = perm[used : used + (-(-ctx // block))]
+        used += len(table) - (40 if table[:40] == shared else 0)
+        entries.append(BatchEntry(f"d{i}", (1,), (ctx - 1,), tuple(table), 0))
+    if prefill:
+        table = perm[used : used + 6]
+        entries.append(BatchEntry("p", tuple(i % 15 + 1 for i in range(40)), tuple(range(50, 90)), tuple(table), 39))
+    batch = ExecutionBatch(tuple(entries))
+    total = batch.num_tokens
+    q, k, v = (rng.standard_normal((total, 4, 64)).astype(np.float32) for _ in range(3))
+    return model, batch, q, k, v, num_blocks, block
+
+
+@pytest.mark.parametrize(("seed", "sharers", "prefill"), [(0, 0, True), (1, 0, False), (2, 18, False), (3, 18, True)])
+def test_attend_appends_and_attends_like_the_reference_runner(device, seed, sharers, prefill) -> None:
+    """ModelRunner.attend: the caller's keys and values land at the batch's slots (bit for bit)
+    and every query's output matches the oracle's paged attention (1e-5): prefill and decode rows
+    together, a decode-only batch (the append fused into the attention call), and decode rows
+    whose shared prefix makes the runner reorder them."""
+    from oracle.attention import paged_attention
+    from oracle.runner import append as oracle_append, slots_for
+
+    model, batch, q, k, v, num_blocks, block = _attend_case(seed, sharers=sharers, prefill=prefill)
+    runner = ModelRunner(model, num_blocks=num_blocks, block_size=block, device=device)
+    rng = np.random.default_rng(100 + seed)
+    keys0 = rng.standard_normal((num_blocks, block, 4, 64)).astype(np.float32)
+    values0 = rng.standard_normal((num_blocks, block, 4, 64)).astype(np.float32)
+    runner.key_cache[1].copy_(torch.from_numpy(keys0))
+    runner.value_cache[1].copy_(torch.from_numpy(values0))
+    out = runner.attend(batch, *(torch.from_numpy(a).to(device) for a in (q, k, v)), layer=1).cpu().numpy()
+    if sharers:
+        assert runner.last_plan is not None and runner.last_plan.tiles.shape[0] > 0, "prefix tiles"
+    slots = [s for e in batch.entries for s in slots_for(e.seq_id, e.positions, e.block_table, block)]
+    oracle_append(keys0, values0, slots, k, v)
+    assert np.array_equal(runner.key_cache[1].cpu().numpy(), keys0)
+    assert np.array_equal(runner.value_cache[1].cpu().numpy(), values0)
+    offset, worst = 0, 0.0
+    for entry in batch.entries:
+        n = len(entry.token_ids)
+        want = paged_attention(q[offset : offset + n], np.asarray(entry.positions), keys0, values0,
+                               np.asarray(entry.block_table), entry.context_len, 64**-0.5)  # fmt: skip
+        worst = max(worst, float(np.max(np.abs(out[offset : offset + n] - want))))
+        offset += n
+    assert worst < 1e-5

@@ -16,7 +16,7 @@ import torch
 from hypothesis import given, settings
 from hypothesis import strategies as st
 
-from paged_kv_serving_amd.tables import BlockTableArena, _common_prefix
+from paged_kv_serving_amd.tables import BlockTableArena
 
 
 @dataclass(frozen=True)
@@ -30,8 +30,8 @@ def step(arena: BlockTableArena, entries):
     arena.apply(torch.from_numpy(update.index), torch.from_numpy(update.values))
     for entry, row in zip(entries, update.rows.tolist()):
         n = len(entry.block_table)
-        assert tuple(arena.host[row, :n].tolist()) == entry.block_table
-        assert tuple(arena.tables[row, :n].tolist()) == entry.block_table
+        assert tuple(arena.host[row, :n].tolist()) == tuple(entry.block_table)
+        assert tuple(arena.tables[row, :n].tolist()) == tuple(entry.block_table)
     assert len(set(update.rows.tolist())) == len(entries), "one row per entry"
     return update
 
@@ -93,14 +93,6 @@ def test_used_blocks_concatenates_the_visible_prefix() -> None:
     assert arena.used_blocks(update.rows, np.asarray([3, 1])).tolist() == [1, 2, 3, 7]
 
 
-@pytest.mark.parametrize(
-    ("old", "new", "want"),
-    [((), (1,), 0), ((1, 2, 3), (1, 2, 3), 3), ((1, 2, 3), (1, 9, 3), 1), ((1, 2), (1, 2, 5), 2), ((4,), (5,), 0)],
-)
-def test_common_prefix(old, new, want) -> None:
-    assert _common_prefix(old, new) == want
-
-
 @settings(max_examples=60, deadline=None)
 @given(st.data())
 def test_random_table_histories_read_back(data) -> None:
@@ -127,3 +119,40 @@ def test_random_table_histories_read_back(data) -> None:
                 next_block += 1
             entries.append(Entry(name, tuple(table)))
         step(arena, entries)
+
+
+def test_same_tuple_again_sends_nothing_and_an_equal_length_change_travels() -> None:
+    """The walk compares a row's previous tuple with the new one before converting ids: an
+    equal tuple (the same object or an equal one) sends nothing, an equal-length tuple with one
+    changed id sends the entries from that id on."""
+    arena = BlockTableArena("cpu", rows=2, width=4)
+    table = (3, 4, 5)
+    step(arena, [Entry("a", table)])
+    assert step(arena, [Entry("a", table)]).index.size == 0
+    assert step(arena, [Entry("a", tuple([3, 4, 5]))]).index.size == 0
+    changed = step(arena, [Entry("a", (3, 9, 5))])
+    assert changed.values.tolist() == [9, 5]
+
+
+def test_a_list_changed_in_place_is_compared_by_value() -> None:
+    @dataclass
+    class ListEntry:
+        seq_id: str
+        block_table: list
+
+    arena = BlockTableArena("cpu", rows=2, width=4)
+    table = [3, 4, 5]
+    step(arena, [ListEntry("a", table)])
+    table[1] = 8  # the same list object, new content
+    assert step(arena, [ListEntry("a", table)]).values.tolist() == [8, 5]
+
+
+def test_a_walk_that_raises_leaves_no_row_trusted() -> None:
+    """An entry whose table holds a non-integer stops the walk with TypeError after earlier rows
+    were rewritten on the host; the next update sends those rows whole."""
+    arena = BlockTableArena("cpu", rows=4, width=4)
+    step(arena, [Entry("a", (1, 2)), Entry("b", (3,))])
+    with pytest.raises(TypeError):
+        arena.update([Entry("a", (1, 7)), Entry("b", ("x",))])
+    again = step(arena, [Entry("a", (1, 7)), Entry("b", (3,))])
+    assert again.values.tolist() == [1, 7, 3]
