@@ -149,7 +149,8 @@ def build_host(*, verbose: bool = False) -> Path:
         tmp = Path(handle.name)
     try:
         command = [compiler, "-O3", "-std=c++17", "-shared", "-fPIC", "-Wall", "-Wno-missing-field-initializers",
-                   "-I", sysconfig.get_paths()["include"], "-o", str(tmp), str(HOST_SOURCE)]  # fmt: skip
+                   "-I", sysconfig.get_paths()["include"], "-I", str(INCLUDE), "-o", str(tmp),
+                   str(HOST_SOURCE)]  # fmt: skip
         result = subprocess.run(command, capture_output=True, text=True, check=False)
         if verbose or result.returncode != 0:
             if result.stderr.strip():
@@ -168,6 +169,26 @@ def host():
     if not HOST_PATH.exists():
         raise NativeLibraryError(f"{HOST_PATH} is missing: build it with __graft_entry__.build()")
     return importlib.import_module("paged_kv_serving_amd._pkvhost")
+
+
+_BOUND = False
+
+
+def bound_host():
+    """:func:`host` with the library's entry points bound into it (``_pkvhost.bind``), so its
+    ``plan``, ``paged_attention``, ``paged_attention_append`` and ``copy_blocks`` call
+    ``libpkv.so`` directly. Binding loads the library (it must be built)."""
+    global _BOUND
+    ext = host()
+    if not _BOUND:
+        lib = library()
+        with _LOCK:
+            if not _BOUND:
+                address = lambda fn: ctypes.cast(fn, ctypes.c_void_p).value  # noqa: E731
+                ext.bind(address(lib.pkv_plan_batch), address(lib.pkv_paged_attention),
+                         address(lib.pkv_paged_attention_append), address(lib.pkv_copy_blocks))  # fmt: skip
+                _BOUND = True
+    return ext
 
 
 _LOCK = threading.Lock()

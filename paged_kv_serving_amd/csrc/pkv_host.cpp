@@ -2,9 +2,9 @@
 //
 // A batch is a tuple of BatchEntry objects (the reference's or this package's: anything with
 // seq_id, token_ids, positions, block_table and logits_index). Walking them in Python costs about
-// a microsecond per entry and attribute; here one pass reads each entry once. Three functions:
+// a microsecond per entry and attribute; here one pass reads each entry once. Functions:
 //
-//   gather(entries, block_size, tokens, positions, slots, lengths, contexts, logits)
+//   gather(entries, block_size, tokens, positions, slots, lengths, contexts, logits[, stats])
 //       -> (total, problem, entry, position)
 //       Flattens token ids and positions, computes every slot with the reference's rule
 //       (runner.py:149-159: block_table[p // B] * B + p % B with Python's floor division and a
@@ -14,10 +14,16 @@
 //       token ids and positions first, in the reference's order: problem 1 = a position past
 //       the table (the reference's ValueError), 2 = a negative index before its start
 //       (IndexError). Returns total = -(tokens needed), writing nothing, when the token buffers
-//       are too small.
-//   prefix_order(entries, lead, min_rows) -> list | None
+//       are too small. The optional int64 `stats` buffer (>= 8 entries) receives what the
+//       caller validates, so it needs no pass of its own: [min token, max token, min position,
+//       max position, min slot, max slot, min context, 1 if two single-token entries' tables
+//       start with the same block id else 0] (slots of unformed positions count as -1).
+//   prefix_order_rows(rows, lengths, host, held_len, lead, min_rows) -> list | None
 //       The row order that puts decode entries sharing their first `lead` blocks next to each
-//       other (runner.shared_prefix_order), or None when no such run would change.
+//       other (runner.shared_prefix_order), or None when no such run would change. Read from
+//       the block-table arena after its update: entry e has lengths[e] tokens and its table in
+//       arena row rows[e] (held_len[rows[e]] entries of host[rows[e]]), so no block id is
+//       converted from a Python object.
 //   arena_update(entries, row_of, key_of, held_len, held_obj, last_use, host, step, rows, index,
 //                values) -> (changed entries, changed rows) | (-1, longest) | (-2, needed)
 //       The block-table arena's step (tables.BlockTableArena.update): a row per entry (claiming the
@@ -27,9 +33,25 @@
 //       held_obj keeps, per row, the tuple it was last filled from: a scheduler rebuilds each
 //       table tuple from the same int objects every step, so an unchanged table compares equal
 //       by identity, element by element, without converting a single id.
+//   cow_groups(pairs, out) -> list of group sizes
+//       Flattens a list of (src, dst) block copies into the int64 buffer `out` (>= 2 entries
+//       per pair) and splits them, in order, into groups that may each run as one concurrent
+//       pkv_copy_blocks launch (ops.independent_groups): a copy starts a new group when it
+//       reads a block an earlier copy of the group writes, or writes a block an earlier copy of
+//       the group reads or writes.
+//   bind(plan_batch, paged_attention, paged_attention_append, copy_blocks)
+//       Takes the addresses of those libpkv.so entry points (include/pkv.h), so the three calls
+//       below reach the library without ctypes' per-argument conversions.
+//   plan(query_seq, query_positions | None, tables, contexts, block_size, num_heads, head_dim,
+//        partition_size, min_tile_rows, rows, tiles, merge, counts, launch) -> int
+//       pkv_plan_batch on NumPy buffers; returns its PKV_* code.
+//   paged_attention(...), paged_attention_append(...), copy_blocks(...) -> int
+//       The entry points of the same names, with every pointer, stream and handle passed as a
+//       Python int (0 for NULL) in the order of their C declarations; returns the PKV_* code.
 //
-// Buffers are NumPy arrays passed through the buffer protocol (C-contiguous, writable, of the
-// stated element type); nothing here allocates Python-visible memory besides the returned lists.
+// Buffers are NumPy arrays passed through the buffer protocol (C-contiguous, of the stated
+// element type; writable where written); nothing here allocates Python-visible memory besides
+// the returned lists.
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
 
@@ -37,7 +59,10 @@
 #include <cstdint>
 #include <cstring>
 #include <string>
+#include <unordered_set>
 #include <vector>
+
+#include "pkv.h"
 
 namespace {
 
@@ -49,8 +74,9 @@ class Buf {
   ~Buf() {
     if (view_.obj != nullptr) PyBuffer_Release(&view_);
   }
-  bool get(PyObject* obj, const char* what) {
-    if (PyObject_GetBuffer(obj, &view_, PyBUF_WRITABLE | PyBUF_C_CONTIGUOUS | PyBUF_FORMAT) != 0) return false;
+  bool get(PyObject* obj, const char* what, bool writable = true) {
+    const int flags = (writable ? PyBUF_WRITABLE : 0) | PyBUF_C_CONTIGUOUS | PyBUF_FORMAT;
+    if (PyObject_GetBuffer(obj, &view_, flags) != 0) return false;
     if (view_.itemsize != static_cast<Py_ssize_t>(sizeof(T))) {
       PyErr_Format(PyExc_TypeError, "%s must hold %d-byte integers", what, static_cast<int>(sizeof(T)));
       return false;
@@ -97,9 +123,10 @@ int64_t floor_div(int64_t a, int64_t b) {  // Python's a // b for b > 0
 
 PyObject* gather(PyObject*, PyObject* args) {
   PyObject *entries_obj, *tokens_o, *positions_o, *slots_o, *lengths_o, *contexts_o, *logits_o;
+  PyObject* stats_o = Py_None;
   long long block_size;
-  if (!PyArg_ParseTuple(args, "OLOOOOOO", &entries_obj, &block_size, &tokens_o, &positions_o, &slots_o,
-                        &lengths_o, &contexts_o, &logits_o)) {
+  if (!PyArg_ParseTuple(args, "OLOOOOOO|O", &entries_obj, &block_size, &tokens_o, &positions_o, &slots_o,
+                        &lengths_o, &contexts_o, &logits_o, &stats_o)) {
     return nullptr;
   }
   if (block_size < 1) {
@@ -110,14 +137,19 @@ PyObject* gather(PyObject*, PyObject* args) {
   if (entries == nullptr) return nullptr;
   const Py_ssize_t count = PySequence_Fast_GET_SIZE(entries);
   PyObject** items = PySequence_Fast_ITEMS(entries);
-  Buf<int64_t> tokens, positions, slots, lengths, logits;
+  Buf<int64_t> tokens, positions, slots, lengths, logits, stats;
   Buf<int32_t> contexts;
   PyObject* result = nullptr;
   std::vector<PyObject*> toks(count, nullptr), poss(count, nullptr);
+  std::vector<int64_t> firsts;  // first block ids of single-token entries
   int64_t total = 0;
   if (!tokens.get(tokens_o, "tokens") || !positions.get(positions_o, "positions") ||
       !slots.get(slots_o, "slots") || !lengths.get(lengths_o, "lengths") ||
       !contexts.get(contexts_o, "contexts") || !logits.get(logits_o, "logits")) {
+    goto done;
+  }
+  if (stats_o != Py_None && (!stats.get(stats_o, "stats") || stats.size() < 8)) {
+    if (!PyErr_Occurred()) PyErr_SetString(PyExc_ValueError, "stats must hold 8 entries");
     goto done;
   }
   if (lengths.size() < count || contexts.size() < count || logits.size() < count) {
@@ -139,6 +171,8 @@ PyObject* gather(PyObject*, PyObject* args) {
     int64_t at = 0;
     int problem = 0;
     long long bad_entry = 0, bad_position = 0;
+    int64_t lo_tok = INT64_MAX, hi_tok = INT64_MIN, lo_pos = INT64_MAX, hi_pos = INT64_MIN;
+    int64_t lo_slot = INT64_MAX, hi_slot = INT64_MIN, lo_ctx = INT64_MAX;
     for (Py_ssize_t e = 0; e < count; ++e) {
       PyObject* entry = items[e];
       const Py_ssize_t n = PySequence_Fast_GET_SIZE(toks[e]);
@@ -161,6 +195,10 @@ PyObject* gather(PyObject*, PyObject* args) {
         }
         tokens.data()[at + i] = t;
         positions.data()[at + i] = p;
+        lo_tok = std::min(lo_tok, t);
+        hi_tok = std::max(hi_tok, t);
+        lo_pos = std::min(lo_pos, p);
+        hi_pos = std::max(hi_pos, p);
         int64_t index = floor_div(p, block_size);
         if (index < 0) index += width;
         if (index >= width || index < 0) {
@@ -170,6 +208,8 @@ PyObject* gather(PyObject*, PyObject* args) {
             bad_position = p;
           }
           slots.data()[at + i] = -1;
+          lo_slot = std::min<int64_t>(lo_slot, -1);
+          hi_slot = std::max<int64_t>(hi_slot, -1);
           continue;
         }
         int64_t block;
@@ -177,7 +217,15 @@ PyObject* gather(PyObject*, PyObject* args) {
           ok = false;
           break;
         }
-        slots.data()[at + i] = block * block_size + (p - floor_div(p, block_size) * block_size);
+        const int64_t slot = block * block_size + (p - floor_div(p, block_size) * block_size);
+        slots.data()[at + i] = slot;
+        lo_slot = std::min(lo_slot, slot);
+        hi_slot = std::max(hi_slot, slot);
+      }
+      if (ok && n == 1 && width > 0) {
+        int64_t first;
+        if (!as_i64(blocks[0], &first)) ok = false;
+        else firsts.push_back(first);
       }
       Py_DECREF(table);
       if (!ok) goto done;
@@ -185,6 +233,7 @@ PyObject* gather(PyObject*, PyObject* args) {
       int64_t last = 0;
       if (n > 0) last = positions.data()[at + n - 1];
       contexts.data()[e] = static_cast<int32_t>(last + 1);
+      lo_ctx = std::min<int64_t>(lo_ctx, static_cast<int32_t>(last + 1));
       PyObject* index = PyObject_GetAttr(entry, s_logits_index);
       if (index == nullptr) goto done;
       int64_t li = -1;
@@ -196,6 +245,12 @@ PyObject* gather(PyObject*, PyObject* args) {
       logits.data()[e] = li < 0 ? -1 : at + li;
       at += n;
     }
+    if (stats_o != Py_None) {
+      std::sort(firsts.begin(), firsts.end());
+      const bool repeat = std::adjacent_find(firsts.begin(), firsts.end()) != firsts.end();
+      const int64_t values[8] = {lo_tok, hi_tok, lo_pos, hi_pos, lo_slot, hi_slot, lo_ctx, repeat ? 1 : 0};
+      std::memcpy(stats.data(), values, sizeof(values));
+    }
     result = Py_BuildValue("(LiLL)", static_cast<long long>(total), problem, bad_entry, bad_position);
   }
 done:
@@ -205,61 +260,14 @@ done:
   return result;
 }
 
-PyObject* prefix_order(PyObject*, PyObject* args) {
-  PyObject* entries_obj;
-  long long lead, min_rows;
-  if (!PyArg_ParseTuple(args, "OLL", &entries_obj, &lead, &min_rows)) return nullptr;
-  PyObject* entries = PySequence_Fast(entries_obj, "entries must be a sequence");
-  if (entries == nullptr) return nullptr;
-  const Py_ssize_t count = PySequence_Fast_GET_SIZE(entries);
-  PyObject** items = PySequence_Fast_ITEMS(entries);
-  std::vector<Py_ssize_t> decode;
-  std::vector<int64_t> keys;  // lead ids per decode entry
-  PyObject* prev_table = nullptr;  // the previous decode entry's table (owned)
-  std::vector<char> is_decode(count, 0);
-  PyObject* result = nullptr;
-  for (Py_ssize_t e = 0; e < count; ++e) {
-    PyObject* tok = PyObject_GetAttr(items[e], s_token_ids);
-    if (tok == nullptr) goto done;
-    const Py_ssize_t n = PyObject_Length(tok);
-    Py_DECREF(tok);
-    if (n < 0) goto done;
-    if (n != 1) continue;
-    PyObject* table = fast_attr(items[e], s_block_table);
-    if (table == nullptr) goto done;
-    if (PySequence_Fast_GET_SIZE(table) >= lead) {
-      PyObject** blocks = PySequence_Fast_ITEMS(table);
-      PyObject** prev_blocks = prev_table == nullptr ? nullptr : PySequence_Fast_ITEMS(prev_table);
-      const size_t at = keys.size();
-      keys.resize(at + lead);
-      for (long long c = 0; c < lead; ++c) {
-        // Sharers' tables usually hold the very same int objects: reuse the converted id (the
-        // previous table is held, so its items are alive and their addresses unique).
-        if (prev_blocks != nullptr && blocks[c] == prev_blocks[c]) {
-          keys[at + c] = keys[at - lead + c];
-          continue;
-        }
-        int64_t b;
-        if (!as_i64(blocks[c], &b)) {
-          Py_DECREF(table);
-          goto done;
-        }
-        keys[at + c] = b;
-      }
-      Py_XDECREF(prev_table);
-      prev_table = table;  // keeps the reference
-      decode.push_back(e);
-      is_decode[e] = 1;
-    } else {
-      Py_DECREF(table);
-    }
-  }
+// The row order of prefix_order from the decode entries' positions in the batch and their
+// `lead` leading block ids (keys, lead per entry); None when nothing would move.
+PyObject* order_decode_entries(const std::vector<Py_ssize_t>& decode, const std::vector<int64_t>& keys,
+                               long long lead, long long min_rows, Py_ssize_t count) {
   {
     const Py_ssize_t nd = static_cast<Py_ssize_t>(decode.size());
     if (nd < min_rows || lead < 1) {
-      result = Py_None;
-      Py_INCREF(result);
-      goto done;
+      Py_RETURN_NONE;
     }
     auto key = [&](Py_ssize_t k) { return keys.data() + k * lead; };
     auto same = [&](Py_ssize_t a, Py_ssize_t b) { return std::memcmp(key(a), key(b), lead * sizeof(int64_t)) == 0; };
@@ -268,9 +276,27 @@ PyObject* prefix_order(PyObject*, PyObject* args) {
       for (Py_ssize_t k = 0; k < nd; ++k) firsts[k] = key(k)[0];
       std::sort(firsts.begin(), firsts.end());
       if (std::adjacent_find(firsts.begin(), firsts.end()) == firsts.end()) {
-        result = Py_None;
-        Py_INCREF(result);
-        goto done;
+        Py_RETURN_NONE;
+      }
+    }
+    {  // already grouped: every key forms one run of consecutive entries, so nothing moves
+      auto hash = [&](Py_ssize_t k) {
+        uint64_t h = 1469598103934665603ull;  // FNV-1a over the key's ids
+        for (long long c = 0; c < lead; ++c) h = (h ^ static_cast<uint64_t>(key(k)[c])) * 1099511628211ull;
+        return h;
+      };
+      std::unordered_set<uint64_t> finished;  // hashes of runs that have ended
+      bool grouped_already = true;
+      uint64_t run = hash(0);
+      for (Py_ssize_t k = 1; k < nd && grouped_already; ++k) {
+        const bool continues = decode[k] == decode[k - 1] + 1 && same(k - 1, k);
+        if (continues) continue;
+        finished.insert(run);
+        run = hash(k);
+        grouped_already = finished.count(run) == 0;  // a repeated hash (or a collision): sort
+      }
+      if (grouped_already) {
+        Py_RETURN_NONE;
       }
     }
     std::vector<Py_ssize_t> grouped(nd);  // positions in `decode`, stably sorted by key
@@ -284,22 +310,53 @@ PyObject* prefix_order(PyObject*, PyObject* args) {
       if (decode[k + 1] == decode[k] + 1) adjacent += same(k, k + 1);
     }
     if (shared == 0 || shared == adjacent) {
-      result = Py_None;
-      Py_INCREF(result);
-      goto done;
+      Py_RETURN_NONE;
     }
-    result = PyList_New(count);
-    if (result == nullptr) goto done;
+    PyObject* result = PyList_New(count);
+    if (result == nullptr) return nullptr;
     Py_ssize_t at = 0;
     for (Py_ssize_t k = 0; k < nd; ++k) PyList_SET_ITEM(result, at++, PyLong_FromSsize_t(decode[grouped[k]]));
+    std::vector<char> is_decode(count, 0);
+    for (Py_ssize_t k = 0; k < nd; ++k) is_decode[decode[k]] = 1;
     for (Py_ssize_t e = 0; e < count; ++e) {
       if (!is_decode[e]) PyList_SET_ITEM(result, at++, PyLong_FromSsize_t(e));
     }
+    return result;
   }
-done:
-  Py_XDECREF(prev_table);
-  Py_DECREF(entries);
-  return result;
+}
+
+PyObject* prefix_order_rows(PyObject*, PyObject* args) {
+  PyObject *rows_o, *lengths_o, *host_o, *held_o;
+  long long lead, min_rows;
+  if (!PyArg_ParseTuple(args, "OOOOLL", &rows_o, &lengths_o, &host_o, &held_o, &lead, &min_rows)) return nullptr;
+  Buf<int32_t> rows, host, held;
+  Buf<int64_t> lengths;
+  if (!rows.get(rows_o, "rows", false) || !lengths.get(lengths_o, "lengths", false) ||
+      !host.get(host_o, "host", false) || !held.get(held_o, "held_len", false)) {
+    return nullptr;
+  }
+  const Py_ssize_t count = rows.size();
+  const Py_ssize_t num_rows = host.dim(0), width = host.dim(1);
+  if (host.ndim() != 2 || lengths.size() < count || held.size() != num_rows) {
+    PyErr_SetString(PyExc_ValueError, "prefix_order_rows buffers disagree");
+    return nullptr;
+  }
+  std::vector<Py_ssize_t> decode;
+  std::vector<int64_t> keys;
+  if (lead >= 1) {
+    for (Py_ssize_t e = 0; e < count; ++e) {
+      const int32_t row = rows.data()[e];
+      if (row < 0 || row >= num_rows) {
+        PyErr_SetString(PyExc_ValueError, "an arena row is out of range");
+        return nullptr;
+      }
+      if (lengths.data()[e] != 1 || held.data()[row] < lead || lead > width) continue;
+      const int32_t* table = host.data() + static_cast<int64_t>(row) * width;
+      decode.push_back(e);
+      for (long long c = 0; c < lead; ++c) keys.push_back(table[c]);
+    }
+  }
+  return order_decode_entries(decode, keys, lead, min_rows, count);
 }
 
 PyObject* arena_update(PyObject*, PyObject* args) {
@@ -481,10 +538,187 @@ done:
   return result;
 }
 
+PyObject* cow_groups(PyObject*, PyObject* args) {
+  PyObject *pairs_o, *out_o;
+  if (!PyArg_ParseTuple(args, "OO", &pairs_o, &out_o)) return nullptr;
+  PyObject* pairs = PySequence_Fast(pairs_o, "pairs must be a sequence");
+  if (pairs == nullptr) return nullptr;
+  const Py_ssize_t count = PySequence_Fast_GET_SIZE(pairs);
+  PyObject** items = PySequence_Fast_ITEMS(pairs);
+  Buf<int64_t> out;
+  PyObject* result = nullptr;
+  std::vector<Py_ssize_t> sizes;
+  std::unordered_set<int64_t> reads, writes;
+  Py_ssize_t current = 0;
+  if (!out.get(out_o, "out")) goto done;
+  if (out.size() < 2 * count) {
+    PyErr_SetString(PyExc_ValueError, "out holds fewer than two entries per pair");
+    goto done;
+  }
+  for (Py_ssize_t i = 0; i < count; ++i) {
+    PyObject* pair = PySequence_Fast(items[i], "a copy must be a (src, dst) pair");
+    if (pair == nullptr) goto done;
+    int64_t src = 0, dst = 0;
+    const bool ok = PySequence_Fast_GET_SIZE(pair) == 2 && as_i64(PySequence_Fast_GET_ITEM(pair, 0), &src) &&
+                    as_i64(PySequence_Fast_GET_ITEM(pair, 1), &dst);
+    Py_DECREF(pair);
+    if (!ok) {
+      if (!PyErr_Occurred()) PyErr_SetString(PyExc_ValueError, "a copy must be a (src, dst) pair");
+      goto done;
+    }
+    if (current > 0 && (writes.count(src) || reads.count(dst) || writes.count(dst))) {
+      sizes.push_back(current);
+      current = 0;
+      reads.clear();
+      writes.clear();
+    }
+    out.data()[2 * i] = src;
+    out.data()[2 * i + 1] = dst;
+    reads.insert(src);
+    writes.insert(dst);
+    ++current;
+  }
+  if (current > 0) sizes.push_back(current);
+  result = PyList_New(static_cast<Py_ssize_t>(sizes.size()));
+  if (result == nullptr) goto done;
+  for (size_t g = 0; g < sizes.size(); ++g) PyList_SET_ITEM(result, g, PyLong_FromSsize_t(sizes[g]));
+done:
+  Py_DECREF(pairs);
+  return result;
+}
+
+// Entry points of libpkv.so, bound once by bind().
+decltype(&pkv_plan_batch) g_plan_batch = nullptr;
+decltype(&pkv_paged_attention) g_paged_attention = nullptr;
+decltype(&pkv_paged_attention_append) g_paged_attention_append = nullptr;
+decltype(&pkv_copy_blocks) g_copy_blocks = nullptr;
+
+bool bound(const void* fn) {
+  if (fn != nullptr) return true;
+  PyErr_SetString(PyExc_RuntimeError, "_pkvhost.bind() has not been given the library's entry points");
+  return false;
+}
+
+template <typename T>
+T* ptr(unsigned long long address) {
+  return reinterpret_cast<T*>(static_cast<uintptr_t>(address));
+}
+
+PyObject* bind(PyObject*, PyObject* args) {
+  unsigned long long plan, attention, attention_append, copy;
+  if (!PyArg_ParseTuple(args, "KKKK", &plan, &attention, &attention_append, &copy)) return nullptr;
+  if (plan == 0 || attention == 0 || attention_append == 0 || copy == 0) {
+    PyErr_SetString(PyExc_ValueError, "bind() needs four non-null entry points");
+    return nullptr;
+  }
+  g_plan_batch = reinterpret_cast<decltype(g_plan_batch)>(static_cast<uintptr_t>(plan));
+  g_paged_attention = reinterpret_cast<decltype(g_paged_attention)>(static_cast<uintptr_t>(attention));
+  g_paged_attention_append =
+      reinterpret_cast<decltype(g_paged_attention_append)>(static_cast<uintptr_t>(attention_append));
+  g_copy_blocks = reinterpret_cast<decltype(g_copy_blocks)>(static_cast<uintptr_t>(copy));
+  Py_RETURN_NONE;
+}
+
+PyObject* plan(PyObject*, PyObject* args) {
+  PyObject *seq_o, *pos_o, *tables_o, *ctx_o, *rows_o, *tiles_o, *merge_o, *counts_o, *launch_o;
+  int block_size, num_heads, head_dim, partition_size, min_tile_rows;
+  if (!PyArg_ParseTuple(args, "OOOOiiiiiOOOOO", &seq_o, &pos_o, &tables_o, &ctx_o, &block_size, &num_heads,
+                        &head_dim, &partition_size, &min_tile_rows, &rows_o, &tiles_o, &merge_o, &counts_o,
+                        &launch_o)) {
+    return nullptr;
+  }
+  if (!bound(reinterpret_cast<const void*>(g_plan_batch))) return nullptr;
+  Buf<int32_t> seq, pos, tables, ctx, rows, tiles, merge, launch;
+  Buf<int64_t> counts;
+  if (!seq.get(seq_o, "query_seq", false) || (pos_o != Py_None && !pos.get(pos_o, "query_positions", false)) ||
+      !tables.get(tables_o, "tables", false) || !ctx.get(ctx_o, "contexts", false) || !rows.get(rows_o, "rows") ||
+      !tiles.get(tiles_o, "tiles") || !merge.get(merge_o, "merge") || !counts.get(counts_o, "counts") ||
+      !launch.get(launch_o, "launch")) {
+    return nullptr;
+  }
+  if (tables.ndim() != 2 || (pos_o != Py_None && pos.size() != seq.size()) || counts.size() < 3 ||
+      launch.size() < 2 || rows.size() % 2 != 0 || tiles.size() % 4 != 0) {
+    PyErr_SetString(PyExc_ValueError, "plan buffers have inconsistent shapes");
+    return nullptr;
+  }
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = g_plan_batch(seq.data(), pos_o == Py_None ? nullptr : pos.data(), seq.size(), tables.data(),
+                    static_cast<int32_t>(tables.dim(1)), ctx.data(), static_cast<int32_t>(ctx.size()), block_size,
+                    num_heads, head_dim, partition_size, min_tile_rows, rows.data(), rows.size() / 2, tiles.data(),
+                    tiles.size() / 4, merge.data(), merge.size(), counts.data(), launch.data());
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(rc);
+}
+
+PyObject* paged_attention(PyObject*, PyObject* args) {
+  unsigned long long out, queries, qpos, qseq, rows, tiles, merge, kc, vc, tables, ctx, ws, stream;
+  long long q_stride, nq, nrows, ntiles, nmerge, nblocks, ws_bytes;
+  int dtype, block_size, table_stride, nseqs, heads, head_dim, max_ctx, partition, flags, device;
+  float scale;
+  if (!PyArg_ParseTuple(args, "KKLKKLKLKLKLKKiLiKiKiiifiiiKLiK", &out, &queries, &q_stride, &qpos, &qseq, &nq,
+                        &rows, &nrows, &tiles, &ntiles, &merge, &nmerge, &kc, &vc, &dtype, &nblocks, &block_size,
+                        &tables, &table_stride, &ctx, &nseqs, &heads, &head_dim, &scale, &max_ctx, &partition,
+                        &flags, &ws, &ws_bytes, &device, &stream)) {
+    return nullptr;
+  }
+  if (!bound(reinterpret_cast<const void*>(g_paged_attention))) return nullptr;
+  const int rc = g_paged_attention(
+      ptr<float>(out), ptr<const float>(queries), q_stride, ptr<const int32_t>(qpos), ptr<const int32_t>(qseq), nq,
+      ptr<const int32_t>(rows), nrows, ptr<const int32_t>(tiles), ntiles, ptr<const int32_t>(merge), nmerge,
+      ptr<const void>(kc), ptr<const void>(vc), static_cast<pkv_dtype>(dtype), nblocks, block_size,
+      ptr<const int32_t>(tables), table_stride, ptr<const int32_t>(ctx), nseqs, heads, head_dim, scale, max_ctx,
+      partition, flags, ptr<float>(ws), ws_bytes, device, ptr<void>(stream));
+  return PyLong_FromLong(rc);
+}
+
+PyObject* paged_attention_append(PyObject*, PyObject* args) {
+  unsigned long long out, queries, qpos, qseq, rows, merge, kc, vc, tables, ctx, ws, new_k, new_v, slots, stream;
+  long long q_stride, nq, nrows, nmerge, nblocks, ws_bytes, k_stride, v_stride;
+  int dtype, block_size, table_stride, nseqs, heads, head_dim, max_ctx, partition, flags, new_dtype, device;
+  float scale;
+  if (!PyArg_ParseTuple(args, "KKLKKLKLKLKKiLiKiKiiifiiiKLKKiLLKiK", &out, &queries, &q_stride, &qpos, &qseq, &nq,
+                        &rows, &nrows, &merge, &nmerge, &kc, &vc, &dtype, &nblocks, &block_size, &tables,
+                        &table_stride, &ctx, &nseqs, &heads, &head_dim, &scale, &max_ctx, &partition, &flags, &ws,
+                        &ws_bytes, &new_k, &new_v, &new_dtype, &k_stride, &v_stride, &slots, &device, &stream)) {
+    return nullptr;
+  }
+  if (!bound(reinterpret_cast<const void*>(g_paged_attention_append))) return nullptr;
+  const int rc = g_paged_attention_append(
+      ptr<float>(out), ptr<const float>(queries), q_stride, ptr<const int32_t>(qpos), ptr<const int32_t>(qseq), nq,
+      ptr<const int32_t>(rows), nrows, ptr<const int32_t>(merge), nmerge, ptr<void>(kc), ptr<void>(vc),
+      static_cast<pkv_dtype>(dtype), nblocks, block_size, ptr<const int32_t>(tables), table_stride,
+      ptr<const int32_t>(ctx), nseqs, heads, head_dim, scale, max_ctx, partition, flags, ptr<float>(ws), ws_bytes,
+      ptr<const void>(new_k), ptr<const void>(new_v), static_cast<pkv_dtype>(new_dtype), k_stride, v_stride,
+      ptr<const int64_t>(slots), device, ptr<void>(stream));
+  return PyLong_FromLong(rc);
+}
+
+PyObject* copy_blocks(PyObject*, PyObject* args) {
+  unsigned long long kp, vp, pairs, stream;
+  long long npairs, nblocks, block_elems;
+  int dtype, layers, device;
+  if (!PyArg_ParseTuple(args, "KKiKLiLLiK", &kp, &vp, &dtype, &pairs, &npairs, &layers, &nblocks, &block_elems,
+                        &device, &stream)) {
+    return nullptr;
+  }
+  if (!bound(reinterpret_cast<const void*>(g_copy_blocks))) return nullptr;
+  const int rc = g_copy_blocks(ptr<void>(kp), ptr<void>(vp), static_cast<pkv_dtype>(dtype), ptr<const int64_t>(pairs),
+                               npairs, layers, nblocks, block_elems, device, ptr<void>(stream));
+  return PyLong_FromLong(rc);
+}
+
 PyMethodDef kMethods[] = {
     {"gather", gather, METH_VARARGS, "Flatten a batch: tokens, positions, slots, lengths, contexts, logits rows."},
-    {"prefix_order", prefix_order, METH_VARARGS, "Row order grouping decode entries that share leading blocks."},
+    {"prefix_order_rows", prefix_order_rows, METH_VARARGS, "prefix_order from the block-table arena's rows."},
     {"arena_update", arena_update, METH_VARARGS, "One step of the block-table arena."},
+    {"cow_groups", cow_groups, METH_VARARGS, "Flatten block copies and split them into independent groups."},
+    {"bind", bind, METH_VARARGS, "Bind the libpkv.so entry points the calls below use."},
+    {"plan", plan, METH_VARARGS, "pkv_plan_batch on NumPy buffers."},
+    {"paged_attention", paged_attention, METH_VARARGS, "pkv_paged_attention with integer pointers."},
+    {"paged_attention_append", paged_attention_append, METH_VARARGS,
+     "pkv_paged_attention_append with integer pointers."},
+    {"copy_blocks", copy_blocks, METH_VARARGS, "pkv_copy_blocks with integer pointers."},
     {nullptr, nullptr, 0, nullptr},
 };
 

@@ -702,6 +702,34 @@ class NativePlanner:
         self._merge = np.zeros(1024, np.int32)
         self._counts = np.zeros(3, np.int64)
         self._launch = np.zeros(2, np.int32)
+        self._host = None
+
+    def plan_views(
+        self, query_seq: np.ndarray, query_positions: np.ndarray | None, tables: np.ndarray,
+        context_lens: np.ndarray, block_size: int, num_heads: int, head_dim: int, partition_size: int = 0,
+        min_tile_rows: int = MIN_TILE_ROWS,
+    ) -> tuple[np.ndarray, np.ndarray, np.ndarray, int, int]:  # fmt: skip
+        """:meth:`plan` for callers that hand over int32 C-contiguous arrays (``tables`` 2-D) and
+        use the result at once: ``(rows [R, 2], tiles [n, 4], merge [M], partition size, flags)``,
+        where the arrays are views of this planner's buffers, valid until its next call. The
+        library is reached through ``_pkvhost.plan`` rather than ctypes."""
+        host = self._host
+        if host is None:
+            host = self._host = _native.bound_host()
+        while True:
+            rc = host.plan(query_seq, query_positions, tables, context_lens, block_size, num_heads, head_dim,
+                           partition_size, min_tile_rows, self._rows, self._tiles, self._merge, self._counts,
+                           self._launch)  # fmt: skip
+            if rc != _native.PKV_ETOOBIG:
+                break
+            rows, tiles, merge = (int(c) for c in self._counts)
+            self._rows = np.zeros((max(rows, 2 * self._rows.shape[0]), 2), np.int32)
+            self._tiles = np.zeros((max(tiles, 2 * self._tiles.shape[0]), 4), np.int32)
+            self._merge = np.zeros(max(merge, 2 * self._merge.size), np.int32)
+        _native.check(rc, "pkv_plan_batch")
+        rows, tiles, merge = (int(c) for c in self._counts)
+        partition, flags = (int(v) for v in self._launch)
+        return self._rows[:rows], self._tiles[:tiles], self._merge[:merge], partition, flags
 
     def plan(
         self, query_seq: np.ndarray, head_dim: int, num_heads: int, tables: np.ndarray,

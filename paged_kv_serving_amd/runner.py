@@ -168,17 +168,20 @@ class _Staging:
     The sections (int64 first, then int32, each 8-byte aligned) are written into a pinned host
     buffer and copied to a device buffer of the same layout on the runner's stream; the host does
     not wait for the copy. Before a later call rewrites the host buffer it waits for the copy that
-    last read it (an event), which has normally long finished."""
+    last read it (an event), which has normally long finished. The device buffer is rewritten by
+    the next call's copy, which the stream orders after this call's kernels."""
 
     def __init__(self, device: torch.device) -> None:
         self.device = device
         self.host: torch.Tensor | None = None
         self.dev: torch.Tensor | None = None
+        self.base = 0  # device address of self.dev
         self.done = torch.cuda.Event()
         self.pending = False
 
-    def send(self, parts64: list[np.ndarray], parts32: list[np.ndarray]) -> tuple[list[torch.Tensor], list[torch.Tensor]]:
-        """Device int64 and int32 tensors holding ``parts64`` and ``parts32``, in order."""
+    def send(self, parts64: list[np.ndarray], parts32: list[np.ndarray]) -> list[int]:
+        """Copy ``parts64`` then ``parts32`` to the device; returns each part's byte offset in the
+        device buffer (see :meth:`tensor` and :attr:`base`)."""
         n64 = sum(p.size for p in parts64)
         n32 = sum(p.size for p in parts32)
         nbytes = 8 * n64 + 4 * n32 + 8
@@ -188,41 +191,72 @@ class _Staging:
             size = max(nbytes, 2 * (0 if self.host is None else self.host.numel()), 1 << 16)
             self.host = torch.empty(size, dtype=torch.uint8, pin_memory=True)
             self.dev = torch.empty(size, dtype=torch.uint8, device=self.device)
-        host = self.host.numpy()
+            self.base = self.dev.data_ptr()
+            self._host_np = self.host.numpy()
+        host = self._host_np
         off32 = 8 * n64
         if parts64:
             np.concatenate(parts64, out=host[:off32].view(np.int64), casting="same_kind")
         if parts32:
             np.concatenate(parts32, out=host[off32 : off32 + 4 * n32].view(np.int32), casting="same_kind")
-        with torch.cuda.device(self.device):
-            self.dev[: off32 + 4 * n32].copy_(self.host[: off32 + 4 * n32], non_blocking=True)
-            self.done.record(torch.cuda.current_stream(self.device))
+        self.dev[: off32 + 4 * n32].copy_(self.host[: off32 + 4 * n32], non_blocking=True)
+        self.done.record(torch.cuda.current_stream(self.device))
         self.pending = True
-        dev64 = self.dev[:off32].view(torch.int64)
-        dev32 = self.dev[off32 : off32 + 4 * n32].view(torch.int32)
-        return dev64.split([p.size for p in parts64]), dev32.split([p.size for p in parts32])
+        offsets, at = [], 0
+        for part in parts64:
+            offsets.append(at)
+            at += 8 * part.size
+        for part in parts32:
+            offsets.append(at)
+            at += 4 * part.size
+        return offsets
+
+    def tensor(self, offset: int, count: int, dtype: torch.dtype) -> torch.Tensor:
+        """A device tensor view of ``count`` elements of ``dtype`` at byte ``offset``."""
+        size = torch.tensor([], dtype=dtype).element_size()
+        return self.dev[offset : offset + count * size].view(dtype)
 
 
 @dataclass
 class _Step:
     """One iteration's device-side metadata (from :meth:`ModelRunner._prepare`), in the planner's
-    row order; ``token_order`` maps it back to batch order (None: the same)."""
+    row order; ``token_order`` maps it back to batch order (None: the same). Every section lives
+    in the staging buffer at ``staging.base`` + its byte offset; the ``*_at`` fields are those
+    offsets, and :meth:`tensor` gives torch views where torch needs them."""
 
     total: int
-    tokens: torch.Tensor
-    rope_positions: torch.Tensor
-    slots: torch.Tensor
-    query_positions: torch.Tensor
-    query_seq: torch.Tensor
-    contexts: torch.Tensor
-    tables: torch.Tensor
-    plan: ops.AttentionPlan
+    staging: _Staging
+    tokens_at: int
+    rope_at: int
+    slots_at: int
+    logits_at: int
+    qpos_at: int
+    qseq_at: int
+    contexts_at: int
+    plan_rows_at: int
+    plan_tiles_at: int
+    merge_at: int
+    num_plan_rows: int
+    num_tiles: int
+    num_merge: int
+    num_wanted: int
+    partition: int
+    flags: int
     max_context: int
     token_order: np.ndarray | None
-    names: list[str]
-    logits_rows: torch.Tensor
+    entries: tuple
     decode_only: bool
-    workspace: torch.Tensor | None = None
+
+    def tensor(self, name: str) -> torch.Tensor:
+        """int64 views: ``tokens``, ``rope_positions``, ``slots``, ``logits_rows``."""
+        offset, count = {
+            "tokens": (self.tokens_at, self.total), "rope_positions": (self.rope_at, self.total),
+            "slots": (self.slots_at, self.total), "logits_rows": (self.logits_at, self.num_wanted),
+        }[name]  # fmt: skip
+        return self.staging.tensor(offset, count, torch.int64)
+
+    def ptr(self, offset: int) -> int:
+        return self.staging.base + offset
 
 
 class _DeviceWeights:
@@ -290,13 +324,19 @@ class ModelRunner:
         self._tables = BlockTableArena(self.device)
         self._planner = ops.NativePlanner()
         self._staging = _Staging(self.device)
-        self._host = _native.host()
+        self._host = _native.bound_host()
         self._device_index = self.device.index
+        self._stats = np.zeros(8, np.int64)
+        self._kv_code = ops.kv_dtype_code(kv_dtype)
+        self._pairs = np.zeros(512, np.int64)
+        self._workspace: torch.Tensor | None = None
         _native.init_device(self._device_index)  # the library's overlap stream on this device
         self._per_token = (np.zeros(1024, np.int64), np.zeros(1024, np.int64), np.zeros(1024, np.int64))
         self._per_entry = (np.zeros(256, np.int64), np.zeros(256, np.int32), np.zeros(256, np.int64))
-        #: The host plan of the last ``execute`` (rows, tiles, partition size, load hint).
+        #: The host plan of the last call (rows, tiles, merge list, partition size, hints); its
+        #: arrays are views of the planner's buffers, rewritten by the next call.
         self.last_plan: ops.BatchPlan | None = None
+        self._layer_bytes = self._keys[0].numel() * self._keys.element_size()
 
     # --- pool ---------------------------------------------------------------------------
 
@@ -345,10 +385,21 @@ class ModelRunner:
         if not self._pending:
             return 0
         pending, self._pending = self._pending, []
-        for group in ops.independent_groups(pending):
-            pairs = torch.tensor(group, dtype=torch.int64).to(self.device, non_blocking=True)
-            ops.copy_blocks(self._keys, self._values, pairs)
+        sizes, flat = self._cow_groups(pending)
+        start = 0
+        for size in sizes:
+            pairs = torch.from_numpy(flat[2 * start : 2 * (start + size)].copy()).view(-1, 2)
+            ops.copy_blocks(self._keys, self._values, pairs.to(self.device, non_blocking=True))
+            start += size
         return len(pending)
+
+    def _cow_groups(self, pending: list[tuple[int, int]]) -> tuple[list[int], np.ndarray]:
+        """Queued copies flattened to int64 (src, dst) pairs, and the sizes of the consecutive
+        groups that may each run as one launch (``ops.independent_groups``'s rule)."""
+        if self._pairs.size < 2 * len(pending):
+            self._pairs = np.zeros(max(2 * len(pending), 2 * self._pairs.size), np.int64)
+        sizes = self._host.cow_groups(pending, self._pairs)
+        return sizes, self._pairs[: 2 * len(pending)]
 
     def block_fingerprint(self, block_id: int) -> bytes:
         """BLAKE2b-16 of one block's bytes, keys then values (runner.py:135-142)."""
@@ -407,7 +458,7 @@ class ModelRunner:
         while True:
             tokens, positions, slots = self._per_token
             total, problem, entry, position = self._host.gather(
-                entries, self.block_size, tokens, positions, slots, lengths, contexts, logits
+                entries, self.block_size, tokens, positions, slots, lengths, contexts, logits, self._stats
             )
             if total >= 0:
                 break
@@ -426,16 +477,17 @@ class ModelRunner:
         config = self.model.config
         tokens, positions, slots, lengths, context, logits_rows, (problem, bad, position) = self._gather(entries)
         total = tokens.size
+        low_token, high_token, low_pos, high_pos, low_slot, high_slot, low_ctx, repeats = self._stats.tolist()
         # The reference checks token ids, then positions, then forms the slots (runner.py:174-187).
-        if np.any(tokens < 0) or np.any(tokens >= config.vocab_size):
+        if low_token < 0 or high_token >= config.vocab_size:
             raise ValueError("token id outside the vocabulary")
-        if np.any(positions >= config.max_seq_len):
+        if high_pos >= config.max_seq_len:
             raise ValueError("position beyond max_seq_len")
         if problem == 1:
             raise ValueError(f"sequence {entries[bad].seq_id}: position {position} has no block in the table")
         if problem == 2:
             raise IndexError("tuple index out of range")
-        if slots.size and (slots.min() < 0 or slots.max() >= self.capacity_tokens):
+        if low_slot < 0 or high_slot >= self.capacity_tokens:
             raise IndexError("a block table names a block outside the pool")
         # Negative positions run as in the reference: their slot comes from the end of the table
         # (a Python index, runner.py:158), their rotary angle from the end of the tables (a NumPy
@@ -443,18 +495,27 @@ class ModelRunner:
         # attention.py:102-104, 120-121). An entry ending at one has context_len < 1, which the
         # reference's attention refuses (attention.py:76-77).
         rope_positions = positions
-        if positions.size and positions.min() < 0:
-            if positions.min() < -config.max_seq_len:
+        if low_pos < 0:
+            if low_pos < -config.max_seq_len:
                 raise IndexError("position outside the rotary tables")
-            if context.min() < 1:
+            if low_ctx < 1:
                 raise ValueError("context_len must be >= 1")
             rope_positions = np.where(positions < 0, positions + config.max_seq_len, positions)
         # Logits rows, in batch order of the entries that ask for them.
         wanted = logits_rows[logits_rows >= 0]
-        names = [e.seq_id for e in entries if e.logits_index is not None] if wanted.size else []
+        # Block tables live in a device arena between calls; only changed entries travel.
+        update = self._tables.update(entries)
+        rows = update.rows
         # Rows in the order the planner can use: decode entries sharing leading blocks together
-        # (validation above ran in batch order, so errors name the reference's entry).
-        order = self._host.prefix_order(entries, -(-ops.MIN_SHARED_TOKENS // self.block_size), ops.MIN_SHARED_ROWS)
+        # (validation above ran in batch order, so errors name the reference's entry). Only a
+        # batch where two decode entries start in the same block can have such entries; the
+        # order is read from the arena's rows, which hold every table as int32 by now.
+        order = None
+        if repeats:
+            order = self._host.prefix_order_rows(
+                rows, lengths, self._tables.host, self._tables.held_lengths,
+                -(-ops.MIN_SHARED_TOKENS // self.block_size), ops.MIN_SHARED_ROWS,
+            )  # fmt: skip
         token_order = None
         if order is not None:
             order = np.asarray(order, dtype=np.int64)
@@ -465,60 +526,105 @@ class ModelRunner:
             planner_row = np.empty(total, dtype=np.int64)  # batch token index -> planner token index
             planner_row[token_order] = np.arange(total)
             wanted = planner_row[wanted]
-            entries = [entries[i] for i in order.tolist()]
-            lengths, context = lengths[order], context[order]
-
-        # Block tables live in a device arena between calls; only changed entries travel.
-        update = self._tables.update(entries)
+            rows, lengths, context = rows[order], lengths[order], context[order]
         contexts_by_row = np.zeros(self._tables.num_rows, dtype=np.int32)
-        contexts_by_row[update.rows] = context
-        query_seq = np.repeat(update.rows, lengths)
-        host_plan = self._planner.plan(
-            query_seq, config.head_dim, config.n_heads, self._tables.host, contexts_by_row,
-            self.block_size, partition_size=self.partition_size, query_positions=positions,
+        contexts_by_row[rows] = context
+        query_seq = rows if total == len(entries) else np.repeat(rows, lengths)
+        query_pos = positions.astype(np.int32)
+        plan_rows, plan_tiles, merge, partition, flags = self._planner.plan_views(
+            query_seq, query_pos, self._tables.host, contexts_by_row, self.block_size, config.n_heads,
+            config.head_dim, self.partition_size,
         )  # fmt: skip
-        self.last_plan = host_plan
+        self.last_plan = ops.BatchPlan(
+            plan_rows, plan_tiles, partition, bool(flags & _native.PKV_ATTN_SHARED_KV), merge,
+            bool(flags & _native.PKV_ATTN_SHORT_ROWS),
+        )  # fmt: skip
         # Queued copy-on-write pairs travel in the same copy and run before this step's kernels.
-        groups = ops.independent_groups(self._pending) if self._pending else []
+        sizes, flat = self._cow_groups(self._pending) if self._pending else ([], None)
         self._pending = []
-        pairs = [np.asarray(group, dtype=np.int64).ravel() for group in groups]
-        parts64, parts32 = self._staging.send(
-            [tokens, rope_positions, slots, update.index, wanted, *pairs],
-            [positions, query_seq, contexts_by_row, update.values, host_plan.rows.ravel(),
-             host_plan.tiles.ravel(), host_plan.merge],
+        parts64 = [tokens, rope_positions, slots, update.index, wanted]
+        if sizes:
+            parts64.append(flat)
+        offsets = self._staging.send(
+            parts64,
+            [query_pos, query_seq, contexts_by_row, update.values, plan_rows.ravel(), plan_tiles.ravel(), merge],
         )  # fmt: skip
-        tokens_d, rope_d, slots_d, index_d, rows_d = parts64[:5]
-        qpos_d, qseq_d, context_d, values_d, plan_rows_d, plan_tiles_d, merge_d = parts32
-        for pair_d in parts64[5:]:
-            ops.copy_blocks(self._keys, self._values, pair_d.view(-1, 2))
-        self._tables.apply(index_d, values_d)
-        plan = ops.AttentionPlan(
-            rows=plan_rows_d.view(-1, 2), tiles=plan_tiles_d.view(-1, 4),
-            partition_size=host_plan.partition_size, shared_kv=host_plan.shared_kv, merge=merge_d,
-            short_rows=host_plan.short_rows,
-        )  # fmt: skip
-        decode_only = bool(host_plan.tiles.size == 0 and len(entries) == total and
-                           np.array_equal(positions, context.astype(np.int64) - 1))  # fmt: skip
+        tokens_at, rope_at, slots_at, index_at, logits_at = offsets[:5]
+        qpos_at, qseq_at, context_at, values_at, rows_at, tiles_at, merge_at = offsets[-7:]
+        staging = self._staging
+        if sizes:
+            pairs_at = offsets[5]
+            k_pool, v_pool = self._keys, self._values
+            dtype = ops.kv_dtype_code(k_pool.dtype)
+            layers, num_blocks = k_pool.shape[0], k_pool.shape[1]
+            block_elems = k_pool[0, 0].numel()
+            stream = ops._stream(self._device_index)
+            start = 0
+            for size in sizes:
+                rc = self._host.copy_blocks(k_pool.data_ptr(), v_pool.data_ptr(), dtype, staging.base + pairs_at + 16 * start,
+                                            size, layers, num_blocks, block_elems, self._device_index, stream)  # fmt: skip
+                _native.check(rc, "pkv_copy_blocks")
+                start += size
+        if update.index.size:
+            self._tables.apply(staging.tensor(index_at, update.index.size, torch.int64),
+                               staging.tensor(values_at, update.values.size, torch.int32))  # fmt: skip
+        else:
+            self._tables.apply_nothing()
+        # One token per entry: each is a decode row at its last position (context = position + 1).
+        decode_only = plan_tiles.shape[0] == 0 and len(entries) == total
         return _Step(
-            total=total, tokens=tokens_d, rope_positions=rope_d, slots=slots_d, query_positions=qpos_d,
-            query_seq=qseq_d, contexts=context_d, tables=self._tables.tables, plan=plan,
-            max_context=int(context.max()), token_order=token_order, names=names, logits_rows=rows_d,
+            total=total, staging=staging, tokens_at=tokens_at, rope_at=rope_at, slots_at=slots_at,
+            logits_at=logits_at, qpos_at=qpos_at, qseq_at=qseq_at, contexts_at=context_at, plan_rows_at=rows_at,
+            plan_tiles_at=tiles_at, merge_at=merge_at, num_plan_rows=plan_rows.shape[0],
+            num_tiles=plan_tiles.shape[0], num_merge=merge.size, num_wanted=wanted.size, partition=partition,
+            flags=flags, max_context=int(context.max()), token_order=token_order, entries=entries,
             decode_only=decode_only,
         )  # fmt: skip
 
     def _attention(self, step: _Step, layer: int, queries: torch.Tensor, out: torch.Tensor, append=None) -> None:
         """Paged attention of one layer's rotated queries over the pools (and the decode append
-        fused into it when ``append`` = (keys, values) rows is given)."""
+        fused into it when ``append`` = (keys, values) rows is given), called through
+        ``_pkvhost`` with the metadata's device addresses."""
         config = self.model.config
-        need = ops.attention_workspace_bytes(step.total, config.n_heads, config.head_dim, step.max_context,
-                                             step.plan.partition_size)  # fmt: skip
-        if step.workspace is None or step.workspace.numel() * 4 < need:
-            step.workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=self.device)
-        ops.launch_paged_attention(
-            out, queries, step.query_positions, step.query_seq, self._keys[layer], self._values[layer],
-            step.tables, step.contexts, self.model.attention_scale, step.max_context, step.plan,
-            step.workspace, self._device_index, None if append is None else (append[0], append[1], step.slots),
+        heads, dim = config.n_heads, config.head_dim
+        # pkv_attention_workspace_bytes: (head_dim + 2) floats per (query, head, partition) once a
+        # context can span more than one partition.
+        part = step.partition or 512  # 0: the library's default
+        parts = -(-step.max_context // part) if step.max_context > part else 1
+        need = 0 if parts == 1 else step.total * heads * parts * (dim + 2) * 4
+        workspace = self._workspace
+        if workspace is None or workspace.numel() * 4 < need:
+            workspace = self._workspace = torch.empty(max(need // 4, 1), dtype=torch.float32, device=self.device)
+        if step.num_plan_rows == 0 and step.num_tiles == 0:
+            return
+        pools = self._keys
+        key_at = pools.data_ptr() + layer * self._layer_bytes
+        value_at = self._values.data_ptr() + layer * self._layer_bytes
+        tables = self._tables.tables
+        device = self._device_index
+        stream = ops._stream(device)
+        common = (
+            out.data_ptr(), queries.data_ptr(), queries.stride(0), step.ptr(step.qpos_at), step.ptr(step.qseq_at),
+            step.total, step.ptr(step.plan_rows_at) if step.num_plan_rows else 0, step.num_plan_rows,
         )  # fmt: skip
+        tail = (
+            step.ptr(step.merge_at) if step.num_merge else 0, step.num_merge, key_at, value_at, self._kv_code,
+            self.num_blocks, self.block_size, tables.data_ptr(), tables.shape[1], step.ptr(step.contexts_at),
+            tables.shape[0], heads, dim,
+            float(self.model.attention_scale), step.max_context, step.partition, step.flags, workspace.data_ptr(),
+            workspace.numel() * 4,
+        )  # fmt: skip
+        if append is None:
+            rc = self._host.paged_attention(*common, step.ptr(step.plan_tiles_at) if step.num_tiles else 0,
+                                            step.num_tiles, *tail, device, stream)  # fmt: skip
+            _native.check(rc, "pkv_paged_attention")
+            return
+        keys, values = append
+        rc = self._host.paged_attention_append(
+            *common, *tail, keys.data_ptr(), values.data_ptr(), ops.kv_dtype_code(keys.dtype), keys.stride(0),
+            values.stride(0), step.ptr(step.slots_at), device, stream,
+        )  # fmt: skip
+        _native.check(rc, "pkv_paged_attention_append")
 
     def attend(
         self, batch: ExecutionBatch, queries: torch.Tensor, keys: torch.Tensor, values: torch.Tensor,
@@ -538,8 +644,9 @@ class ModelRunner:
             out = torch.empty(shape, dtype=torch.float32, device=self.device)
         if step is None:
             return out
+        device = self.device
         for name, tensor in (("queries", queries), ("keys", keys), ("values", values), ("out", out)):
-            if tuple(tensor.shape) != shape or tensor.dtype != torch.float32 or tensor.device != self.device:
+            if tensor.shape != shape or tensor.dtype != torch.float32 or tensor.device != device:
                 raise ValueError(f"{name} must be float32 {list(shape)} on the runner's device")
         if not out.is_contiguous():
             raise ValueError("out must be contiguous")
@@ -553,7 +660,7 @@ class ModelRunner:
         if step.decode_only:
             self._attention(step, layer, queries, result, append=(keys, values))
         else:
-            ops.append_kv(self._keys[layer], self._values[layer], keys, values, step.slots)
+            ops.append_kv(self._keys[layer], self._values[layer], keys, values, step.tensor("slots"))
             self._attention(step, layer, queries, result)
         if step.token_order is not None:
             out[index] = result
@@ -570,7 +677,8 @@ class ModelRunner:
         w = self._device_weights()
         heads, dim, d_model = config.n_heads, config.head_dim, config.d_model
         eps = config.norm_eps
-        hidden = w.embedding[step.tokens]
+        hidden = w.embedding[step.tensor("tokens")]
+        rope_positions, slots = step.tensor("rope_positions"), step.tensor("slots")
         attended = torch.empty((total, heads, dim), dtype=torch.float32, device=self.device)
         for index, (attn_norm, qkv, out_proj, ffn_norm, gate, up, down) in enumerate(w.layers):
             fused = (_rms_norm(hidden, attn_norm, eps) @ qkv).view(total, 3, heads, dim)
@@ -578,13 +686,14 @@ class ModelRunner:
             # (reference model.py:251-252 then runner.py:195-196).
             queries = ops.rope_append(
                 self._keys[index], self._values[index], fused[:, 0], fused[:, 1], fused[:, 2],
-                step.rope_positions, w.cos, w.sin, step.slots, out=fused[:, 0],
+                rope_positions, w.cos, w.sin, slots, out=fused[:, 0],
             )  # fmt: skip
             self._attention(step, index, queries, attended)
             hidden = hidden + attended.view(total, d_model) @ out_proj
             normed = _rms_norm(hidden, ffn_norm, eps)
             hidden = hidden + (_silu(normed @ gate) * (normed @ up)) @ down
 
-        if not step.names:
+        if not step.num_wanted:
             return [], None
-        return step.names, _rms_norm(hidden[step.logits_rows], w.final_norm, eps) @ w.embedding.T
+        names = [e.seq_id for e in step.entries if e.logits_index is not None]  # batch order
+        return names, _rms_norm(hidden[step.tensor("logits_rows")], w.final_norm, eps) @ w.embedding.T

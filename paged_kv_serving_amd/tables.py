@@ -55,7 +55,8 @@ class BlockTableArena:
         self._step = 0
         # Rows an update touched whose device copy no apply() has written yet. If the caller
         # fails between the two, the next update forgets what they hold.
-        self._unapplied = np.zeros(0, dtype=np.int32)
+        self._none = np.zeros(0, dtype=np.int32)
+        self._unapplied = self._none
         self._index = np.zeros(1024, dtype=np.int64)
         self._values = np.zeros(1024, dtype=np.int32)
         self._rows = np.zeros(64, dtype=np.int32)
@@ -68,6 +69,11 @@ class BlockTableArena:
     @property
     def width(self) -> int:
         return self.host.shape[1]
+
+    @property
+    def held_lengths(self) -> np.ndarray:
+        """int32 per row: how many leading entries of the host row are the row's table."""
+        return self._held_len
 
     def held(self, row: int) -> tuple[int, ...]:
         """The table arena row ``row`` currently holds."""
@@ -88,7 +94,7 @@ class BlockTableArena:
             self._held_len[self._unapplied] = 0
             for row in self._unapplied.tolist():
                 self._held_obj[row] = None
-            self._unapplied = np.zeros(0, dtype=np.int32)
+            self._unapplied = self._none
         self._step += 1
         count = len(entries)
         if self._rows.size < count:
@@ -113,7 +119,11 @@ class BlockTableArena:
         """Write an update's values (device int32) at its flat indices (device int64)."""
         if index.numel():
             self.tables.view(-1).index_copy_(0, index, values)
-        self._unapplied = np.zeros(0, dtype=np.int32)
+        self._unapplied = self._none
+
+    def apply_nothing(self) -> None:
+        """Record that an update with no changed entries has been applied."""
+        self._unapplied = self._none
 
     def used_blocks(self, rows: np.ndarray, block_counts: np.ndarray) -> np.ndarray:
         """The first ``block_counts[i]`` table entries of arena row ``rows[i]``, concatenated."""

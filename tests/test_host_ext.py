@@ -1,14 +1,15 @@
 """The _pkvhost extension (csrc/pkv_host.cpp) against the Python it replaces in the runner, on
 the CPU: the flattened batch, every slot (the reference's rule, runner.py:149-159, including
-Python's floor division and negative indices) and the first slot problem; and the row order
-that groups decode entries sharing their leading blocks (runner.shared_prefix_order)."""
+Python's floor division and negative indices), the first slot problem and the validation
+statistics; the row order that groups decode entries sharing their leading blocks
+(runner.shared_prefix_order); and the copy-on-write grouping (ops.independent_groups)."""
 
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from paged_kv_serving_amd import _native
+from paged_kv_serving_amd import _native, ops
 from paged_kv_serving_amd.runner import BatchEntry, compute_slots, shared_prefix_order
 
 ext = _native.host()
@@ -69,10 +70,7 @@ def test_gather_reports_the_first_slot_problem() -> None:
     assert problem == (2, 0, -40)
 
 
-@pytest.mark.parametrize("seed", range(30))
-def test_prefix_order_matches_the_python_grouping(seed) -> None:
-    rng = np.random.default_rng(seed)
-    block = 16
+def _prefix_case(rng, block):
     stems = [tuple(int(b) for b in rng.integers(0, 1000, 40)) for _ in range(3)]
     entries = []
     for i in range(int(rng.integers(1, 120))):
@@ -83,6 +81,102 @@ def test_prefix_order_matches_the_python_grouping(seed) -> None:
         else:
             n = int(rng.integers(1, 30))
             entries.append(BatchEntry(f"p{i}", tuple(range(n)), tuple(range(n)), tuple(range(3)), None))
-    entries = tuple(entries)
-    lead = -(-512 // block)
-    assert ext.prefix_order(entries, lead, 16) == shared_prefix_order(entries, block)
+    return tuple(entries)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_prefix_order_from_the_arena_matches_the_python_grouping(seed) -> None:
+    from paged_kv_serving_amd.tables import BlockTableArena
+
+    rng = np.random.default_rng(seed)
+    block = 16
+    entries = _prefix_case(rng, block)
+    if seed % 5 == 0:  # already grouped: sharers adjacent, nothing to move
+        entries = tuple(sorted(entries, key=lambda e: (len(e.token_ids) != 1, e.block_table[:32])))
+    arena = BlockTableArena("cpu", rows=4, width=8)  # grows to fit
+    for _ in range(2):  # a fresh arena, then the same tables again (rows reused, nothing uploaded)
+        update = arena.update(entries)
+        arena.apply_nothing()
+        lengths = np.asarray([len(e.token_ids) for e in entries], np.int64)
+        got = ext.prefix_order_rows(update.rows, lengths, arena.host, arena.held_lengths, -(-512 // block), 16)
+        assert got == shared_prefix_order(entries, block)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_gather_statistics_are_the_reductions_the_runner_validates(seed) -> None:
+    rng = np.random.default_rng(seed)
+    block = int(rng.choice([1, 4, 16]))
+    entries = random_entries(rng, block, int(rng.integers(1, 80)), negative=seed % 3 == 0)
+    if seed % 4 == 1:  # two decode rows starting in the same block
+        first = entries[0]
+        entries = entries + (BatchEntry("twin", (1,), (first.positions[-1],), first.block_table, 0),
+                             BatchEntry("twin2", (2,), (first.positions[-1],), first.block_table, 0))
+    count = len(entries)
+    total = sum(len(e.token_ids) for e in entries)
+    tokens, positions, slots = (np.zeros(total, np.int64) for _ in range(3))
+    lengths, contexts, logits = np.zeros(count, np.int64), np.zeros(count, np.int32), np.zeros(count, np.int64)
+    stats = np.zeros(8, np.int64)
+    got = ext.gather(entries, block, tokens, positions, slots, lengths, contexts, logits, stats)
+    assert got[0] == total
+    decode_firsts = [e.block_table[0] for e in entries if len(e.token_ids) == 1]
+    want = [tokens.min(), tokens.max(), positions.min(), positions.max(), slots.min(), slots.max(), contexts.min(),
+            int(len(set(decode_firsts)) < len(decode_firsts))]  # fmt: skip
+    assert stats.tolist() == [int(v) for v in want]
+    assert stats[7] == (1 if seed % 4 == 1 else stats[7])
+
+
+def test_gather_statistics_count_unformed_slots_as_minus_one() -> None:
+    entries = (BatchEntry("a", (3,), (5,), (7,)), BatchEntry("b", (4,), (40,), (1,)))
+    stats = np.zeros(8, np.int64)
+    buffers = [np.zeros(2, np.int64) for _ in range(3)] + [np.zeros(2, np.int64), np.zeros(2, np.int32), np.zeros(2, np.int64)]
+    total, problem, entry, position = ext.gather(entries, 16, *buffers, stats)
+    assert (total, problem, entry, position) == (2, 1, 1, 40)
+    assert stats.tolist() == [3, 4, 5, 40, -1, 7 * 16 + 5, 6, 0]
+
+
+def _python_groups(pairs):
+    return [len(g) for g in ops.independent_groups(pairs)]
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_cow_groups_match_the_python_grouping(seed) -> None:
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(0, 300))
+    ids = int(rng.choice([4, 20, 1000, 100_000]))
+    pairs = [(int(a), int(b)) for a, b in rng.integers(0, ids, (n, 2))]
+    out = np.zeros(2 * n + 2, np.int64)
+    assert ext.cow_groups(pairs, out) == _python_groups(pairs)
+    assert out[: 2 * n].tolist() == [v for pair in pairs for v in pair]
+
+
+def test_cow_groups_of_forks_are_one_group_and_bad_pairs_are_refused() -> None:
+    pairs = [(7, 100 + i) for i in range(256)]  # every child copies the same shared block
+    out = np.zeros(512, np.int64)
+    assert ext.cow_groups(pairs, out) == [256]
+    assert ext.cow_groups([(1, 2), (2, 3), (3, 1)], np.zeros(6, np.int64)) == [1, 1, 1]
+    with pytest.raises(ValueError):
+        ext.cow_groups([(1, 2, 3)], np.zeros(6, np.int64))
+    with pytest.raises(ValueError):
+        ext.cow_groups([(1, 2), (3, 4)], np.zeros(3, np.int64))
+
+
+def test_the_bound_planner_matches_the_ctypes_planner() -> None:
+    from test_host_plan_native import random_batch
+
+    for seed in range(60):
+        case = random_batch(seed)
+        planner = ops.NativePlanner()
+        want = planner.plan(case["query_seq"], case["head_dim"], case["num_heads"], case["tables"],
+                            case["context_lens"], case["block_size"], partition_size=case["partition_size"],
+                            query_positions=case["query_positions"])  # fmt: skip
+        fast = ops.NativePlanner()
+        fast._rows = np.zeros((1, 2), np.int32)  # grows on the first call
+        rows, tiles, merge, partition, flags = fast.plan_views(
+            case["query_seq"].astype(np.int32), case["query_positions"].astype(np.int32), case["tables"],
+            case["context_lens"].astype(np.int32), case["block_size"], case["num_heads"], case["head_dim"],
+            case["partition_size"],
+        )  # fmt: skip
+        assert np.array_equal(rows, want.rows) and np.array_equal(tiles, want.tiles)
+        assert np.array_equal(merge, want.merge) and partition == want.partition_size
+        assert bool(flags & _native.PKV_ATTN_SHARED_KV) == want.shared_kv
+        assert bool(flags & _native.PKV_ATTN_SHORT_ROWS) == want.short_rows
