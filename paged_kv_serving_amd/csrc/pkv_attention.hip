@@ -637,7 +637,6 @@ struct TileShape {
   // chunk each) and the PV reads (4 rows x 16 columns) then spread over all LDS banks, as the
   // padded rows do, while every 16-byte chunk stays whole for the DMA.
   static constexpr int kChunks = kKeys * D / 4;            // 16-byte chunks of one K (or V) tile
-  static constexpr int kDmaPerLane = kChunks / 256;        // DMA loads per lane per K (or V) tile
   static constexpr int kTileFloats = kKeys * D;
   static constexpr int kStageFloats = 2 * kTileFloats;     // K tile then V tile
 };
@@ -648,12 +647,11 @@ __device__ __forceinline__ int swz(int row, int col) {
   return row * D + ((((col >> 2) ^ (row & 7))) << 2) + (col & 3);
 }
 
-// One work item of the tile pass: item `bid` = (partition, tile, head), heads fastest, partitions
-// slowest (a whole tile's work is all in partition 0, so those items come first). Every
-// thread of the workgroup calls it with the same item; it returns early (uniformly) for items
-// outside the tile's partitions. On the direct-to-LDS path (kDma) s_k holds the kTileStages (key
-// tile, value tile) stages and s_v is unused.
-template <typename KVT, int D, bool kPow2Block, bool kDma>
+// One work item of the tile pass staged through registers: item `bid` = (partition, tile, head),
+// heads fastest, partitions slowest (a whole tile's work is all in partition 0, so those items
+// come first). Every thread of the workgroup calls it with the same item; it returns early
+// (uniformly) for items outside the tile's partitions.
+template <typename KVT, int D, bool kPow2Block>
 __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_table, float* s_k,
                                           float* s_v, int* s_vis) {
   static_assert(D % 16 == 0 && D >= 32, "the MFMA tile needs whole 16-wide output tiles");
@@ -755,10 +753,8 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
     mx = column_max(mx);
     // Raise the reference only when a score passes it by more than kLazyLog2 (or it is unset).
     const bool raise = mx > m_ref + kLazyLog2 || (m_ref == -INFINITY && mx > -INFINITY);
-    // The direct-to-LDS step rescales without a branch (alpha is exactly 1 in lanes that keep
-    // their reference), so the step stays one block of straight-line code the compiler can
-    // interleave; the register path skips the multiplies when no lane raises (fewer VGPRs).
-    if (kDma || __builtin_amdgcn_ballot_w64(raise) != 0) {
+    // Skip the multiplies when no lane raises (fewer VGPRs than a branch-free rescale).
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
       const float m_next = raise ? mx : m_ref;
       const float alpha = raise ? fast_exp2(m_ref - m_next) : 1.f;  // exp2(-inf) = 0
       l_part *= alpha;
@@ -777,151 +773,6 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
     }
   };
 
-  if constexpr (kDma) {
-    static_assert(std::is_same_v<KVT, float>, "the direct-to-LDS tiles are float32");
-    // Direct-to-LDS pipeline over kTileStages buffers: the key and value tiles of steps i + 1
-    // .. i + kTileStages - 1 are in flight while step i is multiplied. Step i waits for its own
-    // loads (vmcnt), then one barrier publishes every wavefront's share and also closes step
-    // i - 1, whose buffer the loads of step i + kTileStages - 1 then fill. Those are queued
-    // between the step's two products, in straight-line code the compiler can interleave with
-    // the matrix instructions. Every lane issues the same loads in every step, past the last
-    // step too: a lane whose key is past kend or in a block outside the pool loads row 0 of
-    // block 0 (always in the pool) instead, and the key's bit in the step's mask stays clear.
-    constexpr int kPer = S::kDmaPerLane;
-    static_assert(S::kChunks % kTileThreads == 0, "whole wavefront DMA loads per tile");
-    constexpr int kCpr = D / 4;  // chunks per key row
-    constexpr int kAhead = kTileStages - 1;
-    const uint32_t lds_kv = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_k));
-    // Branch-free address arithmetic (selects, no divergent branches). A block's elements and a
-    // token row's fit 31 bits (launch_tiles takes this path only when block_size * num_heads *
-    // head_dim does).
-    const uint64_t block_elems = static_cast<uint64_t>(a.block_size) * static_cast<uint64_t>(row_stride);
-    const uint32_t row_elems = static_cast<uint32_t>(row_stride);
-    const uint32_t pool_blocks = static_cast<uint32_t>(min<int64_t>(a.num_blocks, INT32_MAX));
-    // Table entry of key kpos (clamped into the window; callers discard it when kpos is out).
-    auto table_at = [&](int kpos) {
-      const int lb = min(max(block_of<kPow2Block>(kpos, a) - b0, 0), kTableSlots - 1);
-      return s_table[lb];
-    };
-    // Element offsets of this lane's kPer chunks of key tile k0, and the tile's key mask.
-    auto prepare = [&](int k0, int lane_v, int64_t (&off)[kPer]) -> uint32_t {
-#pragma unroll
-      for (int u = 0; u < kPer; ++u) {
-        const int chunk = (wave * kPer + u) * kWave + lane_v;
-        const int row = chunk / kCpr;
-        const int col = ((chunk % kCpr) ^ (row & 7)) * 4;
-        const int kpos = k0 + row;
-        const int blk = table_at(kpos);
-        const bool ok = (kpos < kend) & (static_cast<uint32_t>(blk) < pool_blocks);
-        const uint32_t within = kPow2Block ? (kpos & (a.block_size - 1)) : kpos % a.block_size;
-        const uint32_t blk_u = ok ? static_cast<uint32_t>(blk) : 0u;
-        const uint32_t row_off = ok ? within * row_elems : 0u;
-        off[u] = static_cast<int64_t>(blk_u * block_elems) + static_cast<int64_t>(row_off) + head_off + col;
-      }
-      const int kpos = k0 + lane_v;
-      const bool ok = (lane_v < kKeys) & (kpos < kend) &
-                      (static_cast<uint32_t>(table_at(kpos)) < pool_blocks);
-      return static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(ok));
-    };
-    auto fire = [&](int buf, const int64_t (&off)[kPer]) {
-      const uint32_t dst = lds_kv + static_cast<uint32_t>(buf * S::kStageFloats * 4 + wave * kPer * 1024);
-#pragma unroll
-      for (int u = 0; u < kPer; ++u) {
-        load_to_lds16(kcache + off[u], dst + u * 1024);
-        load_to_lds16(vcache + off[u], dst + u * 1024 + S::kTileFloats * 4);
-      }
-    };
-    const int nsteps = kend > kbeg ? (kend - kbeg + kKeys - 1) / kKeys : 0;
-    uint32_t kmask[kAhead];  // key masks of steps i .. i + kAhead - 1
-    wait_vmcnt<0>();  // the query loads above complete before the pipeline's loads are queued
-    if (nsteps > 0) {
-#pragma unroll
-      for (int st = 0; st < kAhead; ++st) {
-        int64_t off[kPer];
-        kmask[st] = prepare(kbeg + st * kKeys, lane, off);
-        fire(st, off);
-      }
-    }
-    int buf = 0;
-    for (int i = 0; i < nsteps; ++i) {
-      const int k0 = kbeg + i * kKeys;
-      wait_vmcnt<(kAhead - 1) * 2 * kPer>();  // this step's loads have landed
-      lds_barrier();
-      const int k_next = k0 + kAhead * kKeys;  // the tile whose loads this step queues
-      if (block_of<kPow2Block>(min(k_next + kKeys, kend) - 1, a) >= b0 + kTableSlots) {
-        // A whole tile moves its table window; no wavefront reads the table between the barrier
-        // above and the one below.
-        b0 = block_of<kPow2Block>(k_next, a);
-        stage_window();
-        lds_barrier();
-      }
-      // The swizzled LDS addresses are lane constants; they are recomputed from an opaque copy
-      // of the lane index each step (a few VALU operations) instead of being hoisted out of the
-      // loop, which would hold about 20 more VGPRs and cost the CU a row-pass workgroup.
-      int lane_o = lane;
-      asm volatile("" : "+v"(lane_o));
-      const int cl = lane_o >> 4;
-      const int nl = lane_o & 15;
-      const float* sk = s_k + buf * S::kStageFloats;
-      const float* sv = sk + S::kTileFloats;
-
-      // S^T blocks: register r of st[j] = S[query n][key k0 + 16j + 4c + r]. Lane (c, n) reads
-      // chunk c * kD4 / 4 + q of key row 16 j + n, swizzled by n & 7.
-      floatx4 st[kSub];
-#pragma unroll
-      for (int j = 0; j < kSub; ++j) st[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < kD4 / 4; ++q) {
-#pragma unroll
-        for (int j = 0; j < kSub; ++j) {
-          const float4 kv = *reinterpret_cast<const float4*>(
-              sk + (16 * j + nl) * D + (((cl * (kD4 / 4) + q) ^ (nl & 7)) << 2));
-          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qreg[4 * q], st[j], 0, 0, 0);
-          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qreg[4 * q + 1], st[j], 0, 0, 0);
-          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qreg[4 * q + 2], st[j], 0, 0, 0);
-          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qreg[4 * q + 3], st[j], 0, 0, 0);
-        }
-      }
-      // Queue step i + kAhead's loads into the buffer step i - 1 used. Their address arithmetic
-      // is scheduled among the PV products below, not the S^T products above (which would keep
-      // more registers live across the S^T loop).
-      __builtin_amdgcn_sched_barrier(0);
-      uint32_t next_mask;
-      {
-        int64_t off[kPer];
-        next_mask = prepare(k_next, lane_o, off);
-        fire(buf == 0 ? kAhead : buf - 1, off);
-      }
-      float pr[kSub][4];
-      softmax_step(st, k0, kmask[0], pr);
-
-      // O^T += V^T P^T. Column 16 b + n of row 16 j + 4 c + step is chunk 4 b + n / 4, swizzled
-      // by (4 c + step) & 7: chunk 4 (b ^ (c & 1)) + ((n / 4) ^ step), so each (j, step) needs one
-      // lane base for even b and one for odd b, and b itself is an immediate offset. The
-      // products are accumulated in the register path's order (j, then step, then b), so both
-      // paths round identically.
-#pragma unroll
-      for (int j = 0; j < kSub; ++j) {
-#pragma unroll
-        for (int step = 0; step < 4; ++step) {
-          const int lane_col = 4 * cl * D + 4 * ((nl >> 2) ^ step) + (nl & 3);
-          const float* v_even = sv + lane_col + 16 * (cl & 1);
-          const float* v_odd = sv + lane_col - 16 * (cl & 1);
-          const int row_off = (16 * j + step) * D;
-#pragma unroll
-          for (int b = 0; b < kNb; ++b) {
-            const float x = (b & 1) ? v_odd[row_off + 16 * b] : v_even[row_off + 16 * b];
-            o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, pr[j][step], o[b], 0, 0, 0);
-          }
-        }
-      }
-#pragma unroll
-      for (int st = 0; st + 1 < kAhead; ++st) kmask[st] = kmask[st + 1];
-      kmask[kAhead - 1] = next_mask;
-      buf = buf == kTileStages - 1 ? 0 : buf + 1;
-    }
-    wait_vmcnt<0>();  // the loads queued past the last step land before the LDS is reused
-  } else {
   // Software pipeline: the raw vectors of key tile k0 + kKeys are loaded into registers while
   // tile k0 is being multiplied; at the top of each step they are widened into LDS.
   constexpr int kVecs = kKeys * kVecPerRow;  // 16-byte vectors per K (or V) tile
@@ -1025,7 +876,6 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
     }
     __syncthreads();
   }
-  }
 
   // Epilogue: register r of tile b is O[query n][16b + 4c + r].
   const float l = column_sum(l_part);
@@ -1033,6 +883,302 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   // A whole tile covered every visible key of its rows: their outputs are final.
   const int row_parts = whole ? 1 : parts_of(my_vis, a.part_size);
   if (p >= row_parts) return;
+  const int64_t qh = (t0 + qi) * a.num_heads + h;
+  if (row_parts == 1) {
+    const float sum = l > 0.f ? l : 1.f;
+    float* dst = a.out + qh * D + 4 * c;
+#pragma unroll
+    for (int b = 0; b < kNb; ++b) {
+      *reinterpret_cast<float4*>(dst + 16 * b) =
+          make_float4(o[b][0] / sum, o[b][1] / sum, o[b][2] / sum, o[b][3] / sum);
+    }
+  } else {
+    const int64_t slot = qh * a.max_parts + p;
+    float* dst = a.ws_acc + slot * D + 4 * c;
+#pragma unroll
+    for (int b = 0; b < kNb; ++b) {
+      *reinterpret_cast<float4*>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
+    }
+    if (c == 0) {
+      a.ws_ml[2 * slot] = m_ref;
+      a.ws_ml[2 * slot + 1] = l;
+    }
+  }
+}
+
+// One work item of the tile pass beside the row pass, float32 pools: the same item as tile_item,
+// with the key and value tiles moved from HBM straight into LDS (global_load_lds_dwordx4)
+// through kTileStages buffers, all but one in flight while one is multiplied, so no register
+// holds a tile on its way. In every step a wavefront whose rows all end before the step's first
+// key skips both products: its keys would all be masked (every score -inf, every probability
+// 0), so its registers would not change.
+template <int D, bool kPow2Block>
+__device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int* s_table, float* s_kv,
+                                              int* s_vis) {
+  static_assert(D % 16 == 0 && D >= 32, "the MFMA tile needs whole 16-wide output tiles");
+  using S = TileShape<D>;
+  constexpr int kKeys = S::kKeys;
+  constexpr int kSub = S::kSub;
+  constexpr int kD4 = S::kD4;
+  constexpr int kNb = S::kNb;
+  constexpr int kPer = S::kChunks / kTileThreads;  // DMA loads per lane per K (or V) tile
+  static_assert(kPer >= 1 && S::kChunks % kTileThreads == 0, "whole wavefront DMA loads per tile");
+  constexpr int kCpr = D / 4;  // 16-byte chunks per key row
+  constexpr int kAhead = kTileStages - 1;
+
+  const int h = static_cast<int>(bid % static_cast<uint32_t>(a.num_heads));
+  const uint32_t rest = bid / static_cast<uint32_t>(a.num_heads);
+  const int64_t tile = rest % static_cast<uint32_t>(a.num_tiles);
+  const int p = static_cast<int>(rest / static_cast<uint32_t>(a.num_tiles));
+  const int32_t* entry = a.tiles + 4 * tile;
+  const int64_t t0 = entry[0];
+  if (t0 < 0 || t0 >= a.num_queries) return;  // a tile outside the batch is skipped
+  // A whole tile is computed by its partition-0 workgroup alone, over every visible key.
+  const bool whole = entry[3] == kTileWhole;
+  if (whole ? p != 0 : (p < entry[2] || (entry[3] > entry[2] && p >= entry[3]))) return;
+  const int nrows = static_cast<int>(min<int64_t>(min(entry[1], kTileRows), a.num_queries - t0));
+  const int seq = a.q_seq[t0];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  if (threadIdx.x < kTileRows) {
+    s_vis[threadIdx.x] = static_cast<int>(threadIdx.x) < nrows ? row_visible(a, t0 + threadIdx.x) : 0;
+  }
+  __syncthreads();
+  // The tile's longest visible row bounds its partitions (every wavefront reads all 64 entries).
+  int tile_vis = s_vis[lane];
+#pragma unroll
+  for (int mask = 32; mask > 0; mask >>= 1) tile_vis = max(tile_vis, __shfl_xor(tile_vis, mask));
+  tile_vis = __builtin_amdgcn_readfirstlane(tile_vis);  // the same in every lane: keep it scalar
+  if (!whole && p >= parts_of(tile_vis, a.part_size)) return;
+  const int s_beg = whole ? 0 : p * a.part_size;
+  const int s_end = whole ? tile_vis : min(s_beg + a.part_size, tile_vis);
+
+  const float* kcache = static_cast<const float*>(a.kcache);
+  const float* vcache = static_cast<const float*>(a.vcache);
+  const int64_t head_off = static_cast<int64_t>(h) * D;
+  const int64_t row_stride = static_cast<int64_t>(a.num_heads) * D;
+  const uint32_t lds_kv = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_kv));
+  // Branch-free address arithmetic (selects, no divergent branches). A block's elements and a
+  // token row's fit 31 bits (launch_tiles takes this path only when block_size * num_heads *
+  // head_dim does).
+  const uint64_t block_elems = static_cast<uint64_t>(a.block_size) * static_cast<uint64_t>(row_stride);
+  const uint32_t row_elems = static_cast<uint32_t>(row_stride);
+  const uint32_t pool_blocks = static_cast<uint32_t>(min<int64_t>(a.num_blocks, INT32_MAX));
+  const int c = lane >> 4;
+  const int n = lane & 15;
+  const int qi = wave * 16 + n;  // this lane's query in the S^T layout
+
+  // The table entries of blocks [b0, b0 + kTableSlots) are staged in LDS. A partition always
+  // fits; a whole tile moves the window forward when the next key tile would leave it.
+  const int last_block = s_end > s_beg ? block_of<kPow2Block>(s_end - 1, a) : -1;
+  int b0 = block_of<kPow2Block>(s_beg, a);
+  auto stage_window = [&]() {
+    const int nb = min(last_block - b0 + 1, kTableSlots);
+    if (nb > 0) stage_table(s_table, a, seq, b0, nb, kTileThreads);
+  };
+  stage_window();
+
+  const int my_vis = s_vis[qi];
+  const bool q_ok = qi < nrows;
+  float qreg[kD4];
+  {
+    // Lanes past the tile read row t0 (always in the batch) and drop it, so every load is
+    // unconditional and the loads of a lane can all be in flight together.
+    const int64_t row = t0 + (q_ok ? qi : 0);
+    const float* qrow = a.queries + row * a.q_stride + static_cast<int64_t>(h) * D + c * kD4;
+    float raw[kD4];
+#pragma unroll
+    for (int i = 0; i < kD4; ++i) raw[i] = qrow[i];
+#pragma unroll
+    for (int i = 0; i < kD4; ++i) qreg[i] = q_ok ? raw[i] * a.scale_log2 : 0.f;
+  }
+  floatx4 o[kNb];
+#pragma unroll
+  for (int b = 0; b < kNb; ++b) o[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_ref = -INFINITY;  // the same in the four lanes of a query
+  float l_part = 0.f;       // this lane's share of the query's sum
+  const int lim = min(my_vis, s_end);
+  int wave_lim = lim;  // the wavefront's last key + 1: steps from there on are all masked
+#pragma unroll
+  for (int mask = 32; mask > 0; mask >>= 1) wave_lim = max(wave_lim, __shfl_xor(wave_lim, mask));
+  wave_lim = __builtin_amdgcn_readfirstlane(wave_lim);
+  __syncthreads();  // s_table ready
+
+  // Table entry of key kpos (clamped into the window; callers discard it when kpos is out).
+  auto table_at = [&](int kpos) {
+    const int lb = min(max(block_of<kPow2Block>(kpos, a) - b0, 0), kTableSlots - 1);
+    return s_table[lb];
+  };
+  // Element offsets of this lane's kPer chunks of key tile k0, and the tile's key mask.
+  auto prepare = [&](int k0, int lane_v, int64_t (&off)[kPer]) -> uint32_t {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int chunk = (wave * kPer + u) * kWave + lane_v;
+      const int row = chunk / kCpr;
+      const int col = ((chunk % kCpr) ^ (row & 7)) * 4;
+      const int kpos = k0 + row;
+      const int blk = table_at(kpos);
+      const bool ok = (kpos < s_end) & (static_cast<uint32_t>(blk) < pool_blocks);
+      const uint32_t within = kPow2Block ? (kpos & (a.block_size - 1)) : kpos % a.block_size;
+      const uint32_t blk_u = ok ? static_cast<uint32_t>(blk) : 0u;
+      const uint32_t row_off = ok ? within * row_elems : 0u;
+      off[u] = static_cast<int64_t>(blk_u * block_elems) + static_cast<int64_t>(row_off) + head_off + col;
+    }
+    const int kpos = k0 + lane_v;
+    const bool ok = (lane_v < kKeys) & (kpos < s_end) &
+                    (static_cast<uint32_t>(table_at(kpos)) < pool_blocks);
+    return static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(ok));
+  };
+  auto fire = [&](int buf, const int64_t (&off)[kPer]) {
+    const uint32_t dst = lds_kv + static_cast<uint32_t>(buf * S::kStageFloats * 4 + wave * kPer * 1024);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      load_to_lds16(kcache + off[u], dst + u * 1024);
+      load_to_lds16(vcache + off[u], dst + u * 1024 + S::kTileFloats * 4);
+    }
+  };
+  // One key tile's scores st -> probabilities pr, updating the running reference and sum. A
+  // key counts when it is below the lane's limit and its bit in kmask is set. The rescale is
+  // branch-free (alpha is exactly 1 in lanes that keep their reference), so the step stays
+  // one block of straight-line code the compiler can interleave.
+  auto softmax_step = [&](floatx4 (&st)[kSub], int k0, uint32_t kmask, float (&pr)[kSub][4]) {
+    float sc[kSub][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kk = 16 * j + 4 * c + r;
+        sc[j][r] = (k0 + kk) < lim && ((kmask >> kk) & 1u) ? st[j][r] : -INFINITY;
+        mx = fmaxf(mx, sc[j][r]);
+      }
+    }
+    mx = column_max(mx);
+    // Raise the reference only when a score passes it by more than kLazyLog2 (or it is unset).
+    const bool raise = mx > m_ref + kLazyLog2 || (m_ref == -INFINITY && mx > -INFINITY);
+    const float m_next = raise ? mx : m_ref;
+    const float alpha = raise ? fast_exp2(m_ref - m_next) : 1.f;  // exp2(-inf) = 0
+    l_part *= alpha;
+#pragma unroll
+    for (int b = 0; b < kNb; ++b) o[b] *= alpha;
+    m_ref = m_next;
+    const float shift = m_ref == -INFINITY ? 0.f : m_ref;
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[j][r] = fast_exp2(sc[j][r] - shift);
+        l_part += pr[j][r];
+      }
+    }
+  };
+
+  // The pipeline: step i waits for its own loads (vmcnt), then one barrier publishes every
+  // wavefront's share and also closes step i - 1, whose buffer the loads of step
+  // i + kTileStages - 1 then fill. Those are queued between the step's two products. Every
+  // lane issues the same loads in every step, past the last step too: a lane whose key is past
+  // the end or in a block outside the pool loads row 0 of block 0 (always in the pool)
+  // instead, and the key's bit in the step's mask stays clear.
+  const int nsteps = s_end > s_beg ? (s_end - s_beg + kKeys - 1) / kKeys : 0;
+  uint32_t kmask[kAhead];  // key masks of steps i .. i + kAhead - 1
+  wait_vmcnt<0>();  // the query loads (and earlier stores) complete before the pipeline's loads
+  if (nsteps > 0) {
+#pragma unroll
+    for (int st = 0; st < kAhead; ++st) {
+      int64_t off[kPer];
+      kmask[st] = prepare(s_beg + st * kKeys, lane, off);
+      fire(st, off);
+    }
+  }
+  int buf = 0;
+  for (int i = 0; i < nsteps; ++i) {
+    const int k0 = s_beg + i * kKeys;
+    wait_vmcnt<(kAhead - 1) * 2 * kPer>();  // this step's loads have landed
+    lds_barrier();
+    const int k_next = k0 + kAhead * kKeys;  // the tile whose loads this step queues
+    if (block_of<kPow2Block>(min(k_next + kKeys, s_end) - 1, a) >= b0 + kTableSlots) {
+      // A whole tile moves its table window; no wavefront reads the table between the barrier
+      // above and the one below.
+      b0 = block_of<kPow2Block>(k_next, a);
+      stage_window();
+      lds_barrier();
+    }
+    const bool work = k0 < wave_lim;  // wavefront-uniform
+    // The swizzled LDS addresses are lane constants; they are recomputed from an opaque copy
+    // of the lane index each step (a few VALU operations) instead of being hoisted out of the
+    // loop, which would hold about 20 more VGPRs and cost the CU a row-pass workgroup.
+    int lane_o = lane;
+    asm volatile("" : "+v"(lane_o));
+    const int cl = lane_o >> 4;
+    const int nl = lane_o & 15;
+    const float* sk = s_kv + buf * S::kStageFloats;
+    const float* sv = sk + S::kTileFloats;
+
+    // S^T blocks: register r of st[j] = S[query n][key k0 + 16j + 4c + r]. Lane (c, n) reads
+    // chunk c * kD4 / 4 + q of key row 16 j + n, swizzled by n & 7.
+    floatx4 st[kSub];
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) st[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (work) {
+#pragma unroll
+      for (int q = 0; q < kD4 / 4; ++q) {
+#pragma unroll
+        for (int j = 0; j < kSub; ++j) {
+          const float4 kv = *reinterpret_cast<const float4*>(
+              sk + (16 * j + nl) * D + (((cl * (kD4 / 4) + q) ^ (nl & 7)) << 2));
+          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qreg[4 * q], st[j], 0, 0, 0);
+          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qreg[4 * q + 1], st[j], 0, 0, 0);
+          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qreg[4 * q + 2], st[j], 0, 0, 0);
+          st[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qreg[4 * q + 3], st[j], 0, 0, 0);
+        }
+      }
+    }
+    // Queue step i + kAhead's loads into the buffer step i - 1 used. Their address arithmetic
+    // is scheduled among the PV products below, not the S^T products above (which would keep
+    // more registers live across the S^T loop).
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t next_mask;
+    {
+      int64_t off[kPer];
+      next_mask = prepare(k_next, lane_o, off);
+      fire(buf == 0 ? kAhead : buf - 1, off);
+    }
+    if (work) {
+      float pr[kSub][4];
+      softmax_step(st, k0, kmask[0], pr);
+      // O^T += V^T P^T. Column 16 b + n of row 16 j + 4 c + step is chunk 4 b + n / 4,
+      // swizzled by (4 c + step) & 7: chunk 4 (b ^ (c & 1)) + ((n / 4) ^ step), so each
+      // (j, step) needs one lane base for even b and one for odd b, and b itself is an
+      // immediate offset. The products are accumulated in the register path's order (j, then
+      // step, then b), so both paths round identically.
+#pragma unroll
+      for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+        for (int step = 0; step < 4; ++step) {
+          const int lane_col = 4 * cl * D + 4 * ((nl >> 2) ^ step) + (nl & 3);
+          const float* v_even = sv + lane_col + 16 * (cl & 1);
+          const float* v_odd = sv + lane_col - 16 * (cl & 1);
+          const int row_off = (16 * j + step) * D;
+#pragma unroll
+          for (int b = 0; b < kNb; ++b) {
+            const float x = (b & 1) ? v_odd[row_off + 16 * b] : v_even[row_off + 16 * b];
+            o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, pr[j][step], o[b], 0, 0, 0);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int st2 = 0; st2 + 1 < kAhead; ++st2) kmask[st2] = kmask[st2 + 1];
+    kmask[kAhead - 1] = next_mask;
+    buf = buf == kTileStages - 1 ? 0 : buf + 1;
+  }
+  wait_vmcnt<0>();  // the loads queued past the last step land before the LDS is reused
+
+  // Epilogue: register r of tile b is O[query n][16b + 4c + r].
+  const float l = column_sum(l_part);
+  // A whole tile covered every visible key of its rows: their outputs are final.
+  const int row_parts = whole ? 1 : parts_of(my_vis, a.part_size);
+  if (!q_ok || p >= row_parts) return;
   const int64_t qh = (t0 + qi) * a.num_heads + h;
   if (row_parts == 1) {
     const float sum = l > 0.f ? l : 1.f;
@@ -1070,17 +1216,18 @@ void tile_partial_kernel(const Params a, uint32_t num_items) {
   __shared__ int s_table[kTableSlots];
   __shared__ int s_vis[kTileRows];
   if constexpr (kDma) {
+    static_assert(std::is_same_v<KVT, float>, "the direct-to-LDS tiles are float32");
     __shared__ __align__(16) float s_kv[kTileStages * S::kStageFloats];
     for (uint32_t item = blockIdx.x; item < num_items; item += gridDim.x) {
       __syncthreads();  // the previous item's reads of LDS are done
-      tile_item<KVT, D, kPow2Block, true>(a, item, s_table, s_kv, nullptr, s_vis);
+      tile_item_dma<D, kPow2Block>(a, item, s_table, s_kv, s_vis);
     }
   } else {
     __shared__ float s_k[S::kKeys * S::kRow];
     __shared__ float s_v[S::kKeys * S::kRow];
     for (uint32_t item = blockIdx.x; item < num_items; item += gridDim.x) {
       __syncthreads();  // the previous item's reads of LDS are done
-      tile_item<KVT, D, kPow2Block, false>(a, item, s_table, s_k, s_v, s_vis);
+      tile_item<KVT, D, kPow2Block>(a, item, s_table, s_k, s_v, s_vis);
     }
   }
 }
@@ -1226,7 +1373,7 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     overlap = overlap_for(device);
     if (overlap != nullptr) overlap_lock = std::unique_lock<std::mutex>(overlap->mu);
   }
-  auto launch_rows_hpw = [&](auto hpw_tag) -> int {
+  auto launch_rows_hpw = [&](auto hpw_tag, hipStream_t rs) -> int {
     constexpr int HPW = decltype(hpw_tag)::value;
     const int64_t items = a.rows ? num_rows : num_rows * static_cast<int64_t>(a.max_parts);
     const int64_t groups = items * (a.num_heads / HPW);
@@ -1235,35 +1382,35 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     // The lean and the appending variants exist for power-of-two block sizes only (the others
     // ignore the hint; attention_call appends separately for them).
     if (pow2 && append && stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, false, true>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, false, true>), grid, dim3(kThreads), 0, rs, a);
     } else if (pow2 && append) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, false, true>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, false, true>), grid, dim3(kThreads), 0, rs, a);
     } else if (pow2 && short_rows && stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, true, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, true, false>), grid, dim3(kThreads), 0, rs, a);
     } else if (pow2 && short_rows) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, true, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, true, false>), grid, dim3(kThreads), 0, rs, a);
     } else if (pow2 && stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, false, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, false, false>), grid, dim3(kThreads), 0, rs, a);
     } else if (pow2) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, false, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, false, false>), grid, dim3(kThreads), 0, rs, a);
     } else if (stream_kv) {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, true, false, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, true, false, false>), grid, dim3(kThreads), 0, rs, a);
     } else {
-      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, false, false, false>), grid, dim3(kThreads), 0, stream, a);
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, false, false, false, false>), grid, dim3(kThreads), 0, rs, a);
     }
     return check_launch();
   };
-  auto launch_rows = [&]() -> int {
+  auto launch_rows = [&](hipStream_t rs) -> int {
     if (num_rows == 0) return PKV_OK;
     if constexpr (kPairHeads<KVT, D>) {
-      if (a.num_heads % 2 == 0) return launch_rows_hpw(std::integral_constant<int, 2>{});
+      if (a.num_heads % 2 == 0) return launch_rows_hpw(std::integral_constant<int, 2>{}, rs);
     }
-    return launch_rows_hpw(std::integral_constant<int, 1>{});
+    return launch_rows_hpw(std::integral_constant<int, 1>{}, rs);
   };
   if (PKV_ATTN_ROWS_FIRST || overlap == nullptr) {
     // Without overlap the order does not matter; with it, rows first takes the CUs first.
     if (overlap != nullptr && hipEventRecord(overlap->fork, stream) != hipSuccess) return PKV_EHIP;
-    const int rc = launch_rows();
+    const int rc = launch_rows(stream);
     if (rc != PKV_OK) return rc;
   } else if (hipEventRecord(overlap->fork, stream) != hipSuccess) {
     return PKV_EHIP;
@@ -1281,7 +1428,7 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     }
   }
   if (!PKV_ATTN_ROWS_FIRST && overlap != nullptr) {
-    const int rc = launch_rows();
+    const int rc = launch_rows(stream);
     if (rc != PKV_OK) return rc;
   }
   if (overlap != nullptr) {
