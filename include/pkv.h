@@ -333,6 +333,39 @@ int pkv_plan_batch(const int32_t* query_seq, const int32_t* query_positions, int
                    int64_t merge_capacity, int64_t* counts_out, int32_t* launch_out);
 
 /*
+ * RMSNorm of rows of float32 activations, optionally after the residual add that feeds it.
+ *
+ * Replaces src/paged_kv_serving/engine/model.py:43-46 (rms_norm) as the runner applies it
+ * (model.py:256-264: before the QKV projection, before the SwiGLU block and before the logits),
+ * and the residual adds in front of the second and third (hidden = hidden + ...):
+ *     if delta: hidden[r] = hidden[r] + delta[r]
+ *     out[r] = hidden[r] / sqrt(mean(hidden[r] ** 2) + eps) * weight
+ *
+ *   out    : float32 [num_rows, dim], row r at r * out_stride. May be `hidden` itself.
+ *   hidden : float32 [num_rows, dim], row r at r * hidden_stride; updated in place when delta is
+ *            given.
+ *   delta  : float32 [num_rows, dim] at r * delta_stride, or NULL (no residual add).
+ *   weight : float32 [dim].
+ * Each product, quotient and square root is the correctly rounded float32 operation; the sum of
+ * squares is accumulated in float32 in a different order than NumPy's pairwise sum.
+ */
+int pkv_rms_norm(float* out, int64_t out_stride, float* hidden, int64_t hidden_stride,
+                 const float* delta, int64_t delta_stride, const float* weight, int64_t num_rows,
+                 int32_t dim, float eps, int device, void* stream);
+
+/*
+ * The SwiGLU gate product: out[r, j] = silu(gate[r, j]) * up[r, j] with
+ * silu(x) = x * (1 / (1 + exp(-clip(x, -60, 60)))).
+ *
+ * Replaces src/paged_kv_serving/engine/model.py:49-51 (silu) and the product at model.py:256-259
+ * (silu(normed @ gate_proj) * (normed @ up_proj)). gate and up are float32 [num_rows, width]
+ * with row r at r * in_stride (for one [num_rows, 2 * width] product of [gate | up] weights: up =
+ * gate + width, in_stride = 2 * width); out is float32 [num_rows, width] at r * out_stride.
+ */
+int pkv_silu_mul(float* out, int64_t out_stride, const float* gate, const float* up,
+                 int64_t in_stride, int64_t num_rows, int32_t width, int device, void* stream);
+
+/*
  * Greedy sampling: the argmax of each logits row, on the device.
  *
  * Replaces src/paged_kv_serving/engine/sampling.py:28-30 (greedy_token: int(np.argmax(logits)))

@@ -38,7 +38,7 @@ INCLUDE = REPO_ROOT / "include"
 LIB_PATH = PACKAGE_DIR / "libpkv.so"
 SOURCES = (
     CSRC / "pkv_copy.hip", CSRC / "pkv_rope.hip", CSRC / "pkv_attention.hip", CSRC / "pkv_sample.hip",
-    CSRC / "pkv_plan.hip",
+    CSRC / "pkv_plan.hip", CSRC / "pkv_model.hip",
 )
 
 # gfx950 only. Packed-FP32 VALU instructions are disabled: the code relies on scalar fp32 FMA.
@@ -86,6 +86,8 @@ EXPORTED_SYMBOLS = (
     "pkv_paged_attention_noalloc",
     "pkv_greedy_tokens",
     "pkv_plan_batch",
+    "pkv_rms_norm",
+    "pkv_silu_mul",
 )
 
 
@@ -287,6 +289,15 @@ def _declare(lib: ctypes.CDLL) -> None:
         _ptr, _ptr,  # counts_out, launch_out
     ]
     lib.pkv_plan_batch.restype = _c_int
+    lib.pkv_rms_norm.argtypes = [
+        _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr,  # out, stride, hidden, stride, delta, stride, weight
+        _i64, _i32, ctypes.c_float, _c_int, _ptr,  # rows, dim, eps, device, stream
+    ]
+    lib.pkv_rms_norm.restype = _c_int
+    lib.pkv_silu_mul.argtypes = [
+        _ptr, _i64, _ptr, _ptr, _i64, _i64, _i32, _c_int, _ptr,  # out, stride, gate, up, in stride, rows, width, device, stream
+    ]
+    lib.pkv_silu_mul.restype = _c_int
 
 
 def library() -> ctypes.CDLL:

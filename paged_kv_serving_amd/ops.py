@@ -36,7 +36,9 @@ __all__ = [
     "plan_rows",
     "tiles_supported",
     "upload_batch_plan",
+    "rms_norm",
     "rope_append",
+    "silu_mul",
     "upload_plan",
 ]
 
@@ -186,6 +188,67 @@ def rope_append(
         device, _stream(device),
     )  # fmt: skip
     _native.check(rc, "pkv_rope_append")
+    return out
+
+
+def _rows_2d(tensor: torch.Tensor, name: str, width: int) -> int:
+    """Row stride (elements) of a float32 ``[rows, >= width]`` tensor with contiguous rows."""
+    if tensor.dim() != 2 or tensor.dtype != torch.float32 or tensor.shape[1] < width:
+        raise ValueError(f"{name} must be float32 [rows, {width}]")
+    if tensor.stride(1) != 1:
+        raise ValueError(f"{name} rows must be contiguous")
+    return tensor.stride(0) if tensor.shape[0] > 1 else tensor.shape[1]
+
+
+def rms_norm(
+    hidden: torch.Tensor, weight: torch.Tensor, eps: float, *, delta: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:  # fmt: skip
+    """``hidden / sqrt(mean(hidden ** 2) + eps) * weight`` over the last axis of float32
+    ``hidden [rows, dim]`` (reference model.py:43-46). With ``delta``, ``hidden += delta`` first,
+    in place (the residual add before the norm, model.py:256-264). ``out`` may be ``hidden``."""
+    device = _device_index(hidden, weight)
+    rows, dim = hidden.shape if hidden.dim() == 2 else (-1, -1)
+    h_stride = _rows_2d(hidden, "hidden", dim)
+    if weight.shape != (dim,) or weight.dtype != torch.float32 or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous float32 [dim] tensor")
+    d_stride = 0
+    if delta is not None:
+        if delta.shape != hidden.shape or delta.device != hidden.device:
+            raise ValueError("delta must match hidden")
+        d_stride = _rows_2d(delta, "delta", dim)
+    if out is None:
+        out = torch.empty((rows, dim), dtype=torch.float32, device=hidden.device)
+    elif out.shape != hidden.shape or out.device != hidden.device:
+        raise ValueError("out must match hidden")
+    o_stride = _rows_2d(out, "out", dim)
+    rc = _native.library().pkv_rms_norm(
+        out.data_ptr(), o_stride, hidden.data_ptr(), h_stride, None if delta is None else delta.data_ptr(),
+        d_stride, weight.data_ptr(), rows, dim, float(eps), device, _stream(device),
+    )  # fmt: skip
+    _native.check(rc, "pkv_rms_norm")
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, width: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(gate) * up`` for float32 ``gate_up [rows, 2 * width]`` holding ``[gate | up]`` (one
+    product with the concatenated weights), as float32 ``[rows, width]`` (reference
+    model.py:49-51 and 256-259)."""
+    device = _device_index(gate_up)
+    if width < 1 or gate_up.dim() != 2 or gate_up.shape[1] != 2 * width:
+        raise ValueError("gate_up must be [rows, 2 * width]")
+    stride = _rows_2d(gate_up, "gate_up", 2 * width)
+    rows = gate_up.shape[0]
+    if out is None:
+        out = torch.empty((rows, width), dtype=torch.float32, device=gate_up.device)
+    elif out.shape != (rows, width) or out.device != gate_up.device:
+        raise ValueError("out must be [rows, width] on gate_up's device")
+    o_stride = _rows_2d(out, "out", width)
+    rc = _native.library().pkv_silu_mul(
+        out.data_ptr(), o_stride, gate_up.data_ptr(), gate_up.data_ptr() + 4 * width, stride, rows, width,
+        device, _stream(device),
+    )  # fmt: skip
+    _native.check(rc, "pkv_silu_mul")
     return out
 
 

@@ -154,14 +154,6 @@ def shared_prefix_order(entries, block_size: int) -> list[int] | None:
     return grouped + rest
 
 
-def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    return x / torch.sqrt(torch.mean(x * x, dim=-1, keepdim=True) + eps) * weight
-
-
-def _silu(x: torch.Tensor) -> torch.Tensor:
-    return x * (1.0 / (1.0 + torch.exp(-torch.clamp(x, -60.0, 60.0))))
-
-
 class _Staging:
     """One call's integer metadata, sent in one asynchronous copy from pinned host memory.
 
@@ -212,8 +204,9 @@ class _Staging:
         return offsets
 
     def tensor(self, offset: int, count: int, dtype: torch.dtype) -> torch.Tensor:
-        """A device tensor view of ``count`` elements of ``dtype`` at byte ``offset``."""
-        size = torch.tensor([], dtype=dtype).element_size()
+        """A device tensor view of ``count`` elements of ``dtype`` (int32 or int64) at byte
+        ``offset``."""
+        size = 8 if dtype == torch.int64 else 4
         return self.dev[offset : offset + count * size].view(dtype)
 
 
@@ -260,7 +253,9 @@ class _Step:
 
 
 class _DeviceWeights:
-    """Device copies of a model's weights and rotary tables, tied to one weights object."""
+    """Device copies of a model's weights and rotary tables, tied to one weights object. Each
+    layer's gate and up projections are stored side by side as one ``[d_model, 2 * d_ff]`` matrix,
+    so the SwiGLU block runs one product for both."""
 
     def __init__(self, model, device: torch.device) -> None:
         def up(array: np.ndarray) -> torch.Tensor:
@@ -271,12 +266,9 @@ class _DeviceWeights:
         self.embedding = up(weights.token_embedding)
         self.final_norm = up(weights.final_norm)
         self.layers = [
-            tuple(
-                up(getattr(layer, name))
-                for name in (
-                    "attn_norm", "qkv_proj", "out_proj", "ffn_norm",
-                    "gate_proj", "up_proj", "down_proj",
-                )  # fmt: skip
+            (
+                up(layer.attn_norm), up(layer.qkv_proj), up(layer.out_proj), up(layer.ffn_norm),
+                up(np.concatenate([layer.gate_proj, layer.up_proj], axis=1)), up(layer.down_proj),
             )
             for layer in weights.layers
         ]
@@ -675,13 +667,16 @@ class ModelRunner:
         config = self.model.config
         total = step.total
         w = self._device_weights()
-        heads, dim, d_model = config.n_heads, config.head_dim, config.d_model
+        heads, dim, d_model, ff = config.n_heads, config.head_dim, config.d_model, config.d_ff
         eps = config.norm_eps
         hidden = w.embedding[step.tensor("tokens")]
         rope_positions, slots = step.tensor("rope_positions"), step.tensor("slots")
         attended = torch.empty((total, heads, dim), dtype=torch.float32, device=self.device)
-        for index, (attn_norm, qkv, out_proj, ffn_norm, gate, up, down) in enumerate(w.layers):
-            fused = (_rms_norm(hidden, attn_norm, eps) @ qkv).view(total, 3, heads, dim)
+        # normed holds the RMSNorm of the running hidden state with the next norm's weights;
+        # each residual add is fused into the norm that follows it (model.py:256-264).
+        normed = ops.rms_norm(hidden, w.layers[0][0] if w.layers else w.final_norm, eps)
+        for index, (_, qkv, out_proj, ffn_norm, gate_up, down) in enumerate(w.layers):
+            fused = (normed @ qkv).view(total, 3, heads, dim)
             # RoPE on q (in place) and k, and the append of k and v, in one kernel
             # (reference model.py:251-252 then runner.py:195-196).
             queries = ops.rope_append(
@@ -689,11 +684,12 @@ class ModelRunner:
                 rope_positions, w.cos, w.sin, slots, out=fused[:, 0],
             )  # fmt: skip
             self._attention(step, index, queries, attended)
-            hidden = hidden + attended.view(total, d_model) @ out_proj
-            normed = _rms_norm(hidden, ffn_norm, eps)
-            hidden = hidden + (_silu(normed @ gate) * (normed @ up)) @ down
+            ops.rms_norm(hidden, ffn_norm, eps, delta=attended.view(total, d_model) @ out_proj, out=normed)
+            gated = ops.silu_mul(normed @ gate_up, ff)
+            following = w.layers[index + 1][0] if index + 1 < len(w.layers) else w.final_norm
+            ops.rms_norm(hidden, following, eps, delta=gated @ down, out=normed)
 
         if not step.num_wanted:
             return [], None
         names = [e.seq_id for e in step.entries if e.logits_index is not None]  # batch order
-        return names, _rms_norm(hidden[step.tensor("logits_rows")], w.final_norm, eps) @ w.embedding.T
+        return names, normed[step.tensor("logits_rows")] @ w.embedding.T

@@ -169,3 +169,19 @@ def test_init_is_idempotent_on_a_device(device) -> None:
     lib = _native.library()
     assert lib.pkv_init(device.index) == 0
     assert lib.pkv_init(device.index) == 0
+
+
+def test_model_ops_refuse_bad_arguments_before_any_launch(lib) -> None:
+    """pkv_rms_norm / pkv_silu_mul validate sizes, strides and eps on the host (no HIP call)."""
+    einval = _native.PKV_EINVAL
+    one = ctypes.c_void_p(16)  # never dereferenced: every call below fails its checks first
+    assert lib.pkv_rms_norm(one, 4, one, 4, None, 0, one, 1, 0, 1e-5, 0, None) == einval  # dim 0
+    assert lib.pkv_rms_norm(one, 3, one, 4, None, 0, one, 1, 4, 1e-5, 0, None) == einval  # out stride
+    assert lib.pkv_rms_norm(one, 4, one, 4, one, 2, one, 1, 4, 1e-5, 0, None) == einval  # delta stride
+    assert lib.pkv_rms_norm(one, 4, one, 4, None, 0, one, 1, 4, -1.0, 0, None) == einval  # eps < 0
+    assert lib.pkv_rms_norm(None, 4, one, 4, None, 0, one, 1, 4, 1e-5, 0, None) == einval  # null out
+    assert lib.pkv_rms_norm(None, 4, None, 4, None, 0, None, 0, 4, 1e-5, 0, None) == _native.PKV_OK  # no rows
+    assert lib.pkv_silu_mul(one, 4, one, one, 8, 1, 0, 0, None) == einval  # width 0
+    assert lib.pkv_silu_mul(one, 4, one, one, 3, 1, 4, 0, None) == einval  # input stride
+    assert lib.pkv_silu_mul(None, 4, one, one, 8, 1, 4, 0, None) == einval  # null out
+    assert lib.pkv_silu_mul(None, 4, None, None, 8, 0, 4, 0, None) == _native.PKV_OK  # no rows
