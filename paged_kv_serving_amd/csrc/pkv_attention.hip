@@ -735,6 +735,10 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   __syncthreads();  // s_table ready
 
   const int lim = min(my_vis, kend);
+  int wave_lim = lim;  // the wavefront's last key + 1: key tiles from there on are all masked
+#pragma unroll
+  for (int mask = 32; mask > 0; mask >>= 1) wave_lim = max(wave_lim, __shfl_xor(wave_lim, mask));
+  wave_lim = __builtin_amdgcn_readfirstlane(wave_lim);
 
   // One key tile's scores st -> probabilities pr, updating the running reference and sum. A key
   // counts when it is below the lane's limit and its bit in kmask is set.
@@ -846,6 +850,12 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
     }
     __syncthreads();
     if (k0 + kKeys < kend) prefetch(k0 + kKeys);
+    // A wavefront whose rows all end before this key tile skips its products: every score would
+    // be masked and every probability 0, so nothing it holds would change.
+    if (k0 >= wave_lim) {
+      __syncthreads();
+      continue;
+    }
 
     // S^T blocks: register r of st[j] = S[query n][key k0 + 16j + 4c + r].
     floatx4 st[kSub];
