@@ -482,3 +482,30 @@ def test_attend_appends_and_attends_like_the_reference_runner(device, seed, shar
         worst = max(worst, float(np.max(np.abs(out[offset : offset + n] - want))))
         offset += n
     assert worst < 1e-5
+
+
+@pytest.mark.parametrize("flush", ["block_view", "execute"])
+def test_queued_copies_with_dependencies_land_in_order(device, models, flush) -> None:
+    """Copies queued by copy_block run as batched launches of independent groups: a chain
+    (1 -> 2, 2 -> 3), a swap back (4 -> 5, 5 -> 4) and a copy over a block read earlier in the
+    same group (6 -> 7, 0 -> 6) must leave the pool exactly as copying one block at a time in
+    queue order (runner.py:128-133). Flushed by block_view, or by the next execute, which sends
+    the pairs in its metadata copy and launches one copy per group before its kernels."""
+    model, _ = models
+    runner = ModelRunner(model, num_blocks=12, block_size=BLOCK_SIZE, device=device)
+    keys, values = runner.key_cache, runner.value_cache  # [layers, blocks, B, H, D]
+    keys.copy_(torch.randn(keys.shape, device=device))
+    values.copy_(torch.randn(values.shape, device=device))
+    want_k, want_v = keys.cpu().numpy().copy(), values.cpu().numpy().copy()
+    pairs = [(1, 2), (2, 3), (4, 5), (5, 4), (6, 7), (0, 6), (9, 10)]
+    for src, dst in pairs:
+        runner.copy_block(src, dst)
+        want_k[:, dst] = want_k[:, src]
+        want_v[:, dst] = want_v[:, src]
+    if flush == "block_view":
+        runner.block_view(0)
+    else:  # a batch writing only block 11, so the copied blocks keep their bytes
+        runner.execute(ExecutionBatch((BatchEntry("x", (1,), (0,), (11,), 0),)))
+        want_k[:, 11], want_v[:, 11] = keys[:, 11].cpu().numpy(), values[:, 11].cpu().numpy()
+    assert np.array_equal(keys.cpu().numpy(), want_k)
+    assert np.array_equal(values.cpu().numpy(), want_v)
