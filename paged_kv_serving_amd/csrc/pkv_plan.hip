@@ -7,8 +7,10 @@
 //   1. Runs of >= min_tile_rows consecutive rows of one sequence become tiles of <= 64 rows
 //      (head_dim 32, 64, 128 or 256); every other row goes to the row pass.
 //   2. With >= 1024 (tile, head) pairs, tiles are whole (one workgroup per tile and head over
-//      every visible key), grouped by chunk, longest chunk first, each chunk's tiles rotated by
-//      the chunk's rank so one head's tiles of a chunk share an XCD's L2.
+//      every visible key), grouped by chunk, longest chunk first; a chunk's tiles run from its
+//      last row's to its first row's in even-ranked chunks and the other way in odd-ranked
+//      ones, so the persistent workgroups that share a head alternate long and short tiles and
+//      reach every second chunk together (sharing its keys through their XCD's L2).
 //   3. >= 16 consecutive row-pass rows whose tables agree over >= 512 leading tokens form a
 //      shared-prefix group; its whole partitions become 64-row tiles read through the first
 //      row's table (a tile never starts at a member whose table ends inside the prefix), and
@@ -112,9 +114,9 @@ void make_whole(std::vector<Tile>& tiles, const int32_t* seq, const std::vector<
     const int64_t c = order[rank];
     const int64_t begin = starts[c];
     const int64_t size = (c + 1 < chunks ? starts[c + 1] : n) - begin;
-    const int64_t shift = rank % size;
+    const bool reverse = rank % 2 == 0;  // even ranks last row first, odd ranks first row first
     for (int64_t i = 0; i < size; ++i) {
-      Tile t = tiles[begin + (i + shift) % size];
+      Tile t = tiles[begin + (reverse ? size - 1 - i : i)];
       t.begin = 0;
       t.end = PKV_TILE_WHOLE;
       whole.push_back(t);

@@ -231,14 +231,16 @@ def test_prefill_tiles_become_whole_when_they_fill_the_gpu() -> None:
     plan = ops.plan_batch(seq, 128, 32, tables, contexts, 16, query_positions=positions)
     assert plan.tiles.shape == (64, 4) and 64 * 32 >= ops.WHOLE_TILE_GROUPS
     assert np.all(plan.tiles[:, 2] == 0) and np.all(plan.tiles[:, 3] == ops.TILE_WHOLE)
-    # chunk by chunk, longest chunk first, each chunk's 8 tiles rotated by the chunk's rank
+    # chunk by chunk, longest chunk first; an even-ranked chunk's 8 tiles from its last rows to
+    # its first, an odd-ranked chunk's from its first rows to its last
     chunks = [int(seq[f]) for f in plan.tiles[:, 0].tolist()]
     assert [chunks[8 * r] for r in range(8)] == np.argsort(-contexts[:8], kind="stable").tolist()
     for r in range(8):
         firsts = plan.tiles[8 * r : 8 * r + 8, 0].tolist()
         assert len({int(seq[f]) for f in firsts}) == 1
         base = 512 * chunks[8 * r]
-        assert firsts == [base + 64 * ((i + r) % 8) for i in range(8)]
+        rows_order = [base + 64 * i for i in range(8)]
+        assert firsts == (rows_order[::-1] if r % 2 == 0 else rows_order)
     _covered(plan, seq, contexts, 16)
     # only decode rows are merged, and only those spanning more than one partition
     visible = np.minimum(contexts[seq], positions + 1)
