@@ -792,8 +792,8 @@ class NativePlanner:
             self._tiles = np.zeros((max(tiles, 2 * self._tiles.shape[0]), 4), np.int32)
             self._merge = np.zeros(max(merge, 2 * self._merge.size), np.int32)
         _native.check(rc, "pkv_plan_batch")
-        rows, tiles, merge = (int(c) for c in self._counts)
-        partition, flags = (int(v) for v in self._launch)
+        rows, tiles, merge = self._counts.tolist()
+        partition, flags = self._launch.tolist()
         return self._rows[:rows], self._tiles[:tiles], self._merge[:merge], partition, flags
 
     def plan(

@@ -456,8 +456,10 @@ class ModelRunner:
                 break
             n = max(-total, 2 * tokens.size)
             self._per_token = (np.zeros(n, np.int64), np.zeros(n, np.int64), np.zeros(n, np.int64))
-        return (tokens[:total].copy(), positions[:total].copy(), slots[:total].copy(), lengths[:count].copy(),
-                contexts[:count].copy(), logits[:count].copy(), (problem, entry, position))  # fmt: skip
+        # Views of the reused buffers: they are consumed (copied into the staging buffer, or
+        # reindexed) before the next call rewrites them.
+        return (tokens[:total], positions[:total], slots[:total], lengths[:count], contexts[:count],
+                logits[:count], (problem, entry, position))  # fmt: skip
 
     def _prepare(self, batch: ExecutionBatch) -> _Step | None:
         """Everything one iteration needs on the device before its first kernel: validation in
