@@ -278,7 +278,12 @@ class _DeviceWeights:
 
 
 class ModelRunner:
-    """Owns the K/V pools on one HIP device and executes ragged batches against them."""
+    """Owns the K/V pools on one HIP device and executes ragged batches against them.
+
+    Work is enqueued on the caller's current stream of the runner's device. Consecutive calls
+    reuse one device metadata buffer and one split-context workspace, so a runner's calls must be
+    ordered on the device (one stream, as the reference engine's serialised steps are); calls of
+    one runner overlapping on two streams would race on those buffers."""
 
     def __init__(
         self,
