@@ -441,20 +441,29 @@ def config3(args) -> dict:
 
 
 def prefill_tiles_alone_ms(args, batch) -> float:
-    """Mean HIP-event time of the batch's prefill chunks as their own attention call: the plan's
-    whole tiles with no row-pass items, so the tile pass runs one workgroup per (tile, head) and
-    nothing beside it (the decode rows' outputs are left unwritten). This is the MFMA-bound part
-    of config 3 measured alone."""
+    """Mean HIP-event time of the batch's prefill chunks as their own attention call: the
+    chunks' rows (the batch's first rows) planned without the decode rows, so the plan holds
+    whole tiles only and the tile pass runs one workgroup per (tile, head) with nothing beside
+    it (the decode rows' outputs are left unwritten). This is the MFMA-bound part of config 3
+    measured alone."""
     import torch
 
     from paged_kv_serving_amd import ops
 
     device = batch.queries.device
     heads, dim = batch.key_cache.shape[2], batch.key_cache.shape[3]
-    host = ops.plan_batch(
-        batch.host_seq, dim, heads, batch.host_tables, batch.host_context, batch.key_cache.shape[1],
+    block = batch.key_cache.shape[1]
+    mixed = ops.plan_batch(
+        batch.host_seq, dim, heads, batch.host_tables, batch.host_context, block,
         partition_size=args.partition, query_positions=batch.host_positions,
     )  # fmt: skip
+    chunk_rows = int((mixed.tiles[:, 0] + mixed.tiles[:, 1]).max())
+    host = ops.plan_batch(
+        batch.host_seq[:chunk_rows], dim, heads, batch.host_tables, batch.host_context, block,
+        partition_size=args.partition, query_positions=batch.host_positions[:chunk_rows],
+    )  # fmt: skip
+    if host.rows.shape[0] != 0 or int(host.tiles[:, 1].sum()) != chunk_rows:
+        raise RuntimeError("the prefill chunks are not the batch's first rows")
     plan = ops.upload_plan(np.zeros((0, 2), np.int32), host.tiles, device,
                            partition_size=host.partition_size, merge=np.zeros(0, np.int32))  # fmt: skip
     need = ops.attention_workspace_bytes(batch.num_queries, heads, dim, batch.max_context_len,

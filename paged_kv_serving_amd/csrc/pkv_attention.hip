@@ -94,6 +94,12 @@ namespace {
 #ifndef PKV_TILE_STAGES
 #define PKV_TILE_STAGES 3
 #endif
+// Register path at head_dim 128: the occupancy target in waves per SIMD (its VGPR budget).
+// Measured on config 3's tiles alone: 3 waves (168 VGPRs) 0.68-0.70 ms, 2 waves (190 VGPRs,
+// value reads double-buffered) 0.73 ms.
+#ifndef PKV_TILE_REG_WAVES
+#define PKV_TILE_REG_WAVES 3
+#endif
 
 constexpr int kWaves = PKV_ATTN_WAVES;  // wavefronts per row_partial workgroup
 constexpr int kThreads = kWaves * kWave;
@@ -563,10 +569,12 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
 //                + s] (from registers). Register r of block j holds S[query n][key 16j + 4c + r].
 //                The kSub chains are independent and interleaved.
 //   O^T = V^T P^T  four steps per 16-key block; in step m the k index of lane group c stands for
-//                key 16j + 4c + m, so lane (c, n) supplies A = V[key 16j + 4c + m][16b + n] for
-//                output tile b (from LDS) and B = P[query n][key 16j + 4c + m], its own register
-//                m. Register r of output tile b holds O[query n][16b + 4c + r]: every lane owns
-//                four dimensions of its own query's output row, so rescaling a row needs only the
+//                key 16j + 4c + m. Output tile b = kW g + e (kW = 4, or 2 at head_dim 32) covers
+//                dims 16 kW g + kW i + e, i = 0..15, so lane (c, n) supplies A = V[key 16j + 4c +
+//                m][16 kW g + kW n + e] for the kW tiles of group g from one LDS read of kW
+//                adjacent floats, and B = P[query n][key 16j + 4c + m], its own register m.
+//                Register r of tile b holds O[query n][16 kW g + kW (4c + r) + e]: every lane owns
+//                dimensions of its own query's output row only, so rescaling a row needs only the
 //                lane's own factor.
 //
 // Online softmax with a lazy reference: probabilities are exp2(s - m_ref), where m_ref is a
@@ -632,10 +640,16 @@ struct TileShape {
   static constexpr int kRow = D + 4;                 // padded LDS row (floats): conflict-free reads
   static constexpr int kD4 = D / 4;
   static constexpr int kNb = D / 16;
+  // Output dims of the O^T products: MFMA row i of output tile b = kW g + e holds dimension
+  // 16 kW g + kW i + e. Lane n's A operands of the kW tiles of group g are then kW adjacent
+  // floats of a value row (one LDS vector read feeds kW products), and registers r of those
+  // tiles in lane (c, n) are the kW adjacent output dims 16 kW g + kW (4 c + r) + [0, kW).
+  static constexpr int kW = kNb >= 4 ? 4 : kNb;
+  static constexpr int kGroups = kNb / kW;
   // Direct-to-LDS stages: unpadded rows of D floats whose 16-byte chunks are XOR-swizzled by
   // (row & 7): chunk q of key row r sits at chunk q ^ (r & 7). The S^T reads (16 rows, one
-  // chunk each) and the PV reads (4 rows x 16 columns) then spread over all LDS banks, as the
-  // padded rows do, while every 16-byte chunk stays whole for the DMA.
+  // chunk each) and the PV reads (4 rows, 16 adjacent chunks each) then spread over all LDS
+  // banks, as the padded rows do, while every 16-byte chunk stays whole for the DMA.
   static constexpr int kChunks = kKeys * D / 4;            // 16-byte chunks of one K (or V) tile
   static constexpr int kTileFloats = kKeys * D;
   static constexpr int kStageFloats = 2 * kTileFloats;     // K tile then V tile
@@ -645,6 +659,28 @@ struct TileShape {
 template <int D>
 __device__ __forceinline__ int swz(int row, int col) {
   return row * D + ((((col >> 2) ^ (row & 7))) << 2) + (col & 3);
+}
+
+// kW adjacent floats, the unit of one value-operand read and one output store of the tile pass.
+template <int W>
+using floatw = float __attribute__((ext_vector_type(W)));
+
+// One query row of the tile pass's O^T products, divided by `sum` (1 for the unnormalised
+// workspace rows), stored at `dst` (the row's dimension 0) when output tile W g + e holds dims
+// 16 W g + W i + e: lane (c, n) writes the W adjacent dims of each (group, register) pair.
+template <int D, int W>
+__device__ __forceinline__ void store_out_row(float* dst, const floatx4 (&o)[D / 16], int c, float sum) {
+  constexpr int kGroups = D / 16 / W;
+#pragma unroll
+  for (int g = 0; g < kGroups; ++g) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      floatw<W> x;
+#pragma unroll
+      for (int e = 0; e < W; ++e) x[e] = o[W * g + e][r] / sum;
+      *reinterpret_cast<floatw<W>*>(dst + 16 * W * g + W * (4 * c + r)) = x;
+    }
+  }
 }
 
 // One work item of the tile pass staged through registers: item `bid` = (partition, tile, head),
@@ -872,22 +908,28 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
     float pr[kSub][4];
     softmax_step(st, k0, kmask, pr);
 
-    // O^T += V^T P^T.
+    // O^T += V^T P^T: lane (c, n) reads the kW adjacent floats of group g of value row
+    // 16 j + 4 c + step in one LDS read.
 #pragma unroll
     for (int j = 0; j < kSub; ++j) {
 #pragma unroll
       for (int step = 0; step < 4; ++step) {
-        const float* vrow = &s_v[(16 * j + 4 * c + step) * kRow + n];
+        const float* vrow = &s_v[(16 * j + 4 * c + step) * kRow + S::kW * n];
 #pragma unroll
-        for (int b = 0; b < kNb; ++b) {
-          o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * b], pr[j][step], o[b], 0, 0, 0);
+        for (int g = 0; g < S::kGroups; ++g) {
+          const floatw<S::kW> x = *reinterpret_cast<const floatw<S::kW>*>(vrow + 16 * S::kW * g);
+#pragma unroll
+          for (int e = 0; e < S::kW; ++e) {
+            const int b = S::kW * g + e;
+            o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], pr[j][step], o[b], 0, 0, 0);
+          }
         }
       }
     }
     __syncthreads();
   }
 
-  // Epilogue: register r of tile b is O[query n][16b + 4c + r].
+  // Epilogue: register r of tile kW g + e is O[query n][16 kW g + kW (4c + r) + e].
   const float l = column_sum(l_part);
   if (!q_ok) return;
   // A whole tile covered every visible key of its rows: their outputs are final.
@@ -895,20 +937,10 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   if (p >= row_parts) return;
   const int64_t qh = (t0 + qi) * a.num_heads + h;
   if (row_parts == 1) {
-    const float sum = l > 0.f ? l : 1.f;
-    float* dst = a.out + qh * D + 4 * c;
-#pragma unroll
-    for (int b = 0; b < kNb; ++b) {
-      *reinterpret_cast<float4*>(dst + 16 * b) =
-          make_float4(o[b][0] / sum, o[b][1] / sum, o[b][2] / sum, o[b][3] / sum);
-    }
+    store_out_row<D, S::kW>(a.out + qh * D, o, c, l > 0.f ? l : 1.f);
   } else {
     const int64_t slot = qh * a.max_parts + p;
-    float* dst = a.ws_acc + slot * D + 4 * c;
-#pragma unroll
-    for (int b = 0; b < kNb; ++b) {
-      *reinterpret_cast<float4*>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
-    }
+    store_out_row<D, S::kW>(a.ws_acc + slot * D, o, c, 1.f);
     if (c == 0) {
       a.ws_ml[2 * slot] = m_ref;
       a.ws_ml[2 * slot + 1] = l;
@@ -935,6 +967,7 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
   static_assert(kPer >= 1 && S::kChunks % kTileThreads == 0, "whole wavefront DMA loads per tile");
   constexpr int kCpr = D / 4;  // 16-byte chunks per key row
   constexpr int kAhead = kTileStages - 1;
+  constexpr int kVw = S::kW;  // output tile kVw g + e holds dims 16 kVw g + kVw i + e
 
   const int h = static_cast<int>(bid % static_cast<uint32_t>(a.num_heads));
   const uint32_t rest = bid / static_cast<uint32_t>(a.num_heads);
@@ -1156,23 +1189,27 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
     if (work) {
       float pr[kSub][4];
       softmax_step(st, k0, kmask[0], pr);
-      // O^T += V^T P^T. Column 16 b + n of row 16 j + 4 c + step is chunk 4 b + n / 4,
-      // swizzled by (4 c + step) & 7: chunk 4 (b ^ (c & 1)) + ((n / 4) ^ step), so each
-      // (j, step) needs one lane base for even b and one for odd b, and b itself is an
-      // immediate offset. The products are accumulated in the register path's order (j, then
-      // step, then b), so both paths round identically.
+      // O^T += V^T P^T. Lane (c, n) reads the kVw adjacent floats at column 16 kVw g + kVw n
+      // of row 16 j + 4 c + step: part of chunk 4 g + n (kVw = 4: the whole chunk) or
+      // g + n / 2 (kVw = 2), swizzled by (4 c + step) & 7, so each step needs one lane base and
+      // j and g are immediate offsets. The products are accumulated in the register path's
+      // order (j, then step, then output tile), so both paths round identically.
 #pragma unroll
       for (int j = 0; j < kSub; ++j) {
 #pragma unroll
         for (int step = 0; step < 4; ++step) {
-          const int lane_col = 4 * cl * D + 4 * ((nl >> 2) ^ step) + (nl & 3);
-          const float* v_even = sv + lane_col + 16 * (cl & 1);
-          const float* v_odd = sv + lane_col - 16 * (cl & 1);
-          const int row_off = (16 * j + step) * D;
+          const int swz_row = 4 * (cl & 1) + step;  // (16 j + 4 c + step) & 7
+          const int col = kVw * nl;
+          const float* vbase = sv + 4 * cl * D + ((((col >> 2) ^ swz_row)) << 2) + (col & 3);
 #pragma unroll
-          for (int b = 0; b < kNb; ++b) {
-            const float x = (b & 1) ? v_odd[row_off + 16 * b] : v_even[row_off + 16 * b];
-            o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x, pr[j][step], o[b], 0, 0, 0);
+          for (int g = 0; g < kNb / kVw; ++g) {
+            const floatw<kVw> x =
+                *reinterpret_cast<const floatw<kVw>*>(vbase + (16 * j + step) * D + 16 * kVw * g);
+#pragma unroll
+            for (int e = 0; e < kVw; ++e) {
+              const int b = kVw * g + e;
+              o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], pr[j][step], o[b], 0, 0, 0);
+            }
           }
         }
       }
@@ -1184,27 +1221,17 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
   }
   wait_vmcnt<0>();  // the loads queued past the last step land before the LDS is reused
 
-  // Epilogue: register r of tile b is O[query n][16b + 4c + r].
+  // Epilogue: register r of tile kVw g + e is O[query n][16 kVw g + kVw (4c + r) + e].
   const float l = column_sum(l_part);
   // A whole tile covered every visible key of its rows: their outputs are final.
   const int row_parts = whole ? 1 : parts_of(my_vis, a.part_size);
   if (!q_ok || p >= row_parts) return;
   const int64_t qh = (t0 + qi) * a.num_heads + h;
   if (row_parts == 1) {
-    const float sum = l > 0.f ? l : 1.f;
-    float* dst = a.out + qh * D + 4 * c;
-#pragma unroll
-    for (int b = 0; b < kNb; ++b) {
-      *reinterpret_cast<float4*>(dst + 16 * b) =
-          make_float4(o[b][0] / sum, o[b][1] / sum, o[b][2] / sum, o[b][3] / sum);
-    }
+    store_out_row<D, kVw>(a.out + qh * D, o, c, l > 0.f ? l : 1.f);
   } else {
     const int64_t slot = qh * a.max_parts + p;
-    float* dst = a.ws_acc + slot * D + 4 * c;
-#pragma unroll
-    for (int b = 0; b < kNb; ++b) {
-      *reinterpret_cast<float4*>(dst + 16 * b) = make_float4(o[b][0], o[b][1], o[b][2], o[b][3]);
-    }
+    store_out_row<D, kVw>(a.ws_acc + slot * D, o, c, 1.f);
     if (c == 0) {
       a.ws_ml[2 * slot] = m_ref;
       a.ws_ml[2 * slot + 1] = l;
@@ -1220,7 +1247,7 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
 // which allows two); the other instantiations have no occupancy target.
 template <typename KVT, int D, bool kPow2Block, bool kDma>
 __global__ __launch_bounds__(kTileThreads)
-__attribute__((amdgpu_waves_per_eu(!kDma && D == 128 ? 3 : 1)))
+__attribute__((amdgpu_waves_per_eu(!kDma && D == 128 ? PKV_TILE_REG_WAVES : 1)))
 void tile_partial_kernel(const Params a, uint32_t num_items) {
   using S = TileShape<D>;
   __shared__ int s_table[kTableSlots];

@@ -7,10 +7,12 @@
 //   1. Runs of >= min_tile_rows consecutive rows of one sequence become tiles of <= 64 rows
 //      (head_dim 32, 64, 128 or 256); every other row goes to the row pass.
 //   2. With >= 1024 (tile, head) pairs, tiles are whole (one workgroup per tile and head over
-//      every visible key), grouped by chunk, longest chunk first; a chunk's tiles run from its
-//      last row's to its first row's in even-ranked chunks and the other way in odd-ranked
-//      ones, so the persistent workgroups that share a head alternate long and short tiles and
-//      reach every second chunk together (sharing its keys through their XCD's L2).
+//      every visible key). Beside row-pass rows they are grouped by chunk, longest chunk
+//      first; a chunk's tiles run from its last row's to its first row's in even-ranked chunks
+//      and the other way in odd-ranked ones, so the persistent workgroups that share a head
+//      alternate long and short tiles and reach every second chunk together (sharing its keys
+//      through their XCD's L2). Without row-pass rows the longest tile comes first (stable), so
+//      the grid ends on its shortest workgroups.
 //   3. >= 16 consecutive row-pass rows whose tables agree over >= 512 leading tokens form a
 //      shared-prefix group; its whole partitions become 64-row tiles read through the first
 //      row's table (a tile never starts at a member whose table ends inside the prefix), and
@@ -78,9 +80,10 @@ int64_t common_prefix(const Tables& t, int64_t a, int64_t b, int64_t limit) {
   return c;
 }
 
-// Rule 2: whole prefill tiles, chunk by chunk.
+// Rule 2: whole prefill tiles. Beside row-pass rows, chunk by chunk; without them (the tile pass
+// runs one workgroup per item, handed out in item order as workgroups finish), longest first.
 void make_whole(std::vector<Tile>& tiles, const int32_t* seq, const std::vector<int64_t>& vis,
-                int32_t num_heads) {
+                int32_t num_heads, bool has_rows) {
   const int64_t n = static_cast<int64_t>(tiles.size());
   if (n == 0 || n * num_heads < kWholeTileGroups) return;
   std::vector<int64_t> longest(n);
@@ -88,6 +91,22 @@ void make_whole(std::vector<Tile>& tiles, const int32_t* seq, const std::vector<
     int64_t m = vis[tiles[t].first];
     for (int32_t r = 1; r < tiles[t].count; ++r) m = std::max(m, vis[tiles[t].first + r]);
     longest[t] = m;
+  }
+  if (!has_rows) {
+    std::vector<int64_t> order(n);
+    for (int64_t t = 0; t < n; ++t) order[t] = t;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int64_t a, int64_t b) { return longest[a] > longest[b]; });
+    std::vector<Tile> whole;
+    whole.reserve(n);
+    for (int64_t t : order) {
+      Tile w = tiles[t];
+      w.begin = 0;
+      w.end = PKV_TILE_WHOLE;
+      whole.push_back(w);
+    }
+    tiles.swap(whole);
+    return;
   }
   std::vector<int64_t> starts;  // a chunk starts where a tile does not continue the previous one
   for (int64_t t = 0; t < n; ++t) {
@@ -281,7 +300,7 @@ extern "C" int pkv_plan_batch(const int32_t* query_seq, const int32_t* query_pos
       vis[q] = p < 0 ? 0 : std::min(ctx, p + 1);
     }
   }
-  make_whole(tiles, seq, vis, num_heads);
+  make_whole(tiles, seq, vis, num_heads, !row_pass.empty());
 
   // Do two row-pass sequences start with the same block? Without that there is neither a
   // shared-prefix group nor a repeated block to look for.

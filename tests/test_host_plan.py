@@ -254,6 +254,24 @@ def test_prefill_tiles_become_whole_when_they_fill_the_gpu() -> None:
     }
 
 
+def test_prefill_tiles_without_row_pass_rows_run_longest_first() -> None:
+    """The 8 chunks on their own: one workgroup per item, so the longest tile comes first."""
+    rng = np.random.default_rng(7)
+    seq, positions, contexts, tables = _mixed(rng, 32)
+    seq, positions = seq[:4096], positions[:4096]
+    plan = ops.plan_batch(seq, 128, 32, tables, contexts, 16, query_positions=positions)
+    assert plan.tiles.shape == (64, 4) and plan.rows.shape[0] == 0
+    assert np.all(plan.tiles[:, 2] == 0) and np.all(plan.tiles[:, 3] == ops.TILE_WHOLE)
+    # tile i of chunk c holds positions o_c + 64 i .. o_c + 64 i + 63: its last row sees
+    # o_c + 64 (i + 1) keys; ties keep row order (chunk, then tile)
+    offsets = contexts[:8] - 512
+    keyed = sorted((-(int(offsets[c]) + 64 * (i + 1)), c, i) for c in range(8) for i in range(8))
+    assert plan.tiles[:, 0].tolist() == [512 * c + 64 * i for _, c, i in keyed]
+    assert plan.tiles[:, 1].tolist() == [64] * 64
+    _covered(plan, seq, contexts, 16)
+    assert plan.merge.size == 0
+
+
 def test_merge_list_without_positions_is_every_row_outside_whole_tiles() -> None:
     tiles = np.array([[0, 64, 0, ops.TILE_WHOLE], [64, 10, 0, 0], [80, 3, 0, ops.TILE_WHOLE]])
     assert ops.merge_rows_for(90, tiles).tolist() == [*range(64, 80), *range(83, 90)]

@@ -127,6 +127,11 @@ def test_whole_tile_batches_plan_the_same() -> None:
     want = ops.plan_batch(seq, 128, 32, tables, contexts, 16, query_positions=positions)
     assert np.any(want.tiles[:, 3] == ops.TILE_WHOLE)
     _same(want, ops.plan_batch_native(seq, 128, 32, tables, contexts, 16, query_positions=positions))
+    # the chunks alone (no row-pass rows: longest tile first)
+    alone = ops.plan_batch(seq[:4096], 128, 32, tables, contexts, 16, query_positions=positions[:4096])
+    assert alone.rows.shape[0] == 0 and np.all(alone.tiles[:, 3] == ops.TILE_WHOLE)
+    _same(alone, ops.plan_batch_native(seq[:4096], 128, 32, tables, contexts, 16,
+                                       query_positions=positions[:4096]))  # fmt: skip
 
 
 def test_small_buffers_grow_and_bad_arguments_are_refused() -> None:
