@@ -775,19 +775,37 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
 #pragma unroll
   for (int mask = 32; mask > 0; mask >>= 1) wave_lim = max(wave_lim, __shfl_xor(wave_lim, mask));
   wave_lim = __builtin_amdgcn_readfirstlane(wave_lim);
+  // Every row of the wavefront sees the keys below wave_full: a key tile that ends by then, with
+  // every key in a block inside the pool (all bits of its key mask set), needs no per-key mask.
+  int wave_full = q_ok ? lim : INT32_MAX;
+#pragma unroll
+  for (int mask = 32; mask > 0; mask >>= 1) wave_full = min(wave_full, __shfl_xor(wave_full, mask));
+  wave_full = __builtin_amdgcn_readfirstlane(wave_full);
+  constexpr uint32_t kAllKeys = kKeys == 32 ? 0xffffffffu : (1u << kKeys) - 1u;
 
   // One key tile's scores st -> probabilities pr, updating the running reference and sum. A key
   // counts when it is below the lane's limit and its bit in kmask is set.
   auto softmax_step = [&](floatx4 (&st)[kSub], int k0, uint32_t kmask, float (&pr)[kSub][4]) {
     float sc[kSub][4];
     float mx = -INFINITY;
+    if (k0 + kKeys <= wave_full && kmask == kAllKeys) {  // wavefront-uniform: nothing masked
 #pragma unroll
-    for (int j = 0; j < kSub; ++j) {
+      for (int j = 0; j < kSub; ++j) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int kk = 16 * j + 4 * c + r;
-        sc[j][r] = (k0 + kk) < lim && ((kmask >> kk) & 1u) ? st[j][r] : -INFINITY;
-        mx = fmaxf(mx, sc[j][r]);
+        for (int r = 0; r < 4; ++r) {
+          sc[j][r] = st[j][r];
+          mx = fmaxf(mx, sc[j][r]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kk = 16 * j + 4 * c + r;
+          sc[j][r] = (k0 + kk) < lim && ((kmask >> kk) & 1u) ? st[j][r] : -INFINITY;
+          mx = fmaxf(mx, sc[j][r]);
+        }
       }
     }
     mx = column_max(mx);
@@ -1045,6 +1063,13 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
 #pragma unroll
   for (int mask = 32; mask > 0; mask >>= 1) wave_lim = max(wave_lim, __shfl_xor(wave_lim, mask));
   wave_lim = __builtin_amdgcn_readfirstlane(wave_lim);
+  // Every row of the wavefront sees the keys below wave_full: a key tile that ends by then, with
+  // every key in a block inside the pool (all bits of its key mask set), needs no per-key mask.
+  int wave_full = q_ok ? lim : INT32_MAX;
+#pragma unroll
+  for (int mask = 32; mask > 0; mask >>= 1) wave_full = min(wave_full, __shfl_xor(wave_full, mask));
+  wave_full = __builtin_amdgcn_readfirstlane(wave_full);
+  constexpr uint32_t kAllKeys = kKeys == 32 ? 0xffffffffu : (1u << kKeys) - 1u;
   __syncthreads();  // s_table ready
 
   // Table entry of key kpos (clamped into the window; callers discard it when kpos is out).
@@ -1087,13 +1112,24 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
   auto softmax_step = [&](floatx4 (&st)[kSub], int k0, uint32_t kmask, float (&pr)[kSub][4]) {
     float sc[kSub][4];
     float mx = -INFINITY;
+    if (k0 + kKeys <= wave_full && kmask == kAllKeys) {  // wavefront-uniform: nothing masked
 #pragma unroll
-    for (int j = 0; j < kSub; ++j) {
+      for (int j = 0; j < kSub; ++j) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int kk = 16 * j + 4 * c + r;
-        sc[j][r] = (k0 + kk) < lim && ((kmask >> kk) & 1u) ? st[j][r] : -INFINITY;
-        mx = fmaxf(mx, sc[j][r]);
+        for (int r = 0; r < 4; ++r) {
+          sc[j][r] = st[j][r];
+          mx = fmaxf(mx, sc[j][r]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kSub; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kk = 16 * j + 4 * c + r;
+          sc[j][r] = (k0 + kk) < lim && ((kmask >> kk) & 1u) ? st[j][r] : -INFINITY;
+          mx = fmaxf(mx, sc[j][r]);
+        }
       }
     }
     mx = column_max(mx);
@@ -1254,7 +1290,11 @@ void tile_partial_kernel(const Params a, uint32_t num_items) {
   __shared__ int s_vis[kTileRows];
   if constexpr (kDma) {
     static_assert(std::is_same_v<KVT, float>, "the direct-to-LDS tiles are float32");
-    __shared__ __align__(16) float s_kv[kTileStages * S::kStageFloats];
+    // The stages are dynamic LDS (kTileStages * S::kStageFloats floats, sized at launch). From
+    // a static array of their size the compiler would infer one wave per SIMD and reserve the
+    // registers of that occupancy (257 instead of the 152 used), which leaves room for one
+    // row-pass workgroup per CU instead of two.
+    extern __shared__ __align__(16) float s_kv[];
     for (uint32_t item = blockIdx.x; item < num_items; item += gridDim.x) {
       __syncthreads();  // the previous item's reads of LDS are done
       tile_item_dma<D, kPow2Block>(a, item, s_table, s_kv, s_vis);
@@ -1383,10 +1423,13 @@ int launch_tiles(const Params& a, int64_t num_tiles, int64_t max_groups, bool le
     constexpr bool kDmaType = PKV_TILE_DMA && std::is_same_v<KVT, float>;
     const bool block_fits = static_cast<int64_t>(a.block_size) * a.num_heads * D <= INT32_MAX;
     const bool dma = kDmaType && max_groups > 0 && !lean_rows && block_fits;
+    const size_t stage_bytes = kTileStages * TileShape<D>::kStageFloats * sizeof(float);
     if (dma && pow2) {
-      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true, kDmaType>), grid, dim3(kTileThreads), 0, stream, a, n);
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true, kDmaType>), grid, dim3(kTileThreads), stage_bytes,
+                         stream, a, n);
     } else if (dma) {
-      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false, kDmaType>), grid, dim3(kTileThreads), 0, stream, a, n);
+      hipLaunchKernelGGL((tile_partial_kernel<KVT, D, false, kDmaType>), grid, dim3(kTileThreads), stage_bytes,
+                         stream, a, n);
     } else if (pow2) {
       hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true, false>), grid, dim3(kTileThreads), 0, stream, a, n);
     } else {
