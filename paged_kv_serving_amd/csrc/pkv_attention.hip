@@ -44,6 +44,11 @@
 // and kept per device; host code never passes the array's own name to a kernel).
 static __device__ __align__(256) float scratch[PKV_STATIC_SCRATCH_BYTES / sizeof(float)];
 
+// Sixteen zero bytes in global memory: the tile pass loads the key and value vectors of a key
+// past the end, or in a block outside the pool, from here. Such a key's probability is 0, and
+// 0 times whatever a pool row holds (inf or NaN included) would not be 0.
+static __device__ __align__(16) uint4 zero_vector = {0u, 0u, 0u, 0u};
+
 namespace pkv {
 namespace {
 
@@ -840,34 +845,35 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   // The prefetched tile's key mask (keys before kend in blocks inside the pool), a wavefront
   // ballot kept in scalar registers until the tile's scores are masked.
   uint32_t mask_next = 0u;
+  const uint32_t pool_blocks = static_cast<uint32_t>(min<int64_t>(a.num_blocks, INT32_MAX));
   auto prefetch = [&](int k0) {
     {
       const int kpos = k0 + lane;
       const int lb = min(max(block_of<kPow2Block>(kpos, a) - b0, 0), kTableSlots - 1);
       const int blk = s_table[lb];
-      const bool ok = lane < kKeys && kpos < kend && blk >= 0 && blk < a.num_blocks;
+      const bool ok = (lane < kKeys) & (kpos < kend) & (static_cast<uint32_t>(blk) < pool_blocks);
       mask_next = static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(ok));
     }
+    // One branch per vector: a key past kend or in a block outside the pool keeps zeros (its
+    // table entry is read at a clamped index and not used).
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
       const int v = threadIdx.x + u * kTileThreads;
+      const int row = v / kVecPerRow;
+      const int col = (v - row * kVecPerRow) * kEpv;
+      const int kpos = k0 + row;
+      const int lb = min(max(block_of<kPow2Block>(kpos, a) - b0, 0), kTableSlots - 1);
+      const int blk = s_table[lb];
+      const bool ok = (kVecs % kTileThreads == 0 || v < kVecs) & (kpos < kend) &
+                      (static_cast<uint32_t>(blk) < pool_blocks);
       kraw[u] = make_uint4(0, 0, 0, 0);
       vraw[u] = make_uint4(0, 0, 0, 0);
-      if (v < kVecs) {
-        const int row = v / kVecPerRow;
-        const int kpos = k0 + row;
-        if (kpos < kend) {
-          const int lb = block_of<kPow2Block>(kpos, a) - b0;
-          const int blk = s_table[lb];
-          if (blk >= 0 && blk < a.num_blocks) {
-            const int col = (v - row * kVecPerRow) * kEpv;
-            const int64_t off =
-                (static_cast<int64_t>(blk) * a.block_size + (kpos - (lb + b0) * a.block_size)) *
-                    row_stride + head_off + col;
-            kraw[u] = *reinterpret_cast<const uint4*>(kcache + off);
-            vraw[u] = *reinterpret_cast<const uint4*>(vcache + off);
-          }
-        }
+      if (ok) {
+        const int64_t off =
+            (static_cast<int64_t>(blk) * a.block_size + (kpos - (lb + b0) * a.block_size)) * row_stride +
+            head_off + col;
+        kraw[u] = *reinterpret_cast<const uint4*>(kcache + off);
+        vraw[u] = *reinterpret_cast<const uint4*>(vcache + off);
       }
     }
   };
@@ -882,7 +888,7 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
       b0 = block_of<kPow2Block>(next, a);
       stage_window();
     }
-    // Widen the prefetched tile (zeros past kend) into LDS as float32.
+    // Widen the prefetched tile (zeros for keys past kend or outside the pool) into LDS as float32.
 #pragma unroll
     for (int u = 0; u < kPerThread; ++u) {
       const int v = threadIdx.x + u * kTileThreads;
@@ -1077,8 +1083,10 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
     const int lb = min(max(block_of<kPow2Block>(kpos, a) - b0, 0), kTableSlots - 1);
     return s_table[lb];
   };
-  // Element offsets of this lane's kPer chunks of key tile k0, and the tile's key mask.
-  auto prepare = [&](int k0, int lane_v, int64_t (&off)[kPer]) -> uint32_t {
+  // Element offsets of this lane's kPer chunks of key tile k0 (bit u of `valid`: chunk u's key
+  // is before the end and in the pool), and the tile's key mask.
+  auto prepare = [&](int k0, int lane_v, int64_t (&off)[kPer], uint32_t& valid) -> uint32_t {
+    valid = 0u;
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int chunk = (wave * kPer + u) * kWave + lane_v;
@@ -1091,18 +1099,22 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
       const uint32_t blk_u = ok ? static_cast<uint32_t>(blk) : 0u;
       const uint32_t row_off = ok ? within * row_elems : 0u;
       off[u] = static_cast<int64_t>(blk_u * block_elems) + static_cast<int64_t>(row_off) + head_off + col;
+      valid |= ok ? 1u << u : 0u;
     }
     const int kpos = k0 + lane_v;
     const bool ok = (lane_v < kKeys) & (kpos < s_end) &
                     (static_cast<uint32_t>(table_at(kpos)) < pool_blocks);
     return static_cast<uint32_t>(__builtin_amdgcn_ballot_w64(ok));
   };
-  auto fire = [&](int buf, const int64_t (&off)[kPer]) {
+  // Queue the chunks' loads into stage `buf`; an invalid chunk loads zero_vector.
+  auto fire = [&](int buf, const int64_t (&off)[kPer], uint32_t valid) {
     const uint32_t dst = lds_kv + static_cast<uint32_t>(buf * S::kStageFloats * 4 + wave * kPer * 1024);
+    const float* zero = reinterpret_cast<const float*>(&zero_vector);
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      load_to_lds16(kcache + off[u], dst + u * 1024);
-      load_to_lds16(vcache + off[u], dst + u * 1024 + S::kTileFloats * 4);
+      const bool ok = (valid >> u) & 1u;
+      load_to_lds16(ok ? kcache + off[u] : zero, dst + u * 1024);
+      load_to_lds16(ok ? vcache + off[u] : zero, dst + u * 1024 + S::kTileFloats * 4);
     }
   };
   // One key tile's scores st -> probabilities pr, updating the running reference and sum. A
@@ -1156,8 +1168,8 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
   // wavefront's share and also closes step i - 1, whose buffer the loads of step
   // i + kTileStages - 1 then fill. Those are queued between the step's two products. Every
   // lane issues the same loads in every step, past the last step too: a lane whose key is past
-  // the end or in a block outside the pool loads row 0 of block 0 (always in the pool)
-  // instead, and the key's bit in the step's mask stays clear.
+  // the end or in a block outside the pool loads zero_vector instead, and the key's bit in the
+  // step's mask stays clear.
   const int nsteps = s_end > s_beg ? (s_end - s_beg + kKeys - 1) / kKeys : 0;
   uint32_t kmask[kAhead];  // key masks of steps i .. i + kAhead - 1
   wait_vmcnt<0>();  // the query loads (and earlier stores) complete before the pipeline's loads
@@ -1165,8 +1177,9 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
 #pragma unroll
     for (int st = 0; st < kAhead; ++st) {
       int64_t off[kPer];
-      kmask[st] = prepare(s_beg + st * kKeys, lane, off);
-      fire(st, off);
+      uint32_t valid;
+      kmask[st] = prepare(s_beg + st * kKeys, lane, off, valid);
+      fire(st, off, valid);
     }
   }
   int buf = 0;
@@ -1219,8 +1232,9 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
     uint32_t next_mask;
     {
       int64_t off[kPer];
-      next_mask = prepare(k_next, lane_o, off);
-      fire(buf == 0 ? kAhead : buf - 1, off);
+      uint32_t valid;
+      next_mask = prepare(k_next, lane_o, off, valid);
+      fire(buf == 0 ? kAhead : buf - 1, off, valid);
     }
     if (work) {
       float pr[kSub][4];

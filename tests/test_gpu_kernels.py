@@ -573,6 +573,61 @@ def test_tiles_beside_rows_equal_tiles_alone(device, dim, block, whole) -> None:
         assert np.array_equal(got[tile_rows], solo[tile_rows]), partition
 
 
+@pytest.mark.parametrize("kv", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("whole", [False, True], ids=["partitions", "whole"])
+def test_nan_in_a_block_no_table_holds_reaches_no_output(device, kv, whole) -> None:
+    """The tile pass loads the keys past a tile's end (its last 32-key step is partial) as zeros,
+    on both staging paths: beside row-pass rows (float32: straight into LDS) and alone (through
+    registers). So a pool block that no table holds may contain NaN or inf, as the reference
+    never reads it, and no output changes."""
+    say("unreferenced NaN block", kv, whole)
+    rng = np.random.default_rng(77 + whole)
+    dim, block, max_ctx = 128, 16, 700
+    kc, vc, tables, contexts, positions, seq_of, q = _ragged_case(
+        rng, heads=2, dim=dim, block=block, pool=5 * max_ctx // block + 8, seqs=6, max_ctx=max_ctx,
+        prefill=True, max_rows=150,
+    )  # fmt: skip
+    extra = [rng.permutation(kc.shape[0])[: -(-c // block)] for c in (max_ctx - 3, 37)]
+    tables = list(tables) + extra
+    contexts = np.concatenate([contexts, [max_ctx - 3, 37]])
+    positions = np.concatenate([positions, [max_ctx - 4, 36]])
+    seq_of = np.concatenate([seq_of, [len(tables) - 2, len(tables) - 1]])
+    q = np.concatenate([q, rng.standard_normal((2,) + q.shape[1:]).astype(np.float32)])
+    spare = sorted(set(range(1, kc.shape[0])) - {int(b) for t in tables for b in t})[0]
+    tables = [np.where(np.asarray(t) == 0, spare, t) for t in tables]  # no table holds block 0
+    kc[0], vc[0] = np.nan, np.inf
+    scale = dim**-0.5
+    if kv == torch.bfloat16:
+        kc, vc = bf16_round(kc), bf16_round(vc)
+    want, _ = _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale)
+    width = max(len(t) for t in tables)
+    padded = np.full((len(tables), width), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    args = (
+        torch.from_numpy(q).to(device), torch.from_numpy(positions.astype(np.int32)).to(device),
+        torch.from_numpy(seq_of.astype(np.int32)).to(device),
+        torch.from_numpy(kc).to(device).to(kv), torch.from_numpy(vc).to(device).to(kv),
+        torch.from_numpy(padded).to(device), torch.from_numpy(contexts.astype(np.int32)).to(device),
+        scale,
+    )  # fmt: skip
+    rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)
+    visible = np.minimum(contexts[seq_of], positions + 1)
+    assert rows.shape[0] >= 2 and tiles.shape[0] >= 2
+    assert any(visible[t0 : t0 + n].max() % 32 for t0, n, _, _ in tiles)  # a partial last key step
+    if whole:
+        tiles[:, 3] = ops.TILE_WHOLE
+    tile_rows = np.concatenate([np.arange(t0, t0 + n) for t0, n, _, _ in tiles])
+    merge = ops.merge_rows_for(seq_of.size, tiles, visible, 512) if whole else None
+    mc = int(contexts.max())
+    beside = ops.upload_plan(ops.expand_rows(rows, visible, 0), tiles, device, merge=merge)
+    alone = ops.upload_plan(np.zeros((0, 2), np.int32), tiles, device, merge=merge)
+    for name, plan, done in (("beside", beside, np.arange(seq_of.size)), ("alone", alone, tile_rows)):
+        got = ops.paged_attention_ragged(*args, max_context_len=mc, plan=plan).cpu().numpy()[done]
+        assert np.all(np.isfinite(got)), name
+        assert np.max(np.abs(got - want[done])) < FP32_TOL, name
+
+
 def _attention_skipping_bad_blocks(q, positions, seq_of, kc, vc, tables, contexts, scale):
     """float64 attention in which keys whose block id lies outside the pool take no part (the
     library's rule for such table entries; the reference would raise on them)."""
