@@ -48,6 +48,11 @@ typedef enum pkv_dtype {
 #define PKV_ATTN_SHORT_ROWS 2 /* the row pass's items are short (a few hundred keys): launch a
                                 lighter workgroup so more of them are in flight at once */
 
+#define PKV_ATTN_DOMINANT_TILES 4 /* the tile pass carries more of the call's time than the row
+                                    pass beside it: run it as three register-staged workgroups
+                                    per CU (the row workgroups fill in around them) instead of
+                                    one (float32, staged straight into LDS) or two per CU */
+
 /* pkv_paged_attention tile record: end partition of a tile computed whole by one workgroup. */
 #define PKV_TILE_WHOLE (-1)
 
@@ -220,8 +225,9 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *                      >= max_context_len (checked).
  *   partition_size   : keys per split-context partition, a positive multiple of 16, <= 1024;
  *                      0 selects the library default (512).
- *   flags            : PKV_ATTN_SHARED_KV and/or PKV_ATTN_SHORT_ROWS, or 0. Both only choose
- *                      how the kernels run; the results agree within float32 rounding.
+ *   flags            : PKV_ATTN_SHARED_KV, PKV_ATTN_SHORT_ROWS and/or PKV_ATTN_DOMINANT_TILES,
+ *                      or 0. They only choose how the kernels run; the results agree within
+ *                      float32 rounding (PKV_ATTN_DOMINANT_TILES: bit for bit).
  *   workspace        : float32 scratch of pkv_attention_workspace_bytes(...) bytes (may be
  *                      NULL when that is 0); 16-byte aligned when num_tiles > 0.
  * A query whose every key is masked gets a zero output (attention.py:120-121).
@@ -315,6 +321,8 @@ int pkv_paged_attention_append(
  *   block_tables               : int32 [num_seqs, block_table_stride], host; every sequence a
  *                                query names must hold ceil(context / block_size) entries.
  *   context_lens               : int32 [num_seqs], host.
+ *   kv_dtype                   : the pools' element type; it weighs the row pass's bytes
+ *                                against the tile pass's products for PKV_ATTN_DOMINANT_TILES.
  *   partition_size             : 0 lets the planner choose; a positive value is kept.
  *   min_tile_rows              : the shortest run of one sequence's rows made into tiles (8).
  *   rows_out [rows_capacity, 2], tiles_out [tiles_capacity, 4], merge_out [merge_capacity] :
@@ -327,7 +335,7 @@ int pkv_paged_attention_append(
 int pkv_plan_batch(const int32_t* query_seq, const int32_t* query_positions, int64_t num_queries,
                    const int32_t* block_tables, int32_t block_table_stride,
                    const int32_t* context_lens, int32_t num_seqs, int32_t block_size,
-                   int32_t num_heads, int32_t head_dim, int32_t partition_size,
+                   int32_t num_heads, int32_t head_dim, pkv_dtype kv_dtype, int32_t partition_size,
                    int32_t min_tile_rows, int32_t* rows_out, int64_t rows_capacity,
                    int32_t* tiles_out, int64_t tiles_capacity, int32_t* merge_out,
                    int64_t merge_capacity, int64_t* counts_out, int32_t* launch_out);

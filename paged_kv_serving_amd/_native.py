@@ -64,6 +64,7 @@ PKV_F32 = 0
 PKV_BF16 = 1
 PKV_ATTN_SHARED_KV = 1
 PKV_ATTN_SHORT_ROWS = 2
+PKV_ATTN_DOMINANT_TILES = 4
 PKV_TILE_WHOLE = -1
 
 PKV_OK = 0
@@ -284,7 +285,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pkv_plan_batch.argtypes = [
         _ptr, _ptr, _i64,  # query_seq, query_positions, num_queries
         _ptr, _i32, _ptr, _i32,  # block_tables, stride, context_lens, num_seqs
-        _i32, _i32, _i32, _i32, _i32,  # block_size, num_heads, head_dim, partition_size, min_tile_rows
+        _i32, _i32, _i32, _i32,  # block_size, num_heads, head_dim, kv_dtype
+        _i32, _i32,  # partition_size, min_tile_rows
         _ptr, _i64, _ptr, _i64, _ptr, _i64,  # rows, capacity, tiles, capacity, merge, capacity
         _ptr, _ptr,  # counts_out, launch_out
     ]

@@ -74,10 +74,6 @@ namespace {
 #ifndef PKV_ATTN_ROWS_FIRST
 #define PKV_ATTN_ROWS_FIRST 0
 #endif
-// Tile-pass workgroups per CU while the row pass runs beside it (0: one workgroup per item).
-#ifndef PKV_ATTN_TILE_GROUPS_PER_CU
-#define PKV_ATTN_TILE_GROUPS_PER_CU 1
-#endif
 // Workgroup order of the row pass: 0 = the hardware's round robin over the 8 XCDs (consecutive
 // workgroups, i.e. neighbouring heads of one token, on different XCDs); 1 = each XCD walks one
 // contiguous eighth of the grid. Measured on MI355X (64 x 4k decode): 0 reads at 6.79 TB/s,
@@ -1395,7 +1391,7 @@ struct DeviceResources {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr;
   hipEvent_t join = nullptr;
-  int64_t tile_groups = 0;  // tile-pass workgroups beside the row pass (0: one per item)
+  int64_t cus = 0;  // compute units (the tile pass's persistent grid beside the row pass)
 };
 
 DeviceResources g_devices[kMaxDevices];
@@ -1420,23 +1416,34 @@ DeviceResources* overlap_for(int device) {
   return r.ready.load(std::memory_order_acquire) ? &r : nullptr;
 }
 
-// max_groups > 0: a persistent grid of that many workgroups beside the row pass, staged straight
-// into LDS for float32 pools unless the row pass runs its lean workgroups (those pack many per CU,
-// and the 100 KiB of stages would crowd them out: the prefix-sharing step's attention took
-// 0.30 instead of 0.23 ms).
+// cus == 0: one workgroup per item (the tile pass alone). cus > 0: a persistent grid beside the
+// row pass, of one workgroup per CU staged straight into LDS (float32 pools beside full-size row
+// workgroups), else of two register-staged workgroups per CU, or of three with
+// PKV_ATTN_DOMINANT_TILES. Measured on MI355X (config 3's shape, 30-240 decode rows):
+//  - float32 beside full rows: one direct-to-LDS workgroup per CU is best while the tile pass's
+//    time is below about 1.1 times the row pass's (1.44 ms against 1.57 / 1.46 ms with two /
+//    three register-staged ones at 120 decode rows), three register-staged ones above it
+//    (0.86 against 0.99 ms at 30 rows);
+//  - bfloat16 (always register-staged): one per CU leaves the tile pass far behind (1.82 ms at
+//    120 decode rows), two are best below the same crossover (1.11 ms), three above it;
+//  - beside lean row workgroups the 100 KiB of direct-to-LDS stages would crowd them out (the
+//    prefix-sharing step's attention took 0.30 instead of 0.23 ms); one, two or three
+//    register-staged workgroups per CU tie there in float32, and two are best in bfloat16
+//    (0.146 against 0.173 ms with one).
 template <typename KVT, int D>
-int launch_tiles(const Params& a, int64_t num_tiles, int64_t max_groups, bool lean_rows,
-                 hipStream_t stream) {
+int launch_tiles(const Params& a, int64_t num_tiles, int64_t cus, bool lean_rows, hipStream_t stream) {
   if constexpr (D % 16 == 0 && D >= 32) {
     const int64_t items = num_tiles * static_cast<int64_t>(a.max_parts) * a.num_heads;
     if (items > 0x7fffffff) return PKV_EUNSUPPORTED;
-    const int64_t groups = max_groups > 0 && max_groups < items ? max_groups : items;
-    const dim3 grid(static_cast<uint32_t>(groups));
-    const auto n = static_cast<uint32_t>(items);
     const bool pow2 = (a.block_size & (a.block_size - 1)) == 0;
     constexpr bool kDmaType = PKV_TILE_DMA && std::is_same_v<KVT, float>;
     const bool block_fits = static_cast<int64_t>(a.block_size) * a.num_heads * D <= INT32_MAX;
-    const bool dma = kDmaType && max_groups > 0 && !lean_rows && block_fits;
+    const bool dominant = (a.flags & PKV_ATTN_DOMINANT_TILES) != 0;
+    const bool dma = kDmaType && cus > 0 && !lean_rows && !dominant && block_fits;
+    const int64_t max_groups = cus * (dma ? 1 : dominant ? 3 : 2);
+    const int64_t groups = max_groups > 0 && max_groups < items ? max_groups : items;
+    const dim3 grid(static_cast<uint32_t>(groups));
+    const auto n = static_cast<uint32_t>(items);
     const size_t stage_bytes = kTileStages * TileShape<D>::kStageFloats * sizeof(float);
     if (dma && pow2) {
       hipLaunchKernelGGL((tile_partial_kernel<KVT, D, true, kDmaType>), grid, dim3(kTileThreads), stage_bytes,
@@ -1513,7 +1520,7 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     if (overlap != nullptr) {
       // fork: the tile pass starts when the caller's stream reaches the fork point
       if (hipStreamWaitEvent(overlap->stream, overlap->fork, 0) != hipSuccess) return PKV_EHIP;
-      const int rc = launch_tiles<KVT, D>(a, num_tiles, overlap->tile_groups, short_rows, overlap->stream);
+      const int rc = launch_tiles<KVT, D>(a, num_tiles, overlap->cus, short_rows, overlap->stream);
       if (rc != PKV_OK) return rc;
       if (hipEventRecord(overlap->join, overlap->stream) != hipSuccess) return PKV_EHIP;
     } else {
@@ -1627,7 +1634,7 @@ extern "C" int pkv_init(int device) {
   r.stream = stream;
   r.fork = fork;
   r.join = join;
-  r.tile_groups = static_cast<int64_t>(cus) * PKV_ATTN_TILE_GROUPS_PER_CU;
+  r.cus = cus;
   r.ready.store(true, std::memory_order_release);
   return PKV_OK;
 }
@@ -1657,7 +1664,7 @@ int attention_call(float* out, const float* queries, int64_t query_token_stride,
                    void* stream, const AppendSource* append) {
   const int part = resolve_partition(partition_size);
   if (part < 0) return PKV_EINVAL;
-  if (flags & ~(PKV_ATTN_SHARED_KV | PKV_ATTN_SHORT_ROWS)) return PKV_EINVAL;
+  if (flags & ~(PKV_ATTN_SHARED_KV | PKV_ATTN_SHORT_ROWS | PKV_ATTN_DOMINANT_TILES)) return PKV_EINVAL;
   const bool stream_kv = (flags & PKV_ATTN_SHARED_KV) == 0;
   if (num_queries < 0 || num_rows < 0 || num_tiles < 0 || num_merge_rows < -1 || num_blocks < 1 ||
       block_size < 1 ||

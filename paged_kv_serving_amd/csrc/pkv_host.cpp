@@ -43,7 +43,7 @@
 //       Takes the addresses of those libpkv.so entry points (include/pkv.h), so the three calls
 //       below reach the library without ctypes' per-argument conversions.
 //   plan(query_seq, query_positions | None, tables, contexts, block_size, num_heads, head_dim,
-//        partition_size, min_tile_rows, rows, tiles, merge, counts, launch) -> int
+//        kv_dtype, partition_size, min_tile_rows, rows, tiles, merge, counts, launch) -> int
 //       pkv_plan_batch on NumPy buffers; returns its PKV_* code.
 //   paged_attention(...), paged_attention_append(...), copy_blocks(...) -> int
 //       The entry points of the same names, with every pointer, stream and handle passed as a
@@ -621,10 +621,10 @@ PyObject* bind(PyObject*, PyObject* args) {
 
 PyObject* plan(PyObject*, PyObject* args) {
   PyObject *seq_o, *pos_o, *tables_o, *ctx_o, *rows_o, *tiles_o, *merge_o, *counts_o, *launch_o;
-  int block_size, num_heads, head_dim, partition_size, min_tile_rows;
-  if (!PyArg_ParseTuple(args, "OOOOiiiiiOOOOO", &seq_o, &pos_o, &tables_o, &ctx_o, &block_size, &num_heads,
-                        &head_dim, &partition_size, &min_tile_rows, &rows_o, &tiles_o, &merge_o, &counts_o,
-                        &launch_o)) {
+  int block_size, num_heads, head_dim, kv_dtype, partition_size, min_tile_rows;
+  if (!PyArg_ParseTuple(args, "OOOOiiiiiiOOOOO", &seq_o, &pos_o, &tables_o, &ctx_o, &block_size, &num_heads,
+                        &head_dim, &kv_dtype, &partition_size, &min_tile_rows, &rows_o, &tiles_o, &merge_o,
+                        &counts_o, &launch_o)) {
     return nullptr;
   }
   if (!bound(reinterpret_cast<const void*>(g_plan_batch))) return nullptr;
@@ -645,7 +645,8 @@ PyObject* plan(PyObject*, PyObject* args) {
   Py_BEGIN_ALLOW_THREADS
   rc = g_plan_batch(seq.data(), pos_o == Py_None ? nullptr : pos.data(), seq.size(), tables.data(),
                     static_cast<int32_t>(tables.dim(1)), ctx.data(), static_cast<int32_t>(ctx.size()), block_size,
-                    num_heads, head_dim, partition_size, min_tile_rows, rows.data(), rows.size() / 2, tiles.data(),
+                    num_heads, head_dim, static_cast<pkv_dtype>(kv_dtype), partition_size, min_tile_rows,
+                    rows.data(), rows.size() / 2, tiles.data(),
                     tiles.size() / 4, merge.data(), merge.size(), counts.data(), launch.data());
   Py_END_ALLOW_THREADS
   return PyLong_FromLong(rc);

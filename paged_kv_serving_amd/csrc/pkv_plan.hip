@@ -21,7 +21,12 @@
 //      prefix with about 512 tile workgroups; without groups 1024 when rows x heads x
 //      ceil(context / 1024) >= 8192, else 512. An explicit size is kept.
 //   5. PKV_ATTN_SHARED_KV when >= 25% of the block ids the row pass still reads repeat;
-//      PKV_ATTN_SHORT_ROWS when the row-pass items average < 256 keys.
+//      PKV_ATTN_SHORT_ROWS when the row-pass items average < 256 keys; PKV_ATTN_DOMINANT_TILES
+//      when the call has both passes and the tile pass's estimated time is at least 1.1 times
+//      the row pass's: a tile key costs 4 * head_dim products at about 100 TFLOP/s, a row key
+//      2 * head_dim * element-size bytes at about 6.8 TB/s, i.e.
+//      tile_keys * 34 >= row_keys * element_size * 275 (measured crossover on MI355X, config 3's
+//      chunks beside 30-240 decode rows in float32 and bfloat16).
 //   6. Row-pass items: every partition a row still needs, longest first (stable), so the grid
 //      ends on its shortest workgroups.
 #include <stdint.h>
@@ -45,6 +50,8 @@ constexpr int64_t kTargetPrefixGroups = 512;
 constexpr int kMinPrefixPartition = 256;
 constexpr int64_t kWholeTileGroups = 1024;
 constexpr int64_t kShortRowKeys = 256;
+constexpr int64_t kDominantTileWeight = 34;  // rule 5: tile_keys * 34 >= row_keys * esize * 275
+constexpr int64_t kDominantRowWeight = 275;
 constexpr int kDefaultPlanPartition = 512;
 
 struct Tile {
@@ -237,14 +244,16 @@ extern "C" int pkv_plan_batch(const int32_t* query_seq, const int32_t* query_pos
                               int64_t num_queries, const int32_t* block_tables,
                               int32_t block_table_stride, const int32_t* context_lens,
                               int32_t num_seqs, int32_t block_size, int32_t num_heads,
-                              int32_t head_dim, int32_t partition_size, int32_t min_tile_rows,
+                              int32_t head_dim, pkv_dtype kv_dtype, int32_t partition_size,
+                              int32_t min_tile_rows,
                               int32_t* rows_out, int64_t rows_capacity, int32_t* tiles_out,
                               int64_t tiles_capacity, int32_t* merge_out, int64_t merge_capacity,
                               int64_t* counts_out, int32_t* launch_out) {
   using namespace pkv;
+  const int esize = dtype_size(kv_dtype);
   if (num_queries < 0 || num_seqs < 0 || block_size < 1 || num_heads < 1 || head_dim < 1 ||
-      partition_size < 0 || min_tile_rows < 1 || block_table_stride < 0 || !counts_out ||
-      !launch_out) {
+      esize == 0 || partition_size < 0 || min_tile_rows < 1 || block_table_stride < 0 ||
+      !counts_out || !launch_out) {
     return PKV_EINVAL;
   }
   if (num_queries > 0 && (!query_seq || !context_lens || !block_tables || num_seqs == 0)) {
@@ -455,7 +464,22 @@ extern "C" int pkv_plan_batch(const int32_t* query_seq, const int32_t* query_pos
     if (keep[q] && (partition <= 0 || vis[q] > partition)) merge_out[at++] = static_cast<int32_t>(q);
   }
   const bool short_rows = num_items > 0 && key_sum < kShortRowKeys * num_items;
+  // The keys the tile pass reads per head: a whole tile every visible key of its rows, a
+  // partitioned one those in its partitions.
+  int64_t tile_keys = 0;
+  for (const Tile& t : tiles) {
+    const int64_t lo = t.end == PKV_TILE_WHOLE ? 0 : static_cast<int64_t>(t.begin) * part;
+    const bool to_last = t.end == PKV_TILE_WHOLE || t.end <= t.begin;
+    for (int32_t r = 0; r < t.count; ++r) {
+      const int64_t v = vis[t.first + r];
+      const int64_t hi = to_last ? v : std::min<int64_t>(v, static_cast<int64_t>(t.end) * part);
+      tile_keys += std::max<int64_t>(hi - lo, 0);
+    }
+  }
+  const bool dominant = num_items > 0 && !tiles.empty() &&
+                        tile_keys * kDominantTileWeight >= key_sum * esize * kDominantRowWeight;
   launch_out[0] = partition;
-  launch_out[1] = (shared_kv ? PKV_ATTN_SHARED_KV : 0) | (short_rows ? PKV_ATTN_SHORT_ROWS : 0);
+  launch_out[1] = (shared_kv ? PKV_ATTN_SHARED_KV : 0) | (short_rows ? PKV_ATTN_SHORT_ROWS : 0) |
+                  (dominant ? PKV_ATTN_DOMINANT_TILES : 0);
   return PKV_OK;
 }

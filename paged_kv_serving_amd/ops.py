@@ -26,6 +26,7 @@ __all__ = [
     "greedy_tokens",
     "independent_groups",
     "kv_dtype_code",
+    "kv_dtype_size",
     "merge_rows_for",
     "paged_attention_ragged",
     "BatchPlan",
@@ -346,8 +347,9 @@ class AttentionPlan:
     the partitions of a prefix whose blocks they share. Every (row, partition) is covered
     exactly once. ``merge``: int32 ``[M]``, the rows whose partition results the reduce pass
     merges (None: every row, which is only correct without whole tiles). ``partition_size``
-    (0: library default), ``shared_kv`` and ``short_rows`` (the lighter row-pass workgroup for
-    short items) choose the launch.
+    (0: library default), ``shared_kv``, ``short_rows`` (the lighter row-pass workgroup for
+    short items) and ``dominant_tiles`` (three tile-pass workgroups per CU beside the rows)
+    choose the launch.
     """
 
     rows: torch.Tensor
@@ -356,6 +358,7 @@ class AttentionPlan:
     shared_kv: bool = False
     merge: torch.Tensor | None = None
     short_rows: bool = False
+    dominant_tiles: bool = False
 
     @property
     def num_rows(self) -> int:
@@ -471,7 +474,7 @@ def batch_hints(
 @dataclass(frozen=True)
 class BatchPlan:
     """A host plan: ``rows [R, 2]``, ``tiles [n, 4]`` and ``merge [M]`` (int32, the
-    :class:`AttentionPlan` layout), the partition size and the load hint."""
+    :class:`AttentionPlan` layout), the partition size and the launch hints."""
 
     rows: np.ndarray
     tiles: np.ndarray
@@ -479,6 +482,7 @@ class BatchPlan:
     shared_kv: bool
     merge: np.ndarray | None = None
     short_rows: bool = False
+    dominant_tiles: bool = False
 
 
 def _padded_tables(tables, sid: np.ndarray, used: np.ndarray, width: int) -> np.ndarray:
@@ -674,7 +678,7 @@ def merge_rows_for(
 def plan_batch(
     query_seq: np.ndarray, head_dim: int, num_heads: int, tables, context_lens: np.ndarray,
     block_size: int, *, partition_size: int = 0, min_tile_rows: int = MIN_TILE_ROWS,
-    query_positions: np.ndarray | None = None,
+    query_positions: np.ndarray | None = None, kv_dtype: torch.dtype = torch.float32,
 ) -> BatchPlan:  # fmt: skip
     """The full host plan of a ragged call: the row/tile split of :func:`plan_rows`, shared-prefix
     tiles, whole prefill tiles, the reduce's merge list, the partition size and the load hint.
@@ -688,7 +692,9 @@ def plan_batch(
     list to rows that span several partitions. A nonzero ``partition_size`` is kept as given.
     Shared-prefix groups and the load hint are only searched for when two row-pass sequences
     start with the same block; tables that repeat ids only past their first block get the
-    streaming hint (the hint chooses a load path, never a result).
+    streaming hint (the hint chooses a load path, never a result). ``kv_dtype`` (the pools'
+    element type) weighs the row pass's bytes against the tile pass's products for the
+    ``dominant_tiles`` hint (:func:`_dominant_tiles`).
     """
     seq = np.asarray(query_seq, dtype=np.int64)
     contexts = np.asarray(context_lens, dtype=np.int64)
@@ -762,11 +768,42 @@ def plan_batch(
         ids = table[(col >= pair_first[:, None]) & (col < reads[:, None])]
     merge = merge_rows_for(seq.size, tiles, visible, int(partition))
     items = expand_rows(rows, visible, int(partition))
-    short = False
+    short = dominant = False
     if items.shape[0]:
-        keys = np.minimum(partition, visible[items[:, 0]] - items[:, 1].astype(np.int64) * partition)
-        short = bool(np.mean(np.maximum(keys, 0)) < SHORT_ROW_KEYS)
-    return BatchPlan(items, tiles, int(partition), _repeated_fraction_reached(ids), merge, short)
+        keys = np.maximum(np.minimum(partition, visible[items[:, 0]] - items[:, 1].astype(np.int64) * partition), 0)
+        short = bool(np.mean(keys) < SHORT_ROW_KEYS)
+        dominant = _dominant_tiles(tiles, visible, int(partition), int(keys.sum()), kv_dtype_size(kv_dtype))
+    return BatchPlan(items, tiles, int(partition), _repeated_fraction_reached(ids), merge, short, dominant)
+
+
+#: The dominant-tiles hint: a call with both passes sets it when the tile pass's estimated time
+#: is at least 1.1 times the row pass's. A tile key costs 4 * head_dim products at about
+#: 100 TFLOP/s, a row key 2 * head_dim * element-size bytes at about 6.8 TB/s, so the test is
+#: tile_keys * DOMINANT_TILE_WEIGHT >= row_keys * element_size * DOMINANT_ROW_WEIGHT. Measured
+#: crossover on MI355X: config 3's chunks beside 30-240 decode rows, float32 and bfloat16.
+DOMINANT_TILE_WEIGHT = 34
+DOMINANT_ROW_WEIGHT = 275
+
+
+def kv_dtype_size(dtype: torch.dtype) -> int:
+    """Bytes per element of a KV pool dtype (float32 or bfloat16)."""
+    kv_dtype_code(dtype)  # validates
+    return 2 if dtype == torch.bfloat16 else 4
+
+
+def _dominant_tiles(tiles: np.ndarray, visible: np.ndarray, partition: int, row_keys: int, esize: int) -> bool:
+    """Whether the tile pass dominates a call whose row pass reads ``row_keys`` keys per head:
+    a whole tile reads every visible key of its rows, a partitioned one the keys in its
+    partitions."""
+    if tiles.shape[0] == 0 or row_keys == 0:
+        return False
+    tile_keys = 0
+    for first, count, begin, end in tiles.tolist():
+        v = visible[first : first + count]
+        lo = 0 if end == TILE_WHOLE else begin * partition
+        hi = v if end == TILE_WHOLE or end <= begin else np.minimum(v, end * partition)
+        tile_keys += int(np.maximum(hi - lo, 0).sum())
+    return tile_keys * DOMINANT_TILE_WEIGHT >= row_keys * esize * DOMINANT_ROW_WEIGHT
 
 
 class NativePlanner:
@@ -786,7 +823,7 @@ class NativePlanner:
     def plan_views(
         self, query_seq: np.ndarray, query_positions: np.ndarray | None, tables: np.ndarray,
         context_lens: np.ndarray, block_size: int, num_heads: int, head_dim: int, partition_size: int = 0,
-        min_tile_rows: int = MIN_TILE_ROWS,
+        min_tile_rows: int = MIN_TILE_ROWS, kv_dtype: torch.dtype = torch.float32,
     ) -> tuple[np.ndarray, np.ndarray, np.ndarray, int, int]:  # fmt: skip
         """:meth:`plan` for callers that hand over int32 C-contiguous arrays (``tables`` 2-D) and
         use the result at once: ``(rows [R, 2], tiles [n, 4], merge [M], partition size, flags)``,
@@ -797,8 +834,8 @@ class NativePlanner:
             host = self._host = _native.bound_host()
         while True:
             rc = host.plan(query_seq, query_positions, tables, context_lens, block_size, num_heads, head_dim,
-                           partition_size, min_tile_rows, self._rows, self._tiles, self._merge, self._counts,
-                           self._launch)  # fmt: skip
+                           kv_dtype_code(kv_dtype), partition_size, min_tile_rows, self._rows, self._tiles,
+                           self._merge, self._counts, self._launch)  # fmt: skip
             if rc != _native.PKV_ETOOBIG:
                 break
             rows, tiles, merge = (int(c) for c in self._counts)
@@ -814,6 +851,7 @@ class NativePlanner:
         self, query_seq: np.ndarray, head_dim: int, num_heads: int, tables: np.ndarray,
         context_lens: np.ndarray, block_size: int, *, partition_size: int = 0,
         min_tile_rows: int = MIN_TILE_ROWS, query_positions: np.ndarray | None = None,
+        kv_dtype: torch.dtype = torch.float32,
     ) -> BatchPlan:  # fmt: skip
         """Arguments as :func:`plan_batch`, except that ``tables`` is a 2-D int32 array (one
         padded row per sequence index, as the runner's block-table arena holds them)."""
@@ -828,7 +866,7 @@ class NativePlanner:
             rc = lib.pkv_plan_batch(
                 seq.ctypes.data, None if positions is None else positions.ctypes.data, seq.size,
                 table.ctypes.data, table.shape[1], contexts.ctypes.data, contexts.size,
-                block_size, num_heads, head_dim, partition_size, min_tile_rows,
+                block_size, num_heads, head_dim, kv_dtype_code(kv_dtype), partition_size, min_tile_rows,
                 self._rows.ctypes.data, self._rows.shape[0], self._tiles.ctypes.data, self._tiles.shape[0],
                 self._merge.ctypes.data, self._merge.size, self._counts.ctypes.data, self._launch.ctypes.data,
             )  # fmt: skip
@@ -844,7 +882,7 @@ class NativePlanner:
         return BatchPlan(
             self._rows[:rows].copy(), self._tiles[:tiles].copy(), partition,
             bool(flags & _native.PKV_ATTN_SHARED_KV), self._merge[:merge].copy(),
-            bool(flags & _native.PKV_ATTN_SHORT_ROWS),
+            bool(flags & _native.PKV_ATTN_SHORT_ROWS), bool(flags & _native.PKV_ATTN_DOMINANT_TILES),
         )  # fmt: skip
 
 
@@ -860,6 +898,16 @@ def plan_batch_native(query_seq, head_dim, num_heads, tables, context_lens, bloc
     return NativePlanner().plan(query_seq, head_dim, num_heads, tables, context_lens, block_size, **kwargs)
 
 
+def _plan_flags(plan: AttentionPlan | None, shared_kv: bool) -> int:
+    """pkv_paged_attention flags of a call with ``plan``."""
+    flags = _native.PKV_ATTN_SHARED_KV if shared_kv else 0
+    if plan is not None and plan.short_rows:
+        flags |= _native.PKV_ATTN_SHORT_ROWS
+    if plan is not None and plan.dominant_tiles:
+        flags |= _native.PKV_ATTN_DOMINANT_TILES
+    return flags
+
+
 def launch_paged_attention(
     out: torch.Tensor, queries: torch.Tensor, query_positions: torch.Tensor, query_seq: torch.Tensor,
     key_cache: torch.Tensor, value_cache: torch.Tensor, block_tables: torch.Tensor,
@@ -873,7 +921,7 @@ def launch_paged_attention(
     pools' device; a workspace of ``attention_workspace_bytes`` bytes; for ``append``, the decode
     shape. The library still validates sizes and pointers before enqueueing anything."""
     num_queries, heads, dim = out.shape
-    flags = (_native.PKV_ATTN_SHARED_KV if plan.shared_kv else 0) | (_native.PKV_ATTN_SHORT_ROWS if plan.short_rows else 0)
+    flags = _plan_flags(plan, plan.shared_kv)
     merge = plan.merge
     num_merge = -1 if merge is None else int(merge.shape[0])
     num_rows, num_tiles = int(plan.rows.shape[0]), int(plan.tiles.shape[0])
@@ -906,6 +954,7 @@ def launch_paged_attention(
 def upload_plan(
     rows: np.ndarray, tiles: np.ndarray, device: torch.device, *, partition_size: int = 0,
     shared_kv: bool = False, merge: np.ndarray | None = None, short_rows: bool = False,
+    dominant_tiles: bool = False,
 ) -> AttentionPlan:
     """Copy a host plan (``rows [R, 2]``, ``tiles [n, 4]``, ``merge [M]``) to the device in one
     transfer. Without a merge list, one is derived when a tile is whole (every row no whole tile
@@ -924,12 +973,14 @@ def upload_plan(
         rows=data[: rows.size].view(-1, 2), tiles=data[rows.size : end_tiles].view(-1, 4),
         partition_size=partition_size, shared_kv=shared_kv,
         merge=None if merge is None else data[end_tiles:], short_rows=short_rows,
+        dominant_tiles=dominant_tiles,
     )  # fmt: skip
 
 
 def upload_batch_plan(plan: BatchPlan, device: torch.device) -> AttentionPlan:
     return upload_plan(plan.rows, plan.tiles, device, partition_size=plan.partition_size,
-                       shared_kv=plan.shared_kv, merge=plan.merge, short_rows=plan.short_rows)  # fmt: skip
+                       shared_kv=plan.shared_kv, merge=plan.merge, short_rows=plan.short_rows,
+                       dominant_tiles=plan.dominant_tiles)  # fmt: skip
 
 
 def attention_workspace_bytes(
@@ -1056,9 +1107,7 @@ def paged_attention_ragged(
                 raise ValueError("plan.merge must be contiguous")
             num_merge = int(merge.shape[0])
             merge_ptr = merge.data_ptr() if num_merge else None
-    flags = (_native.PKV_ATTN_SHARED_KV if shared_kv else 0) | (
-        _native.PKV_ATTN_SHORT_ROWS if plan is not None and plan.short_rows else 0
-    )
+    flags = _plan_flags(plan, shared_kv)
     if append is not None:
         new_keys, new_values, slot_mapping = append
         if _device_index(new_keys, new_values, slot_mapping) != device:

@@ -532,11 +532,11 @@ class ModelRunner:
         query_pos = positions.astype(np.int32)
         plan_rows, plan_tiles, merge, partition, flags = self._planner.plan_views(
             query_seq, query_pos, self._tables.host, contexts_by_row, self.block_size, config.n_heads,
-            config.head_dim, self.partition_size,
+            config.head_dim, self.partition_size, kv_dtype=self._keys.dtype,
         )  # fmt: skip
         self.last_plan = ops.BatchPlan(
             plan_rows, plan_tiles, partition, bool(flags & _native.PKV_ATTN_SHARED_KV), merge,
-            bool(flags & _native.PKV_ATTN_SHORT_ROWS),
+            bool(flags & _native.PKV_ATTN_SHORT_ROWS), bool(flags & _native.PKV_ATTN_DOMINANT_TILES),
         )  # fmt: skip
         # Queued copy-on-write pairs travel in the same copy and run before this step's kernels.
         sizes, flat = self._cow_groups(self._pending) if self._pending else ([], None)

@@ -63,7 +63,7 @@ class AttentionBatch:
         heads, dim = self.key_cache.shape[2], self.key_cache.shape[3]
         host = ops.plan_batch_native(
             self.host_seq, dim, heads, self.host_tables, self.host_context, self.key_cache.shape[1],
-            partition_size=partition_size, query_positions=self.host_positions,
+            partition_size=partition_size, query_positions=self.host_positions, kv_dtype=self.key_cache.dtype,
         )  # fmt: skip
         self.plan = ops.upload_batch_plan(host, self.queries.device)
 
@@ -158,8 +158,10 @@ def _assemble(
     for i, table in enumerate(tables):
         padded[i, : len(table)] = table
     plan = ops.upload_batch_plan(
-        ops.plan_batch_native(seq, head_dim, heads, tables, context, block_size, query_positions=positions), device
-    )
+        ops.plan_batch_native(seq, head_dim, heads, tables, context, block_size, query_positions=positions,
+                              kv_dtype=kv_dtype),
+        device,
+    )  # fmt: skip
     return AttentionBatch(
         key_cache=key_cache,
         value_cache=value_cache,

@@ -10,6 +10,8 @@ identical inputs and differ only by float32 accumulation order).
 
 from __future__ import annotations
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -524,9 +526,10 @@ def test_whole_tiles_match_the_oracle(device, dim, kv, block) -> None:
 @pytest.mark.parametrize("whole", [False, True], ids=["partitions", "whole"])
 def test_tiles_beside_rows_equal_tiles_alone(device, dim, block, whole) -> None:
     """Beside row-pass rows the float32 tile pass is a persistent grid that loads key and value
-    tiles straight into LDS; on its own it runs one workgroup per item through registers. Both
-    form the same sums in the same order, so the tile rows come out bit-identical; and both
-    match the oracle. At block_size 1 whole tiles move their staged table window."""
+    tiles straight into LDS (or, with the dominant-tiles hint, three register-staged workgroups
+    per CU); on its own it runs one workgroup per item through registers. All form the same sums
+    in the same order, so the tile rows come out bit-identical; and they match the oracle. At
+    block_size 1 whole tiles move their staged table window."""
     say("tile paths", dim, block, whole)
     rng = np.random.default_rng(dim * 7 + block + whole)
     max_ctx = 1400 if block == 1 else 800
@@ -569,8 +572,11 @@ def test_tiles_beside_rows_equal_tiles_alone(device, dim, block, whole) -> None:
         mc = int(contexts.max())
         got = ops.paged_attention_ragged(*args, max_context_len=mc, plan=beside).cpu().numpy()
         solo = ops.paged_attention_ragged(*args, max_context_len=mc, plan=alone).cpu().numpy()
+        dominant = dataclasses.replace(beside, dominant_tiles=True)
+        hinted = ops.paged_attention_ragged(*args, max_context_len=mc, plan=dominant).cpu().numpy()
         assert np.max(np.abs(got - want)) < FP32_TOL, partition
         assert np.array_equal(got[tile_rows], solo[tile_rows]), partition
+        assert np.array_equal(hinted, got), partition
 
 
 @pytest.mark.parametrize("kv", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
@@ -626,6 +632,60 @@ def test_nan_in_a_block_no_table_holds_reaches_no_output(device, kv, whole) -> N
         got = ops.paged_attention_ragged(*args, max_context_len=mc, plan=plan).cpu().numpy()[done]
         assert np.all(np.isfinite(got)), name
         assert np.max(np.abs(got - want[done])) < FP32_TOL, name
+
+
+@pytest.mark.parametrize("block", [16, 5])
+@pytest.mark.parametrize("whole", [False, True], ids=["partitions", "whole"])
+@pytest.mark.parametrize("short", [False, True], ids=["rows", "lean-rows"])
+def test_bf16_tiles_beside_rows_in_every_grid_shape(device, block, whole, short) -> None:
+    """A bfloat16 pool's tile pass beside row-pass rows (two register-staged workgroups per CU,
+    three with the dominant-tiles hint, beside full or lean row workgroups) and alone (one per
+    item) give bit-identical tile rows, and match the oracle on the bf16-rounded pools."""
+    say("bf16 tile grids", block, whole, short)
+    rng = np.random.default_rng(90 + block + 2 * whole + 4 * short)
+    dim, max_ctx = 128, 800
+    kc, vc, tables, contexts, positions, seq_of, q = _ragged_case(
+        rng, heads=2, dim=dim, block=block, pool=5 * max_ctx // block + 8, seqs=6, max_ctx=max_ctx,
+        prefill=True, max_rows=150,
+    )  # fmt: skip
+    extra = [rng.permutation(kc.shape[0])[: -(-c // block)] for c in (max_ctx - 3, 37)]
+    tables = list(tables) + extra
+    contexts = np.concatenate([contexts, [max_ctx - 3, 37]])
+    positions = np.concatenate([positions, [max_ctx - 4, 36]])
+    seq_of = np.concatenate([seq_of, [len(tables) - 2, len(tables) - 1]])
+    q = np.concatenate([q, rng.standard_normal((2,) + q.shape[1:]).astype(np.float32)])
+    kc, vc = bf16_round(kc), bf16_round(vc)
+    scale = dim**-0.5
+    want, _ = _oracle(kc, vc, tables, contexts, positions, seq_of, q, scale)
+    width = max(len(t) for t in tables)
+    padded = np.full((len(tables), width), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    args = (
+        torch.from_numpy(q).to(device), torch.from_numpy(positions.astype(np.int32)).to(device),
+        torch.from_numpy(seq_of.astype(np.int32)).to(device),
+        torch.from_numpy(kc).to(device).to(torch.bfloat16), torch.from_numpy(vc).to(device).to(torch.bfloat16),
+        torch.from_numpy(padded).to(device), torch.from_numpy(contexts.astype(np.int32)).to(device),
+        scale,
+    )  # fmt: skip
+    rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)
+    assert rows.shape[0] >= 2 and tiles.shape[0] >= 2
+    if whole:
+        tiles[:, 3] = ops.TILE_WHOLE
+    tile_rows = np.concatenate([np.arange(t0, t0 + n) for t0, n, _, _ in tiles])
+    visible = np.minimum(contexts[seq_of], positions + 1)
+    merge = ops.merge_rows_for(seq_of.size, tiles, visible, 512) if whole else None
+    mc = int(contexts.max())
+    beside = ops.upload_plan(ops.expand_rows(rows, visible, 0), tiles, device, merge=merge, short_rows=short)
+    outs = [
+        ops.paged_attention_ragged(*args, max_context_len=mc, plan=plan).cpu().numpy()
+        for plan in (beside, dataclasses.replace(beside, dominant_tiles=True))
+    ]
+    alone = ops.upload_plan(np.zeros((0, 2), np.int32), tiles, device, merge=merge)
+    solo = ops.paged_attention_ragged(*args, max_context_len=mc, plan=alone).cpu().numpy()
+    assert np.max(np.abs(outs[0] - want)) < FP32_TOL
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0][tile_rows], solo[tile_rows])
 
 
 def _attention_skipping_bad_blocks(q, positions, seq_of, kc, vc, tables, contexts, scale):

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
+import torch
 
 from paged_kv_serving_amd import ops
 
@@ -270,6 +271,31 @@ def test_prefill_tiles_without_row_pass_rows_run_longest_first() -> None:
     assert plan.tiles[:, 1].tolist() == [64] * 64
     _covered(plan, seq, contexts, 16)
     assert plan.merge.size == 0
+
+
+@pytest.mark.parametrize(
+    ("decode", "kv", "dominant"),
+    [(120, torch.float32, False), (60, torch.float32, True), (120, torch.bfloat16, True),
+     (240, torch.bfloat16, False)],
+)  # fmt: skip
+def test_dominant_tiles_when_the_tile_pass_outweighs_the_rows(decode, kv, dominant) -> None:
+    """The 8 chunks beside 60-240 decode rows: the hint turns on past the measured crossover
+    (the tile pass's estimated time 1.1 times the row pass's; here 0.87 and 1.79 in float32 at
+    120 and 60 rows), and a bfloat16 pool's rows weigh half as much (1.75 at 120 rows, 0.87 at
+    240); never without rows or without tiles."""
+    rng = np.random.default_rng(7)
+    seq, positions, contexts, tables = _mixed(rng, 32)
+    seq, positions = seq[: 4096 + decode], positions[: 4096 + decode]
+    if decode > 120:  # more decode rows than _mixed draws: repeat them
+        extra = np.arange(8, 8 + decode - 120) % 120 + 8
+        seq = np.concatenate([seq, extra])
+        positions = np.concatenate([positions, contexts[extra] - 1])
+    plan = ops.plan_batch(seq, 128, 32, tables, contexts, 16, query_positions=positions, kv_dtype=kv)
+    assert plan.tiles.shape[0] == 64 and plan.rows.shape[0] > 0
+    assert plan.dominant_tiles == dominant
+    alone = ops.plan_batch(seq[:4096], 128, 32, tables, contexts, 16, query_positions=positions[:4096], kv_dtype=kv)
+    rows = ops.plan_batch(seq[4096:], 128, 32, tables, contexts, 16, query_positions=positions[4096:], kv_dtype=kv)
+    assert not alone.dominant_tiles and not rows.dominant_tiles
 
 
 def test_merge_list_without_positions_is_every_row_outside_whole_tiles() -> None:

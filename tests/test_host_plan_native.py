@@ -2,13 +2,14 @@
 runner (ops.plan_batch), on the CPU: the same rows, tiles, merge list, partition size and flags,
 bit for bit, over seeded random batches that mix decode rows, prefill runs of every length,
 shared prefixes (with members whose tables end inside the prefix), positions that hide part of
-the context, block sizes 1-32, head dims with and without a tile kernel, and given or chosen
-partition sizes."""
+the context, block sizes 1-32, head dims with and without a tile kernel, given or chosen
+partition sizes, and float32 or bfloat16 pools."""
 
 from __future__ import annotations
 
 import numpy as np
 import pytest
+import torch
 
 from paged_kv_serving_amd import _native, ops
 
@@ -17,7 +18,9 @@ def _same(a: ops.BatchPlan, b: ops.BatchPlan) -> None:
     assert np.array_equal(np.asarray(a.rows, np.int32).reshape(-1, 2), b.rows), "rows"
     assert np.array_equal(np.asarray(a.tiles, np.int32).reshape(-1, 4), b.tiles), "tiles"
     assert np.array_equal(np.asarray(a.merge, np.int32), b.merge), "merge"
-    assert (a.partition_size, a.shared_kv, a.short_rows) == (b.partition_size, b.shared_kv, b.short_rows)
+    assert (a.partition_size, a.shared_kv, a.short_rows, a.dominant_tiles) == (
+        b.partition_size, b.shared_kv, b.short_rows, b.dominant_tiles
+    )
 
 
 def random_batch(seed: int):
@@ -80,13 +83,16 @@ def random_batch(seed: int):
 @pytest.mark.parametrize("seed", range(300))
 def test_the_native_planner_matches_the_python_planner(seed) -> None:
     case = random_batch(seed)
+    kv = torch.bfloat16 if seed % 2 else torch.float32
     want = ops.plan_batch(
         case["query_seq"], case["head_dim"], case["num_heads"], case["tables"], case["context_lens"],
         case["block_size"], partition_size=case["partition_size"], query_positions=case["query_positions"],
+        kv_dtype=kv,
     )  # fmt: skip
     got = ops.plan_batch_native(
         case["query_seq"], case["head_dim"], case["num_heads"], case["tables"], case["context_lens"],
         case["block_size"], partition_size=case["partition_size"], query_positions=case["query_positions"],
+        kv_dtype=kv,
     )  # fmt: skip
     _same(want, got)
 
@@ -149,4 +155,7 @@ def test_small_buffers_grow_and_bad_arguments_are_refused() -> None:
     seq = np.asarray([0, 5], np.int32)  # sequence 5 does not exist
     ctx = np.asarray([10], np.int32)
     assert lib.pkv_plan_batch(seq.ctypes.data, None, 2, tables.ctypes.data, 256, ctx.ctypes.data, 1, 16, 32, 128,
-                              0, 8, None, 0, None, 0, None, 0, counts.ctypes.data, launch.ctypes.data) == -1  # fmt: skip
+                              0, 0, 8, None, 0, None, 0, None, 0, counts.ctypes.data, launch.ctypes.data) == -1  # fmt: skip
+    seq = np.asarray([0], np.int32)
+    assert lib.pkv_plan_batch(seq.ctypes.data, None, 1, tables.ctypes.data, 256, ctx.ctypes.data, 1, 16, 32, 128,
+                              7, 0, 8, None, 0, None, 0, None, 0, counts.ctypes.data, launch.ctypes.data) == -1  # fmt: skip
