@@ -24,7 +24,8 @@ tile_blocks 8, plus the runner.py:195-196 append) on a bounded sample of the sam
 single-threaded BLAS as the reference pins it.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--partition P] [--no-cpu]
-       python bench.py --config {1,3,4,5}   (the other BASELINE.json configurations)
+       python bench.py --config {1,3,4,5}   (the other BASELINE.json configurations;
+                                         --config 3 --kv bf16: its shape on bfloat16 pools)
        python bench.py --micro              (the reference's published micro-benchmarks)
 """
 
@@ -56,6 +57,8 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--partition", type=int, default=0, help="keys per partition (0: default)")
     parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--kv", choices=("f32", "bf16"), default="f32",
+                        help="config 3's K/V pool type (the configuration itself is float32)")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     parser.add_argument("--cpu-seqs", type=int, default=64, help="sequences in the CPU sample")
     parser.add_argument("--cpu-repeats", type=int, default=5, help="timed CPU steps (median)")
@@ -411,7 +414,8 @@ def config3(args) -> dict:
 
     from paged_kv_serving_amd.workloads import mixed_batch
 
-    batch = mixed_batch(seed=args.seed, device=torch.device("cuda", 0))
+    kv = torch.bfloat16 if args.kv == "bf16" else torch.float32
+    batch = mixed_batch(seed=args.seed, device=torch.device("cuda", 0), kv_dtype=kv)
     offsets = batch.host_positions[batch.host_seq < 8].reshape(8, -1)[:, 0]
     # causal prefill FLOPs: each chunk row i at offset o sees o + i + 1 keys; QK^T and PV, 2 each
     visible = sum(int((o + np.arange(1, 513)).sum()) for o in offsets)
@@ -431,11 +435,12 @@ def config3(args) -> dict:
             **rope,
         }
 
+    pool = "bf16 K/V (fp32 arithmetic)" if args.kv == "bf16" else "fp32"
     return run_attention_config(
         args, batch, dtype="f32", extra=extra,
         metric="mixed ragged batch: query tokens/s, attention GB/s and append GB/s (config 3)",
         workload="config3 mixed: 8 prefill chunks x 512 tokens at offsets U[0,2048] + 120 decode "
-        "rows ctx U[256,4096], 32x128 fp32, block 16, 40000-block shuffled pool; step = append "
+        f"rows ctx U[256,4096], 32x128 {pool}, block 16, 40000-block shuffled pool; step = append "
         "4216 tokens + one ragged attention call (MFMA tiles for chunks, row pass for decode)",
     )  # fmt: skip
 
@@ -455,12 +460,13 @@ def prefill_tiles_alone_ms(args, batch) -> float:
     block = batch.key_cache.shape[1]
     mixed = ops.plan_batch(
         batch.host_seq, dim, heads, batch.host_tables, batch.host_context, block,
-        partition_size=args.partition, query_positions=batch.host_positions,
+        partition_size=args.partition, query_positions=batch.host_positions, kv_dtype=batch.key_cache.dtype,
     )  # fmt: skip
     chunk_rows = int((mixed.tiles[:, 0] + mixed.tiles[:, 1]).max())
     host = ops.plan_batch(
         batch.host_seq[:chunk_rows], dim, heads, batch.host_tables, batch.host_context, block,
         partition_size=args.partition, query_positions=batch.host_positions[:chunk_rows],
+        kv_dtype=batch.key_cache.dtype,
     )  # fmt: skip
     if host.rows.shape[0] != 0 or int(host.tiles[:, 1].sum()) != chunk_rows:
         raise RuntimeError("the prefill chunks are not the batch's first rows")
