@@ -89,7 +89,7 @@ def test_random_batch_through_the_planner_matches_the_oracle(device, seed) -> No
         rows = np.nonzero(seq_of == s)[0]
         want[rows] = paged_attention(q[rows], positions[rows], kc, vc, table, int(ctx), scale)
     host = ops.plan_batch(seq_of, dim, heads, tables, contexts, block, partition_size=partition,
-                          query_positions=positions)  # fmt: skip
+                          query_positions=positions, kv_dtype=kv)  # fmt: skip
     width = max(len(t) for t in tables)
     padded = np.full((len(tables), width), -3, dtype=np.int32)  # padding is never read
     for i, t in enumerate(tables):
@@ -102,4 +102,4 @@ def test_random_batch_through_the_planner_matches_the_oracle(device, seed) -> No
         scale, max_context_len=int(contexts.max()), plan=ops.upload_batch_plan(host, device),
     ).cpu().numpy()  # fmt: skip
     err = float(np.max(np.abs(got - want)))
-    assert err < FP32_TOL, (seed, err, host.tiles.shape[0], host.partition_size)
+    assert err < FP32_TOL, (seed, err, host.tiles.shape[0], host.partition_size, host.dominant_tiles)
