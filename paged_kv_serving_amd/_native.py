@@ -179,8 +179,9 @@ _BOUND = False
 
 def bound_host():
     """:func:`host` with the library's entry points bound into it (``_pkvhost.bind``), so its
-    ``plan``, ``paged_attention``, ``paged_attention_append`` and ``copy_blocks`` call
-    ``libpkv.so`` directly. Binding loads the library (it must be built)."""
+    ``plan``, ``paged_attention``, ``paged_attention_append``, ``copy_blocks``, ``rms_norm``,
+    ``silu_mul`` and ``rope_append`` call ``libpkv.so`` directly. Binding loads the library (it
+    must be built)."""
     global _BOUND
     ext = host()
     if not _BOUND:
@@ -189,7 +190,9 @@ def bound_host():
             if not _BOUND:
                 address = lambda fn: ctypes.cast(fn, ctypes.c_void_p).value  # noqa: E731
                 ext.bind(address(lib.pkv_plan_batch), address(lib.pkv_paged_attention),
-                         address(lib.pkv_paged_attention_append), address(lib.pkv_copy_blocks))  # fmt: skip
+                         address(lib.pkv_paged_attention_append), address(lib.pkv_copy_blocks),
+                         address(lib.pkv_rms_norm), address(lib.pkv_silu_mul),
+                         address(lib.pkv_rope_append))  # fmt: skip
                 _BOUND = True
     return ext
 

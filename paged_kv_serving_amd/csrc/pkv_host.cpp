@@ -39,13 +39,15 @@
 //       pkv_copy_blocks launch (ops.independent_groups): a copy starts a new group when it
 //       reads a block an earlier copy of the group writes, or writes a block an earlier copy of
 //       the group reads or writes.
-//   bind(plan_batch, paged_attention, paged_attention_append, copy_blocks)
-//       Takes the addresses of those libpkv.so entry points (include/pkv.h), so the three calls
-//       below reach the library without ctypes' per-argument conversions.
+//   bind(plan_batch, paged_attention, paged_attention_append, copy_blocks, rms_norm, silu_mul,
+//        rope_append)
+//       Takes the addresses of those libpkv.so entry points (include/pkv.h), so the calls below
+//       reach the library without ctypes' per-argument conversions.
 //   plan(query_seq, query_positions | None, tables, contexts, block_size, num_heads, head_dim,
 //        kv_dtype, partition_size, min_tile_rows, rows, tiles, merge, counts, launch) -> int
 //       pkv_plan_batch on NumPy buffers; returns its PKV_* code.
-//   paged_attention(...), paged_attention_append(...), copy_blocks(...) -> int
+//   paged_attention(...), paged_attention_append(...), copy_blocks(...), rms_norm(...),
+//   silu_mul(...), rope_append(...) -> int
 //       The entry points of the same names, with every pointer, stream and handle passed as a
 //       Python int (0 for NULL) in the order of their C declarations; returns the PKV_* code.
 //
@@ -592,6 +594,9 @@ decltype(&pkv_plan_batch) g_plan_batch = nullptr;
 decltype(&pkv_paged_attention) g_paged_attention = nullptr;
 decltype(&pkv_paged_attention_append) g_paged_attention_append = nullptr;
 decltype(&pkv_copy_blocks) g_copy_blocks = nullptr;
+decltype(&pkv_rms_norm) g_rms_norm = nullptr;
+decltype(&pkv_silu_mul) g_silu_mul = nullptr;
+decltype(&pkv_rope_append) g_rope_append = nullptr;
 
 bool bound(const void* fn) {
   if (fn != nullptr) return true;
@@ -605,10 +610,12 @@ T* ptr(unsigned long long address) {
 }
 
 PyObject* bind(PyObject*, PyObject* args) {
-  unsigned long long plan, attention, attention_append, copy;
-  if (!PyArg_ParseTuple(args, "KKKK", &plan, &attention, &attention_append, &copy)) return nullptr;
-  if (plan == 0 || attention == 0 || attention_append == 0 || copy == 0) {
-    PyErr_SetString(PyExc_ValueError, "bind() needs four non-null entry points");
+  unsigned long long plan, attention, attention_append, copy, norm, gate, rope;
+  if (!PyArg_ParseTuple(args, "KKKKKKK", &plan, &attention, &attention_append, &copy, &norm, &gate, &rope)) {
+    return nullptr;
+  }
+  if (plan == 0 || attention == 0 || attention_append == 0 || copy == 0 || norm == 0 || gate == 0 || rope == 0) {
+    PyErr_SetString(PyExc_ValueError, "bind() needs seven non-null entry points");
     return nullptr;
   }
   g_plan_batch = reinterpret_cast<decltype(g_plan_batch)>(static_cast<uintptr_t>(plan));
@@ -616,6 +623,9 @@ PyObject* bind(PyObject*, PyObject* args) {
   g_paged_attention_append =
       reinterpret_cast<decltype(g_paged_attention_append)>(static_cast<uintptr_t>(attention_append));
   g_copy_blocks = reinterpret_cast<decltype(g_copy_blocks)>(static_cast<uintptr_t>(copy));
+  g_rms_norm = reinterpret_cast<decltype(g_rms_norm)>(static_cast<uintptr_t>(norm));
+  g_silu_mul = reinterpret_cast<decltype(g_silu_mul)>(static_cast<uintptr_t>(gate));
+  g_rope_append = reinterpret_cast<decltype(g_rope_append)>(static_cast<uintptr_t>(rope));
   Py_RETURN_NONE;
 }
 
@@ -709,6 +719,53 @@ PyObject* copy_blocks(PyObject*, PyObject* args) {
   return PyLong_FromLong(rc);
 }
 
+PyObject* rms_norm(PyObject*, PyObject* args) {
+  unsigned long long out, hidden, delta, weight, stream;
+  long long out_stride, hidden_stride, delta_stride, rows;
+  int dim, device;
+  float eps;
+  if (!PyArg_ParseTuple(args, "KLKLKLKLifiK", &out, &out_stride, &hidden, &hidden_stride, &delta, &delta_stride,
+                        &weight, &rows, &dim, &eps, &device, &stream)) {
+    return nullptr;
+  }
+  if (!bound(reinterpret_cast<const void*>(g_rms_norm))) return nullptr;
+  const int rc = g_rms_norm(ptr<float>(out), out_stride, ptr<float>(hidden), hidden_stride, ptr<const float>(delta),
+                            delta_stride, ptr<const float>(weight), rows, dim, eps, device, ptr<void>(stream));
+  return PyLong_FromLong(rc);
+}
+
+PyObject* silu_mul(PyObject*, PyObject* args) {
+  unsigned long long out, gate, up, stream;
+  long long out_stride, in_stride, rows;
+  int width, device;
+  if (!PyArg_ParseTuple(args, "KLKKLLiiK", &out, &out_stride, &gate, &up, &in_stride, &rows, &width, &device,
+                        &stream)) {
+    return nullptr;
+  }
+  if (!bound(reinterpret_cast<const void*>(g_silu_mul))) return nullptr;
+  const int rc = g_silu_mul(ptr<float>(out), out_stride, ptr<const float>(gate), ptr<const float>(up), in_stride,
+                            rows, width, device, ptr<void>(stream));
+  return PyLong_FromLong(rc);
+}
+
+PyObject* rope_append(PyObject*, PyObject* args) {
+  unsigned long long rot, q, k, v, pos, cos_t, sin_t, kp, vp, slots, stream;
+  long long rot_stride, q_stride, k_stride, v_stride, table_rows, nslots, tokens;
+  int dtype, heads, dim, device;
+  if (!PyArg_ParseTuple(args, "KLKKKLLLKKKLKKiLKLiiiK", &rot, &rot_stride, &q, &k, &v, &q_stride, &k_stride,
+                        &v_stride, &pos, &cos_t, &sin_t, &table_rows, &kp, &vp, &dtype, &nslots, &slots, &tokens,
+                        &heads, &dim, &device, &stream)) {
+    return nullptr;
+  }
+  if (!bound(reinterpret_cast<const void*>(g_rope_append))) return nullptr;
+  const int rc = g_rope_append(ptr<float>(rot), rot_stride, ptr<const float>(q), ptr<const float>(k),
+                               ptr<const float>(v), q_stride, k_stride, v_stride, ptr<const int64_t>(pos),
+                               ptr<const float>(cos_t), ptr<const float>(sin_t), table_rows, ptr<void>(kp),
+                               ptr<void>(vp), static_cast<pkv_dtype>(dtype), nslots, ptr<const int64_t>(slots),
+                               tokens, heads, dim, device, ptr<void>(stream));
+  return PyLong_FromLong(rc);
+}
+
 PyMethodDef kMethods[] = {
     {"gather", gather, METH_VARARGS, "Flatten a batch: tokens, positions, slots, lengths, contexts, logits rows."},
     {"prefix_order_rows", prefix_order_rows, METH_VARARGS, "prefix_order from the block-table arena's rows."},
@@ -720,6 +777,9 @@ PyMethodDef kMethods[] = {
     {"paged_attention_append", paged_attention_append, METH_VARARGS,
      "pkv_paged_attention_append with integer pointers."},
     {"copy_blocks", copy_blocks, METH_VARARGS, "pkv_copy_blocks with integer pointers."},
+    {"rms_norm", rms_norm, METH_VARARGS, "pkv_rms_norm with integer pointers."},
+    {"silu_mul", silu_mul, METH_VARARGS, "pkv_silu_mul with integer pointers."},
+    {"rope_append", rope_append, METH_VARARGS, "pkv_rope_append with integer pointers."},
     {nullptr, nullptr, 0, nullptr},
 };
 

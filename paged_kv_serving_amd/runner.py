@@ -677,24 +677,46 @@ class ModelRunner:
         heads, dim, d_model, ff = config.n_heads, config.head_dim, config.d_model, config.d_ff
         eps = config.norm_eps
         hidden = w.embedding[step.tensor("tokens")]
-        rope_positions, slots = step.tensor("rope_positions"), step.tensor("slots")
         attended = torch.empty((total, heads, dim), dtype=torch.float32, device=self.device)
+        # The per-layer kernels go through _pkvhost with raw addresses: every tensor below is a
+        # contiguous float32 matrix this method allocated (or a projection's output), so the
+        # shapes ops.rms_norm / silu_mul / rope_append check hold by construction.
+        host, device, stream = self._host, self._device_index, ops._stream(self._device_index)
+        row = heads * dim  # = d_model
         # normed holds the RMSNorm of the running hidden state with the next norm's weights;
         # each residual add is fused into the norm that follows it (model.py:256-264).
-        normed = ops.rms_norm(hidden, w.layers[0][0] if w.layers else w.final_norm, eps)
+        normed = torch.empty((total, d_model), dtype=torch.float32, device=self.device)
+
+        def norm(weight: torch.Tensor, delta: torch.Tensor | None) -> None:
+            rc = host.rms_norm(normed.data_ptr(), d_model, hidden.data_ptr(), d_model,
+                               0 if delta is None else delta.data_ptr(), d_model, weight.data_ptr(), total,
+                               d_model, eps, device, stream)  # fmt: skip
+            _native.check(rc, "pkv_rms_norm")
+
+        norm(w.layers[0][0] if w.layers else w.final_norm, None)
+        positions_at, slots_at = step.ptr(step.rope_at), step.ptr(step.slots_at)
+        num_slots = self.num_blocks * self.block_size
         for index, (_, qkv, out_proj, ffn_norm, gate_up, down) in enumerate(w.layers):
-            fused = (normed @ qkv).view(total, 3, heads, dim)
+            fused = normed @ qkv  # [T, 3 * d_model]: q | k | v per token
             # RoPE on q (in place) and k, and the append of k and v, in one kernel
             # (reference model.py:251-252 then runner.py:195-196).
-            queries = ops.rope_append(
-                self._keys[index], self._values[index], fused[:, 0], fused[:, 1], fused[:, 2],
-                rope_positions, w.cos, w.sin, slots, out=fused[:, 0],
+            base = fused.data_ptr()
+            rc = host.rope_append(
+                base, 3 * row, base, base + 4 * row, base + 8 * row, 3 * row, 3 * row, 3 * row, positions_at,
+                w.cos.data_ptr(), w.sin.data_ptr(), w.cos.shape[0], self._keys.data_ptr() + index * self._layer_bytes,
+                self._values.data_ptr() + index * self._layer_bytes, self._kv_code, num_slots, slots_at, total,
+                heads, dim, device, stream,
             )  # fmt: skip
+            _native.check(rc, "pkv_rope_append")
+            queries = fused.view(total, 3, heads, dim)[:, 0]
             self._attention(step, index, queries, attended)
-            ops.rms_norm(hidden, ffn_norm, eps, delta=attended.view(total, d_model) @ out_proj, out=normed)
-            gated = ops.silu_mul(normed @ gate_up, ff)
-            following = w.layers[index + 1][0] if index + 1 < len(w.layers) else w.final_norm
-            ops.rms_norm(hidden, following, eps, delta=gated @ down, out=normed)
+            norm(ffn_norm, attended.view(total, d_model) @ out_proj)
+            gate = normed @ gate_up  # [T, 2 * d_ff]: gate | up
+            gated = torch.empty((total, ff), dtype=torch.float32, device=self.device)
+            rc = host.silu_mul(gated.data_ptr(), ff, gate.data_ptr(), gate.data_ptr() + 4 * ff, 2 * ff, total, ff,
+                               device, stream)  # fmt: skip
+            _native.check(rc, "pkv_silu_mul")
+            norm(w.layers[index + 1][0] if index + 1 < len(w.layers) else w.final_norm, gated @ down)
 
         if not step.num_wanted:
             return [], None

@@ -180,3 +180,22 @@ def test_the_bound_planner_matches_the_ctypes_planner() -> None:
         assert np.array_equal(merge, want.merge) and partition == want.partition_size
         assert bool(flags & _native.PKV_ATTN_SHARED_KV) == want.shared_kv
         assert bool(flags & _native.PKV_ATTN_SHORT_ROWS) == want.short_rows
+
+
+def test_the_bound_model_ops_reach_the_library_and_check_their_arguments() -> None:
+    """_pkvhost.rms_norm / silu_mul / rope_append pass their arguments to pkv_rms_norm /
+    pkv_silu_mul / pkv_rope_append unchanged: empty calls succeed and malformed ones are refused,
+    both before any device work (so this runs without a GPU)."""
+    host = _native.bound_host()
+    ok, einval = _native.PKV_OK, _native.PKV_EINVAL
+    one = 16  # an address never dereferenced: every call below returns first
+    assert host.rms_norm(0, 4, 0, 4, 0, 0, 0, 0, 4, 1e-5, 0, 0) == ok  # no rows
+    assert host.rms_norm(one, 4, one, 4, 0, 0, one, 1, 0, 1e-5, 0, 0) == einval  # dim 0
+    assert host.rms_norm(one, 3, one, 4, 0, 0, one, 1, 4, 1e-5, 0, 0) == einval  # out stride < dim
+    assert host.rms_norm(one, 4, one, 4, 0, 0, one, 1, 4, -1.0, 0, 0) == einval  # eps < 0
+    assert host.silu_mul(0, 4, 0, 0, 8, 0, 4, 0, 0) == ok
+    assert host.silu_mul(one, 4, one, one, 3, 1, 4, 0, 0) == einval  # input stride < width
+    rope = [one, 64, one, one, one, 64, 64, 64, one, one, one, 16, one, one, 0, 100, one, 2, 2, 32, 0, 0]
+    assert host.rope_append(*rope[:17], 0, *rope[18:]) == ok  # no tokens
+    assert host.rope_append(*rope[:19], 31, *rope[20:]) == einval  # odd head_dim
+    assert host.rope_append(*rope[:14], 7, *rope[15:]) == einval  # unknown pool dtype
