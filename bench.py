@@ -364,7 +364,8 @@ def config2(args) -> dict:
 
 def runner_step_timing(args, batch, *, cow_pairs=None) -> dict:
     """The same step through ``ModelRunner.attend``, as a serving loop runs it: reference-style
-    BatchEntry objects (block tables as tuples), host validation and slots, the block-table arena
+    BatchEntry objects (one per sequence, its consecutive query rows as one chunk; block tables
+    as tuples), host validation and slots, the block-table arena
     update, the host plan (pkv_plan_batch), one metadata copy from pinned memory, the queued
     copy-on-write flush (config 4), the append + attention call, and the synchronisation that
     ends a step. Wall time per step, median; the runner has its own pool of the batch's size and
@@ -382,12 +383,14 @@ def runner_step_timing(args, batch, *, cow_pairs=None) -> dict:
     config = ModelConfig(vocab_size=2, d_model=heads * dim, n_layers=1, n_heads=heads, d_ff=1,
                          max_seq_len=int(batch.max_context_len) + 1)  # fmt: skip
     model = SimpleNamespace(config=config, weights=None, rope=None, attention_scale=float(batch.scale))
-    runner = ModelRunner(model, num_blocks=num_blocks, block_size=block, device=device)
+    runner = ModelRunner(model, num_blocks=num_blocks, block_size=block, device=device, kv_dtype=batch.key_cache.dtype)
     entries = []
-    for t in range(batch.num_queries):
-        s = int(batch.host_seq[t])
-        entries.append(BatchEntry(f"s{s}", (0,), (int(batch.host_positions[t]),),
-                                  tuple(int(b) for b in batch.host_tables[s]), 0))  # fmt: skip
+    seq, pos = batch.host_seq, batch.host_positions
+    starts = np.flatnonzero(np.r_[True, seq[1:] != seq[:-1]])  # runs of one sequence's rows
+    for first, end in zip(starts.tolist(), np.r_[starts[1:], seq.size].tolist()):
+        s = int(seq[first])
+        entries.append(BatchEntry(f"s{s}", (0,) * (end - first), tuple(int(p) for p in pos[first:end]),
+                                  tuple(int(b) for b in batch.host_tables[s]), end - first - 1))  # fmt: skip
     step_batch = ExecutionBatch(tuple(entries))
 
     def step() -> None:
@@ -436,8 +439,14 @@ def config3(args) -> dict:
         }
 
     pool = "bf16 K/V (fp32 arithmetic)" if args.kv == "bf16" else "fp32"
+    def extra_with_runner(result, attention_ms):
+        out = extra(result, attention_ms)
+        out.update(runner_step_timing(args, batch))
+        out["runner_step_over_kernel"] = round(out["runner_step_ms"] / (attention_ms + result["append_us"] * 1e-3), 4)
+        return out
+
     return run_attention_config(
-        args, batch, dtype="f32", extra=extra,
+        args, batch, dtype="f32", extra=extra_with_runner,
         metric="mixed ragged batch: query tokens/s, attention GB/s and append GB/s (config 3)",
         workload="config3 mixed: 8 prefill chunks x 512 tokens at offsets U[0,2048] + 120 decode "
         f"rows ctx U[256,4096], 32x128 {pool}, block 16, 40000-block shuffled pool; step = append "
