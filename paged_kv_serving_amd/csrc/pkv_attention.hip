@@ -259,7 +259,7 @@ __device__ __forceinline__ uint4 load_row(const uint4* p) {
 // One 16-byte pool vector (16 / sizeof(KVT) elements) of a new key or value row, from element
 // `elem` of the append source, in the pool's element type: equal types copy bits, float32 into a
 // bfloat16 pool rounds to nearest even, exactly what pkv_append stores.
-__device__ __forceinline__ uint4 new_row_vector(const Params& a, const void* src, int64_t elem, float) {
+__device__ __forceinline__ uint4 new_row_vector(const Params&, const void* src, int64_t elem, float) {
   return *reinterpret_cast<const uint4*>(static_cast<const float*>(src) + elem);
 }
 __device__ __forceinline__ uint4 new_row_vector(const Params& a, const void* src, int64_t elem, uint16_t) {
@@ -782,7 +782,7 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
 #pragma unroll
   for (int mask = 32; mask > 0; mask >>= 1) wave_full = min(wave_full, __shfl_xor(wave_full, mask));
   wave_full = __builtin_amdgcn_readfirstlane(wave_full);
-  constexpr uint32_t kAllKeys = kKeys == 32 ? 0xffffffffu : (1u << kKeys) - 1u;
+  constexpr uint32_t kAllKeys = static_cast<uint32_t>((uint64_t{1} << kKeys) - 1u);
 
   // One key tile's scores st -> probabilities pr, updating the running reference and sum. A key
   // counts when it is below the lane's limit and its bit in kmask is set.
@@ -1071,7 +1071,7 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
 #pragma unroll
   for (int mask = 32; mask > 0; mask >>= 1) wave_full = min(wave_full, __shfl_xor(wave_full, mask));
   wave_full = __builtin_amdgcn_readfirstlane(wave_full);
-  constexpr uint32_t kAllKeys = kKeys == 32 ? 0xffffffffu : (1u << kKeys) - 1u;
+  constexpr uint32_t kAllKeys = static_cast<uint32_t>((uint64_t{1} << kKeys) - 1u);
   __syncthreads();  // s_table ready
 
   // Table entry of key kpos (clamped into the window; callers discard it when kpos is out).
