@@ -71,6 +71,9 @@ namespace {
 #ifndef PKV_ATTN_OVERLAP
 #define PKV_ATTN_OVERLAP 1
 #endif
+// Launch order of an overlapped call: 0 = the tile pass first (on the second stream), 1 = the
+// row pass first. Measured on config 3's mixed call: 1.437-1.439 ms tiles first, 1.478-1.480 ms
+// rows first.
 #ifndef PKV_ATTN_ROWS_FIRST
 #define PKV_ATTN_ROWS_FIRST 0
 #endif
