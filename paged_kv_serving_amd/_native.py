@@ -180,8 +180,9 @@ _BOUND = False
 def bound_host():
     """:func:`host` with the library's entry points bound into it (``_pkvhost.bind``), so its
     ``plan``, ``paged_attention``, ``paged_attention_append``, ``copy_blocks``, ``rms_norm``,
-    ``silu_mul`` and ``rope_append`` call ``libpkv.so`` directly. Binding loads the library (it
-    must be built)."""
+    ``silu_mul`` and ``rope_append`` call ``libpkv.so`` directly, and ``stage`` calls the
+    ``hipMemcpyAsync`` of the HIP runtime ``libpkv.so`` is linked against (looked up through the
+    library's handle, so it is that runtime's). Binding loads the library (it must be built)."""
     global _BOUND
     ext = host()
     if not _BOUND:
@@ -192,7 +193,7 @@ def bound_host():
                 ext.bind(address(lib.pkv_plan_batch), address(lib.pkv_paged_attention),
                          address(lib.pkv_paged_attention_append), address(lib.pkv_copy_blocks),
                          address(lib.pkv_rms_norm), address(lib.pkv_silu_mul),
-                         address(lib.pkv_rope_append))  # fmt: skip
+                         address(lib.pkv_rope_append), address(lib.hipMemcpyAsync))  # fmt: skip
                 _BOUND = True
     return ext
 

@@ -40,9 +40,16 @@
 //       reads a block an earlier copy of the group writes, or writes a block an earlier copy of
 //       the group reads or writes.
 //   bind(plan_batch, paged_attention, paged_attention_append, copy_blocks, rms_norm, silu_mul,
-//        rope_append)
+//        rope_append, memcpy_async)
 //       Takes the addresses of those libpkv.so entry points (include/pkv.h), so the calls below
-//       reach the library without ctypes' per-argument conversions.
+//       reach the library without ctypes' per-argument conversions, and of hipMemcpyAsync as the
+//       HIP runtime that libpkv.so is linked against exports it.
+//   stage(parts64, parts32, host, device_address, stream) -> list of byte offsets | None
+//       A runner call's metadata transfer: the int64 arrays of the list parts64, then the int32
+//       arrays of parts32, packed back to back into the pinned uint8 buffer `host` and copied to
+//       device_address with one hipMemcpyAsync on `stream`. Returns each part's byte offset, or
+//       None (nothing written) when `host` is too small; the caller keeps the device buffer at
+//       least as large as `host`.
 //   plan(query_seq, query_positions | None, tables, contexts, block_size, num_heads, head_dim,
 //        kv_dtype, partition_size, min_tile_rows, rows, tiles, merge, counts, launch) -> int
 //       pkv_plan_batch on NumPy buffers; returns its PKV_* code.
@@ -60,6 +67,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <unordered_set>
 #include <vector>
@@ -597,6 +605,11 @@ decltype(&pkv_copy_blocks) g_copy_blocks = nullptr;
 decltype(&pkv_rms_norm) g_rms_norm = nullptr;
 decltype(&pkv_silu_mul) g_silu_mul = nullptr;
 decltype(&pkv_rope_append) g_rope_append = nullptr;
+// hipMemcpyAsync by its C signature (hipError_t and hipMemcpyKind are int-sized enums, hipStream_t
+// a pointer), so this host-only extension needs no HIP headers.
+using MemcpyAsyncFn = int (*)(void* dst, const void* src, size_t bytes, int kind, void* stream);
+MemcpyAsyncFn g_memcpy_async = nullptr;
+constexpr int kHostToDevice = 1;  // hipMemcpyHostToDevice
 
 bool bound(const void* fn) {
   if (fn != nullptr) return true;
@@ -610,12 +623,14 @@ T* ptr(unsigned long long address) {
 }
 
 PyObject* bind(PyObject*, PyObject* args) {
-  unsigned long long plan, attention, attention_append, copy, norm, gate, rope;
-  if (!PyArg_ParseTuple(args, "KKKKKKK", &plan, &attention, &attention_append, &copy, &norm, &gate, &rope)) {
+  unsigned long long plan, attention, attention_append, copy, norm, gate, rope, memcpy_async;
+  if (!PyArg_ParseTuple(args, "KKKKKKKK", &plan, &attention, &attention_append, &copy, &norm, &gate, &rope,
+                        &memcpy_async)) {
     return nullptr;
   }
-  if (plan == 0 || attention == 0 || attention_append == 0 || copy == 0 || norm == 0 || gate == 0 || rope == 0) {
-    PyErr_SetString(PyExc_ValueError, "bind() needs seven non-null entry points");
+  if (plan == 0 || attention == 0 || attention_append == 0 || copy == 0 || norm == 0 || gate == 0 || rope == 0 ||
+      memcpy_async == 0) {
+    PyErr_SetString(PyExc_ValueError, "bind() needs eight non-null entry points");
     return nullptr;
   }
   g_plan_batch = reinterpret_cast<decltype(g_plan_batch)>(static_cast<uintptr_t>(plan));
@@ -626,7 +641,65 @@ PyObject* bind(PyObject*, PyObject* args) {
   g_rms_norm = reinterpret_cast<decltype(g_rms_norm)>(static_cast<uintptr_t>(norm));
   g_silu_mul = reinterpret_cast<decltype(g_silu_mul)>(static_cast<uintptr_t>(gate));
   g_rope_append = reinterpret_cast<decltype(g_rope_append)>(static_cast<uintptr_t>(rope));
+  g_memcpy_async = reinterpret_cast<MemcpyAsyncFn>(static_cast<uintptr_t>(memcpy_async));
   Py_RETURN_NONE;
+}
+
+PyObject* stage(PyObject*, PyObject* args) {
+  PyObject *p64_o, *p32_o, *host_o;
+  unsigned long long device_address, stream;
+  if (!PyArg_ParseTuple(args, "O!O!OKK", &PyList_Type, &p64_o, &PyList_Type, &p32_o, &host_o, &device_address,
+                        &stream)) {
+    return nullptr;
+  }
+  if (!bound(reinterpret_cast<const void*>(g_memcpy_async))) return nullptr;
+  const Py_ssize_t n64 = PyList_GET_SIZE(p64_o), n32 = PyList_GET_SIZE(p32_o);
+  Buf<uint8_t> host;
+  std::unique_ptr<Buf<int64_t>[]> b64(new Buf<int64_t>[n64]);
+  std::unique_ptr<Buf<int32_t>[]> b32(new Buf<int32_t>[n32]);
+  if (!host.get(host_o, "host")) return nullptr;
+  Py_ssize_t bytes = 0;
+  for (Py_ssize_t i = 0; i < n64; ++i) {
+    if (!b64[i].get(PyList_GET_ITEM(p64_o, i), "an int64 part", false)) return nullptr;
+    bytes += 8 * b64[i].size();
+  }
+  for (Py_ssize_t i = 0; i < n32; ++i) {
+    if (!b32[i].get(PyList_GET_ITEM(p32_o, i), "an int32 part", false)) return nullptr;
+    bytes += 4 * b32[i].size();
+  }
+  if (bytes > host.size()) Py_RETURN_NONE;
+  if (bytes > 0 && device_address == 0) {
+    PyErr_SetString(PyExc_ValueError, "stage() needs a device buffer");
+    return nullptr;
+  }
+  PyObject* offsets = PyList_New(n64 + n32);
+  if (offsets == nullptr) return nullptr;
+  uint8_t* base = host.data();
+  Py_ssize_t at = 0;
+  for (Py_ssize_t i = 0; i < n64 + n32; ++i) {
+    const bool wide = i < n64;
+    const void* src = wide ? static_cast<const void*>(b64[i].data()) : static_cast<const void*>(b32[i - n64].data());
+    const Py_ssize_t len = wide ? 8 * b64[i].size() : 4 * b32[i - n64].size();
+    PyObject* offset = PyLong_FromSsize_t(at);
+    if (offset == nullptr) {
+      Py_DECREF(offsets);
+      return nullptr;
+    }
+    PyList_SET_ITEM(offsets, i, offset);
+    if (len > 0) std::memcpy(base + at, src, static_cast<size_t>(len));
+    at += len;
+  }
+  if (bytes > 0) {
+    const int rc = g_memcpy_async(reinterpret_cast<void*>(static_cast<uintptr_t>(device_address)), base,
+                                  static_cast<size_t>(bytes), kHostToDevice,
+                                  reinterpret_cast<void*>(static_cast<uintptr_t>(stream)));
+    if (rc != 0) {
+      Py_DECREF(offsets);
+      PyErr_Format(PyExc_RuntimeError, "hipMemcpyAsync of the call's metadata failed (hipError_t %d)", rc);
+      return nullptr;
+    }
+  }
+  return offsets;
 }
 
 PyObject* plan(PyObject*, PyObject* args) {
@@ -780,6 +853,7 @@ PyMethodDef kMethods[] = {
     {"rms_norm", rms_norm, METH_VARARGS, "pkv_rms_norm with integer pointers."},
     {"silu_mul", silu_mul, METH_VARARGS, "pkv_silu_mul with integer pointers."},
     {"rope_append", rope_append, METH_VARARGS, "pkv_rope_append with integer pointers."},
+    {"stage", stage, METH_VARARGS, "Pack a call's metadata into pinned memory and copy it to the device."},
     {nullptr, nullptr, 0, nullptr},
 };
 

@@ -157,50 +157,41 @@ def shared_prefix_order(entries, block_size: int) -> list[int] | None:
 class _Staging:
     """One call's integer metadata, sent in one asynchronous copy from pinned host memory.
 
-    The sections (int64 first, then int32, each 8-byte aligned) are written into a pinned host
-    buffer and copied to a device buffer of the same layout on the runner's stream; the host does
-    not wait for the copy. Before a later call rewrites the host buffer it waits for the copy that
+    The sections (the int64 ones first, 8-byte aligned, then the int32 ones) are packed into a
+    pinned host buffer and copied to a device buffer of the same layout on the runner's stream by
+    one C++ call (``_pkvhost.stage``: the packing and one ``hipMemcpyAsync``); the host does not
+    wait for the copy. Before a later call rewrites the host buffer it waits for the copy that
     last read it (an event), which has normally long finished. The device buffer is rewritten by
     the next call's copy, which the stream orders after this call's kernels."""
 
-    def __init__(self, device: torch.device) -> None:
+    def __init__(self, device: torch.device, host_ext) -> None:
         self.device = device
+        self._ext = host_ext
         self.host: torch.Tensor | None = None
         self.dev: torch.Tensor | None = None
         self.base = 0  # device address of self.dev
         self.done = torch.cuda.Event()
         self.pending = False
+        self._host_np = np.zeros(0, dtype=np.uint8)
 
     def send(self, parts64: list[np.ndarray], parts32: list[np.ndarray]) -> list[int]:
-        """Copy ``parts64`` then ``parts32`` to the device; returns each part's byte offset in the
-        device buffer (see :meth:`tensor` and :attr:`base`)."""
-        n64 = sum(p.size for p in parts64)
-        n32 = sum(p.size for p in parts32)
-        nbytes = 8 * n64 + 4 * n32 + 8
+        """Copy ``parts64`` (int64 arrays) then ``parts32`` (int32 arrays) to the device; returns
+        each part's byte offset in the device buffer (see :meth:`tensor` and :attr:`base`)."""
         if self.pending:
             self.done.synchronize()
-        if self.host is None or self.host.numel() < nbytes:
-            size = max(nbytes, 2 * (0 if self.host is None else self.host.numel()), 1 << 16)
+        stream = torch.cuda.current_stream(self.device)
+        while True:
+            offsets = self._ext.stage(parts64, parts32, self._host_np, self.base, stream.cuda_stream)
+            if offsets is not None:
+                break
+            nbytes = 8 * sum(p.size for p in parts64) + 4 * sum(p.size for p in parts32)
+            size = max(nbytes, 2 * self._host_np.size, 1 << 16)
             self.host = torch.empty(size, dtype=torch.uint8, pin_memory=True)
             self.dev = torch.empty(size, dtype=torch.uint8, device=self.device)
             self.base = self.dev.data_ptr()
             self._host_np = self.host.numpy()
-        host = self._host_np
-        off32 = 8 * n64
-        if parts64:
-            np.concatenate(parts64, out=host[:off32].view(np.int64), casting="same_kind")
-        if parts32:
-            np.concatenate(parts32, out=host[off32 : off32 + 4 * n32].view(np.int32), casting="same_kind")
-        self.dev[: off32 + 4 * n32].copy_(self.host[: off32 + 4 * n32], non_blocking=True)
-        self.done.record(torch.cuda.current_stream(self.device))
+        self.done.record(stream)
         self.pending = True
-        offsets, at = [], 0
-        for part in parts64:
-            offsets.append(at)
-            at += 8 * part.size
-        for part in parts32:
-            offsets.append(at)
-            at += 4 * part.size
         return offsets
 
     def tensor(self, offset: int, count: int, dtype: torch.dtype) -> torch.Tensor:
@@ -320,8 +311,8 @@ class ModelRunner:
         self._weights: _DeviceWeights | None = None
         self._tables = BlockTableArena(self.device)
         self._planner = ops.NativePlanner()
-        self._staging = _Staging(self.device)
         self._host = _native.bound_host()
+        self._staging = _Staging(self.device, self._host)
         self._device_index = self.device.index
         self._stats = np.zeros(8, np.int64)
         self._kv_code = ops.kv_dtype_code(kv_dtype)

@@ -199,3 +199,55 @@ def test_the_bound_model_ops_reach_the_library_and_check_their_arguments() -> No
     assert host.rope_append(*rope[:17], 0, *rope[18:]) == ok  # no tokens
     assert host.rope_append(*rope[:19], 31, *rope[20:]) == einval  # odd head_dim
     assert host.rope_append(*rope[:14], 7, *rope[15:]) == einval  # unknown pool dtype
+
+
+def test_stage_packs_the_parts_and_issues_one_host_to_device_copy() -> None:
+    """_pkvhost.stage packs the int64 parts, then the int32 parts, back to back into the pinned
+    buffer and hands the packed bytes to one hipMemcpyAsync (host to device, on the given stream).
+    hipMemcpyAsync is replaced here by a recording stand-in, so this runs without a GPU; the
+    real one is bound again afterwards."""
+    import ctypes
+
+    lib = _native.library()
+    host = _native.bound_host()
+    address = lambda fn: ctypes.cast(fn, ctypes.c_void_p).value  # noqa: E731
+    entry_points = [address(getattr(lib, name)) for name in (
+        "pkv_plan_batch", "pkv_paged_attention", "pkv_paged_attention_append", "pkv_copy_blocks",
+        "pkv_rms_norm", "pkv_silu_mul", "pkv_rope_append")]  # fmt: skip
+    calls = []
+
+    def record(dst, src, size, kind, stream):
+        calls.append((dst, ctypes.string_at(src, size), kind, stream))
+        return 0
+
+    fake = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                            ctypes.c_void_p)(record)  # fmt: skip
+    host.bind(*entry_points, address(fake))
+    try:
+        p64 = [np.arange(3, dtype=np.int64) - 5, np.zeros(0, np.int64), np.array([1 << 40], np.int64)]
+        p32 = [np.array([7, -8, 9], np.int32), np.zeros(0, np.int32), np.array([2**31 - 1], np.int32)]
+        buf = np.full(64, 0xAB, dtype=np.uint8)
+        offsets = host.stage(p64, p32, buf, 4096, 77)
+        want = np.concatenate(p64).tobytes() + np.concatenate(p32).tobytes()
+        assert offsets == [0, 24, 24, 32, 44, 44]
+        assert buf[: len(want)].tobytes() == want and np.all(buf[len(want) :] == 0xAB)
+        assert calls == [(4096, want, 1, 77)]
+        # Too small a buffer: nothing written, nothing copied, None so the caller can grow it.
+        small = np.zeros(len(want) - 1, np.uint8)
+        assert host.stage(p64, p32, small, 4096, 77) is None and not small.any() and len(calls) == 1
+        # Nothing to send: offsets only, no copy.
+        assert host.stage([np.zeros(0, np.int64)], [], np.zeros(0, np.uint8), 0, 0) == [0]
+        assert len(calls) == 1
+        with pytest.raises(TypeError):  # a part of the wrong width
+            host.stage([np.zeros(2, np.int32)], [], buf, 4096, 77)
+        with pytest.raises(ValueError, match="contiguous"):  # a part that is not contiguous
+            host.stage([np.arange(8, dtype=np.int64)[::2]], [], buf, 4096, 77)
+        with pytest.raises(ValueError):  # no device buffer for a non-empty copy
+            host.stage(p64, p32, buf, 0, 77)
+        fail = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                ctypes.c_void_p)(lambda *args: 1)  # fmt: skip
+        host.bind(*entry_points, address(fail))
+        with pytest.raises(RuntimeError, match="hipMemcpyAsync"):
+            host.stage(p64, p32, buf, 4096, 77)
+    finally:
+        host.bind(*entry_points, address(lib.hipMemcpyAsync))
