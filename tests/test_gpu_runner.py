@@ -484,6 +484,45 @@ def test_attend_appends_and_attends_like_the_reference_runner(device, seed, shar
     assert worst < 1e-5
 
 
+def test_attend_metadata_of_growing_and_shrinking_batches(device) -> None:
+    """One runner's calls whose metadata grows past the first staging buffer (64 KiB: a
+    3,000-token prefill chunk sends 72 KiB of int64 sections alone) and shrinks again: every
+    call's slots and outputs match the oracle, so each call read its own sections."""
+    from oracle.attention import paged_attention
+    from oracle.runner import append as oracle_append, slots_for
+
+    rng = np.random.default_rng(11)
+    config = ModelConfig(vocab_size=16, d_model=64, n_layers=1, n_heads=2, d_ff=32, max_seq_len=4096)
+    model = LanguageModel(config, random_weights(config, seed=11))
+    block, num_blocks = 16, 600
+    runner = ModelRunner(model, num_blocks=num_blocks, block_size=block, device=device)
+    keys = rng.standard_normal((num_blocks, block, 2, 32)).astype(np.float32)
+    values = rng.standard_normal((num_blocks, block, 2, 32)).astype(np.float32)
+    runner.key_cache[0].copy_(torch.from_numpy(keys))
+    runner.value_cache[0].copy_(torch.from_numpy(values))
+    perm = [int(b) for b in rng.permutation(num_blocks)]
+    small = (BatchEntry("a", (1,), (40,), tuple(perm[:3]), 0), BatchEntry("b", (2,), (7,), tuple(perm[3:4]), 0))
+    long_table = tuple(perm[4:4 + 3000 // block + 1])
+    large = small + (BatchEntry("c", tuple(i % 15 + 1 for i in range(3000)), tuple(range(3000)), long_table, 2999),)
+    for entries in (small, large, small, large):
+        batch = ExecutionBatch(entries)
+        total = batch.num_tokens
+        q, k, v = (rng.standard_normal((total, 2, 32)).astype(np.float32) for _ in range(3))
+        out = runner.attend(batch, *(torch.from_numpy(a).to(device) for a in (q, k, v))).cpu().numpy()
+        slots = [s for e in entries for s in slots_for(e.seq_id, e.positions, e.block_table, block)]
+        oracle_append(keys, values, slots, k, v)
+        assert np.array_equal(runner.key_cache[0].cpu().numpy(), keys)
+        assert np.array_equal(runner.value_cache[0].cpu().numpy(), values)
+        offset = 0
+        for entry in entries:
+            n = len(entry.token_ids)
+            want = paged_attention(q[offset : offset + n], np.asarray(entry.positions), keys, values,
+                                   np.asarray(entry.block_table), entry.context_len, 32**-0.5)  # fmt: skip
+            assert float(np.max(np.abs(out[offset : offset + n] - want))) < 1e-5, (total, entry.seq_id)
+            offset += n
+    assert runner._staging.host.numel() > 1 << 16
+
+
 @pytest.mark.parametrize("flush", ["block_view", "execute"])
 def test_queued_copies_with_dependencies_land_in_order(device, models, flush) -> None:
     """Copies queued by copy_block run as batched launches of independent groups: a chain
