@@ -293,7 +293,13 @@ int pkv_paged_attention_noalloc(float* out, const float* queries, int64_t query_
  * sits at query_positions[t]. Preconditions, which the caller checks: each sequence has exactly
  * one query row in the call, that row's position is below its context_len and below
  * max_context_len, and slot_mapping[t] is the slot the block table gives that position (as in
- * runner.py:149-159). A slot outside the pool is not written, as in pkv_append.
+ * runner.py:149-159). A slot outside the pool is not written, as in pkv_append. No row may read a
+ * block another row writes: the block holding each row's new slot must occur exactly once among
+ * the blocks every row reads (table entries [0, ceil(visible length / block_size)) of each row's
+ * sequence), namely in its own row's table at that position. A written key reaches only its own
+ * row, so a second reader of the block (the same sequence twice, tables sharing the block being
+ * written, a table naming it twice) would race with the write; such a batch takes pkv_append
+ * followed by pkv_paged_attention, which the Python runner chooses by this rule.
  */
 int pkv_paged_attention_append(
     float* out, const float* queries, int64_t query_token_stride, const int32_t* query_positions,

@@ -39,6 +39,15 @@
 //       pkv_copy_blocks launch (ops.independent_groups): a copy starts a new group when it
 //       reads a block an earlier copy of the group writes, or writes a block an earlier copy of
 //       the group reads or writes.
+//   exclusive_writes(rows, contexts, host, block_size, marks) -> bool
+//       Whether a batch of single-token entries at their last positions (entry e: arena row
+//       rows[e], context contexts[e], so it writes position contexts[e] - 1) may append inside
+//       the attention call: True when each written block occurs exactly once among the blocks
+//       every entry reads (host[rows[e]][0 .. ceil(contexts[e] / B))), which is its own writer's
+//       entry for that position. Otherwise some row reads a slot another row (or its own row,
+//       through a repeated table entry) writes in the same step, and only an append that
+//       completes before attention reads it as the reference does (runner.py:195-212). `marks`
+//       is an int32 buffer with one zero per pool block; it is left all zero.
 //   bind(plan_batch, paged_attention, paged_attention_append, copy_blocks, rms_norm, silu_mul,
 //        rope_append, memcpy_async)
 //       Takes the addresses of those libpkv.so entry points (include/pkv.h), so the calls below
@@ -597,6 +606,69 @@ done:
   return result;
 }
 
+PyObject* exclusive_writes(PyObject*, PyObject* args) {
+  PyObject *rows_o, *contexts_o, *host_o, *marks_o;
+  long long block_size;
+  if (!PyArg_ParseTuple(args, "OOOLO", &rows_o, &contexts_o, &host_o, &block_size, &marks_o)) return nullptr;
+  Buf<int32_t> rows, contexts, host, marks;
+  if (!rows.get(rows_o, "rows", false) || !contexts.get(contexts_o, "contexts", false) ||
+      !host.get(host_o, "host", false) || !marks.get(marks_o, "marks")) {
+    return nullptr;
+  }
+  const Py_ssize_t count = rows.size();
+  const Py_ssize_t num_rows = host.dim(0), width = host.dim(1);
+  if (host.ndim() != 2 || contexts.size() < count || block_size < 1) {
+    PyErr_SetString(PyExc_ValueError, "exclusive_writes buffers disagree");
+    return nullptr;
+  }
+  const int64_t num_blocks = marks.size();
+  int32_t* mark = marks.data();
+  // The visible blocks of entry e, [0, ceil(context / B)), clamped to the row; -1 on a bad row.
+  auto visible = [&](Py_ssize_t e, const int32_t** table) -> int64_t {
+    const int32_t row = rows.data()[e];
+    const int64_t ctx = contexts.data()[e];
+    if (row < 0 || row >= num_rows || ctx < 1) return -1;
+    *table = host.data() + static_cast<int64_t>(row) * width;
+    return std::min<int64_t>((ctx + block_size - 1) / block_size, width);
+  };
+  // 1. Flag every written block (the block of position context - 1).
+  bool ok = true;
+  std::vector<int32_t> written;
+  written.reserve(count);
+  for (Py_ssize_t e = 0; e < count; ++e) {
+    const int32_t* table = nullptr;
+    const int64_t nb = visible(e, &table);
+    const int64_t index = nb < 0 ? -1 : (contexts.data()[e] - 1) / block_size;
+    if (index < 0 || index >= nb) {
+      ok = false;  // a row the kernels cannot place: take the general path, which reports it
+      break;
+    }
+    const int32_t w = table[index];
+    if (w < 0 || w >= num_blocks) continue;  // outside the pool: no row reads or writes it
+    if (mark[w] != 0) {
+      ok = false;  // two rows write one block
+      break;
+    }
+    mark[w] = 1;
+    written.push_back(w);
+  }
+  // 2. Count the occurrences of flagged blocks among every entry's visible blocks: each written
+  // block must occur once, in its writer's own table.
+  for (Py_ssize_t e = 0; e < count && ok; ++e) {
+    const int32_t* table = nullptr;
+    const int64_t nb = visible(e, &table);
+    for (int64_t i = 0; i < nb; ++i) {
+      const int32_t b = table[i];
+      if (b >= 0 && b < num_blocks && mark[b] != 0 && ++mark[b] > 2) {
+        ok = false;
+        break;
+      }
+    }
+  }
+  for (int32_t w : written) mark[w] = 0;
+  return PyBool_FromLong(ok);
+}
+
 // Entry points of libpkv.so, bound once by bind().
 decltype(&pkv_plan_batch) g_plan_batch = nullptr;
 decltype(&pkv_paged_attention) g_paged_attention = nullptr;
@@ -844,6 +916,8 @@ PyMethodDef kMethods[] = {
     {"prefix_order_rows", prefix_order_rows, METH_VARARGS, "prefix_order from the block-table arena's rows."},
     {"arena_update", arena_update, METH_VARARGS, "One step of the block-table arena."},
     {"cow_groups", cow_groups, METH_VARARGS, "Flatten block copies and split them into independent groups."},
+    {"exclusive_writes", exclusive_writes, METH_VARARGS,
+     "True when no decode row reads a block another row (or its own, elsewhere) writes."},
     {"bind", bind, METH_VARARGS, "Bind the libpkv.so entry points the calls below use."},
     {"plan", plan, METH_VARARGS, "pkv_plan_batch on NumPy buffers."},
     {"paged_attention", paged_attention, METH_VARARGS, "pkv_paged_attention with integer pointers."},

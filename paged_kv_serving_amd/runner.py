@@ -317,6 +317,7 @@ class ModelRunner:
         self._stats = np.zeros(8, np.int64)
         self._kv_code = ops.kv_dtype_code(kv_dtype)
         self._pairs = np.zeros(512, np.int64)
+        self._marks = np.zeros(num_blocks, np.int32)  # one per pool block, for exclusive_writes
         self._workspace: torch.Tensor | None = None
         _native.init_device(self._device_index)  # the library's overlap stream on this device
         self._per_token = (np.zeros(1024, np.int64), np.zeros(1024, np.int64), np.zeros(1024, np.int64))
@@ -372,13 +373,15 @@ class ModelRunner:
         """Launch every queued copy-on-write copy, in order. Returns the number of copies."""
         if not self._pending:
             return 0
-        pending, self._pending = self._pending, []
+        pending = self._pending
         sizes, flat = self._cow_groups(pending)
         start = 0
         for size in sizes:
             pairs = torch.from_numpy(flat[2 * start : 2 * (start + size)].copy()).view(-1, 2)
             ops.copy_blocks(self._keys, self._values, pairs.to(self.device, non_blocking=True))
             start += size
+        # Dequeued only once every group is enqueued (a failed launch leaves them queued).
+        self._pending = []
         return len(pending)
 
     def _cow_groups(self, pending: list[tuple[int, int]]) -> tuple[list[int], np.ndarray]:
@@ -530,8 +533,10 @@ class ModelRunner:
             bool(flags & _native.PKV_ATTN_SHORT_ROWS), bool(flags & _native.PKV_ATTN_DOMINANT_TILES),
         )  # fmt: skip
         # Queued copy-on-write pairs travel in the same copy and run before this step's kernels.
+        # They leave the queue only once every group is enqueued: if the copy or a launch
+        # raises, the next call (or flush) issues them again (a group's copies read no block the
+        # group writes, so running a group twice leaves what running it once does).
         sizes, flat = self._cow_groups(self._pending) if self._pending else ([], None)
-        self._pending = []
         parts64 = [tokens, rope_positions, slots, update.index, wanted]
         if sizes:
             parts64.append(flat)
@@ -555,13 +560,21 @@ class ModelRunner:
                                             size, layers, num_blocks, block_elems, self._device_index, stream)  # fmt: skip
                 _native.check(rc, "pkv_copy_blocks")
                 start += size
+            self._pending = []
         if update.index.size:
             self._tables.apply(staging.tensor(index_at, update.index.size, torch.int64),
                                staging.tensor(values_at, update.values.size, torch.int32))  # fmt: skip
         else:
             self._tables.apply_nothing()
         # One token per entry: each is a decode row at its last position (context = position + 1).
-        decode_only = plan_tiles.shape[0] == 0 and len(entries) == total
+        # Its append may ride inside the attention call only when no other row reads the block it
+        # writes: the fused kernel hands a written key to its own row alone, while the reference
+        # writes every slot before any attention (runner.py:195-212). A sequence twice in one
+        # batch, or tables that share the block being written, take the append-then-attention
+        # path.
+        decode_only = plan_tiles.shape[0] == 0 and len(entries) == total and self._host.exclusive_writes(
+            rows, context, self._tables.host, self.block_size, self._marks
+        )  # fmt: skip
         return _Step(
             total=total, staging=staging, tokens_at=tokens_at, rope_at=rope_at, slots_at=slots_at,
             logits_at=logits_at, qpos_at=qpos_at, qseq_at=qseq_at, contexts_at=context_at, plan_rows_at=rows_at,

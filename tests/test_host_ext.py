@@ -251,3 +251,59 @@ def test_stage_packs_the_parts_and_issues_one_host_to_device_copy() -> None:
             host.stage(p64, p32, buf, 4096, 77)
     finally:
         host.bind(*entry_points, address(lib.hipMemcpyAsync))
+
+
+def exclusive_by_brute_force(tables, contexts, block_size, num_blocks) -> bool:
+    """Each written block (that of position context - 1) occurs once among all visible blocks."""
+    visible = [b for t, c in zip(tables, contexts) for b in t[: -(-c // block_size)]]
+    for table, ctx in zip(tables, contexts):
+        written = table[(ctx - 1) // block_size]
+        if 0 <= written < num_blocks and visible.count(written) != 1:
+            return False
+    return True
+
+
+def exclusive(tables, contexts, block_size, num_blocks) -> bool:
+    width = max(len(t) for t in tables)
+    host = np.zeros((len(tables) + 3, width + 2), np.int32)  # arena rows in scrambled order
+    rows = np.random.default_rng(len(tables)).permutation(host.shape[0])[: len(tables)].astype(np.int32)
+    for row, table in zip(rows, tables):
+        host[row, : len(table)] = table
+    marks = np.zeros(num_blocks, np.int32)
+    got = ext.exclusive_writes(rows, np.asarray(contexts, np.int32), host, block_size, marks)
+    assert not marks.any(), "the marks buffer is left all zero"
+    return got
+
+
+def test_exclusive_writes_decides_when_the_decode_append_may_be_fused() -> None:
+    """ModelRunner fuses a decode batch's append into attention only when no row reads a block
+    another row writes (the reference writes every slot first, runner.py:195-212)."""
+    private = [(0, 1, 2), (3, 4), (5,)]
+    assert exclusive(private, [40, 20, 3], 16, 8)
+    # the same sequence twice (positions p and p + 1): the first row's block is read by the second
+    assert not exclusive([(0, 1, 2), (0, 1, 2)], [40, 41], 16, 8)
+    # two tables share the block being written (a partially filled shared block without COW)
+    assert not exclusive([(0, 1, 2), (3, 2)], [40, 20], 16, 8)
+    # a shared *earlier* block is read by both, but nobody writes it: still exclusive
+    assert exclusive([(0, 1, 2), (0, 4)], [40, 20], 16, 8)
+    # a table naming its written block twice reads the written slot at another position too
+    assert not exclusive([(2, 1, 2)], [40], 16, 8)
+    # two rows writing one block
+    assert not exclusive([(0, 7), (1, 7)], [20, 25], 16, 8)
+    # blocks past the visible ones do not count
+    assert exclusive([(0, 1, 5), (5, 6)], [20, 20], 16, 8)
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_exclusive_writes_matches_the_brute_force_rule(seed) -> None:
+    rng = np.random.default_rng(seed)
+    block = int(rng.choice([1, 4, 16]))
+    num_blocks = int(rng.integers(8, 200))
+    tables, contexts = [], []
+    for _ in range(int(rng.integers(1, 30))):
+        ctx = int(rng.integers(1, 6 * block + 1))
+        need = -(-ctx // block) + int(rng.integers(0, 3))
+        # a few ids past the pool, which no pass reads
+        tables.append(tuple(int(b) for b in rng.integers(0, num_blocks + 3, need)))
+        contexts.append(ctx)
+    assert exclusive(tables, contexts, block, num_blocks) == exclusive_by_brute_force(tables, contexts, block, num_blocks)
