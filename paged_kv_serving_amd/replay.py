@@ -36,7 +36,7 @@ from paged_kv_serving_amd.kvcache import KVCacheManager, PrefixReuse
 from paged_kv_serving_amd.prefix_cache import PrefixCache
 from paged_kv_serving_amd.sequence import Request, Sequence
 
-__all__ = ["ReplayMismatch", "ReplayResult", "Trace", "TraceReplay", "digest_ints", "weights_sha256"]
+__all__ = ["ReplayMismatch", "ReplayResult", "StaticReplay", "Trace", "TraceReplay", "digest_ints", "weights_sha256"]
 
 
 class ReplayMismatch(AssertionError):
@@ -77,6 +77,7 @@ class Trace:
     iterations: list[dict]
     summary: dict
     logits: np.ndarray | None = None
+    kind: str = "engine"  # "engine": the continuous Engine; "static": the StaticBatchingEngine
 
     @classmethod
     def load(cls, path: str | Path) -> Trace:
@@ -87,7 +88,7 @@ class Trace:
         rows = path.with_name(path.stem + "_logits.npy")
         logits = np.load(rows) if rows.exists() else None
         fields = ("name", "model", "engine", "requests", "tokens", "events", "iterations", "summary")
-        return cls(**{k: data[k] for k in fields}, logits=logits)
+        return cls(**{k: data[k] for k in fields}, logits=logits, kind=data.get("kind", "engine"))
 
     def model_config(self) -> ModelConfig:
         m = self.model
@@ -298,3 +299,67 @@ class TraceReplay:
             result.rows.extend(logits[e.seq_id] for e in wanted)
         result.row_seqs.extend((e.seq_id, e.context_len) for e in wanted)
         result.iterations += 1
+
+
+class StaticReplay:
+    """Replays a recorded run of the reference's StaticBatchingEngine (static.py:183-226) on a
+    runner. That engine owns no KV-cache manager: each of its ``batch_size`` slots is a fixed
+    contiguous run of ``blocks_per_slot`` blocks (static.py:123-137), every group starts with a
+    prefill padded to its longest prompt whose logits are read at each row's own last prompt
+    token, and its decode rounds re-run finished rows at their last position. The batches are
+    executed as recorded (token ids included, padding and re-runs too) on a runner made as the
+    engine makes its own (static.py:124-126: ``batch_size * blocks_per_slot`` blocks).
+
+    With ``check=True`` every block table must be one whole slot region and every slot mapping
+    the reference's. A row's context in :attr:`ReplayResult.row_seqs` is the position its logits
+    are read at, plus one."""
+
+    def __init__(self, trace: Trace, runner, *, check: bool = True, greedy: bool = False) -> None:
+        if trace.kind != "static":
+            raise ValueError(f"{trace.name} is not a static-batching trace")
+        self.trace = trace
+        self.runner = runner
+        self.check = check
+        self.greedy = greedy
+        self.block_size = trace.engine["block_size"]
+        self.per_slot = trace.engine["blocks_per_slot"]
+
+    def batch(self, iteration: int):
+        from paged_kv_serving_amd.runner import BatchEntry, ExecutionBatch
+
+        entries = []
+        for seq_id, start, tokens, logits_index, table in self.trace.iterations[iteration]["entries"]:
+            first = table[0] if table else -1
+            if self.check and (first % self.per_slot or table != list(range(first, first + self.per_slot))):
+                raise ReplayMismatch(f"{self.trace.name} iteration {iteration}: {seq_id}'s table is not a slot region")
+            entries.append(
+                BatchEntry(
+                    seq_id=seq_id,
+                    token_ids=tuple(tokens),
+                    positions=tuple(range(start, start + len(tokens))),
+                    block_table=tuple(table),
+                    logits_index=None if logits_index < 0 else logits_index,
+                )
+            )
+        return ExecutionBatch(tuple(entries))
+
+    def run(self) -> ReplayResult:
+        from paged_kv_serving_amd.runner import compute_slots
+
+        result = ReplayResult()
+        for iteration, record in enumerate(self.trace.iterations):
+            batch = self.batch(iteration)
+            if self.check:
+                slots = compute_slots(batch.entries, self.block_size).tolist()
+                if slots != record["slots"]:
+                    raise ReplayMismatch(f"{self.trace.name} iteration {iteration}: slot mapping differs")
+            wanted = [e for e in batch.entries if e.logits_index is not None]
+            if self.greedy:
+                tokens = self.runner.execute_greedy(batch)
+                result.greedy.extend(tokens[e.seq_id] for e in wanted)
+            else:
+                logits = self.runner.execute(batch)
+                result.rows.extend(logits[e.seq_id] for e in wanted)
+            result.row_seqs.extend((e.seq_id, e.positions[e.logits_index] + 1) for e in wanted)
+            result.iterations += 1
+        return result

@@ -64,8 +64,11 @@ REFERENCE = Path(os.environ.get("PKV_REFERENCE", "/root/reference"))
 
 
 def _reference():
-    """The reference's engine modules, loaded from its sources."""
+    """The reference's engine modules, loaded from its sources (no bytecode is written next to
+    them: the reference tree stays as it is)."""
     import typing_extensions
+
+    sys.dont_write_bytecode = True
 
     if not hasattr(typing, "Self"):
         typing.Self = typing_extensions.Self
@@ -78,7 +81,8 @@ def _reference():
         module = types.ModuleType(name)
         module.__path__ = [str(path)]
         sys.modules[name] = module
-    names = ("config", "blocks", "kvcache", "model", "runner", "engine", "sequence", "equivalence", "weights")
+    names = ("config", "blocks", "kvcache", "model", "runner", "engine", "sequence", "equivalence", "weights",
+             "static")  # fmt: skip
     return types.SimpleNamespace(**{n: importlib.import_module(f"paged_kv_serving.engine.{n}") for n in names})
 
 
@@ -375,12 +379,111 @@ def sharing(ref, name: str, seed: int, *, block_size: int, num_blocks: int, n_he
     return run_trace(ref, name, model, seed, engine_config, requests)
 
 
+class StaticLog:
+    """The StaticBatchingEngine's runner (static.py:124): runs the reference runner and records
+    every batch as the engine built it (explicit token ids, so the padded prefill and the
+    re-run rows of finished sequences are kept), its slot mapping and its logits rows."""
+
+    def __init__(self, runner) -> None:
+        self.runner = runner
+        self.iterations: list[dict] = []
+        self.rows: list[np.ndarray] = []
+
+    def execute(self, batch):
+        result = self.runner.execute(batch)
+        entries, slots = [], []
+        for entry in batch.entries:
+            start = entry.positions[0]
+            if list(entry.positions) != list(range(start, start + entry.num_tokens)):
+                raise RuntimeError("the static engine ran non-consecutive positions")
+            index = -1 if entry.logits_index is None else entry.logits_index
+            entries.append([entry.seq_id, start, list(entry.token_ids), index, list(entry.block_table)])
+            slots.extend(int(s) for s in self.runner._slots(entry))
+            if entry.logits_index is not None:
+                self.rows.append(np.asarray(result[entry.seq_id], dtype=np.float32).copy())
+        self.iterations.append({"entries": entries, "slots": slots})
+        return result
+
+
+def static_batching(ref):
+    """StaticBatchingEngine (static.py:79-257), the caller of ModelRunner.execute whose batches
+    differ from the continuous engine's: fixed groups of batch_size requests, a prefill padded to
+    the group's longest prompt with logits read at each row's own last prompt token
+    (static.py:188-198), block tables of a whole contiguous slot region however short the
+    context (static.py:135-137), and decode rounds to the group's longest request in which
+    finished rows are re-run at their last position (static.py:204-226). Fourteen requests in
+    groups of six over a block-8 pool; one request ends exactly at max_context_tokens and is then
+    re-run at the region's last slot while a longer request of its group decodes on; two sample
+    at temperature 0.8."""
+    config = ref.config.ModelConfig(vocab_size=96, d_model=128, n_layers=2, n_heads=4, d_ff=256, max_seq_len=256)
+    model = ref.model.LanguageModel(config, ref.model.random_weights(config, seed=21))
+    engine = ref.static.StaticBatchingEngine(model, batch_size=6, max_context_tokens=96, block_size=8,
+                                             clock=lambda: 0.0, sleep=lambda _: None)  # fmt: skip
+    log = StaticLog(engine.runner)
+    engine.runner = log
+    rng = np.random.default_rng(21)
+    requests = []
+    for i in range(14):
+        length = int(rng.integers(4, 41))
+        new = int(rng.integers(2, 25))
+        if i in (3, 4):  # st-3 fills its slot region; st-4 keeps the group running after it
+            length, new = (40, 96 - 40) if i == 3 else (10, 60)
+        requests.append(
+            ref.sequence.Request(
+                request_id=f"st-{i}",
+                prompt_token_ids=tuple(int(t) for t in rng.integers(0, 96, length)),
+                sampling=ref.sequence.SamplingParams(
+                    max_new_tokens=new, temperature=0.8 if i in (5, 9) else 0.0, seed=100 + i
+                ),
+            )
+        )
+    outputs = engine.generate(requests)
+    by_id = {r.request_id: r for r in requests}
+    tokens = {}
+    for out in outputs:
+        seq_id = ref.sequence.new_sequence_id(out.request_id, 0)
+        tokens[seq_id] = [*by_id[out.request_id].prompt_token_ids, *out.token_ids]
+    trace = {
+        "format": 1,
+        "kind": "static",
+        "name": "static_batching",
+        "model": {
+            "vocab_size": config.vocab_size, "d_model": config.d_model, "n_layers": config.n_layers,
+            "n_heads": config.n_heads, "d_ff": config.d_ff, "max_seq_len": config.max_seq_len,
+            "rope_theta": config.rope_theta, "norm_eps": config.norm_eps, "seed": 21,
+            "weights_sha256": weights_sha256(model.weights),
+        },
+        "engine": {
+            "batch_size": engine.batch_size, "max_context_tokens": engine.max_context_tokens,
+            "block_size": engine.block_size, "blocks_per_slot": engine.blocks_per_slot,
+            "num_blocks": engine.runner.runner.num_blocks,
+        },
+        "requests": [
+            {"request_id": r.request_id, "prompt": list(r.prompt_token_ids), "n": r.n, "key_id": r.key_id,
+             "max_new_tokens": r.sampling.max_new_tokens, "temperature": r.sampling.temperature,
+             "seed": r.sampling.seed}
+            for r in requests
+        ],
+        "tokens": tokens,
+        "events": [],
+        "iterations": log.iterations,
+        "summary": {
+            "iterations": len(log.iterations),
+            "logits_rows": len(log.rows),
+            "padding_tokens": engine.total_padding_tokens,
+            "wasted_decode_tokens": engine.total_wasted_decode_tokens,
+        },
+    }  # fmt: skip
+    return trace, np.stack(log.rows)
+
+
 WORKLOADS = {
     "config1": config1,
     "engine_equivalence": engine_equivalence,
     "sharing_b8": lambda ref: sharing(ref, "sharing_b8", 11, block_size=8, num_blocks=40, n_heads=2, d_model=64),
     "sharing_b4": lambda ref: sharing(ref, "sharing_b4", 12, block_size=4, num_blocks=48, n_heads=4, d_model=64),
     "sharing_b16": lambda ref: sharing(ref, "sharing_b16", 13, block_size=16, num_blocks=16, n_heads=2, d_model=256),
+    "static_batching": static_batching,
 }
 
 

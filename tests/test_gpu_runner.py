@@ -548,3 +548,46 @@ def test_queued_copies_with_dependencies_land_in_order(device, models, flush) ->
         want_k[:, 11], want_v[:, 11] = keys[:, 11].cpu().numpy(), values[:, 11].cpu().numpy()
     assert np.array_equal(keys.cpu().numpy(), want_k)
     assert np.array_equal(values.cpu().numpy(), want_v)
+
+
+@pytest.mark.parametrize("case", ["same_sequence_twice", "shared_written_block", "private"])
+def test_decode_rows_reading_a_block_another_row_writes(device, case) -> None:
+    """A decode batch whose rows read a slot another row of the same call writes: the reference
+    writes every new key and value before any attention (runner.py:195-212), so each reader sees
+    the new bytes. The runner then appends before attending instead of fusing the append into the
+    attention call; a batch of private tables still takes the fused path. Outputs match the
+    oracle (1e-5) and the pool matches its append bit for bit."""
+    from oracle.attention import paged_attention
+    from oracle.runner import append as oracle_append, slots_for
+
+    rng = np.random.default_rng(7)
+    config = ModelConfig(vocab_size=16, d_model=256, n_layers=1, n_heads=4, d_ff=32, max_seq_len=4096)
+    model = LanguageModel(config, random_weights(config, seed=7))
+    block, num_blocks = 16, 400
+    perm = [int(b) for b in rng.permutation(num_blocks)]
+    a, b, c = tuple(perm[:40]), tuple(perm[40:70]), tuple(perm[70:75])
+    if case == "same_sequence_twice":  # one sequence at positions p and p + 1 (same block)
+        entries = [BatchEntry("x", (1,), (600,), a, 0), BatchEntry("y", (1,), (300,), b, 0),
+                   BatchEntry("x", (2,), (601,), a, 0)]  # fmt: skip
+    elif case == "shared_written_block":  # y's table ends in the block x writes
+        entries = [BatchEntry("x", (1,), (600,), a, 0), BatchEntry("y", (1,), (70,), c[:4] + (a[37],), 0)]
+    else:
+        entries = [BatchEntry("x", (1,), (600,), a, 0), BatchEntry("y", (1,), (70,), c, 0)]
+    batch = ExecutionBatch(tuple(entries))
+    runner = ModelRunner(model, num_blocks=num_blocks, block_size=block, device=device)
+    keys = rng.standard_normal((num_blocks, block, 4, 64)).astype(np.float32)
+    values = rng.standard_normal((num_blocks, block, 4, 64)).astype(np.float32)
+    runner.key_cache[0].copy_(torch.from_numpy(keys))
+    runner.value_cache[0].copy_(torch.from_numpy(values))
+    q, k, v = (rng.standard_normal((len(entries), 4, 64)).astype(np.float32) for _ in range(3))
+    step = runner._prepare(batch)
+    assert step.decode_only == (case == "private")
+    out = runner.attend(batch, *(torch.from_numpy(t).to(device) for t in (q, k, v))).cpu().numpy()
+    slots = [s for e in entries for s in slots_for(e.seq_id, e.positions, e.block_table, block)]
+    oracle_append(keys, values, slots, k, v)
+    assert np.array_equal(runner.key_cache[0].cpu().numpy(), keys)
+    assert np.array_equal(runner.value_cache[0].cpu().numpy(), values)
+    for i, entry in enumerate(entries):
+        want = paged_attention(q[i : i + 1], np.asarray(entry.positions), keys, values, np.asarray(entry.block_table),
+                               entry.context_len, 64**-0.5)  # fmt: skip
+        assert float(np.max(np.abs(out[i] - want[0]))) < 1e-5, (case, entry.seq_id)

@@ -77,7 +77,7 @@ def test_random_weights_follow_the_reference_draw_order() -> None:
     from oracle.model import random_weights as oracle_weights
     from paged_kv_serving_amd.model import random_weights
 
-    for name in NAMES:
+    for name in (*NAMES, "static_batching"):
         trace = load(name)
         config = trace.model_config()
         want = trace.model["weights_sha256"]
@@ -107,3 +107,53 @@ def test_a_different_allocation_order_is_caught() -> None:
     replay.blocks._ring_v[:] = replay.blocks._ring_v[::-1].copy()  # the same free set, other order
     with pytest.raises(ReplayMismatch, match="table of"):
         replay.run()
+
+
+def static_recompute_gap(model, trace, result) -> float:
+    """Largest |row - reference_forward(tokens)[context - 1]| over a static replay's rows; a row's
+    context ends at the position its logits are read at (a padded prefill row: its last prompt
+    token; a re-run finished row: its last token)."""
+    dense: dict[str, np.ndarray] = {}
+    worst = 0.0
+    for row, (seq_id, context) in zip(result.rows, result.row_seqs):
+        if seq_id not in dense:
+            dense[seq_id] = model.reference_forward(trace.tokens[seq_id])
+        worst = max(worst, float(np.max(np.abs(dense[seq_id][context - 1] - row))))
+    return worst
+
+
+def test_the_static_batching_run_replays_on_the_numpy_runner() -> None:
+    """The reference StaticBatchingEngine's recorded batches (static.py:183-226: padded prefill
+    read at each row's own last prompt token, whole slot regions as tables, finished rows re-run
+    at their last position) on the oracle runner: slots bit for bit, every row within 1e-4 of the
+    reference's recorded row and of the cache-free recompute."""
+    from paged_kv_serving_amd.replay import StaticReplay
+
+    trace = load("static_batching")
+    assert trace.kind == "static"
+    model = trace.language_model()
+    oracle = OracleModel(model.config, model.weights)
+    runner = OracleRunner(oracle, num_blocks=trace.engine["num_blocks"], block_size=trace.engine["block_size"])
+    result = StaticReplay(trace, runner).run()
+    rows = np.stack(result.rows)
+    assert rows.shape == trace.logits.shape == (trace.summary["logits_rows"], model.config.vocab_size)
+    assert float(np.max(np.abs(rows - trace.logits))) < 1e-4
+    assert static_recompute_gap(oracle, trace, result) < 1e-4
+    # what the run is for: padded rows, re-run finished rows, a context that reaches the limit
+    assert trace.summary["padding_tokens"] > 0 and trace.summary["wasted_decode_tokens"] > 0
+    padded = [e for it in trace.iterations for e in it["entries"] if len(e[2]) > 1 and e[3] != len(e[2]) - 1]
+    assert padded, "a prefill row read before its padded end"
+    limit = trace.engine["max_context_tokens"]
+    assert any(e[1] == limit - 1 for it in trace.iterations for e in it["entries"]), "a row at the context limit"
+
+
+def test_a_static_replay_catches_a_wrong_slot_mapping() -> None:
+    from paged_kv_serving_amd.replay import StaticReplay
+
+    trace = load("static_batching")
+    trace.iterations[3]["slots"][0] += 1  # planted mistake in the record
+    model = trace.language_model()
+    runner = OracleRunner(OracleModel(model.config, model.weights), num_blocks=trace.engine["num_blocks"],
+                          block_size=trace.engine["block_size"])  # fmt: skip
+    with pytest.raises(ReplayMismatch, match="iteration 3"):
+        StaticReplay(trace, runner).run()
