@@ -1,7 +1,7 @@
 // Byte-moving kernels of the KV data path: the slot-mapped append and the batched copy-on-write
-// block copy. Both are pure HBM streams: every thread moves one 16-byte vector per step, and the
-// grid is laid out so that one workgroup covers a contiguous 4 KiB (append) or 16 KiB (copy)
-// stretch of a token row or a block.
+// block copy. Both are pure HBM streams: every thread moves one 16-byte vector, and the grid is
+// laid out so that one workgroup covers a contiguous 4 KiB (append) or 8 KiB (copy) stretch of a
+// token row or a block.
 #include "pkv_common.h"
 
 namespace pkv {
@@ -152,21 +152,32 @@ int launch_append(void* key_pool, void* value_pool, int64_t num_slots, const voi
 
 // --------------------------------------------------------------------------------------------
 // Copy-on-write. grid = (pairs * chunks of one block, layers * 2); y = layer * 2 + (0 keys,
-// 1 values). Unit is the widest of 16/4/1 bytes that divides the block; each thread moves
-// kUnroll units, issuing every load before the first store.
+// 1 values). Unit is the widest of 16/4/1 bytes that divides the block; each of kCowThreads
+// threads moves kUnroll units, issuing every load before the first store.
+//
+// Layout measured on MI355X (256 distinct random pairs of 256 KiB float32 blocks, K and V, i.e.
+// 128 MiB read + 128 MiB written; mean of 50 launches, three rounds): one 16-byte unit per
+// thread in 512-thread workgroups (8 KiB each) with non-temporal stores 40.2-40.6 us (6.6-6.7
+// TB/s); the same with ordinary stores 41.6-42.9 us; 256 threads 42.6 us (non-temporal stores)
+// and 44.4 us; 1024 threads 41.0 us; two units per thread 41.4-41.6 us; four units per thread
+// in 256-thread workgroups with non-temporal loads (16 KiB each, the earlier layout) 46.5-47.3
+// us; non-temporal loads cost 2-4 us at every layout. One unit per thread keeps the most
+// independent 16-byte transfers in flight across the chip for a copy this small.
 // --------------------------------------------------------------------------------------------
 #ifndef PKV_COPY_NT_LOAD
-#define PKV_COPY_NT_LOAD 1
+#define PKV_COPY_NT_LOAD 0
 #endif
 #ifndef PKV_COPY_NT_STORE
-#define PKV_COPY_NT_STORE 0
+#define PKV_COPY_NT_STORE 1
 #endif
 #ifndef PKV_COPY_UNROLL
-#define PKV_COPY_UNROLL 4
+#define PKV_COPY_UNROLL 1
 #endif
+#ifndef PKV_COPY_THREADS
+#define PKV_COPY_THREADS 512
+#endif
+constexpr int kCowThreads = PKV_COPY_THREADS;
 
-// The source block is read once, so it is loaded non-temporally; the destination is read again
-// by the same step's attention, so by default it is stored normally and may stay in the caches.
 template <typename UnitT>
 __device__ __forceinline__ UnitT load_unit(const UnitT* p) {
 #if PKV_COPY_NT_LOAD
@@ -185,7 +196,7 @@ __device__ __forceinline__ void store_unit(UnitT* p, UnitT v) {
 }
 
 template <typename UnitT, int kUnroll>
-__global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
+__global__ __launch_bounds__(kCowThreads) void copy_blocks_kernel(
     char* __restrict__ key_pool, char* __restrict__ value_pool, const int64_t* __restrict__ pairs,
     int64_t num_blocks, int64_t block_units, int64_t chunks) {
   const int64_t pair = blockIdx.x / chunks;
@@ -198,16 +209,16 @@ __global__ __launch_bounds__(kCopyThreads) void copy_blocks_kernel(
   UnitT* base = reinterpret_cast<UnitT*>(pool) + layer * num_blocks * block_units;
   const UnitT* from = base + src * block_units;
   UnitT* to = base + dst * block_units;
-  const int64_t first = chunk * (kCopyThreads * kUnroll) + threadIdx.x;
+  const int64_t first = chunk * (kCowThreads * kUnroll) + threadIdx.x;
   UnitT buf[kUnroll];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = first + static_cast<int64_t>(u) * kCopyThreads;
+    const int64_t i = first + static_cast<int64_t>(u) * kCowThreads;
     if (i < block_units) buf[u] = load_unit(from + i);
   }
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int64_t i = first + static_cast<int64_t>(u) * kCopyThreads;
+    const int64_t i = first + static_cast<int64_t>(u) * kCowThreads;
     if (i < block_units) store_unit(to + i, buf[u]);
   }
 }
@@ -217,13 +228,13 @@ int launch_copy(void* key_pool, void* value_pool, const int64_t* pairs, int64_t 
                 int32_t num_layers, int64_t num_blocks, int64_t block_bytes, hipStream_t stream) {
   constexpr int kUnroll = PKV_COPY_UNROLL;
   const int64_t units = block_bytes / static_cast<int64_t>(sizeof(UnitT));
-  const int64_t per_group = static_cast<int64_t>(kCopyThreads) * kUnroll;
+  const int64_t per_group = static_cast<int64_t>(kCowThreads) * kUnroll;
   const int64_t chunks = (units + per_group - 1) / per_group;
   if (chunks * num_pairs > 0x7fffffff || 2 * static_cast<int64_t>(num_layers) > 65535) {
     return PKV_EUNSUPPORTED;
   }
   const dim3 grid(static_cast<uint32_t>(chunks * num_pairs), static_cast<uint32_t>(2 * num_layers));
-  hipLaunchKernelGGL((copy_blocks_kernel<UnitT, kUnroll>), grid, dim3(kCopyThreads), 0, stream,
+  hipLaunchKernelGGL((copy_blocks_kernel<UnitT, kUnroll>), grid, dim3(kCowThreads), 0, stream,
                      static_cast<char*>(key_pool), static_cast<char*>(value_pool), pairs,
                      num_blocks, units, chunks);
   return check_launch();
