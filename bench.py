@@ -23,7 +23,11 @@ oracle's NumPy restatement of the reference path (reference attention.py:42-121 
 tile_blocks 8, plus the runner.py:195-196 append) on a bounded sample of the same workload,
 single-threaded BLAS as the reference pins it.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--partition P] [--no-cpu]
+The default run then times the other BASELINE.json configurations in the same process (configs
+1, 3, 4 and 5, up to 20 steps each) and adds their figures as ``other_configs``; the headline
+``value`` and ``roofline`` stay config 2's.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--partition P] [--no-cpu] [--no-others]
        python bench.py --config {1,3,4,5}   (the other BASELINE.json configurations;
                                          --config 3 --kv bf16: its shape on bfloat16 pools)
        python bench.py --micro              (the reference's published micro-benchmarks)
@@ -60,6 +64,8 @@ def parse() -> argparse.Namespace:
     parser.add_argument("--kv", choices=("f32", "bf16"), default="f32",
                         help="config 3's K/V pool type (the configuration itself is float32)")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    parser.add_argument("--no-others", action="store_true",
+                        help="config 2 only: skip the other configurations of the default run")
     parser.add_argument("--cpu-seqs", type=int, default=64, help="sequences in the CPU sample")
     parser.add_argument("--cpu-repeats", type=int, default=5, help="timed CPU steps (median)")
     parser.add_argument("--micro", action="store_true",
@@ -657,16 +663,24 @@ def config4(args) -> dict:
         "cow_distinct_sources_gbps": round(step.cow_bytes() / (distinct_ms * 1e-3) / 1e9, 1),
         "cow_distinct_sources_frac_of_peak": round(step.cow_bytes() / (distinct_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
     })  # fmt: skip
+    # Attention rates on the distinct blocks read (the roofline's bytes); the rate over the bytes
+    # the tables name (the prefix once per sequence) is kept under its own name, for the record.
+    logical_gbps = result.pop("attention_gbps")
+    result.pop("attention_frac_of_peak")
     result.update({
         "cow_pairs": len(step.host_pairs),
-        "cow_us": round(cow_ms * 1e3, 2),
-        "cow_gbps": round(step.cow_bytes() / (cow_ms * 1e-3) / 1e9, 1),
-        "cow_frac_of_peak": round(step.cow_bytes() / (cow_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        # the workload's copies all read one shared source block: a time, not an HBM rate
+        "cow_shared_source_us": round(cow_ms * 1e3, 2),
         "unique_context_bytes": unique,
-        "attention_unique_gbps": round(unique / (result["attention_ms"] * 1e-3) / 1e9, 1),
-        "note": "attention_gbps counts the shared prefix once per sequence (logical bytes); "
-        "attention_unique_gbps counts distinct blocks; cow_gbps re-reads one cached source block "
-        "256 times, cow_distinct_sources_gbps is the HBM-bound copy rate",
+        "attention_gbps": round(unique_rate, 1),
+        "attention_frac_of_peak": round(unique_rate / HBM_PEAK_GBPS, 4),
+        "attention_table_bytes_gbps": logical_gbps,
+        "note": "attention_gbps / attention_frac_of_peak count each distinct K/V block once "
+        "(unique_context_bytes); attention_table_bytes_gbps counts the shared prefix once per "
+        "sequence, which the caches serve, and is not an HBM rate. cow_shared_source_us times the "
+        "workload's 256 copies of one shared source block (cache-served after its first read); "
+        "cow_distinct_sources_* is the same launch over 256 distinct random sources, the copy's "
+        "HBM rate",
     })  # fmt: skip
     return result
 
@@ -734,6 +748,45 @@ def config1(args) -> dict:
         "reference_published": "1453.36 output tok/s (engine_throughput_24_requests, i5-8500, "
         "bench/results/latest.json:46-53; a different workload, for orientation only)",
     }
+
+
+#: What each other configuration contributes to the default run's ``other_configs`` object.
+OTHER_FIELDS = {
+    3: ("attention_ms", "attention_gbps", "attention_frac_of_peak", "prefill_gflop", "prefill_tiles_alone_ms",
+        "prefill_tiles_alone_tflops", "prefill_tiles_alone_frac_of_fp32_mfma_peak", "append_us", "append_gbps",
+        "rope_append_us", "rope_append_gbps", "runner_step_ms", "runner_step_over_kernel"),
+    4: ("cow_shared_source_us", "cow_distinct_sources_us", "cow_distinct_sources_gbps",
+        "cow_distinct_sources_frac_of_peak", "attention_ms", "attention_gbps", "attention_frac_of_peak",
+        "unique_context_bytes", "runner_step_ms", "runner_step_over_kernel"),
+    5: ("attention_ms", "attention_gbps", "attention_frac_of_peak", "attention_tokens_per_s"),
+    1: ("value", "unit", "ms_per_step", "seconds_per_run", "generated_tokens", "greedy_tokens_equal_reference"),
+}  # fmt: skip
+
+
+def other_configs(args) -> dict:
+    """BASELINE.json's other configurations (configs[0], [2], [3], [4]: config 1 end to end,
+    configs 3, 4 and 5 of one layer), each timed in this process after the headline with up to
+    20 steps, so the default run's line carries them: the fields of ``OTHER_FIELDS`` from each
+    config's own line (``bench.py --config N`` prints all of it), its roofline fraction, and the
+    wall time the config took here."""
+    import torch
+
+    sub = argparse.Namespace(**{**vars(args), "steps": min(args.steps, 20), "warmup": min(args.warmup, 5),
+                                "partition": 0, "kv": "f32"})  # fmt: skip
+    runners = {3: config3, 4: config4, 5: config5, 1: config1}
+    out = {}
+    for number, run in runners.items():
+        start = time.perf_counter()
+        line = run(sub)
+        picked = {key: line[key] for key in OTHER_FIELDS[number] if key in line}
+        if "roofline" in line:
+            picked["roofline_frac"] = line["roofline"]["frac"]
+        picked["workload"] = line["config"]["workload"]
+        picked["wall_s"] = round(time.perf_counter() - start, 2)
+        out[f"config{number}"] = picked
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
 
 
 def _host_timed(function, runs: int, warmup: int = 5) -> dict:
@@ -931,6 +984,8 @@ def main() -> int:
         # The known-size dispatch that calibrates the rocprofv3 FETCH_SIZE/WRITE_SIZE counters.
         peak = copy_peak(torch.device("cuda", 0))
         result["copy_peak_gbps"] = peak["copy_peak_gbps"]
+        if not args.no_others:
+            result["other_configs"] = other_configs(args)
         if not args.no_cpu:
             result["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(result), flush=True)
