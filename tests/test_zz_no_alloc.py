@@ -3,10 +3,12 @@
 It takes pkv_paged_attention's arguments without the workspace and uses the library's static
 per-device scratch instead. Two calls in a row (a mixed batch with MFMA tiles, decode rows and a
 split-context reduce, then a smaller decode batch) must give exactly what pkv_paged_attention
-gives with a caller workspace for the same plan, and match the oracle; the first call runs before
-anything else has touched the library on the device in a fresh process (it then finds the
-device's copy of the scratch itself). A batch whose workspace exceeds the scratch is refused
-before anything is enqueued.
+gives with a caller workspace for the same plan, and match the oracle. Which call finds the
+device's copy of the scratch (hipGetSymbolAddress) depends on the process: run alone in a fresh
+process, this file's first no-alloc call is the library's first attention call on the device and
+finds it itself (nothing before it calls pkv_init: the append is the only library call); after
+other tests, pkv_init has found it already and the call reuses that address. A batch whose
+workspace exceeds the scratch is refused before anything is enqueued.
 """
 
 from __future__ import annotations
@@ -78,6 +80,8 @@ def _oracle_gap(batch, got, seqs) -> float:
 
 
 def test_two_calls_in_a_row_match_the_workspace_entry_point(device) -> None:
+    fresh = device.index not in _native._READY  # nothing has called pkv_init on this device yet
+    print("no-alloc: first attention call of the process" if fresh else "no-alloc: pkv_init ran before", flush=True)
     first = mixed_batch(seed=3, num_prefill=2, chunk=96, offset_high=1500, num_decode=40, decode_low=300,
                         decode_high=3000, heads=8, head_dim=128, num_blocks=8000, device=device)  # fmt: skip
     first.replan(0)
