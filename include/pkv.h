@@ -71,7 +71,9 @@ typedef enum pkv_dtype {
  * row-streaming pass. Idempotent and thread-safe; the resources live until the process ends.
  * Call it once per device before the first attention call that should overlap its passes, and
  * before capturing attention calls into a HIP graph. Without it, calls run both passes one
- * after the other on the caller's stream (same results).
+ * after the other on the caller's stream (same results). Calls whose row pass has fewer than
+ * 2,048 workgroups (row items x head groups) also run both passes on the caller's stream: the
+ * fork and join onto the second stream cost more host time than such a call's device time.
  *
  * No counterpart in the reference (it has no device); the resources replace nothing there.
  */
@@ -378,6 +380,23 @@ int pkv_rms_norm(float* out, int64_t out_stride, float* hidden, int64_t hidden_s
  */
 int pkv_silu_mul(float* out, int64_t out_stride, const float* gate, const float* up,
                  int64_t in_stride, int64_t num_rows, int32_t width, int device, void* stream);
+
+/*
+ * Row gather: out[r, :] = src[index[r], :] for r < num_rows, float32 rows of `width` values;
+ * a row whose index lies outside [0, src_rows) is written as zeros.
+ *
+ * Replaces the two row lookups of the reference's forward pass: the embedding lookup
+ * (src/paged_kv_serving/engine/model.py:262-263, token_embedding[token_ids]) and the choice of
+ * the rows that ask for logits (runner.py:215-227, hidden[wanted]). The runner validates token ids
+ * before the call, as the reference does (runner.py:175-176).
+ *
+ *   out   : float32, row r at r * out_stride (out_stride >= width).
+ *   src   : float32 [src_rows, ...], row i at i * src_stride (src_stride >= width).
+ *   index : int64 [num_rows], device memory.
+ */
+int pkv_gather_rows(float* out, int64_t out_stride, const float* src, int64_t src_stride,
+                    int64_t src_rows, const int64_t* index, int64_t num_rows, int32_t width,
+                    int device, void* stream);
 
 /*
  * Greedy sampling: the argmax of each logits row, on the device.

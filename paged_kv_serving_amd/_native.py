@@ -89,6 +89,7 @@ EXPORTED_SYMBOLS = (
     "pkv_plan_batch",
     "pkv_rms_norm",
     "pkv_silu_mul",
+    "pkv_gather_rows",
 )
 
 
@@ -180,9 +181,10 @@ _BOUND = False
 def bound_host():
     """:func:`host` with the library's entry points bound into it (``_pkvhost.bind``), so its
     ``plan``, ``paged_attention``, ``paged_attention_append``, ``copy_blocks``, ``rms_norm``,
-    ``silu_mul`` and ``rope_append`` call ``libpkv.so`` directly, and ``stage`` calls the
-    ``hipMemcpyAsync`` of the HIP runtime ``libpkv.so`` is linked against (looked up through the
-    library's handle, so it is that runtime's). Binding loads the library (it must be built)."""
+    ``silu_mul``, ``rope_append`` and ``forward`` call ``libpkv.so`` directly, and ``stage`` and
+    ``forward`` call the ``hipMemcpyAsync`` / ``hipGetDevice`` / ``hipSetDevice`` of the HIP
+    runtime ``libpkv.so`` is linked against (looked up through the library's handle, so they are
+    that runtime's). Binding loads the library (it must be built)."""
     global _BOUND
     ext = host()
     if not _BOUND:
@@ -193,7 +195,9 @@ def bound_host():
                 ext.bind(address(lib.pkv_plan_batch), address(lib.pkv_paged_attention),
                          address(lib.pkv_paged_attention_append), address(lib.pkv_copy_blocks),
                          address(lib.pkv_rms_norm), address(lib.pkv_silu_mul),
-                         address(lib.pkv_rope_append), address(lib.hipMemcpyAsync))  # fmt: skip
+                         address(lib.pkv_rope_append), address(lib.hipMemcpyAsync),
+                         address(lib.pkv_gather_rows), address(lib.pkv_greedy_tokens),
+                         address(lib.hipGetDevice), address(lib.hipSetDevice))  # fmt: skip
                 _BOUND = True
     return ext
 
@@ -304,6 +308,10 @@ def _declare(lib: ctypes.CDLL) -> None:
         _ptr, _i64, _ptr, _ptr, _i64, _i64, _i32, _c_int, _ptr,  # out, stride, gate, up, in stride, rows, width, device, stream
     ]
     lib.pkv_silu_mul.restype = _c_int
+    lib.pkv_gather_rows.argtypes = [
+        _ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _i32, _c_int, _ptr,  # out, stride, src, stride, src rows, index, rows, width, device, stream
+    ]
+    lib.pkv_gather_rows.restype = _c_int
 
 
 def library() -> ctypes.CDLL:

@@ -1,6 +1,7 @@
 // The elementwise and row-wise steps of the decoder's forward pass around the KV data path, each
 // one launch instead of a chain of framework kernels: RMSNorm, optionally fused with the residual
-// add that precedes it, and the SwiGLU gate product. The matrix products stay on hipBLASLt.
+// add that precedes it, the SwiGLU gate product, and the row gather of the embedding lookup and
+// of the logits rows. The matrix products are rocBLAS/hipBLASLt GEMMs.
 //
 // Both follow the float32 expressions of the reference model (src/paged_kv_serving/engine/
 // model.py:43-51) operation by operation. Products, quotients and square roots are IEEE float32
@@ -77,8 +78,58 @@ __global__ __launch_bounds__(kGateThreads) void silu_mul_kernel(float* __restric
   }
 }
 
+// out[r] = src[index[r]] (float32 rows of `width`), or zeros when index[r] lies outside
+// [0, src_rows). One wavefront per row; kVec: 16-byte accesses (both row starts aligned).
+template <bool kVec>
+__global__ __launch_bounds__(kNormThreads) void gather_rows_kernel(float* __restrict__ out, int64_t out_stride,
+                                                                    const float* __restrict__ src,
+                                                                    int64_t src_stride,
+                                                                    const int64_t* __restrict__ index,
+                                                                    int64_t num_rows, int32_t width,
+                                                                    int64_t src_rows) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kNormRows + threadIdx.x / kWave;
+  if (row >= num_rows) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t at = index[row];
+  const bool ok = at >= 0 && at < src_rows;
+  float* o = out + row * out_stride;
+  const float* s = src + (ok ? at : 0) * src_stride;
+  if constexpr (kVec) {
+    for (int j = 4 * lane; j < width; j += 4 * kWave) {
+      const float4 v = ok ? *reinterpret_cast<const float4*>(s + j) : make_float4(0.f, 0.f, 0.f, 0.f);
+      *reinterpret_cast<float4*>(o + j) = v;
+    }
+  } else {
+    for (int j = lane; j < width; j += kWave) o[j] = ok ? s[j] : 0.f;
+  }
+}
+
 }  // namespace
 }  // namespace pkv
+
+extern "C" int pkv_gather_rows(float* out, int64_t out_stride, const float* src, int64_t src_stride,
+                               int64_t src_rows, const int64_t* index, int64_t num_rows, int32_t width,
+                               int device, void* stream) {
+  using namespace pkv;
+  if (num_rows < 0 || width < 1 || src_rows < 0 || out_stride < width || src_stride < width) return PKV_EINVAL;
+  if (num_rows == 0) return PKV_OK;
+  if (!out || !src || !index) return PKV_EINVAL;
+  const int64_t blocks = (num_rows + kNormRows - 1) / kNormRows;
+  if (blocks > 0x7fffffff) return PKV_EUNSUPPORTED;
+  DeviceGuard guard(device);
+  if (!guard.ok()) return PKV_EHIP;
+  (void)hipGetLastError();
+  const bool vec = width % 4 == 0 && out_stride % 4 == 0 && src_stride % 4 == 0 && aligned16(out) && aligned16(src);
+  auto s = static_cast<hipStream_t>(stream);
+  if (vec) {
+    hipLaunchKernelGGL(gather_rows_kernel<true>, dim3(static_cast<uint32_t>(blocks)), dim3(kNormThreads), 0, s, out,
+                       out_stride, src, src_stride, index, num_rows, width, src_rows);
+  } else {
+    hipLaunchKernelGGL(gather_rows_kernel<false>, dim3(static_cast<uint32_t>(blocks)), dim3(kNormThreads), 0, s, out,
+                       out_stride, src, src_stride, index, num_rows, width, src_rows);
+  }
+  return check_launch();
+}
 
 extern "C" int pkv_rms_norm(float* out, int64_t out_stride, float* hidden, int64_t hidden_stride,
                             const float* delta, int64_t delta_stride, const float* weight,

@@ -95,3 +95,27 @@ def test_silu_mul_edge_values(device) -> None:
     assert np.isfinite(got[3]) and np.isfinite(got[4]) and got[3] < 0 and got[4] < 0
     assert np.isnan(got[5])
     np.testing.assert_allclose(got[[0, 1, 2, 3, 4, 6, 7]], want[[0, 1, 2, 3, 4, 6, 7]], rtol=1e-6)
+
+
+@pytest.mark.parametrize("width,stride", [(128, 128), (30, 33), (64, 96)])
+def test_gather_rows_picks_rows_and_zeroes_ids_outside_the_table(device, width, stride) -> None:
+    """pkv_gather_rows: out[r] = src[index[r]] (the embedding lookup and the logits rows of the
+    forward pass, model.py:262-263 and runner.py:215-227), zeros for an index outside the table;
+    16-byte accesses when aligned, scalar otherwise."""
+    import torch
+
+    from paged_kv_serving_amd import _native
+
+    rng = np.random.default_rng(width + stride)
+    src = rng.standard_normal((50, stride)).astype(np.float32)
+    index = np.asarray([3, 0, 49, 7, 7, -1, 50, 12], dtype=np.int64)
+    d_src, d_index = _to(device, src), torch.from_numpy(index).to(device)
+    out = torch.full((index.size, width + 3), 5.0, device=device)
+    rc = _native.library().pkv_gather_rows(out.data_ptr(), width + 3, d_src.data_ptr(), stride, 50,
+                                           d_index.data_ptr(), index.size, width, device.index, None)  # fmt: skip
+    assert rc == 0
+    got = out.cpu().numpy()
+    for r, i in enumerate(index):
+        want = src[i, :width] if 0 <= i < 50 else np.zeros(width, np.float32)
+        assert np.array_equal(got[r, :width], want), r
+        assert np.all(got[r, width:] == 5.0)  # nothing past the row's width is written

@@ -98,6 +98,15 @@ def test_bad_arguments_are_refused_before_any_device_work(lib) -> None:
     assert lib.pkv_tile_head_dim_supported(16) == 0
 
 
+def test_gather_rows_arguments_are_refused_before_any_device_work(lib) -> None:
+    fake = ctypes.c_void_p(4096)
+    assert lib.pkv_gather_rows(fake, 8, fake, 8, 10, fake, 0, 8, 0, None) == 0  # no rows: nothing to do
+    assert lib.pkv_gather_rows(fake, 4, fake, 8, 10, fake, 2, 8, 0, None) == -1  # out stride below width
+    assert lib.pkv_gather_rows(fake, 8, fake, 4, 10, fake, 2, 8, 0, None) == -1  # src stride below width
+    assert lib.pkv_gather_rows(fake, 8, fake, 8, 10, fake, 2, 0, 0, None) == -1  # width 0
+    assert lib.pkv_gather_rows(None, 8, fake, 8, 10, fake, 2, 8, 0, None) == -1  # null output
+
+
 def test_rope_append_arguments_are_refused_before_any_device_work(lib) -> None:
     # Placeholder addresses: every call below returns before touching them or the device.
     fake = [ctypes.c_void_p(4096 * (i + 1)) for i in range(9)]
