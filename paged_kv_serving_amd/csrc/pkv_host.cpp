@@ -49,10 +49,23 @@
 //       completes before attention reads it as the reference does (runner.py:195-212). `marks`
 //       is an int32 buffer with one zero per pool block; it is left all zero.
 //   bind(plan_batch, paged_attention, paged_attention_append, copy_blocks, rms_norm, silu_mul,
-//        rope_append, memcpy_async)
+//        rope_append, memcpy_async[, gather_rows, greedy_tokens, get_device, set_device])
 //       Takes the addresses of those libpkv.so entry points (include/pkv.h), so the calls below
-//       reach the library without ctypes' per-argument conversions, and of hipMemcpyAsync as the
-//       HIP runtime that libpkv.so is linked against exports it.
+//       reach the library without ctypes' per-argument conversions, and of hipMemcpyAsync,
+//       hipGetDevice and hipSetDevice as the HIP runtime that libpkv.so is linked against
+//       exports them.
+//   forward(fields, layers, eps, scale) -> None
+//       One ModelRunner iteration's forward pass (the reference's runner.py:189-227 with
+//       model.py:243-264), every launch enqueued from here on `stream` with the device made
+//       current for the call: the embedding rows (pkv_gather_rows), per layer RMSNorm, the QKV
+//       product, RoPE + append, paged attention, the output product with its residual add fused
+//       into the next norm, the [gate | up] product, the SwiGLU gate and the down product; then
+//       the logits rows, their product with the tied embedding, and greedy sampling when an
+//       output address is given. The products are rocBLAS sgemm calls (the rocBLAS the process
+//       has loaded, one handle per device, used by one forward pass at a time). `fields` holds
+//       the integers of the Field enum below (addresses, sizes, the attention plan); `layers`
+//       one tuple of six weight addresses per layer (attn_norm, qkv, out_proj, ffn_norm,
+//       [gate | up], down). Raises RuntimeError naming the first step that failed.
 //   stage(parts64, parts32, host, device_address, stream) -> list of byte offsets | None
 //       A runner call's metadata transfer: the int64 arrays of the list parts64, then the int32
 //       arrays of parts32, packed back to back into the pinned uint8 buffer `host` and copied to
@@ -73,10 +86,13 @@
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
 
+#include <dlfcn.h>
+
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <unordered_set>
 #include <vector>
@@ -677,6 +693,13 @@ decltype(&pkv_copy_blocks) g_copy_blocks = nullptr;
 decltype(&pkv_rms_norm) g_rms_norm = nullptr;
 decltype(&pkv_silu_mul) g_silu_mul = nullptr;
 decltype(&pkv_rope_append) g_rope_append = nullptr;
+decltype(&pkv_gather_rows) g_gather_rows = nullptr;
+decltype(&pkv_greedy_tokens) g_greedy_tokens = nullptr;
+// hipGetDevice / hipSetDevice of the same runtime, by their C signatures.
+using GetDeviceFn = int (*)(int* device);
+using SetDeviceFn = int (*)(int device);
+GetDeviceFn g_get_device = nullptr;
+SetDeviceFn g_set_device = nullptr;
 // hipMemcpyAsync by its C signature (hipError_t and hipMemcpyKind are int-sized enums, hipStream_t
 // a pointer), so this host-only extension needs no HIP headers.
 using MemcpyAsyncFn = int (*)(void* dst, const void* src, size_t bytes, int kind, void* stream);
@@ -696,8 +719,9 @@ T* ptr(unsigned long long address) {
 
 PyObject* bind(PyObject*, PyObject* args) {
   unsigned long long plan, attention, attention_append, copy, norm, gate, rope, memcpy_async;
-  if (!PyArg_ParseTuple(args, "KKKKKKKK", &plan, &attention, &attention_append, &copy, &norm, &gate, &rope,
-                        &memcpy_async)) {
+  unsigned long long gather_rows = 0, greedy = 0, get_device = 0, set_device = 0;
+  if (!PyArg_ParseTuple(args, "KKKKKKKK|KKKK", &plan, &attention, &attention_append, &copy, &norm, &gate, &rope,
+                        &memcpy_async, &gather_rows, &greedy, &get_device, &set_device)) {
     return nullptr;
   }
   if (plan == 0 || attention == 0 || attention_append == 0 || copy == 0 || norm == 0 || gate == 0 || rope == 0 ||
@@ -705,6 +729,10 @@ PyObject* bind(PyObject*, PyObject* args) {
     PyErr_SetString(PyExc_ValueError, "bind() needs eight non-null entry points");
     return nullptr;
   }
+  g_gather_rows = reinterpret_cast<decltype(g_gather_rows)>(static_cast<uintptr_t>(gather_rows));
+  g_greedy_tokens = reinterpret_cast<decltype(g_greedy_tokens)>(static_cast<uintptr_t>(greedy));
+  g_get_device = reinterpret_cast<GetDeviceFn>(static_cast<uintptr_t>(get_device));
+  g_set_device = reinterpret_cast<SetDeviceFn>(static_cast<uintptr_t>(set_device));
   g_plan_batch = reinterpret_cast<decltype(g_plan_batch)>(static_cast<uintptr_t>(plan));
   g_paged_attention = reinterpret_cast<decltype(g_paged_attention)>(static_cast<uintptr_t>(attention));
   g_paged_attention_append =
@@ -911,6 +939,228 @@ PyObject* rope_append(PyObject*, PyObject* args) {
   return PyLong_FromLong(rc);
 }
 
+// --- the forward pass of one iteration ---------------------------------------------------------
+
+// rocBLAS by its C signatures (rocblas_handle is a pointer, rocblas_status and rocblas_operation
+// are int-sized enums, rocblas_int is int32), so this extension needs no ROCm headers. The library
+// is the one already loaded in the process (torch's), found by its soname, else loaded.
+using BlasCreateFn = int (*)(void** handle);
+using BlasSetStreamFn = int (*)(void* handle, void* stream);
+using BlasSgemmFn = int (*)(void* handle, int trans_a, int trans_b, int32_t m, int32_t n, int32_t k,
+                            const float* alpha, const float* a, int32_t lda, const float* b, int32_t ldb,
+                            const float* beta, float* c, int32_t ldc);
+constexpr int kBlasNone = 111;       // rocblas_operation_none
+constexpr int kBlasTranspose = 112;  // rocblas_operation_transpose
+constexpr int kMaxDevices = 64;
+
+struct Blas {
+  BlasCreateFn create = nullptr;
+  BlasSetStreamFn set_stream = nullptr;
+  BlasSgemmFn sgemm = nullptr;
+  void* handles[kMaxDevices] = {};
+  // A device's handle is bound to one stream at a time: its forward passes run one after another.
+  std::mutex device_mu[kMaxDevices];
+};
+Blas g_blas;
+
+bool load_blas() {
+  if (g_blas.sgemm != nullptr) return true;
+  void* lib = dlopen("librocblas.so.5", RTLD_NOW | RTLD_NOLOAD);
+  if (lib == nullptr) lib = dlopen("librocblas.so.5", RTLD_NOW | RTLD_LOCAL);
+  if (lib == nullptr) lib = dlopen("/opt/rocm/lib/librocblas.so.5", RTLD_NOW | RTLD_LOCAL);
+  if (lib == nullptr) {
+    PyErr_Format(PyExc_RuntimeError, "rocBLAS is not available: %s", dlerror());
+    return false;
+  }
+  g_blas.create = reinterpret_cast<BlasCreateFn>(dlsym(lib, "rocblas_create_handle"));
+  g_blas.set_stream = reinterpret_cast<BlasSetStreamFn>(dlsym(lib, "rocblas_set_stream"));
+  g_blas.sgemm = reinterpret_cast<BlasSgemmFn>(dlsym(lib, "rocblas_sgemm"));
+  if (g_blas.create == nullptr || g_blas.set_stream == nullptr || g_blas.sgemm == nullptr) {
+    g_blas.sgemm = nullptr;
+    PyErr_SetString(PyExc_RuntimeError, "rocBLAS lacks rocblas_create_handle / rocblas_set_stream / rocblas_sgemm");
+    return false;
+  }
+  return true;
+}
+
+// Row-major C[m, n] = A[m, k] B[k, n] (B given transposed, as [n, k], when b_transposed), leading
+// dimensions in elements. In rocBLAS's column-major terms: C^T = B^T A^T.
+int gemm(void* handle, int64_t m, int64_t n, int64_t k, const float* a, int64_t lda, const float* b, int64_t ldb,
+         bool b_transposed, float* c, int64_t ldc) {
+  static const float one = 1.f, zero = 0.f;
+  return g_blas.sgemm(handle, b_transposed ? kBlasTranspose : kBlasNone, kBlasNone, static_cast<int32_t>(n),
+                      static_cast<int32_t>(m), static_cast<int32_t>(k), &one, b, static_cast<int32_t>(ldb), a,
+                      static_cast<int32_t>(lda), &zero, c, static_cast<int32_t>(ldc));
+}
+
+// Integer fields of forward()'s first argument, in order.
+enum Field {
+  kDevice, kStream, kTokens, kWanted, kModel, kHeads, kHeadDim, kFf, kVocab,
+  kTokenIds, kRopePositions, kSlots, kLogitsRows,
+  kEmbedding, kFinalNorm, kCos, kSin, kTableRows,
+  kKeyPool, kValuePool, kLayerBytes, kKvDtype, kNumSlots,
+  kHidden, kNormed, kFused, kAttended, kTmp, kGate, kGated, kPicked, kLogits,
+  kQueryPositions, kQuerySeq, kPlanRows, kNumPlanRows, kPlanTiles, kNumTiles, kMerge, kNumMerge,
+  kNumBlocks, kBlockSize, kTables, kTableStride, kContexts, kNumSeqs,
+  kMaxContext, kPartition, kFlags, kWorkspace, kWorkspaceBytes, kGreedyOut,
+  kNumFields
+};
+
+PyObject* forward(PyObject*, PyObject* args) {
+  PyObject *ints_o, *layers_o;
+  float eps, scale;
+  if (!PyArg_ParseTuple(args, "OO!ff", &ints_o, &PyList_Type, &layers_o, &eps, &scale)) return nullptr;
+  for (const void* fn : {reinterpret_cast<const void*>(g_rms_norm), reinterpret_cast<const void*>(g_rope_append),
+                         reinterpret_cast<const void*>(g_paged_attention), reinterpret_cast<const void*>(g_silu_mul),
+                         reinterpret_cast<const void*>(g_gather_rows), reinterpret_cast<const void*>(g_greedy_tokens),
+                         reinterpret_cast<const void*>(g_get_device), reinterpret_cast<const void*>(g_set_device)}) {
+    if (!bound(fn)) return nullptr;
+  }
+  if (!load_blas()) return nullptr;
+  PyObject* ints = PySequence_Fast(ints_o, "forward() takes a sequence of integers");
+  if (ints == nullptr) return nullptr;
+  if (PySequence_Fast_GET_SIZE(ints) != kNumFields) {
+    Py_DECREF(ints);
+    PyErr_Format(PyExc_ValueError, "forward() takes %d integers", static_cast<int>(kNumFields));
+    return nullptr;
+  }
+  int64_t v[kNumFields];
+  for (int i = 0; i < kNumFields; ++i) {
+    PyObject* item = PySequence_Fast_GET_ITEM(ints, i);
+    v[i] = PyLong_AsLongLong(item);
+    if (PyErr_Occurred()) {
+      Py_DECREF(ints);
+      return nullptr;
+    }
+  }
+  Py_DECREF(ints);
+  const Py_ssize_t num_layers = PyList_GET_SIZE(layers_o);
+  std::vector<int64_t> layer(6 * num_layers);
+  for (Py_ssize_t l = 0; l < num_layers; ++l) {
+    PyObject* t = PyList_GET_ITEM(layers_o, l);
+    if (!PyTuple_Check(t) || PyTuple_GET_SIZE(t) != 6) {
+      PyErr_SetString(PyExc_ValueError, "a layer is a tuple of six weight addresses");
+      return nullptr;
+    }
+    for (int j = 0; j < 6; ++j) {
+      layer[6 * l + j] = PyLong_AsLongLong(PyTuple_GET_ITEM(t, j));
+      if (PyErr_Occurred()) return nullptr;
+    }
+  }
+  const int device = static_cast<int>(v[kDevice]);
+  void* stream = ptr<void>(v[kStream]);
+  const int64_t T = v[kTokens], W = v[kWanted], d = v[kModel], ff = v[kFf], vocab = v[kVocab];
+  const int heads = static_cast<int>(v[kHeads]), dim = static_cast<int>(v[kHeadDim]);
+  if (device < 0 || device >= kMaxDevices || T < 1 || W < 0 || d != static_cast<int64_t>(heads) * dim || ff < 1 ||
+      vocab < 1 || 3 * d > INT32_MAX || 2 * ff > INT32_MAX || T > INT32_MAX) {
+    PyErr_SetString(PyExc_ValueError, "forward() sizes are out of range");
+    return nullptr;
+  }
+  auto f = [&](Field i) { return ptr<float>(v[i]); };
+  const char* failed = nullptr;
+  int rc = 0;
+  int previous = -1;
+  if (g_get_device(&previous) != 0 || (previous != device && g_set_device(device) != 0)) {
+    PyErr_Format(PyExc_RuntimeError, "cannot make device %d current", device);
+    return nullptr;
+  }
+  Py_BEGIN_ALLOW_THREADS
+  std::lock_guard<std::mutex> device_lock(g_blas.device_mu[device]);
+  void*& handle = g_blas.handles[device];
+  if (handle == nullptr && g_blas.create(&handle) != 0) {
+    handle = nullptr;
+    failed = "rocblas_create_handle";
+  }
+  if (failed == nullptr && g_blas.set_stream(handle, stream) != 0) failed = "rocblas_set_stream";
+  auto check = [&](int code, const char* what) {
+    if (failed == nullptr && code != 0) {
+      rc = code;
+      failed = what;
+    }
+    return failed == nullptr;
+  };
+  // hidden = embedding[tokens]; normed = rms_norm(hidden) with the first norm's weights
+  float* hidden = f(kHidden);
+  float* normed = f(kNormed);
+  float* fused = f(kFused);
+  float* attended = f(kAttended);
+  float* tmp = f(kTmp);
+  float* gate = f(kGate);
+  float* gated = f(kGated);
+  auto norm = [&](int64_t weight, const float* delta) {
+    return check(g_rms_norm(normed, d, hidden, d, delta, d, ptr<const float>(weight), T, static_cast<int32_t>(d), eps,
+                            device, stream),
+                 "pkv_rms_norm");
+  };
+  if (failed == nullptr) {
+    check(g_gather_rows(hidden, d, ptr<const float>(v[kEmbedding]), d, vocab, ptr<const int64_t>(v[kTokenIds]), T,
+                        static_cast<int32_t>(d), device, stream),
+          "pkv_gather_rows (embedding)");
+  }
+  if (failed == nullptr) norm(num_layers > 0 ? layer[0] : v[kFinalNorm], nullptr);
+  const int64_t row = d;  // heads * head_dim
+  for (Py_ssize_t l = 0; l < num_layers && failed == nullptr; ++l) {
+    const int64_t* w = &layer[6 * l];  // attn_norm, qkv, out_proj, ffn_norm, gate_up, down
+    char* kp = ptr<char>(v[kKeyPool]) + l * v[kLayerBytes];
+    char* vp = ptr<char>(v[kValuePool]) + l * v[kLayerBytes];
+    // fused = normed @ qkv: [T, 3d], q | k | v per token (model.py:248-249)
+    if (!check(gemm(handle, T, 3 * d, d, normed, d, ptr<const float>(w[1]), 3 * d, false, fused, 3 * d), "rocblas_sgemm (qkv)")) break;
+    // RoPE on q (in place) and k, and the append of k and v (model.py:251-252, runner.py:195-196)
+    if (!check(g_rope_append(fused, 3 * row, fused, fused + row, fused + 2 * row, 3 * row, 3 * row, 3 * row,
+                             ptr<const int64_t>(v[kRopePositions]), ptr<const float>(v[kCos]), ptr<const float>(v[kSin]),
+                             v[kTableRows], kp, vp, static_cast<pkv_dtype>(v[kKvDtype]), v[kNumSlots],
+                             ptr<const int64_t>(v[kSlots]), T, heads, dim, device, stream),
+               "pkv_rope_append")) {
+      break;
+    }
+    // attention over the pools (runner.py:198-212)
+    if (v[kNumPlanRows] > 0 || v[kNumTiles] > 0) {
+      if (!check(g_paged_attention(attended, fused, 3 * row, ptr<const int32_t>(v[kQueryPositions]),
+                                   ptr<const int32_t>(v[kQuerySeq]), T, ptr<const int32_t>(v[kPlanRows]), v[kNumPlanRows],
+                                   ptr<const int32_t>(v[kPlanTiles]), v[kNumTiles], ptr<const int32_t>(v[kMerge]),
+                                   v[kNumMerge], kp, vp, static_cast<pkv_dtype>(v[kKvDtype]), v[kNumBlocks],
+                                   static_cast<int32_t>(v[kBlockSize]), ptr<const int32_t>(v[kTables]),
+                                   static_cast<int32_t>(v[kTableStride]), ptr<const int32_t>(v[kContexts]),
+                                   static_cast<int32_t>(v[kNumSeqs]), heads, dim, scale,
+                                   static_cast<int32_t>(v[kMaxContext]), static_cast<int32_t>(v[kPartition]),
+                                   static_cast<int32_t>(v[kFlags]), f(kWorkspace), v[kWorkspaceBytes], device, stream),
+                 "pkv_paged_attention")) {
+        break;
+      }
+    }
+    // hidden += attended @ out_proj, then the feed-forward norm (model.py:283, 256)
+    if (!check(gemm(handle, T, d, d, attended, d, ptr<const float>(w[2]), d, false, tmp, d), "rocblas_sgemm (out_proj)")) break;
+    if (!norm(w[3], tmp)) break;
+    // gated = silu(normed @ gate) * (normed @ up), one product of [gate | up] (model.py:257-258)
+    if (!check(gemm(handle, T, 2 * ff, d, normed, d, ptr<const float>(w[4]), 2 * ff, false, gate, 2 * ff), "rocblas_sgemm (gate_up)")) break;
+    if (!check(g_silu_mul(gated, ff, gate, gate + ff, 2 * ff, T, static_cast<int32_t>(ff), device, stream), "pkv_silu_mul")) break;
+    // hidden += gated @ down, then the next norm (the next layer's attention norm, or the final one)
+    if (!check(gemm(handle, T, d, ff, gated, ff, ptr<const float>(w[5]), d, false, tmp, d), "rocblas_sgemm (down)")) break;
+    norm(l + 1 < num_layers ? layer[6 * (l + 1)] : v[kFinalNorm], tmp);
+  }
+  // logits of the rows that ask for them: normed[rows] @ embedding^T (runner.py:215-227,
+  // model.py:259-261), then greedy sampling when asked
+  if (failed == nullptr && W > 0) {
+    float* picked = f(kPicked);
+    float* logits = f(kLogits);
+    if (check(g_gather_rows(picked, d, normed, d, T, ptr<const int64_t>(v[kLogitsRows]), W, static_cast<int32_t>(d),
+                            device, stream),
+              "pkv_gather_rows (logits rows)") &&
+        check(gemm(handle, W, vocab, d, picked, d, ptr<const float>(v[kEmbedding]), d, true, logits, vocab),
+              "rocblas_sgemm (logits)") &&
+        v[kGreedyOut] != 0) {
+      check(g_greedy_tokens(ptr<int32_t>(v[kGreedyOut]), logits, vocab, W, vocab, device, stream), "pkv_greedy_tokens");
+    }
+  }
+  if (previous != device) g_set_device(previous);
+  Py_END_ALLOW_THREADS
+  if (failed != nullptr) {
+    PyErr_Format(PyExc_RuntimeError, "%s failed (code %d)", failed, rc);
+    return nullptr;
+  }
+  Py_RETURN_NONE;
+}
+
 PyMethodDef kMethods[] = {
     {"gather", gather, METH_VARARGS, "Flatten a batch: tokens, positions, slots, lengths, contexts, logits rows."},
     {"prefix_order_rows", prefix_order_rows, METH_VARARGS, "prefix_order from the block-table arena's rows."},
@@ -928,6 +1178,7 @@ PyMethodDef kMethods[] = {
     {"silu_mul", silu_mul, METH_VARARGS, "pkv_silu_mul with integer pointers."},
     {"rope_append", rope_append, METH_VARARGS, "pkv_rope_append with integer pointers."},
     {"stage", stage, METH_VARARGS, "Pack a call's metadata into pinned memory and copy it to the device."},
+    {"forward", forward, METH_VARARGS, "One iteration's forward pass: rocBLAS products and the library's kernels."},
     {nullptr, nullptr, 0, nullptr},
 };
 

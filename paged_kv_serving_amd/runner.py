@@ -3,19 +3,21 @@
 It owns the K/V pools in HBM, shaped ``[layers, num_blocks, block_size, heads, head_dim]``
 exactly like the reference's NumPy pools (runner.py:112-114), and is both the reference's
 ``EngineExecutor`` (``execute(batch) -> {seq_id: float32[vocab]}``, engine.py:64-73) and its
-``BlockStore`` (``copy_block(src, dst)``, blocks.py:43-48). Per layer of :meth:`execute`:
+``BlockStore`` (``copy_block(src, dst)``, blocks.py:43-48). Per layer of :meth:`execute`, all
+enqueued by one C++ call of the host extension:
 
-    torch (hipBLASLt) : RMSNorm, fused QKV projection
-    pkv_rope_append   : RoPE on q (in place) and k, and the scatter of the rotated keys and the
-                        values into their slots, in one launch
+    pkv_rms_norm        : RMSNorm, with the preceding residual add fused into it
+    rocBLAS sgemm       : the fused QKV projection
+    pkv_rope_append     : RoPE on q (in place) and k, and the scatter of the rotated keys and the
+                          values into their slots, in one launch
     pkv_paged_attention : every query of the ragged batch against its block table in one call:
                           decode rows stream K/V per row, prefill runs go to the fp32 MFMA tile
                           pass, then the split-context reduce when a context spans partitions
-    torch             : output projection, SwiGLU
+    rocBLAS sgemm, pkv_silu_mul : the output projection and the SwiGLU block
 
 Slot mappings are computed on the host with the reference's closed form and validation
 (runner.py:149-159), so they are bit-exact with the reference by construction; they, the
-positions and the block tables reach the device in two small copies per call.
+positions and the changed block-table entries reach the device in one copy per call.
 
 Copy-on-write copies requested through :meth:`copy_block` are queued and flushed as batched
 ``pkv_copy_blocks`` launches before anything reads or writes the pool (the next
@@ -266,6 +268,8 @@ class _DeviceWeights:
         cos, sin = model.rope
         self.cos = up(cos)
         self.sin = up(sin)
+        #: Per layer the six addresses the host extension's forward pass reads.
+        self.addresses = [tuple(t.data_ptr() for t in layer) for layer in self.layers]
 
 
 class ModelRunner:
@@ -319,6 +323,8 @@ class ModelRunner:
         self._pairs = np.zeros(512, np.int64)
         self._marks = np.zeros(num_blocks, np.int32)  # one per pool block, for exclusive_writes
         self._workspace: torch.Tensor | None = None
+        self._forward_ws: torch.Tensor | None = None  # the forward pass's activations
+        self._greedy_out: torch.Tensor | None = None  # its greedy token ids
         _native.init_device(self._device_index)  # the library's overlap stream on this device
         self._per_token = (np.zeros(1024, np.int64), np.zeros(1024, np.int64), np.zeros(1024, np.int64))
         self._per_entry = (np.zeros(256, np.int64), np.zeros(256, np.int32), np.zeros(256, np.int64))
@@ -424,17 +430,17 @@ class ModelRunner:
         names, logits = self._forward(batch)
         if not names:
             return {}
-        host = logits.cpu().numpy()
+        host = logits.cpu().numpy()  # a copy: the next call rewrites the device rows
         return {name: host[i] for i, name in enumerate(names)}
 
     def execute_greedy(self, batch: ExecutionBatch) -> dict[str, int]:
         """:meth:`execute` followed by greedy sampling on the device: the argmax token id of each
         logits row (reference sampling.py:28-30), one int32 per row copied to the host."""
-        names, logits = self._forward(batch)
+        names, tokens = self._forward(batch, greedy=True)
         if not names:
             return {}
-        tokens = ops.greedy_tokens(logits).cpu().numpy()
-        return {name: int(tokens[i]) for i, name in enumerate(names)}
+        picked = tokens.cpu().numpy()
+        return {name: int(picked[i]) for i, name in enumerate(names)}
 
     def _gather(self, entries):
         """One C++ walk over the entries (``_pkvhost.gather``): token ids, positions and slots
@@ -669,60 +675,63 @@ class ModelRunner:
             out[index] = result
         return out
 
-    def _forward(self, batch: ExecutionBatch) -> tuple[list[str], torch.Tensor | None]:
-        """The forward pass of one iteration: (seq ids, device logits [rows, vocab]) of the
-        entries that ask for logits, in batch order."""
+    def _forward(self, batch: ExecutionBatch, *, greedy: bool = False):
+        """The forward pass of one iteration: (seq ids of the entries that ask for logits, in
+        batch order; their device logits [rows, vocab], or with ``greedy`` their argmax token ids,
+        int32 [rows]). Both are views of buffers the next call rewrites.
+
+        Every launch is enqueued by one C++ call (``_pkvhost.forward``): per layer RMSNorm with the
+        residual add fused into it, the QKV product, RoPE + append, paged attention, the output,
+        [gate | up] and down products (rocBLAS) and the SwiGLU gate; then the logits rows and
+        their product with the tied embedding (model.py:243-264, runner.py:189-227)."""
         step = self._prepare(batch)
         if step is None:
             return [], None
         config = self.model.config
-        total = step.total
+        total, wanted = step.total, step.num_wanted
         w = self._device_weights()
-        heads, dim, d_model, ff = config.n_heads, config.head_dim, config.d_model, config.d_ff
-        eps = config.norm_eps
-        hidden = w.embedding[step.tensor("tokens")]
-        attended = torch.empty((total, heads, dim), dtype=torch.float32, device=self.device)
-        # The per-layer kernels go through _pkvhost with raw addresses: every tensor below is a
-        # contiguous float32 matrix this method allocated (or a projection's output), so the
-        # shapes ops.rms_norm / silu_mul / rope_append check hold by construction.
-        host, device, stream = self._host, self._device_index, ops._stream(self._device_index)
-        row = heads * dim  # = d_model
-        # normed holds the RMSNorm of the running hidden state with the next norm's weights;
-        # each residual add is fused into the norm that follows it (model.py:256-264).
-        normed = torch.empty((total, d_model), dtype=torch.float32, device=self.device)
-
-        def norm(weight: torch.Tensor, delta: torch.Tensor | None) -> None:
-            rc = host.rms_norm(normed.data_ptr(), d_model, hidden.data_ptr(), d_model,
-                               0 if delta is None else delta.data_ptr(), d_model, weight.data_ptr(), total,
-                               d_model, eps, device, stream)  # fmt: skip
-            _native.check(rc, "pkv_rms_norm")
-
-        norm(w.layers[0][0] if w.layers else w.final_norm, None)
-        positions_at, slots_at = step.ptr(step.rope_at), step.ptr(step.slots_at)
-        num_slots = self.num_blocks * self.block_size
-        for index, (_, qkv, out_proj, ffn_norm, gate_up, down) in enumerate(w.layers):
-            fused = normed @ qkv  # [T, 3 * d_model]: q | k | v per token
-            # RoPE on q (in place) and k, and the append of k and v, in one kernel
-            # (reference model.py:251-252 then runner.py:195-196).
-            base = fused.data_ptr()
-            rc = host.rope_append(
-                base, 3 * row, base, base + 4 * row, base + 8 * row, 3 * row, 3 * row, 3 * row, positions_at,
-                w.cos.data_ptr(), w.sin.data_ptr(), w.cos.shape[0], self._keys.data_ptr() + index * self._layer_bytes,
-                self._values.data_ptr() + index * self._layer_bytes, self._kv_code, num_slots, slots_at, total,
-                heads, dim, device, stream,
-            )  # fmt: skip
-            _native.check(rc, "pkv_rope_append")
-            queries = fused.view(total, 3, heads, dim)[:, 0]
-            self._attention(step, index, queries, attended)
-            norm(ffn_norm, attended.view(total, d_model) @ out_proj)
-            gate = normed @ gate_up  # [T, 2 * d_ff]: gate | up
-            gated = torch.empty((total, ff), dtype=torch.float32, device=self.device)
-            rc = host.silu_mul(gated.data_ptr(), ff, gate.data_ptr(), gate.data_ptr() + 4 * ff, 2 * ff, total, ff,
-                               device, stream)  # fmt: skip
-            _native.check(rc, "pkv_silu_mul")
-            norm(w.layers[index + 1][0] if index + 1 < len(w.layers) else w.final_norm, gated @ down)
-
-        if not step.num_wanted:
+        d, ff, vocab = config.d_model, config.d_ff, config.vocab_size
+        # One float32 workspace, sections 64-float aligned: hidden, normed, fused q|k|v, attended,
+        # the residual delta, [gate | up], the gate product, the logits rows and their logits.
+        sizes = (total * d, total * d, 3 * total * d, total * d, total * d, 2 * total * ff, total * ff,
+                 wanted * d, wanted * vocab)  # fmt: skip
+        offsets, need = [], 0
+        for size in sizes:
+            offsets.append(need)
+            need += -(-size // 64) * 64
+        if self._forward_ws is None or self._forward_ws.numel() < need:
+            self._forward_ws = torch.empty(max(need, 2 * (0 if self._forward_ws is None else self._forward_ws.numel())),
+                                           dtype=torch.float32, device=self.device)  # fmt: skip
+        if greedy and (self._greedy_out is None or self._greedy_out.numel() < wanted):
+            self._greedy_out = torch.empty(max(wanted, 64), dtype=torch.int32, device=self.device)
+        base = self._forward_ws.data_ptr()
+        at = [base + 4 * o for o in offsets]
+        heads, dim = config.n_heads, config.head_dim
+        part = step.partition or 512  # 0: the library's default
+        parts = -(-step.max_context // part) if step.max_context > part else 1
+        ws_need = 0 if parts == 1 else total * heads * parts * (dim + 2) * 4
+        workspace = self._workspace
+        if workspace is None or workspace.numel() * 4 < ws_need:
+            workspace = self._workspace = torch.empty(max(ws_need // 4, 1), dtype=torch.float32, device=self.device)
+        tables = self._tables.tables
+        fields = (
+            self._device_index, ops._stream(self._device_index), total, wanted, d, heads, dim, ff, vocab,
+            step.ptr(step.tokens_at), step.ptr(step.rope_at), step.ptr(step.slots_at), step.ptr(step.logits_at),
+            w.embedding.data_ptr(), w.final_norm.data_ptr(), w.cos.data_ptr(), w.sin.data_ptr(), w.cos.shape[0],
+            self._keys.data_ptr(), self._values.data_ptr(), self._layer_bytes, self._kv_code,
+            self.num_blocks * self.block_size, *at,
+            step.ptr(step.qpos_at), step.ptr(step.qseq_at),
+            step.ptr(step.plan_rows_at) if step.num_plan_rows else 0, step.num_plan_rows,
+            step.ptr(step.plan_tiles_at) if step.num_tiles else 0, step.num_tiles,
+            step.ptr(step.merge_at) if step.num_merge else 0, step.num_merge,
+            self.num_blocks, self.block_size, tables.data_ptr(), tables.shape[1], step.ptr(step.contexts_at),
+            tables.shape[0], step.max_context, step.partition, step.flags, workspace.data_ptr(), workspace.numel() * 4,
+            self._greedy_out.data_ptr() if greedy and wanted else 0,
+        )  # fmt: skip
+        self._host.forward(fields, w.addresses, float(config.norm_eps), float(self.model.attention_scale))
+        if not wanted:
             return [], None
         names = [e.seq_id for e in step.entries if e.logits_index is not None]  # batch order
-        return names, normed[step.tensor("logits_rows")] @ w.embedding.T
+        if greedy:
+            return names, self._greedy_out[:wanted]
+        return names, self._forward_ws[offsets[-1] : offsets[-1] + wanted * vocab].view(wanted, vocab)
