@@ -1386,6 +1386,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(const Params a, 
 // caller's stream. Each device has its own mutex: it serialises the fork/join enqueue sequence
 // of calls from several host threads on that device (calls on other devices do not wait).
 constexpr int kMaxDevices = 64;
+constexpr int64_t kOverlapMinRowGroups = 2048;  // 8 row-pass workgroups per CU
 
 struct DeviceResources {
   std::mutex mu;
@@ -1473,7 +1474,13 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
   const bool append = a.new_keys != nullptr;
   std::unique_lock<std::mutex> overlap_lock;
   DeviceResources* overlap = nullptr;
-  if (PKV_ATTN_OVERLAP && num_tiles > 0 && num_rows > 0) {
+  // The second stream pays off only when the row pass alone would keep the GPU busy long enough
+  // to hide the tile pass: its fork and join cost about 40 us of host time per call (two event
+  // records, two stream waits), more than a small call's whole device time. Below
+  // kOverlapMinRowGroups row-pass workgroups both passes run on the caller's stream, tiles first.
+  const int64_t row_groups = (a.rows ? num_rows : num_rows * static_cast<int64_t>(a.max_parts)) *
+                             (kPairHeads<KVT, D> && a.num_heads % 2 == 0 ? a.num_heads / 2 : a.num_heads);
+  if (PKV_ATTN_OVERLAP && num_tiles > 0 && num_rows > 0 && row_groups >= kOverlapMinRowGroups) {
     overlap = overlap_for(device);
     if (overlap != nullptr) overlap_lock = std::unique_lock<std::mutex>(overlap->mu);
   }
