@@ -128,6 +128,23 @@ class BlockManager:
             raise InvariantError(f"block id {bad} is outside the pool")
         return self._owners_v[ids]
 
+    def shared_positions(self, table, lo: int, hi: int) -> list[int]:
+        """Indices ``i`` in ``[lo, hi)`` whose block ``table[i]`` has more than one owner. A few
+        entries (a decode step writes one block) are read one by one from the owner array; longer
+        stretches take one NumPy gather (:meth:`counts_of`)."""
+        if hi - lo > 8:
+            owners = self.counts_of(table[lo:hi])
+            return [lo + int(k) for k in (owners > 1).nonzero()[0]]
+        size, counts = self._size, self._owners
+        shared = []
+        for index in range(lo, hi):
+            block = table[index]
+            if not 0 <= block < size:
+                raise InvariantError(f"block id {block} is outside the pool")
+            if counts[block] > 1:
+                shared.append(index)
+        return shared
+
     def free_order(self) -> list[int]:
         """The free ids, oldest first: the order in which they will be allocated."""
         return self._take_view(self._nfree).tolist()

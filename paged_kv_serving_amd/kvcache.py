@@ -151,10 +151,7 @@ class KVCacheManager:
         grow = self.blocks_required(sequence, up_to_tokens)
         lo = sequence.num_computed_tokens // size
         hi = min(-(-up_to_tokens // size), len(table))
-        shared: list[int] = []
-        if hi > lo:
-            owners = self.blocks.counts_of(table[lo:hi])
-            shared = [lo + int(k) for k in (owners > 1).nonzero()[0]]
+        shared = self.blocks.shared_positions(table, lo, hi) if hi > lo else []
         needed = grow + len(shared)
         if needed:
             self.prefix_cache.evict_until_free(needed)

@@ -169,9 +169,13 @@ class TraceReplay:
             request = self._requests[seq_id.rsplit("#", 1)[0]]
             seq = Sequence(seq_id, request)
             self.sequences[seq_id] = seq
-        tokens = self.trace.tokens[seq_id]
-        if len(seq.token_ids) != num_tokens:
-            seq.token_ids = tokens[:num_tokens]
+        have = len(seq.token_ids)
+        if have != num_tokens:
+            tokens = self.trace.tokens[seq_id]
+            if have + 1 == num_tokens:  # one token sampled since the last call
+                seq.token_ids.append(tokens[have])
+            else:
+                seq.token_ids = tokens[:num_tokens]
         if num_computed is not None:
             seq.num_computed_tokens = num_computed
         return seq
@@ -207,9 +211,11 @@ class TraceReplay:
     def _attach(self, seq_id, record, num_tokens, num_computed, reuse, table_after, hashes_after) -> None:
         seq = self._sequence(seq_id, num_tokens, num_computed)
         got = self.cache.attach_prefix(seq, record=record)
-        self._expect(f"attach_prefix({seq_id})", [got.blocks, got.tokens, got.queried_blocks], reuse)
-        self._expect(f"table of {seq_id} after attach", seq.block_table, table_after)
-        self._expect(f"hash chain of {seq_id}", [len(seq.block_hashes), _digest_hashes(seq.block_hashes)], hashes_after)
+        if self.check:
+            self._expect(f"attach_prefix({seq_id})", [got.blocks, got.tokens, got.queried_blocks], reuse)
+            self._expect(f"table of {seq_id} after attach", seq.block_table, table_after)
+            self._expect(f"hash chain of {seq_id}", [len(seq.block_hashes), _digest_hashes(seq.block_hashes)],
+                         hashes_after)  # fmt: skip
 
     def _record(self, queried, hits) -> None:
         self.cache.record_prefix(PrefixReuse(blocks=hits, tokens=hits * self.block_size, queried_blocks=queried))
@@ -225,9 +231,10 @@ class TraceReplay:
             done = True
         except BlockAllocationError:
             done = False
-        self._expect(f"reserve({seq_id}, {up_to}) succeeded", done, ok)
-        self._expect(f"table of {seq_id} after reserve", seq.block_table, table_after)
-        self._expect(f"copy-on-write pairs of reserve({seq_id})", self.store.pairs[start:], copies)
+        if self.check:
+            self._expect(f"reserve({seq_id}, {up_to}) succeeded", done, ok)
+            self._expect(f"table of {seq_id} after reserve", seq.block_table, table_after)
+            self._expect(f"copy-on-write pairs of reserve({seq_id})", self.store.pairs[start:], copies)
 
     def _fork(self, parent_id, num_tokens, num_computed, child_id, child_tokens, table_after) -> None:
         parent = self._sequence(parent_id, num_tokens, num_computed)
@@ -241,8 +248,11 @@ class TraceReplay:
 
     def _publish(self, seq_id, num_tokens, num_computed, published, hashes_after) -> None:
         seq = self._sequence(seq_id, num_tokens, num_computed)
-        self._expect(f"publish_full_blocks({seq_id})", self.cache.publish_full_blocks(seq), published)
-        self._expect(f"hash chain of {seq_id}", [len(seq.block_hashes), _digest_hashes(seq.block_hashes)], hashes_after)
+        got = self.cache.publish_full_blocks(seq)
+        if self.check:
+            self._expect(f"publish_full_blocks({seq_id})", got, published)
+            self._expect(f"hash chain of {seq_id}", [len(seq.block_hashes), _digest_hashes(seq.block_hashes)],
+                         hashes_after)  # fmt: skip
 
     def _evictable(self, value) -> None:
         self._expect("evictable_blocks()", self.cache.evictable_blocks(), value)
@@ -271,7 +281,8 @@ class TraceReplay:
         entries = []
         for seq_id, start, count, logits_index, table in self.trace.iterations[iteration]["entries"]:
             seq = self.sequences[seq_id]
-            self._expect(f"iteration {iteration} table of {seq_id}", seq.block_table, table)
+            if self.check:
+                self._expect(f"iteration {iteration} table of {seq_id}", seq.block_table, table)
             entries.append(
                 BatchEntry(
                     seq_id=seq_id,

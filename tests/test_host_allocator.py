@@ -483,3 +483,25 @@ def test_scope_bytes() -> None:
     shared, _ = prefix(scope="global")
     assert per_key.scope_bytes("alice") != per_key.scope_bytes("bob")
     assert shared.scope_bytes("alice") == shared.scope_bytes("bob")
+
+
+def test_shared_positions_reads_short_and_long_stretches_alike() -> None:
+    """BlockManager.shared_positions (reserve's check for blocks it must copy before writing):
+    the scalar read of a few entries and the NumPy gather of a long stretch give the same
+    indices, and an id outside the pool is an InvariantError on both paths."""
+    import random
+
+    from paged_kv_serving_amd.blocks import BlockManager, InvariantError, RecordingBlockStore
+
+    rng = random.Random(3)
+    pool = BlockManager(num_blocks=64, block_size=4, store=RecordingBlockStore())
+    ids = pool.allocate_many(40)
+    for block in rng.sample(ids, 15):
+        pool.incref(block)
+    table = [rng.choice(ids) for _ in range(30)]
+    want = [i for i, b in enumerate(table) if pool.ref_count(b) > 1]
+    for lo, hi in ((0, 30), (3, 9), (5, 6), (10, 30), (29, 30)):
+        assert pool.shared_positions(table, lo, hi) == [i for i in want if lo <= i < hi], (lo, hi)
+    for bad, hi in ((64, 2), (-1, 20)):
+        with pytest.raises(InvariantError, match="outside the pool"):
+            pool.shared_positions([ids[0], bad] + ids[:18], 0, hi)
