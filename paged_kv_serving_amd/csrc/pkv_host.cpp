@@ -33,12 +33,13 @@
 //       held_obj keeps, per row, the tuple it was last filled from: a scheduler rebuilds each
 //       table tuple from the same int objects every step, so an unchanged table compares equal
 //       by identity, element by element, without converting a single id.
-//   cow_groups(pairs, out) -> list of group sizes
+//   cow_groups(pairs, out[, marks]) -> list of group sizes
 //       Flattens a list of (src, dst) block copies into the int64 buffer `out` (>= 2 entries
 //       per pair) and splits them, in order, into groups that may each run as one concurrent
 //       pkv_copy_blocks launch (ops.independent_groups): a copy starts a new group when it
 //       reads a block an earlier copy of the group writes, or writes a block an earlier copy of
-//       the group reads or writes.
+//       the group reads or writes. `marks` (uint8, one zero per pool block, left all zero)
+//       replaces the hash sets that track the group's blocks.
 //   exclusive_writes(rows, contexts, host, block_size, marks) -> bool
 //       Whether a batch of single-token entries at their last positions (entry e: arena row
 //       rows[e], context contexts[e], so it writes position contexts[e] - 1) may append inside
@@ -574,18 +575,29 @@ done:
 }
 
 PyObject* cow_groups(PyObject*, PyObject* args) {
-  PyObject *pairs_o, *out_o;
-  if (!PyArg_ParseTuple(args, "OO", &pairs_o, &out_o)) return nullptr;
+  PyObject *pairs_o, *out_o, *marks_o = Py_None;
+  if (!PyArg_ParseTuple(args, "OO|O", &pairs_o, &out_o, &marks_o)) return nullptr;
   PyObject* pairs = PySequence_Fast(pairs_o, "pairs must be a sequence");
   if (pairs == nullptr) return nullptr;
   const Py_ssize_t count = PySequence_Fast_GET_SIZE(pairs);
   PyObject** items = PySequence_Fast_ITEMS(pairs);
   Buf<int64_t> out;
+  Buf<uint8_t> marks;
   PyObject* result = nullptr;
   std::vector<Py_ssize_t> sizes;
+  // Blocks read (bit 0) and written (bit 1) by the current group: one byte per pool block when
+  // `marks` (all zero, left all zero) is given, else hash sets.
   std::unordered_set<int64_t> reads, writes;
+  std::vector<int64_t> touched;
+  uint8_t* mark = nullptr;
+  int64_t num_marks = 0;
   Py_ssize_t current = 0;
   if (!out.get(out_o, "out")) goto done;
+  if (marks_o != Py_None) {
+    if (!marks.get(marks_o, "marks")) goto done;
+    mark = marks.data();
+    num_marks = marks.size();
+  }
   if (out.size() < 2 * count) {
     PyErr_SetString(PyExc_ValueError, "out holds fewer than two entries per pair");
     goto done;
@@ -601,16 +613,33 @@ PyObject* cow_groups(PyObject*, PyObject* args) {
       if (!PyErr_Occurred()) PyErr_SetString(PyExc_ValueError, "a copy must be a (src, dst) pair");
       goto done;
     }
-    if (current > 0 && (writes.count(src) || reads.count(dst) || writes.count(dst))) {
+    // Ids outside the marks (the runner checks them at copy_block) are tracked in the sets.
+    const bool src_marked = src >= 0 && src < num_marks;
+    const bool dst_marked = dst >= 0 && dst < num_marks;
+    const bool conflict = (src_marked ? (mark[src] & 2) != 0 : writes.count(src) != 0) ||
+                          (dst_marked ? mark[dst] != 0 : (reads.count(dst) != 0 || writes.count(dst) != 0));
+    if (current > 0 && conflict) {
       sizes.push_back(current);
       current = 0;
       reads.clear();
       writes.clear();
+      for (int64_t b : touched) mark[b] = 0;
+      touched.clear();
     }
     out.data()[2 * i] = src;
     out.data()[2 * i + 1] = dst;
-    reads.insert(src);
-    writes.insert(dst);
+    if (src_marked) {
+      mark[src] |= 1;
+      touched.push_back(src);
+    } else {
+      reads.insert(src);
+    }
+    if (dst_marked) {
+      mark[dst] |= 2;
+      touched.push_back(dst);
+    } else {
+      writes.insert(dst);
+    }
     ++current;
   }
   if (current > 0) sizes.push_back(current);
@@ -618,6 +647,7 @@ PyObject* cow_groups(PyObject*, PyObject* args) {
   if (result == nullptr) goto done;
   for (size_t g = 0; g < sizes.size(); ++g) PyList_SET_ITEM(result, g, PyLong_FromSsize_t(sizes[g]));
 done:
+  for (int64_t b : touched) mark[b] = 0;
   Py_DECREF(pairs);
   return result;
 }

@@ -322,6 +322,8 @@ class ModelRunner:
         self._kv_code = ops.kv_dtype_code(kv_dtype)
         self._pairs = np.zeros(512, np.int64)
         self._marks = np.zeros(num_blocks, np.int32)  # one per pool block, for exclusive_writes
+        self._cow_marks = np.zeros(num_blocks, np.uint8)  # one per pool block, for cow_groups
+        self._cow_staging = _Staging(self.device, self._host)  # the queued copies' pairs
         self._workspace: torch.Tensor | None = None
         self._forward_ws: torch.Tensor | None = None  # the forward pass's activations
         self._greedy_out: torch.Tensor | None = None  # its greedy token ids
@@ -376,17 +378,27 @@ class ModelRunner:
         self._pending.append((int(source), int(destination)))
 
     def flush_copies(self) -> int:
-        """Launch every queued copy-on-write copy, in order. Returns the number of copies."""
+        """Launch every queued copy-on-write copy, in order: one ``pkv_copy_blocks`` launch per
+        group of independent copies, their pairs sent in one asynchronous copy of their own.
+        Returns the number of copies."""
         if not self._pending:
             return 0
         pending = self._pending
         sizes, flat = self._cow_groups(pending)
+        (offset,) = self._cow_staging.send([flat], [])
+        pairs_at = self._cow_staging.base + offset
+        k_pool, v_pool = self._keys, self._values
+        layers, num_blocks = k_pool.shape[0], k_pool.shape[1]
+        block_elems = k_pool[0, 0].numel()
+        stream = ops._stream(self._device_index)
         start = 0
         for size in sizes:
-            pairs = torch.from_numpy(flat[2 * start : 2 * (start + size)].copy()).view(-1, 2)
-            ops.copy_blocks(self._keys, self._values, pairs.to(self.device, non_blocking=True))
+            rc = self._host.copy_blocks(k_pool.data_ptr(), v_pool.data_ptr(), self._kv_code, pairs_at + 16 * start, size,
+                                        layers, num_blocks, block_elems, self._device_index, stream)  # fmt: skip
+            _native.check(rc, "pkv_copy_blocks")
             start += size
-        # Dequeued only once every group is enqueued (a failed launch leaves them queued).
+        # Dequeued only once every group is enqueued (a failed launch leaves them queued; a group
+        # reads no block it writes, so running it twice leaves what running it once does).
         self._pending = []
         return len(pending)
 
@@ -395,7 +407,7 @@ class ModelRunner:
         groups that may each run as one launch (``ops.independent_groups``'s rule)."""
         if self._pairs.size < 2 * len(pending):
             self._pairs = np.zeros(max(2 * len(pending), 2 * self._pairs.size), np.int64)
-        sizes = self._host.cow_groups(pending, self._pairs)
+        sizes = self._host.cow_groups(pending, self._pairs, self._cow_marks)
         return sizes, self._pairs[: 2 * len(pending)]
 
     def block_fingerprint(self, block_id: int) -> bytes:
@@ -473,6 +485,10 @@ class ModelRunner:
         entries = batch.entries
         if not entries:
             return None
+        # Copies queued by copy_block (the scheduler's copy-on-write, issued before this step in
+        # the reference, blocks.py:162-164) start first, so the device copies while the host
+        # prepares the step; the stream orders them before this step's appends and attention.
+        self.flush_copies()
         config = self.model.config
         tokens, positions, slots, lengths, context, logits_rows, (problem, bad, position) = self._gather(entries)
         total = tokens.size
@@ -538,14 +554,7 @@ class ModelRunner:
             plan_rows, plan_tiles, partition, bool(flags & _native.PKV_ATTN_SHARED_KV), merge,
             bool(flags & _native.PKV_ATTN_SHORT_ROWS), bool(flags & _native.PKV_ATTN_DOMINANT_TILES),
         )  # fmt: skip
-        # Queued copy-on-write pairs travel in the same copy and run before this step's kernels.
-        # They leave the queue only once every group is enqueued: if the copy or a launch
-        # raises, the next call (or flush) issues them again (a group's copies read no block the
-        # group writes, so running a group twice leaves what running it once does).
-        sizes, flat = self._cow_groups(self._pending) if self._pending else ([], None)
         parts64 = [tokens, rope_positions, slots, update.index, wanted]
-        if sizes:
-            parts64.append(flat)
         offsets = self._staging.send(
             parts64,
             [query_pos, query_seq, contexts_by_row, update.values, plan_rows.ravel(), plan_tiles.ravel(), merge],
@@ -553,20 +562,6 @@ class ModelRunner:
         tokens_at, rope_at, slots_at, index_at, logits_at = offsets[:5]
         qpos_at, qseq_at, context_at, values_at, rows_at, tiles_at, merge_at = offsets[-7:]
         staging = self._staging
-        if sizes:
-            pairs_at = offsets[5]
-            k_pool, v_pool = self._keys, self._values
-            dtype = ops.kv_dtype_code(k_pool.dtype)
-            layers, num_blocks = k_pool.shape[0], k_pool.shape[1]
-            block_elems = k_pool[0, 0].numel()
-            stream = ops._stream(self._device_index)
-            start = 0
-            for size in sizes:
-                rc = self._host.copy_blocks(k_pool.data_ptr(), v_pool.data_ptr(), dtype, staging.base + pairs_at + 16 * start,
-                                            size, layers, num_blocks, block_elems, self._device_index, stream)  # fmt: skip
-                _native.check(rc, "pkv_copy_blocks")
-                start += size
-            self._pending = []
         if update.index.size:
             self._tables.apply(staging.tensor(index_at, update.index.size, torch.int64),
                                staging.tensor(values_at, update.values.size, torch.int32))  # fmt: skip

@@ -147,6 +147,12 @@ def test_cow_groups_match_the_python_grouping(seed) -> None:
     out = np.zeros(2 * n + 2, np.int64)
     assert ext.cow_groups(pairs, out) == _python_groups(pairs)
     assert out[: 2 * n].tolist() == [v for pair in pairs for v in pair]
+    # with the per-block marks (some ids past them fall back to the sets): the same groups, and
+    # the marks are left all zero
+    marks = np.zeros(min(ids, 900), np.uint8)
+    out2 = np.zeros(2 * n + 2, np.int64)
+    assert ext.cow_groups(pairs, out2, marks) == _python_groups(pairs)
+    assert np.array_equal(out, out2) and not marks.any()
 
 
 def test_cow_groups_of_forks_are_one_group_and_bad_pairs_are_refused() -> None:
