@@ -534,8 +534,11 @@ class ModelRunner:
         token_order = None
         if order is not None:
             order = np.asarray(order, dtype=np.int64)
-            batch_starts = np.cumsum(lengths) - lengths
-            token_order = np.concatenate([np.arange(batch_starts[i], batch_starts[i] + lengths[i]) for i in order])
+            if total == len(entries):  # one token per entry: tokens move as their entries do
+                token_order = order
+            else:  # entry order[r]'s tokens, consecutively: token j of run r is start + (j - run offset)
+                starts, runs = (np.cumsum(lengths) - lengths)[order], lengths[order]
+                token_order = np.repeat(starts - (np.cumsum(runs) - runs), runs) + np.arange(total)
             tokens, positions, slots = tokens[token_order], positions[token_order], slots[token_order]
             rope_positions = rope_positions[token_order]
             planner_row = np.empty(total, dtype=np.int64)  # batch token index -> planner token index
