@@ -72,10 +72,15 @@ namespace {
 #define PKV_ATTN_OVERLAP 1
 #endif
 // Launch order of an overlapped call: 0 = the tile pass first (on the second stream), 1 = the
-// row pass first. Measured on config 3's mixed call: 1.437-1.439 ms tiles first, 1.478-1.480 ms
-// rows first.
+// row pass first (the fork event is recorded before it, so the tile pass still waits only for
+// the work queued before the call). Measured with the current passes, same box, two alternating
+// runs: config 3's mixed call 1.4795-1.4814 ms rows first against 1.4787-1.4794 tiles first,
+// config 4's attention 0.2386-0.2387 against 0.2337-0.2399 ms; rows first starts the device on
+// the row pass before the host's two stream waits (about 9.5 us each), so config 4's runner
+// step takes 0.398-0.399 instead of 0.419-0.427 ms. (Before the tile grid rules, tiles first
+// had been 40 us faster on config 3.)
 #ifndef PKV_ATTN_ROWS_FIRST
-#define PKV_ATTN_ROWS_FIRST 0
+#define PKV_ATTN_ROWS_FIRST 1
 #endif
 // Workgroup order of the row pass: 0 = the hardware's round robin over the 8 XCDs (consecutive
 // workgroups, i.e. neighbouring heads of one token, on different XCDs); 1 = each XCD walks one
