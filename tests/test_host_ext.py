@@ -313,3 +313,22 @@ def test_exclusive_writes_matches_the_brute_force_rule(seed) -> None:
         tables.append(tuple(int(b) for b in rng.integers(0, num_blocks + 3, need)))
         contexts.append(ctx)
     assert exclusive(tables, contexts, block, num_blocks) == exclusive_by_brute_force(tables, contexts, block, num_blocks)
+
+
+def test_forward_refuses_bad_arguments_before_any_device_work() -> None:
+    """_pkvhost.forward (the runner's whole forward pass as one call) checks its field count and
+    sizes before it touches a device, so these run on any machine."""
+    bound = _native.bound_host()
+    with pytest.raises(ValueError, match="integers"):
+        bound.forward((0,) * 5, [], 1e-5, 0.1)
+    fields = [0] * 52
+    fields[2], fields[3], fields[4], fields[5], fields[6], fields[7], fields[8] = 4, 1, 64, 2, 16, 32, 10
+    with pytest.raises(ValueError, match="out of range"):  # d_model != heads * head_dim
+        bound.forward(tuple(fields), [], 1e-5, 0.1)
+    fields[6] = 32
+    fields[2] = 0  # no tokens
+    with pytest.raises(ValueError, match="out of range"):
+        bound.forward(tuple(fields), [], 1e-5, 0.1)
+    fields[2] = 4
+    with pytest.raises(ValueError, match="six weight addresses"):
+        bound.forward(tuple(fields), [(1, 2, 3)], 1e-5, 0.1)
