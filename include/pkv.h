@@ -190,6 +190,15 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  *   query_positions  : int32 [num_queries], absolute position of each query (the causal mask:
  *                      key position > query position is masked, attention.py:102-104).
  *   query_seq        : int32 [num_queries], index of the sequence each query belongs to.
+ *   caller_rows      : int32 [num_queries] or NULL. Query t's row of `queries` and of `out`
+ *                      (and of the new keys, values and slots of pkv_paged_attention_append) is
+ *                      caller_rows[t]; NULL means t. Every other per-query array (positions,
+ *                      sequences, the plan's rows, tiles and merge list) is indexed by t. This
+ *                      lets a plan order the queries its own way (rows sharing a prefix next to
+ *                      each other) while the caller keeps its token order: no copy of the
+ *                      queries in and of the outputs back. caller_rows must be a permutation of
+ *                      [0, num_queries); a query whose entry lies outside that range is skipped
+ *                      (its output row is not written).
  *   rows, num_rows   : the plan's row-pass work items, int32 [num_rows, 2] = (query row,
  *                      partition): one workgroup per item and group of heads computes that
  *                      partition of that row with the row-streaming pass (the right pass for
@@ -241,7 +250,8 @@ int pkv_tile_head_dim_supported(int32_t head_dim);
  */
 int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,
                         const int32_t* query_positions, const int32_t* query_seq,
-                        int64_t num_queries, const int32_t* rows, int64_t num_rows,
+                        int64_t num_queries, const int32_t* caller_rows, const int32_t* rows,
+                        int64_t num_rows,
                         const int32_t* tiles, int64_t num_tiles, const int32_t* merge_rows,
                         int64_t num_merge_rows, const void* key_cache,
                         const void* value_cache, pkv_dtype kv_dtype, int64_t num_blocks,
@@ -268,7 +278,8 @@ int pkv_paged_attention(float* out, const float* queries, int64_t query_token_st
  */
 int pkv_paged_attention_noalloc(float* out, const float* queries, int64_t query_token_stride,
                                 const int32_t* query_positions, const int32_t* query_seq,
-                                int64_t num_queries, const int32_t* rows, int64_t num_rows,
+                                int64_t num_queries, const int32_t* caller_rows,
+                                const int32_t* rows, int64_t num_rows,
                                 const int32_t* tiles, int64_t num_tiles,
                                 const int32_t* merge_rows, int64_t num_merge_rows,
                                 const void* key_cache, const void* value_cache,
@@ -291,8 +302,10 @@ int pkv_paged_attention_noalloc(float* out, const float* queries, int64_t query_
  * Arguments are pkv_paged_attention's (without tiles: every query row goes through the row pass)
  * plus new_keys / new_values ([num_queries, num_heads, head_dim] of new_dtype with token strides
  * new_key_token_stride / new_value_token_stride, 16-byte aligned rows; bfloat16 only into a
- * bfloat16 pool) and slot_mapping (int64 [num_queries]), as for pkv_append. Row t's new token
- * sits at query_positions[t]. Preconditions, which the caller checks: each sequence has exactly
+ * bfloat16 pool) and slot_mapping (int64 [num_queries]), as for pkv_append; all three in the
+ * caller's row order, like queries and out (with caller_rows, query t's new token is row
+ * caller_rows[t] of new_keys / new_values and goes to slot_mapping[caller_rows[t]]). Query t's
+ * new token sits at query_positions[t]. Preconditions, which the caller checks: each sequence has exactly
  * one query row in the call, that row's position is below its context_len and below
  * max_context_len, and slot_mapping[t] is the slot the block table gives that position (as in
  * runner.py:149-159). A slot outside the pool is not written, as in pkv_append. No row may read a
@@ -305,7 +318,8 @@ int pkv_paged_attention_noalloc(float* out, const float* queries, int64_t query_
  */
 int pkv_paged_attention_append(
     float* out, const float* queries, int64_t query_token_stride, const int32_t* query_positions,
-    const int32_t* query_seq, int64_t num_queries, const int32_t* rows, int64_t num_rows,
+    const int32_t* query_seq, int64_t num_queries, const int32_t* caller_rows, const int32_t* rows,
+    int64_t num_rows,
     const int32_t* merge_rows, int64_t num_merge_rows, void* key_cache, void* value_cache,
     pkv_dtype kv_dtype, int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
     int32_t block_table_stride, const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,

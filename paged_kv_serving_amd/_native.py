@@ -181,8 +181,9 @@ _BOUND = False
 def bound_host():
     """:func:`host` with the library's entry points bound into it (``_pkvhost.bind``), so its
     ``plan``, ``paged_attention``, ``paged_attention_append``, ``copy_blocks``, ``rms_norm``,
-    ``silu_mul``, ``rope_append`` and ``forward`` call ``libpkv.so`` directly, and ``stage`` and
-    ``forward`` call the ``hipMemcpyAsync`` / ``hipGetDevice`` / ``hipSetDevice`` of the HIP
+    ``silu_mul``, ``rope_append``, ``append``, ``forward`` and ``CopyQueue.flush`` call ``libpkv.so``
+    directly, and ``stage``, ``forward``, ``CopyQueue.flush`` and ``event_create`` call the
+    ``hipMemcpyAsync`` / ``hipGetDevice`` / ``hipSetDevice`` / ``hipEvent*`` functions of the HIP
     runtime ``libpkv.so`` is linked against (looked up through the library's handle, so they are
     that runtime's). Binding loads the library (it must be built)."""
     global _BOUND
@@ -197,7 +198,10 @@ def bound_host():
                          address(lib.pkv_rms_norm), address(lib.pkv_silu_mul),
                          address(lib.pkv_rope_append), address(lib.hipMemcpyAsync),
                          address(lib.pkv_gather_rows), address(lib.pkv_greedy_tokens),
-                         address(lib.hipGetDevice), address(lib.hipSetDevice))  # fmt: skip
+                         address(lib.hipGetDevice), address(lib.hipSetDevice),
+                         address(lib.hipEventCreateWithFlags), address(lib.hipEventRecord),
+                         address(lib.hipEventSynchronize), address(lib.hipEventDestroy),
+                         address(lib.pkv_append))  # fmt: skip
                 _BOUND = True
     return ext
 
@@ -248,7 +252,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pkv_tile_head_dim_supported.restype = _c_int
     lib.pkv_paged_attention.argtypes = [
         _ptr, _ptr, _i64,  # out, queries, query_token_stride
-        _ptr, _ptr, _i64,  # query_positions, query_seq, num_queries
+        _ptr, _ptr, _i64, _ptr,  # query_positions, query_seq, num_queries, caller_rows
         _ptr, _i64, _ptr, _i64,  # rows, num_rows, tiles, num_tiles
         _ptr, _i64,  # merge_rows, num_merge_rows
         _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size
@@ -261,7 +265,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pkv_paged_attention.restype = _c_int
     lib.pkv_paged_attention_noalloc.argtypes = [
         _ptr, _ptr, _i64,  # out, queries, query_token_stride
-        _ptr, _ptr, _i64,  # query_positions, query_seq, num_queries
+        _ptr, _ptr, _i64, _ptr,  # query_positions, query_seq, num_queries, caller_rows
         _ptr, _i64, _ptr, _i64,  # rows, num_rows, tiles, num_tiles
         _ptr, _i64,  # merge_rows, num_merge_rows
         _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size
@@ -273,7 +277,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pkv_paged_attention_noalloc.restype = _c_int
     lib.pkv_paged_attention_append.argtypes = [
         _ptr, _ptr, _i64,  # out, queries, query_token_stride
-        _ptr, _ptr, _i64,  # query_positions, query_seq, num_queries
+        _ptr, _ptr, _i64, _ptr,  # query_positions, query_seq, num_queries, caller_rows
         _ptr, _i64,  # rows, num_rows
         _ptr, _i64,  # merge_rows, num_merge_rows
         _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size

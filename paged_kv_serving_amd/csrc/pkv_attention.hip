@@ -140,8 +140,10 @@ struct Params {
   float* out;              // [T, H, D]
   float* ws_acc;           // [T, H, max_parts, D]
   float* ws_ml;            // [T, H, max_parts, 2]
-  const float* queries;    // row t at t * q_stride
+  const float* queries;    // row q_rows[t] (t without q_rows) at that row * q_stride
   int64_t q_stride;
+  const int32_t* q_rows;   // [T] or null: the row of queries / out / new_keys / new_values of
+                           // planner row t (null: t itself); every other [T] array is by t
   const int32_t* q_pos;    // [T]
   const int32_t* q_seq;    // [T]
   const int32_t* rows;     // row_partial: [R, 2] = (query row, partition) items; null: every
@@ -169,13 +171,14 @@ struct Params {
   int32_t max_ctx;
   float scale_log2;        // scale * log2(e)
   // The decode append fused into the row pass (new_keys null: none). Query row t's own key and
-  // value row (token t of new_keys / new_values) is written to pool slot new_slots[t] by the
-  // row-pass workgroups whose partition holds position q_pos[t], which also use it as that key.
-  const void* new_keys;    // [T, H, D] of new_dtype, token t at t * new_key_stride elements
+  // value row (row r = io_row(t) of new_keys / new_values) is written to pool slot new_slots[r]
+  // by the row-pass workgroups whose partition holds position q_pos[t], which also use it as
+  // that key.
+  const void* new_keys;    // [T, H, D] of new_dtype, row r at r * new_key_stride elements
   const void* new_values;
   int64_t new_key_stride;
   int64_t new_value_stride;
-  const int64_t* new_slots;  // [T]
+  const int64_t* new_slots;  // [T], by io_row like new_keys
   int64_t num_slots;       // pool token rows (num_blocks * block_size)
   int32_t new_dtype;       // PKV_F32 or PKV_BF16 (bfloat16 only into a bfloat16 pool)
 };
@@ -292,6 +295,15 @@ __device__ __forceinline__ int row_visible(const Params& a, int64_t t) {
   return min(visible_len(a.ctx_lens[seq], a.q_pos[t]), a.max_ctx);
 }
 
+// Row of the caller's queries / out / new key and value arrays that planner row t reads and
+// writes (t itself without q_rows); -1 when q_rows names a row outside the batch, which the
+// kernels then skip.
+__device__ __forceinline__ int64_t io_row(const Params& a, int64_t t) {
+  if (a.q_rows == nullptr) return t;
+  const int64_t r = a.q_rows[t];
+  return r >= 0 && r < a.num_queries ? r : -1;
+}
+
 __device__ __forceinline__ int parts_of(int visible, int part_size) {
   return visible > part_size ? (visible + part_size - 1) / part_size : 1;
 }
@@ -308,14 +320,14 @@ __device__ __forceinline__ void stage_table(int* s_table, const Params& a, int s
   for (int i = threadIdx.x; i < nb; i += threads) s_table[i] = table[i];
 }
 
-// Write one query row's partition result: final output when the row fits one partition,
-// otherwise the unnormalised (max, sum, acc) for the reduce pass.
-__device__ __forceinline__ void store_result(const Params& a, int64_t t, int h, int p, int nparts,
-                                             int d, int D, float acc, float big, float sum,
-                                             bool write_ml) {
+// Write one query row's partition result: final output (row r of out) when the row fits one
+// partition, otherwise the unnormalised (max, sum, acc) of planner row t for the reduce pass.
+__device__ __forceinline__ void store_result(const Params& a, int64_t t, int64_t r, int h, int p,
+                                             int nparts, int d, int D, float acc, float big,
+                                             float sum, bool write_ml) {
   const int64_t qh = t * a.num_heads + h;
   if (nparts == 1) {
-    a.out[qh * D + d] = acc / (sum > 0.f ? sum : 1.f);
+    a.out[(r * a.num_heads + h) * D + d] = acc / (sum > 0.f ? sum : 1.f);
   } else {
     const int64_t slot = qh * a.max_parts + p;
     a.ws_acc[slot * D + d] = acc;
@@ -362,6 +374,8 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
     p = static_cast<int>(rest % static_cast<uint32_t>(a.max_parts));
   }
   if (t < 0 || t >= a.num_queries || p < 0) return;  // an item outside the batch is skipped
+  const int64_t r = io_row(a, t);
+  if (r < 0) return;
 
   const int seq = a.q_seq[t];
   const int kv_len = row_visible(a, t);
@@ -384,7 +398,7 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   // e of head h + i / kVph; the heads of a group are adjacent in both queries and pools.
   float qv[L::kDpl];
   {
-    const float* qrow = a.queries + t * a.q_stride + static_cast<int64_t>(h) * D;
+    const float* qrow = a.queries + r * a.q_stride + static_cast<int64_t>(h) * D;
 #pragma unroll
     for (int i = 0; i < L::kVpl; ++i) {
 #pragma unroll
@@ -413,8 +427,8 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   // With the fused append, the key position of this row's own new token (else none), and where
   // its head group's key and value rows start in the append source.
   const int own_pos = kAppend ? a.q_pos[t] : -1;
-  const int64_t own_key = t * a.new_key_stride + head_off;
-  const int64_t own_value = t * a.new_value_stride + head_off;
+  const int64_t own_key = r * a.new_key_stride + head_off;
+  const int64_t own_value = r * a.new_value_stride + head_off;
 
   for (int it = wave; it < n_iter; it += kWaves) {
     const int base = kbeg + it * L::kIterTok;
@@ -443,7 +457,7 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
           kraw[rr][i] = new_row_vector(a, a.new_keys, own_key + e, KVT{});
           vraw[rr][i] = new_row_vector(a, a.new_values, own_value + e, KVT{});
         }
-        const int64_t slot = a.new_slots[t];
+        const int64_t slot = a.new_slots[r];
         if (slot >= 0 && slot < a.num_slots) {
           uint4* kd = reinterpret_cast<uint4*>(const_cast<KVT*>(kcache) + slot * row_stride + head_off);
           uint4* vd = reinterpret_cast<uint4*>(const_cast<KVT*>(vcache) + slot * row_stride + head_off);
@@ -563,7 +577,7 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
       lsum = fmaf(s_l[k * HPW + hh], w, lsum);
       sum_acc = fmaf(s_acc[k * kSlice + x], w, sum_acc);
     }
-    store_result(a, t, h + hh, p, nparts, d, D, sum_acc, big, lsum, d == 0);
+    store_result(a, t, r, h + hh, p, nparts, d, D, sum_acc, big, lsum, d == 0);
   }
 }
 
@@ -754,12 +768,14 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   const int my_vis = s_vis[qi];
   const bool q_ok = qi < nrows;
 
+  // This lane's row of queries and out (-1: a caller row outside the batch, skipped).
+  const int io = static_cast<int>(io_row(a, t0 + (q_ok ? qi : 0)));
   float qreg[kD4];
   {
     // Lanes past the tile read row t0 (always in the batch) and drop it, so every load is
     // unconditional and the 32 loads of a lane can all be in flight together.
-    const int64_t row = t0 + (q_ok ? qi : 0);
-    const float* qrow = a.queries + row * a.q_stride + static_cast<int64_t>(h) * D + c * kD4;
+    const float* qrow =
+        a.queries + static_cast<int64_t>(io < 0 ? 0 : io) * a.q_stride + static_cast<int64_t>(h) * D + c * kD4;
     float raw[kD4];
 #pragma unroll
     for (int s = 0; s < kD4; ++s) raw[s] = qrow[s];
@@ -965,7 +981,9 @@ __device__ __forceinline__ void tile_item(const Params& a, uint32_t bid, int* s_
   if (p >= row_parts) return;
   const int64_t qh = (t0 + qi) * a.num_heads + h;
   if (row_parts == 1) {
-    store_out_row<D, S::kW>(a.out + qh * D, o, c, l > 0.f ? l : 1.f);
+    if (io >= 0) {
+      store_out_row<D, S::kW>(a.out + (static_cast<int64_t>(io) * a.num_heads + h) * D, o, c, l > 0.f ? l : 1.f);
+    }
   } else {
     const int64_t slot = qh * a.max_parts + p;
     store_out_row<D, S::kW>(a.ws_acc + slot * D, o, c, 1.f);
@@ -1051,12 +1069,14 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
 
   const int my_vis = s_vis[qi];
   const bool q_ok = qi < nrows;
+  // This lane's row of queries and out (-1: a caller row outside the batch, skipped).
+  const int io = static_cast<int>(io_row(a, t0 + (q_ok ? qi : 0)));
   float qreg[kD4];
   {
     // Lanes past the tile read row t0 (always in the batch) and drop it, so every load is
     // unconditional and the loads of a lane can all be in flight together.
-    const int64_t row = t0 + (q_ok ? qi : 0);
-    const float* qrow = a.queries + row * a.q_stride + static_cast<int64_t>(h) * D + c * kD4;
+    const float* qrow =
+        a.queries + static_cast<int64_t>(io < 0 ? 0 : io) * a.q_stride + static_cast<int64_t>(h) * D + c * kD4;
     float raw[kD4];
 #pragma unroll
     for (int i = 0; i < kD4; ++i) raw[i] = qrow[i];
@@ -1282,7 +1302,9 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
   if (!q_ok || p >= row_parts) return;
   const int64_t qh = (t0 + qi) * a.num_heads + h;
   if (row_parts == 1) {
-    store_out_row<D, kVw>(a.out + qh * D, o, c, l > 0.f ? l : 1.f);
+    if (io >= 0) {
+      store_out_row<D, kVw>(a.out + (static_cast<int64_t>(io) * a.num_heads + h) * D, o, c, l > 0.f ? l : 1.f);
+    }
   } else {
     const int64_t slot = qh * a.max_parts + p;
     store_out_row<D, kVw>(a.ws_acc + slot * D, o, c, 1.f);
@@ -1345,6 +1367,8 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(const Params a, 
   if (t < 0 || t >= a.num_queries) return;  // a row outside the batch is skipped
   const int nparts = parts_of(row_visible(a, t), a.part_size);
   if (nparts == 1) return;  // written by the partial pass
+  const int64_t r = io_row(a, t);
+  if (r < 0) return;
   const int d = (static_cast<int>(threadIdx.x) % kTpi) * 4;
   const int64_t qh = t * a.num_heads + h;
   const float* ml = a.ws_ml + 2 * qh * a.max_parts;
@@ -1375,7 +1399,7 @@ __global__ __launch_bounds__(kReduceThreads) void reduce_kernel(const Params a, 
     for (int e = 0; e < 4; ++e) acc[e] = fmaf(v[e], w, acc[e]);
   }
   const float sum = lsum > 0.f ? lsum : 1.f;
-  float* dst = a.out + qh * D + d;
+  float* dst = a.out + (r * a.num_heads + h) * D + d;
   if constexpr (kVec) {
     *reinterpret_cast<float4*>(dst) = make_float4(acc[0] / sum, acc[1] / sum, acc[2] / sum, acc[3] / sum);
   } else {
@@ -1669,7 +1693,7 @@ struct AppendSource {
 
 int attention_call(float* out, const float* queries, int64_t query_token_stride,
                    const int32_t* query_positions, const int32_t* query_seq, int64_t num_queries,
-                   const int32_t* rows, int64_t num_rows, const int32_t* tiles, int64_t num_tiles,
+                   const int32_t* caller_rows, const int32_t* rows, int64_t num_rows, const int32_t* tiles, int64_t num_tiles,
                    const int32_t* merge_rows, int64_t num_merge_rows, const void* key_cache,
                    const void* value_cache, pkv_dtype kv_dtype, int64_t num_blocks,
                    int32_t block_size, const int32_t* block_tables, int32_t block_table_stride,
@@ -1750,6 +1774,7 @@ int attention_call(float* out, const float* queries, int64_t query_token_stride,
   a.q_stride = query_token_stride;
   a.q_pos = query_positions;
   a.q_seq = query_seq;
+  a.q_rows = caller_rows;
   a.rows = rows;
   a.tiles = tiles;
   a.merge_rows = merge_rows;
@@ -1801,7 +1826,8 @@ int attention_call(float* out, const float* queries, int64_t query_token_stride,
 
 extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t query_token_stride,
                                    const int32_t* query_positions, const int32_t* query_seq,
-                                   int64_t num_queries, const int32_t* rows, int64_t num_rows,
+                                   int64_t num_queries, const int32_t* caller_rows,
+                                   const int32_t* rows, int64_t num_rows,
                                    const int32_t* tiles, int64_t num_tiles,
                                    const int32_t* merge_rows, int64_t num_merge_rows,
                                    const void* key_cache, const void* value_cache,
@@ -1813,7 +1839,7 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
                                    int32_t flags, float* workspace, int64_t workspace_bytes,
                                    int device, void* stream) {
   return pkv::attention_call(out, queries, query_token_stride, query_positions, query_seq,
-                             num_queries, rows, num_rows, tiles, num_tiles, merge_rows,
+                             num_queries, caller_rows, rows, num_rows, tiles, num_tiles, merge_rows,
                              num_merge_rows, key_cache, value_cache, kv_dtype, num_blocks,
                              block_size, block_tables, block_table_stride, context_lens, num_seqs,
                              num_heads, head_dim, scale, max_context_len, partition_size, flags,
@@ -1822,7 +1848,8 @@ extern "C" int pkv_paged_attention(float* out, const float* queries, int64_t que
 
 extern "C" int pkv_paged_attention_noalloc(
     float* out, const float* queries, int64_t query_token_stride, const int32_t* query_positions,
-    const int32_t* query_seq, int64_t num_queries, const int32_t* rows, int64_t num_rows,
+    const int32_t* query_seq, int64_t num_queries, const int32_t* caller_rows, const int32_t* rows,
+    int64_t num_rows,
     const int32_t* tiles, int64_t num_tiles, const int32_t* merge_rows, int64_t num_merge_rows,
     const void* key_cache, const void* value_cache, pkv_dtype kv_dtype, int64_t num_blocks,
     int32_t block_size, const int32_t* block_tables, int32_t block_table_stride,
@@ -1849,7 +1876,7 @@ extern "C" int pkv_paged_attention_noalloc(
     }
   }
   return pkv::attention_call(out, queries, query_token_stride, query_positions, query_seq,
-                             num_queries, rows, num_rows, tiles, num_tiles, merge_rows,
+                             num_queries, caller_rows, rows, num_rows, tiles, num_tiles, merge_rows,
                              num_merge_rows, key_cache, value_cache, kv_dtype, num_blocks,
                              block_size, block_tables, block_table_stride, context_lens, num_seqs,
                              num_heads, head_dim, scale, max_context_len, partition_size, flags,
@@ -1859,7 +1886,8 @@ extern "C" int pkv_paged_attention_noalloc(
 
 extern "C" int pkv_paged_attention_append(
     float* out, const float* queries, int64_t query_token_stride, const int32_t* query_positions,
-    const int32_t* query_seq, int64_t num_queries, const int32_t* rows, int64_t num_rows,
+    const int32_t* query_seq, int64_t num_queries, const int32_t* caller_rows, const int32_t* rows,
+    int64_t num_rows,
     const int32_t* merge_rows, int64_t num_merge_rows, void* key_cache, void* value_cache,
     pkv_dtype kv_dtype, int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
     int32_t block_table_stride, const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,
@@ -1870,7 +1898,8 @@ extern "C" int pkv_paged_attention_append(
   const pkv::AppendSource append{new_keys, new_values, new_dtype, new_key_token_stride,
                                  new_value_token_stride, slot_mapping};
   return pkv::attention_call(out, queries, query_token_stride, query_positions, query_seq,
-                             num_queries, rows, num_rows, nullptr, 0, merge_rows, num_merge_rows,
+                             num_queries, caller_rows, rows, num_rows, nullptr, 0, merge_rows,
+                             num_merge_rows,
                              key_cache, value_cache, kv_dtype, num_blocks, block_size,
                              block_tables, block_table_stride, context_lens, num_seqs, num_heads,
                              head_dim, scale, max_context_len, partition_size, flags, workspace,

@@ -33,13 +33,13 @@
 //       held_obj keeps, per row, the tuple it was last filled from: a scheduler rebuilds each
 //       table tuple from the same int objects every step, so an unchanged table compares equal
 //       by identity, element by element, without converting a single id.
-//   cow_groups(pairs, out[, marks]) -> list of group sizes
-//       Flattens a list of (src, dst) block copies into the int64 buffer `out` (>= 2 entries
-//       per pair) and splits them, in order, into groups that may each run as one concurrent
-//       pkv_copy_blocks launch (ops.independent_groups): a copy starts a new group when it
-//       reads a block an earlier copy of the group writes, or writes a block an earlier copy of
-//       the group reads or writes. `marks` (uint8, one zero per pool block, left all zero)
-//       replaces the hash sets that track the group's blocks.
+//   CopyQueue(num_blocks)
+//       A runner's queued copy-on-write copies. push(src, dst) checks and queues one copy (the
+//       runner's copy_block); groups() gives the sizes of the consecutive groups that may each
+//       run as one concurrent pkv_copy_blocks launch (ops.independent_groups: a copy starts a
+//       new group when it reads a block an earlier copy of the group writes, or writes a block
+//       an earlier copy of the group reads or writes); flush(...) sends the pairs to the device
+//       and launches one pkv_copy_blocks per group; clear() and items() drop and list them.
 //   exclusive_writes(rows, contexts, host, block_size, marks) -> bool
 //       Whether a batch of single-token entries at their last positions (entry e: arena row
 //       rows[e], context contexts[e], so it writes position contexts[e] - 1) may append inside
@@ -50,11 +50,14 @@
 //       completes before attention reads it as the reference does (runner.py:195-212). `marks`
 //       is an int32 buffer with one zero per pool block; it is left all zero.
 //   bind(plan_batch, paged_attention, paged_attention_append, copy_blocks, rms_norm, silu_mul,
-//        rope_append, memcpy_async[, gather_rows, greedy_tokens, get_device, set_device])
+//        rope_append, memcpy_async[, gather_rows, greedy_tokens, get_device, set_device,
+//        event_create, event_record, event_synchronize, event_destroy, append])
 //       Takes the addresses of those libpkv.so entry points (include/pkv.h), so the calls below
 //       reach the library without ctypes' per-argument conversions, and of hipMemcpyAsync,
-//       hipGetDevice and hipSetDevice as the HIP runtime that libpkv.so is linked against
-//       exports them.
+//       hipGetDevice, hipSetDevice and hipEventCreateWithFlags / Record / Synchronize / Destroy
+//       as the HIP runtime that libpkv.so is linked against exports them.
+//   event_create(device) -> int, event_destroy(event)
+//       A timing-free HIP event on `device` as an integer handle (for stage), and its release.
 //   forward(fields, layers, eps, scale) -> None
 //       One ModelRunner iteration's forward pass (the reference's runner.py:189-227 with
 //       model.py:243-264), every launch enqueued from here on `stream` with the device made
@@ -67,17 +70,18 @@
 //       the integers of the Field enum below (addresses, sizes, the attention plan); `layers`
 //       one tuple of six weight addresses per layer (attn_norm, qkv, out_proj, ffn_norm,
 //       [gate | up], down). Raises RuntimeError naming the first step that failed.
-//   stage(parts64, parts32, host, device_address, stream) -> list of byte offsets | None
+//   stage(parts64, parts32, host, device_address, stream[, event]) -> list of byte offsets | None
 //       A runner call's metadata transfer: the int64 arrays of the list parts64, then the int32
 //       arrays of parts32, packed back to back into the pinned uint8 buffer `host` and copied to
-//       device_address with one hipMemcpyAsync on `stream`. Returns each part's byte offset, or
-//       None (nothing written) when `host` is too small; the caller keeps the device buffer at
-//       least as large as `host`.
+//       device_address with one hipMemcpyAsync on `stream`. With an event (event_create), it
+//       first waits for the event (the previous copy out of `host` has finished) and records it
+//       after the copy. Returns each part's byte offset, or None (nothing written) when `host` is
+//       too small; the caller keeps the device buffer at least as large as `host`.
 //   plan(query_seq, query_positions | None, tables, contexts, block_size, num_heads, head_dim,
 //        kv_dtype, partition_size, min_tile_rows, rows, tiles, merge, counts, launch) -> int
 //       pkv_plan_batch on NumPy buffers; returns its PKV_* code.
 //   paged_attention(...), paged_attention_append(...), copy_blocks(...), rms_norm(...),
-//   silu_mul(...), rope_append(...) -> int
+//   silu_mul(...), rope_append(...), append(...) -> int
 //       The entry points of the same names, with every pointer, stream and handle passed as a
 //       Python int (0 for NULL) in the order of their C declarations; returns the PKV_* code.
 //
@@ -574,84 +578,6 @@ done:
   return result;
 }
 
-PyObject* cow_groups(PyObject*, PyObject* args) {
-  PyObject *pairs_o, *out_o, *marks_o = Py_None;
-  if (!PyArg_ParseTuple(args, "OO|O", &pairs_o, &out_o, &marks_o)) return nullptr;
-  PyObject* pairs = PySequence_Fast(pairs_o, "pairs must be a sequence");
-  if (pairs == nullptr) return nullptr;
-  const Py_ssize_t count = PySequence_Fast_GET_SIZE(pairs);
-  PyObject** items = PySequence_Fast_ITEMS(pairs);
-  Buf<int64_t> out;
-  Buf<uint8_t> marks;
-  PyObject* result = nullptr;
-  std::vector<Py_ssize_t> sizes;
-  // Blocks read (bit 0) and written (bit 1) by the current group: one byte per pool block when
-  // `marks` (all zero, left all zero) is given, else hash sets.
-  std::unordered_set<int64_t> reads, writes;
-  std::vector<int64_t> touched;
-  uint8_t* mark = nullptr;
-  int64_t num_marks = 0;
-  Py_ssize_t current = 0;
-  if (!out.get(out_o, "out")) goto done;
-  if (marks_o != Py_None) {
-    if (!marks.get(marks_o, "marks")) goto done;
-    mark = marks.data();
-    num_marks = marks.size();
-  }
-  if (out.size() < 2 * count) {
-    PyErr_SetString(PyExc_ValueError, "out holds fewer than two entries per pair");
-    goto done;
-  }
-  for (Py_ssize_t i = 0; i < count; ++i) {
-    PyObject* pair = PySequence_Fast(items[i], "a copy must be a (src, dst) pair");
-    if (pair == nullptr) goto done;
-    int64_t src = 0, dst = 0;
-    const bool ok = PySequence_Fast_GET_SIZE(pair) == 2 && as_i64(PySequence_Fast_GET_ITEM(pair, 0), &src) &&
-                    as_i64(PySequence_Fast_GET_ITEM(pair, 1), &dst);
-    Py_DECREF(pair);
-    if (!ok) {
-      if (!PyErr_Occurred()) PyErr_SetString(PyExc_ValueError, "a copy must be a (src, dst) pair");
-      goto done;
-    }
-    // Ids outside the marks (the runner checks them at copy_block) are tracked in the sets.
-    const bool src_marked = src >= 0 && src < num_marks;
-    const bool dst_marked = dst >= 0 && dst < num_marks;
-    const bool conflict = (src_marked ? (mark[src] & 2) != 0 : writes.count(src) != 0) ||
-                          (dst_marked ? mark[dst] != 0 : (reads.count(dst) != 0 || writes.count(dst) != 0));
-    if (current > 0 && conflict) {
-      sizes.push_back(current);
-      current = 0;
-      reads.clear();
-      writes.clear();
-      for (int64_t b : touched) mark[b] = 0;
-      touched.clear();
-    }
-    out.data()[2 * i] = src;
-    out.data()[2 * i + 1] = dst;
-    if (src_marked) {
-      mark[src] |= 1;
-      touched.push_back(src);
-    } else {
-      reads.insert(src);
-    }
-    if (dst_marked) {
-      mark[dst] |= 2;
-      touched.push_back(dst);
-    } else {
-      writes.insert(dst);
-    }
-    ++current;
-  }
-  if (current > 0) sizes.push_back(current);
-  result = PyList_New(static_cast<Py_ssize_t>(sizes.size()));
-  if (result == nullptr) goto done;
-  for (size_t g = 0; g < sizes.size(); ++g) PyList_SET_ITEM(result, g, PyLong_FromSsize_t(sizes[g]));
-done:
-  for (int64_t b : touched) mark[b] = 0;
-  Py_DECREF(pairs);
-  return result;
-}
-
 PyObject* exclusive_writes(PyObject*, PyObject* args) {
   PyObject *rows_o, *contexts_o, *host_o, *marks_o;
   long long block_size;
@@ -723,6 +649,7 @@ decltype(&pkv_copy_blocks) g_copy_blocks = nullptr;
 decltype(&pkv_rms_norm) g_rms_norm = nullptr;
 decltype(&pkv_silu_mul) g_silu_mul = nullptr;
 decltype(&pkv_rope_append) g_rope_append = nullptr;
+decltype(&pkv_append) g_append = nullptr;
 decltype(&pkv_gather_rows) g_gather_rows = nullptr;
 decltype(&pkv_greedy_tokens) g_greedy_tokens = nullptr;
 // hipGetDevice / hipSetDevice of the same runtime, by their C signatures.
@@ -735,6 +662,36 @@ SetDeviceFn g_set_device = nullptr;
 using MemcpyAsyncFn = int (*)(void* dst, const void* src, size_t bytes, int kind, void* stream);
 MemcpyAsyncFn g_memcpy_async = nullptr;
 constexpr int kHostToDevice = 1;  // hipMemcpyHostToDevice
+// hipEventCreateWithFlags / hipEventRecord / hipEventSynchronize / hipEventDestroy, likewise
+// (hipEvent_t is a pointer).
+using EventCreateFn = int (*)(void** event, unsigned flags);
+using EventRecordFn = int (*)(void* event, void* stream);
+using EventFn = int (*)(void* event);
+EventCreateFn g_event_create = nullptr;
+EventRecordFn g_event_record = nullptr;
+EventFn g_event_synchronize = nullptr;
+EventFn g_event_destroy = nullptr;
+constexpr unsigned kEventDisableTiming = 2;  // hipEventDisableTiming
+
+// A timing-free event created on `device` (made current for the call, then restored); null with
+// a RuntimeError set on failure.
+void* make_event(int device) {
+  if (g_event_create == nullptr || g_get_device == nullptr || g_set_device == nullptr) {
+    PyErr_SetString(PyExc_RuntimeError, "_pkvhost.bind() has not been given the HIP event entry points");
+    return nullptr;
+  }
+  int previous = 0;
+  void* event = nullptr;
+  int rc = g_get_device(&previous);
+  if (rc == 0 && previous != device) rc = g_set_device(device);
+  if (rc == 0) rc = g_event_create(&event, kEventDisableTiming);
+  if (previous != device) g_set_device(previous);
+  if (rc != 0 || event == nullptr) {
+    PyErr_Format(PyExc_RuntimeError, "hipEventCreateWithFlags failed (hipError_t %d)", rc);
+    return nullptr;
+  }
+  return event;
+}
 
 bool bound(const void* fn) {
   if (fn != nullptr) return true;
@@ -750,8 +707,10 @@ T* ptr(unsigned long long address) {
 PyObject* bind(PyObject*, PyObject* args) {
   unsigned long long plan, attention, attention_append, copy, norm, gate, rope, memcpy_async;
   unsigned long long gather_rows = 0, greedy = 0, get_device = 0, set_device = 0;
-  if (!PyArg_ParseTuple(args, "KKKKKKKK|KKKK", &plan, &attention, &attention_append, &copy, &norm, &gate, &rope,
-                        &memcpy_async, &gather_rows, &greedy, &get_device, &set_device)) {
+  unsigned long long event_create = 0, event_record = 0, event_synchronize = 0, event_destroy = 0, append = 0;
+  if (!PyArg_ParseTuple(args, "KKKKKKKK|KKKKKKKKK", &plan, &attention, &attention_append, &copy, &norm, &gate, &rope,
+                        &memcpy_async, &gather_rows, &greedy, &get_device, &set_device, &event_create,
+                        &event_record, &event_synchronize, &event_destroy, &append)) {
     return nullptr;
   }
   if (plan == 0 || attention == 0 || attention_append == 0 || copy == 0 || norm == 0 || gate == 0 || rope == 0 ||
@@ -772,17 +731,41 @@ PyObject* bind(PyObject*, PyObject* args) {
   g_silu_mul = reinterpret_cast<decltype(g_silu_mul)>(static_cast<uintptr_t>(gate));
   g_rope_append = reinterpret_cast<decltype(g_rope_append)>(static_cast<uintptr_t>(rope));
   g_memcpy_async = reinterpret_cast<MemcpyAsyncFn>(static_cast<uintptr_t>(memcpy_async));
+  g_event_create = reinterpret_cast<EventCreateFn>(static_cast<uintptr_t>(event_create));
+  g_event_record = reinterpret_cast<EventRecordFn>(static_cast<uintptr_t>(event_record));
+  g_event_synchronize = reinterpret_cast<EventFn>(static_cast<uintptr_t>(event_synchronize));
+  g_event_destroy = reinterpret_cast<EventFn>(static_cast<uintptr_t>(event_destroy));
+  g_append = reinterpret_cast<decltype(g_append)>(static_cast<uintptr_t>(append));
+  Py_RETURN_NONE;
+}
+
+PyObject* event_create(PyObject*, PyObject* args) {
+  int device;
+  if (!PyArg_ParseTuple(args, "i", &device)) return nullptr;
+  void* event = make_event(device);
+  if (event == nullptr) return nullptr;
+  return PyLong_FromVoidPtr(event);
+}
+
+PyObject* event_destroy(PyObject*, PyObject* args) {
+  unsigned long long event;
+  if (!PyArg_ParseTuple(args, "K", &event)) return nullptr;
+  if (event != 0 && g_event_destroy != nullptr) g_event_destroy(reinterpret_cast<void*>(static_cast<uintptr_t>(event)));
   Py_RETURN_NONE;
 }
 
 PyObject* stage(PyObject*, PyObject* args) {
   PyObject *p64_o, *p32_o, *host_o;
-  unsigned long long device_address, stream;
-  if (!PyArg_ParseTuple(args, "O!O!OKK", &PyList_Type, &p64_o, &PyList_Type, &p32_o, &host_o, &device_address,
-                        &stream)) {
+  unsigned long long device_address, stream, event = 0;
+  if (!PyArg_ParseTuple(args, "O!O!OKK|K", &PyList_Type, &p64_o, &PyList_Type, &p32_o, &host_o, &device_address,
+                        &stream, &event)) {
     return nullptr;
   }
   if (!bound(reinterpret_cast<const void*>(g_memcpy_async))) return nullptr;
+  if (event != 0 && (g_event_record == nullptr || g_event_synchronize == nullptr)) {
+    PyErr_SetString(PyExc_RuntimeError, "_pkvhost.bind() has not been given the HIP event entry points");
+    return nullptr;
+  }
   const Py_ssize_t n64 = PyList_GET_SIZE(p64_o), n32 = PyList_GET_SIZE(p32_o);
   Buf<uint8_t> host;
   std::unique_ptr<Buf<int64_t>[]> b64(new Buf<int64_t>[n64]);
@@ -801,6 +784,14 @@ PyObject* stage(PyObject*, PyObject* args) {
   if (bytes > 0 && device_address == 0) {
     PyErr_SetString(PyExc_ValueError, "stage() needs a device buffer");
     return nullptr;
+  }
+  // The copy the previous call queued from this buffer must have read it before it is rewritten.
+  if (event != 0) {
+    const int rc = g_event_synchronize(reinterpret_cast<void*>(static_cast<uintptr_t>(event)));
+    if (rc != 0) {
+      PyErr_Format(PyExc_RuntimeError, "hipEventSynchronize failed (hipError_t %d)", rc);
+      return nullptr;
+    }
   }
   PyObject* offsets = PyList_New(n64 + n32);
   if (offsets == nullptr) return nullptr;
@@ -827,6 +818,15 @@ PyObject* stage(PyObject*, PyObject* args) {
       Py_DECREF(offsets);
       PyErr_Format(PyExc_RuntimeError, "hipMemcpyAsync of the call's metadata failed (hipError_t %d)", rc);
       return nullptr;
+    }
+    if (event != 0) {
+      const int rec = g_event_record(reinterpret_cast<void*>(static_cast<uintptr_t>(event)),
+                                     reinterpret_cast<void*>(static_cast<uintptr_t>(stream)));
+      if (rec != 0) {
+        Py_DECREF(offsets);
+        PyErr_Format(PyExc_RuntimeError, "hipEventRecord failed (hipError_t %d)", rec);
+        return nullptr;
+      }
     }
   }
   return offsets;
@@ -866,12 +866,13 @@ PyObject* plan(PyObject*, PyObject* args) {
 }
 
 PyObject* paged_attention(PyObject*, PyObject* args) {
-  unsigned long long out, queries, qpos, qseq, rows, tiles, merge, kc, vc, tables, ctx, ws, stream;
+  unsigned long long out, queries, qpos, qseq, caller_rows, rows, tiles, merge, kc, vc, tables, ctx, ws, stream;
   long long q_stride, nq, nrows, ntiles, nmerge, nblocks, ws_bytes;
   int dtype, block_size, table_stride, nseqs, heads, head_dim, max_ctx, partition, flags, device;
   float scale;
-  if (!PyArg_ParseTuple(args, "KKLKKLKLKLKLKKiLiKiKiiifiiiKLiK", &out, &queries, &q_stride, &qpos, &qseq, &nq,
-                        &rows, &nrows, &tiles, &ntiles, &merge, &nmerge, &kc, &vc, &dtype, &nblocks, &block_size,
+  if (!PyArg_ParseTuple(args, "KKLKKLKKLKLKLKKiLiKiKiiifiiiKLiK", &out, &queries, &q_stride, &qpos, &qseq, &nq,
+                        &caller_rows, &rows, &nrows, &tiles, &ntiles, &merge, &nmerge, &kc, &vc, &dtype, &nblocks,
+                        &block_size,
                         &tables, &table_stride, &ctx, &nseqs, &heads, &head_dim, &scale, &max_ctx, &partition,
                         &flags, &ws, &ws_bytes, &device, &stream)) {
     return nullptr;
@@ -879,7 +880,8 @@ PyObject* paged_attention(PyObject*, PyObject* args) {
   if (!bound(reinterpret_cast<const void*>(g_paged_attention))) return nullptr;
   const int rc = g_paged_attention(
       ptr<float>(out), ptr<const float>(queries), q_stride, ptr<const int32_t>(qpos), ptr<const int32_t>(qseq), nq,
-      ptr<const int32_t>(rows), nrows, ptr<const int32_t>(tiles), ntiles, ptr<const int32_t>(merge), nmerge,
+      ptr<const int32_t>(caller_rows), ptr<const int32_t>(rows), nrows, ptr<const int32_t>(tiles), ntiles,
+      ptr<const int32_t>(merge), nmerge,
       ptr<const void>(kc), ptr<const void>(vc), static_cast<pkv_dtype>(dtype), nblocks, block_size,
       ptr<const int32_t>(tables), table_stride, ptr<const int32_t>(ctx), nseqs, heads, head_dim, scale, max_ctx,
       partition, flags, ptr<float>(ws), ws_bytes, device, ptr<void>(stream));
@@ -887,12 +889,13 @@ PyObject* paged_attention(PyObject*, PyObject* args) {
 }
 
 PyObject* paged_attention_append(PyObject*, PyObject* args) {
-  unsigned long long out, queries, qpos, qseq, rows, merge, kc, vc, tables, ctx, ws, new_k, new_v, slots, stream;
+  unsigned long long out, queries, qpos, qseq, caller_rows, rows, merge, kc, vc, tables, ctx, ws, new_k, new_v, slots,
+      stream;
   long long q_stride, nq, nrows, nmerge, nblocks, ws_bytes, k_stride, v_stride;
   int dtype, block_size, table_stride, nseqs, heads, head_dim, max_ctx, partition, flags, new_dtype, device;
   float scale;
-  if (!PyArg_ParseTuple(args, "KKLKKLKLKLKKiLiKiKiiifiiiKLKKiLLKiK", &out, &queries, &q_stride, &qpos, &qseq, &nq,
-                        &rows, &nrows, &merge, &nmerge, &kc, &vc, &dtype, &nblocks, &block_size, &tables,
+  if (!PyArg_ParseTuple(args, "KKLKKLKKLKLKKiLiKiKiiifiiiKLKKiLLKiK", &out, &queries, &q_stride, &qpos, &qseq, &nq,
+                        &caller_rows, &rows, &nrows, &merge, &nmerge, &kc, &vc, &dtype, &nblocks, &block_size, &tables,
                         &table_stride, &ctx, &nseqs, &heads, &head_dim, &scale, &max_ctx, &partition, &flags, &ws,
                         &ws_bytes, &new_k, &new_v, &new_dtype, &k_stride, &v_stride, &slots, &device, &stream)) {
     return nullptr;
@@ -900,7 +903,8 @@ PyObject* paged_attention_append(PyObject*, PyObject* args) {
   if (!bound(reinterpret_cast<const void*>(g_paged_attention_append))) return nullptr;
   const int rc = g_paged_attention_append(
       ptr<float>(out), ptr<const float>(queries), q_stride, ptr<const int32_t>(qpos), ptr<const int32_t>(qseq), nq,
-      ptr<const int32_t>(rows), nrows, ptr<const int32_t>(merge), nmerge, ptr<void>(kc), ptr<void>(vc),
+      ptr<const int32_t>(caller_rows), ptr<const int32_t>(rows), nrows, ptr<const int32_t>(merge), nmerge,
+      ptr<void>(kc), ptr<void>(vc),
       static_cast<pkv_dtype>(dtype), nblocks, block_size, ptr<const int32_t>(tables), table_stride,
       ptr<const int32_t>(ctx), nseqs, heads, head_dim, scale, max_ctx, partition, flags, ptr<float>(ws), ws_bytes,
       ptr<const void>(new_k), ptr<const void>(new_v), static_cast<pkv_dtype>(new_dtype), k_stride, v_stride,
@@ -921,6 +925,242 @@ PyObject* copy_blocks(PyObject*, PyObject* args) {
                                npairs, layers, nblocks, block_elems, device, ptr<void>(stream));
   return PyLong_FromLong(rc);
 }
+
+// ---- CopyQueue: the runner's queued copy-on-write copies ----------------------------------------
+
+struct CopyQueue {
+  PyObject_HEAD
+  std::vector<int64_t>* pairs;  // flat (src, dst), in queue order
+  std::vector<uint8_t>* marks;  // one per pool block, all zero between flushes
+  int64_t num_blocks;
+  void* event;  // recorded after the pairs' copy to the device; created at the first flush
+};
+
+PyObject* copy_queue_new(PyTypeObject* type, PyObject* args, PyObject* kwds) {
+  static const char* kwlist[] = {"num_blocks", nullptr};
+  long long num_blocks;
+  if (!PyArg_ParseTupleAndKeywords(args, kwds, "L", const_cast<char**>(kwlist), &num_blocks)) return nullptr;
+  if (num_blocks < 1) {
+    PyErr_SetString(PyExc_ValueError, "num_blocks must be >= 1");
+    return nullptr;
+  }
+  CopyQueue* self = reinterpret_cast<CopyQueue*>(type->tp_alloc(type, 0));
+  if (self == nullptr) return nullptr;
+  self->num_blocks = num_blocks;
+  self->event = nullptr;
+  try {
+    self->pairs = new std::vector<int64_t>();
+    self->marks = new std::vector<uint8_t>(static_cast<size_t>(num_blocks), 0);
+  } catch (const std::bad_alloc&) {
+    Py_DECREF(self);
+    return PyErr_NoMemory();
+  }
+  return reinterpret_cast<PyObject*>(self);
+}
+
+void copy_queue_dealloc(CopyQueue* self) {
+  delete self->pairs;
+  delete self->marks;
+  if (self->event != nullptr && g_event_destroy != nullptr) g_event_destroy(self->event);
+  Py_TYPE(self)->tp_free(reinterpret_cast<PyObject*>(self));
+}
+
+// push(source, destination): the reference's copy_block checks (runner.py:128-133 and this
+// package's ModelRunner.copy_block), then the pair joins the queue.
+PyObject* copy_queue_push(CopyQueue* self, PyObject* const* args, Py_ssize_t nargs) {
+  if (nargs != 2) {
+    PyErr_SetString(PyExc_TypeError, "copy_block() takes a source and a destination block id");
+    return nullptr;
+  }
+  const int same = PyObject_RichCompareBool(args[0], args[1], Py_EQ);
+  if (same < 0) return nullptr;
+  if (same) {
+    PyErr_SetString(PyExc_ValueError, "copy-on-write must not copy a block onto itself");
+    return nullptr;
+  }
+  int64_t ids[2];
+  for (int i = 0; i < 2; ++i) {
+    const long long v = PyLong_AsLongLong(args[i]);
+    if (v == -1 && PyErr_Occurred()) {
+      if (!PyErr_ExceptionMatches(PyExc_OverflowError)) return nullptr;
+      PyErr_Clear();
+      ids[i] = -1;  // beyond int64: outside the pool
+    } else {
+      ids[i] = v;
+    }
+  }
+  for (int i = 0; i < 2; ++i) {
+    if (ids[i] < 0 || ids[i] >= self->num_blocks) {
+      PyErr_Format(PyExc_IndexError, "block id %S is outside the pool", args[i]);
+      return nullptr;
+    }
+  }
+  try {
+    self->pairs->push_back(ids[0]);
+    self->pairs->push_back(ids[1]);
+  } catch (const std::bad_alloc&) {
+    return PyErr_NoMemory();
+  }
+  Py_RETURN_NONE;
+}
+
+// Sizes of the consecutive groups of independent queued copies, tracked with one mark byte per
+// block (bit 0 read, bit 1 written by the current group; left all zero). Every id was checked
+// against the pool at push.
+std::vector<size_t> copy_groups(CopyQueue* self) {
+  const std::vector<int64_t>& p = *self->pairs;
+  const size_t n = p.size() / 2;
+  std::vector<size_t> sizes;
+  uint8_t* mark = self->marks->data();
+  std::vector<int64_t> touched;
+  touched.reserve(2 * n);
+  size_t current = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const int64_t src = p[2 * i], dst = p[2 * i + 1];
+    if (current > 0 && ((mark[src] & 2) != 0 || mark[dst] != 0)) {
+      sizes.push_back(current);
+      current = 0;
+      for (int64_t b : touched) mark[b] = 0;
+      touched.clear();
+    }
+    mark[src] |= 1;
+    mark[dst] |= 2;
+    touched.push_back(src);
+    touched.push_back(dst);
+    ++current;
+  }
+  if (current > 0) sizes.push_back(current);
+  for (int64_t b : touched) mark[b] = 0;
+  return sizes;
+}
+
+PyObject* copy_queue_groups(CopyQueue* self, PyObject*) {
+  const std::vector<size_t> sizes = copy_groups(self);
+  PyObject* out = PyList_New(static_cast<Py_ssize_t>(sizes.size()));
+  if (out == nullptr) return nullptr;
+  for (size_t g = 0; g < sizes.size(); ++g) {
+    PyObject* size = PyLong_FromSize_t(sizes[g]);
+    if (size == nullptr) {
+      Py_DECREF(out);
+      return nullptr;
+    }
+    PyList_SET_ITEM(out, static_cast<Py_ssize_t>(g), size);
+  }
+  return out;
+}
+
+Py_ssize_t copy_queue_len(CopyQueue* self) { return static_cast<Py_ssize_t>(self->pairs->size() / 2); }
+
+PyObject* copy_queue_clear(CopyQueue* self, PyObject*) {
+  self->pairs->clear();
+  Py_RETURN_NONE;
+}
+
+PyObject* copy_queue_items(CopyQueue* self, PyObject*) {
+  const std::vector<int64_t>& p = *self->pairs;
+  PyObject* out = PyList_New(static_cast<Py_ssize_t>(p.size() / 2));
+  if (out == nullptr) return nullptr;
+  for (size_t i = 0; i < p.size() / 2; ++i) {
+    PyObject* pair = Py_BuildValue("(LL)", static_cast<long long>(p[2 * i]), static_cast<long long>(p[2 * i + 1]));
+    if (pair == nullptr) {
+      Py_DECREF(out);
+      return nullptr;
+    }
+    PyList_SET_ITEM(out, static_cast<Py_ssize_t>(i), pair);
+  }
+  return out;
+}
+
+// flush(key_pool, value_pool, kv_dtype, layers, block_elems, host, device_address, device, stream)
+//   -> (rc, n)
+// Launches the queued copies in order, as pkv_copy_blocks launches of consecutive groups of
+// independent copies (a copy starts a new group when it reads a block an earlier copy of the
+// group writes, or writes a block an earlier copy of the group reads or writes), their pairs
+// sent in one hipMemcpyAsync from the pinned uint8 buffer `host` to device_address. Before it
+// rewrites `host` it waits for the event recorded after the previous flush's copy. (0, n): n
+// copies launched and dequeued. (0, -bytes): `host` is smaller than the `bytes` the pairs need;
+// nothing was done. (rc, 0): a launch failed with PKV code rc; every copy stays queued (a group
+// reads no block it writes, so a group that ran already leaves the same bytes when it runs again).
+PyObject* copy_queue_flush(CopyQueue* self, PyObject* args) {
+  unsigned long long kp, vp, device_address, stream;
+  int dtype, layers, device;
+  long long block_elems;
+  PyObject* host_o;
+  if (!PyArg_ParseTuple(args, "KKiiLOKiK", &kp, &vp, &dtype, &layers, &block_elems, &host_o, &device_address, &device,
+                        &stream)) {
+    return nullptr;
+  }
+  const std::vector<int64_t>& p = *self->pairs;
+  const size_t n = p.size() / 2;
+  if (n == 0) return Py_BuildValue("(ii)", 0, 0);
+  if (!bound(reinterpret_cast<const void*>(g_copy_blocks)) || !bound(reinterpret_cast<const void*>(g_memcpy_async))) {
+    return nullptr;
+  }
+  if (g_event_record == nullptr || g_event_synchronize == nullptr) {
+    PyErr_SetString(PyExc_RuntimeError, "_pkvhost.bind() has not been given the HIP event entry points");
+    return nullptr;
+  }
+  Buf<uint8_t> host;
+  if (!host.get(host_o, "host")) return nullptr;
+  const Py_ssize_t bytes = static_cast<Py_ssize_t>(16 * n);
+  if (host.size() < bytes) return Py_BuildValue("(in)", 0, -bytes);
+  if (device_address == 0) {
+    PyErr_SetString(PyExc_ValueError, "flush() needs a device buffer");
+    return nullptr;
+  }
+  const std::vector<size_t> sizes = copy_groups(self);
+  if (self->event == nullptr) {
+    self->event = make_event(device);
+    if (self->event == nullptr) return nullptr;
+  } else {
+    const int rc = g_event_synchronize(self->event);
+    if (rc != 0) {
+      PyErr_Format(PyExc_RuntimeError, "hipEventSynchronize failed (hipError_t %d)", rc);
+      return nullptr;
+    }
+  }
+  std::memcpy(host.data(), p.data(), static_cast<size_t>(bytes));
+  void* dev = reinterpret_cast<void*>(static_cast<uintptr_t>(device_address));
+  void* strm = reinterpret_cast<void*>(static_cast<uintptr_t>(stream));
+  int rc = g_memcpy_async(dev, host.data(), static_cast<size_t>(bytes), kHostToDevice, strm);
+  if (rc != 0) {
+    PyErr_Format(PyExc_RuntimeError, "hipMemcpyAsync of the copy pairs failed (hipError_t %d)", rc);
+    return nullptr;
+  }
+  rc = g_event_record(self->event, strm);
+  if (rc != 0) {
+    PyErr_Format(PyExc_RuntimeError, "hipEventRecord failed (hipError_t %d)", rc);
+    return nullptr;
+  }
+  size_t start = 0;
+  for (size_t size : sizes) {
+    rc = g_copy_blocks(ptr<void>(kp), ptr<void>(vp), static_cast<pkv_dtype>(dtype),
+                       reinterpret_cast<const int64_t*>(static_cast<uint8_t*>(dev) + 16 * start),
+                       static_cast<int64_t>(size), layers, self->num_blocks, block_elems, device, strm);
+    if (rc != 0) return Py_BuildValue("(ii)", rc, 0);
+    start += size;
+  }
+  self->pairs->clear();
+  return Py_BuildValue("(in)", 0, static_cast<Py_ssize_t>(n));
+}
+
+PyMethodDef kCopyQueueMethods[] = {
+    {"push", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(copy_queue_push)), METH_FASTCALL,
+     "Queue one block copy (source, destination), checked against the pool."},
+    {"flush", reinterpret_cast<PyCFunction>(copy_queue_flush), METH_VARARGS,
+     "Launch the queued copies as batched pkv_copy_blocks launches: (rc, copies) or (0, -bytes needed)."},
+    {"groups", reinterpret_cast<PyCFunction>(copy_queue_groups), METH_NOARGS,
+     "Sizes of the consecutive groups of independent queued copies (one launch each)."},
+    {"clear", reinterpret_cast<PyCFunction>(copy_queue_clear), METH_NOARGS, "Drop every queued copy."},
+    {"items", reinterpret_cast<PyCFunction>(copy_queue_items), METH_NOARGS, "The queued (source, destination) pairs."},
+    {nullptr, nullptr, 0, nullptr},
+};
+
+PySequenceMethods kCopyQueueSequence = {
+    reinterpret_cast<lenfunc>(copy_queue_len),  // sq_length
+};
+
+PyTypeObject kCopyQueueType = {PyVarObject_HEAD_INIT(nullptr, 0) "_pkvhost.CopyQueue"};
 
 PyObject* rms_norm(PyObject*, PyObject* args) {
   unsigned long long out, hidden, delta, weight, stream;
@@ -948,6 +1188,21 @@ PyObject* silu_mul(PyObject*, PyObject* args) {
   if (!bound(reinterpret_cast<const void*>(g_silu_mul))) return nullptr;
   const int rc = g_silu_mul(ptr<float>(out), out_stride, ptr<const float>(gate), ptr<const float>(up), in_stride,
                             rows, width, device, ptr<void>(stream));
+  return PyLong_FromLong(rc);
+}
+
+PyObject* append(PyObject*, PyObject* args) {
+  unsigned long long kp, vp, k, v, slots, stream;
+  long long nslots, k_stride, v_stride, tokens;
+  int pool_dtype, src_dtype, heads, dim, device;
+  if (!PyArg_ParseTuple(args, "KKiLKKiLLKLiiiK", &kp, &vp, &pool_dtype, &nslots, &k, &v, &src_dtype, &k_stride,
+                        &v_stride, &slots, &tokens, &heads, &dim, &device, &stream)) {
+    return nullptr;
+  }
+  if (!bound(reinterpret_cast<const void*>(g_append))) return nullptr;
+  const int rc = g_append(ptr<void>(kp), ptr<void>(vp), static_cast<pkv_dtype>(pool_dtype), nslots, ptr<const void>(k),
+                          ptr<const void>(v), static_cast<pkv_dtype>(src_dtype), k_stride, v_stride,
+                          ptr<const int64_t>(slots), tokens, heads, dim, device, ptr<void>(stream));
   return PyLong_FromLong(rc);
 }
 
@@ -1146,7 +1401,8 @@ PyObject* forward(PyObject*, PyObject* args) {
     // attention over the pools (runner.py:198-212)
     if (v[kNumPlanRows] > 0 || v[kNumTiles] > 0) {
       if (!check(g_paged_attention(attended, fused, 3 * row, ptr<const int32_t>(v[kQueryPositions]),
-                                   ptr<const int32_t>(v[kQuerySeq]), T, ptr<const int32_t>(v[kPlanRows]), v[kNumPlanRows],
+                                   ptr<const int32_t>(v[kQuerySeq]), T, nullptr, ptr<const int32_t>(v[kPlanRows]),
+                                   v[kNumPlanRows],
                                    ptr<const int32_t>(v[kPlanTiles]), v[kNumTiles], ptr<const int32_t>(v[kMerge]),
                                    v[kNumMerge], kp, vp, static_cast<pkv_dtype>(v[kKvDtype]), v[kNumBlocks],
                                    static_cast<int32_t>(v[kBlockSize]), ptr<const int32_t>(v[kTables]),
@@ -1195,7 +1451,6 @@ PyMethodDef kMethods[] = {
     {"gather", gather, METH_VARARGS, "Flatten a batch: tokens, positions, slots, lengths, contexts, logits rows."},
     {"prefix_order_rows", prefix_order_rows, METH_VARARGS, "prefix_order from the block-table arena's rows."},
     {"arena_update", arena_update, METH_VARARGS, "One step of the block-table arena."},
-    {"cow_groups", cow_groups, METH_VARARGS, "Flatten block copies and split them into independent groups."},
     {"exclusive_writes", exclusive_writes, METH_VARARGS,
      "True when no decode row reads a block another row (or its own, elsewhere) writes."},
     {"bind", bind, METH_VARARGS, "Bind the libpkv.so entry points the calls below use."},
@@ -1207,8 +1462,11 @@ PyMethodDef kMethods[] = {
     {"rms_norm", rms_norm, METH_VARARGS, "pkv_rms_norm with integer pointers."},
     {"silu_mul", silu_mul, METH_VARARGS, "pkv_silu_mul with integer pointers."},
     {"rope_append", rope_append, METH_VARARGS, "pkv_rope_append with integer pointers."},
+    {"append", append, METH_VARARGS, "pkv_append with integer pointers."},
     {"stage", stage, METH_VARARGS, "Pack a call's metadata into pinned memory and copy it to the device."},
     {"forward", forward, METH_VARARGS, "One iteration's forward pass: rocBLAS products and the library's kernels."},
+    {"event_create", event_create, METH_VARARGS, "A timing-free HIP event on a device, as an integer handle."},
+    {"event_destroy", event_destroy, METH_VARARGS, "Destroy an event made by event_create."},
     {nullptr, nullptr, 0, nullptr},
 };
 
@@ -1223,5 +1481,21 @@ PyMODINIT_FUNC PyInit__pkvhost(void) {
   s_positions = PyUnicode_InternFromString("positions");
   s_block_table = PyUnicode_InternFromString("block_table");
   s_logits_index = PyUnicode_InternFromString("logits_index");
-  return PyModule_Create(&kModule);
+  kCopyQueueType.tp_basicsize = sizeof(CopyQueue);
+  kCopyQueueType.tp_flags = Py_TPFLAGS_DEFAULT;
+  kCopyQueueType.tp_doc = "CopyQueue(num_blocks): queued copy-on-write block copies, flushed as batched launches.";
+  kCopyQueueType.tp_new = copy_queue_new;
+  kCopyQueueType.tp_dealloc = reinterpret_cast<destructor>(copy_queue_dealloc);
+  kCopyQueueType.tp_methods = kCopyQueueMethods;
+  kCopyQueueType.tp_as_sequence = &kCopyQueueSequence;
+  if (PyType_Ready(&kCopyQueueType) < 0) return nullptr;
+  PyObject* module = PyModule_Create(&kModule);
+  if (module == nullptr) return nullptr;
+  Py_INCREF(&kCopyQueueType);
+  if (PyModule_AddObject(module, "CopyQueue", reinterpret_cast<PyObject*>(&kCopyQueueType)) < 0) {
+    Py_DECREF(&kCopyQueueType);
+    Py_DECREF(module);
+    return nullptr;
+  }
+  return module;
 }

@@ -71,7 +71,9 @@ def _device_index(*tensors: torch.Tensor) -> int:
 
 
 def _stream(device: int) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle of ``device``'s current stream (torch's own accessor, without building a
+    Stream object)."""
+    return torch._C._cuda_getCurrentRawStream(device)
 
 
 def _rows_contiguous(tensor: torch.Tensor, name: str) -> int:
@@ -913,6 +915,7 @@ def launch_paged_attention(
     key_cache: torch.Tensor, value_cache: torch.Tensor, block_tables: torch.Tensor,
     context_lens: torch.Tensor, scale: float, max_context_len: int, plan: AttentionPlan,
     workspace: torch.Tensor, device: int, append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+    caller_rows: torch.Tensor | None = None,
 ) -> None:  # fmt: skip
     """:func:`paged_attention_ragged` for callers that built every argument themselves (the
     runner): the same C call without re-validating shapes and dtypes on the host. Preconditions
@@ -930,7 +933,8 @@ def launch_paged_attention(
     lib = _native.library()
     common = (
         out.data_ptr(), queries.data_ptr(), queries.stride(0), query_positions.data_ptr(), query_seq.data_ptr(),
-        num_queries, plan.rows.data_ptr() if num_rows else None, num_rows,
+        num_queries, None if caller_rows is None else caller_rows.data_ptr(),
+        plan.rows.data_ptr() if num_rows else None, num_rows,
     )  # fmt: skip
     tail = (
         merge.data_ptr() if num_merge > 0 else None, num_merge, key_cache.data_ptr(), value_cache.data_ptr(),
@@ -1012,8 +1016,15 @@ def paged_attention_ragged(
     plan: AttentionPlan | None = None,
     shared_kv: bool | None = None,
     append: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+    caller_rows: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Causal paged attention of every query row of a ragged batch, in one call.
+
+    ``caller_rows`` (int32 ``[T]``, a permutation of ``range(T)``, or None): query t reads row
+    ``caller_rows[t]`` of ``queries`` and writes that row of the output (and, with ``append``,
+    takes that row of the new keys and values and of ``slot_mapping``), while the positions,
+    sequence indices and plan are indexed by t. A plan can then order the rows its own way (rows
+    sharing a prefix next to each other) without the caller reordering its tensors.
 
     ``append=(new_keys, new_values, slot_mapping)`` fuses a decode step's append into the call
     (``pkv_paged_attention_append``): row t's own key and value row (``[T, H, D]`` float32, or
@@ -1047,9 +1058,12 @@ def paged_attention_ragged(
         raise ValueError("caches must have shape (num_blocks, block_size, heads, head_dim)")
     if not (key_cache.is_contiguous() and value_cache.is_contiguous()):
         raise ValueError("caches must be contiguous")
-    for name, tensor in (("query_positions", query_positions), ("query_seq", query_seq)):
-        if tensor.dtype != torch.int32 or tensor.shape != (num_queries,):
+    for name, tensor in (("query_positions", query_positions), ("query_seq", query_seq), ("caller_rows", caller_rows)):
+        if tensor is not None and (tensor.dtype != torch.int32 or tensor.shape != (num_queries,)):
             raise ValueError(f"{name} must be int32 with one entry per query")
+    if caller_rows is not None and (caller_rows.device != queries.device or not caller_rows.is_contiguous()):
+        raise ValueError("caller_rows must be contiguous and on the queries' device")
+    caller_ptr = None if caller_rows is None else caller_rows.data_ptr()
     if block_tables.dtype != torch.int32 or block_tables.dim() != 2:
         raise ValueError("block_tables must be int32 of shape (num_seqs, max_blocks)")
     if not block_tables.is_contiguous():
@@ -1120,7 +1134,7 @@ def paged_attention_ragged(
             raise ValueError("slot_mapping must be int64 with one slot per query row")
         rc = _native.library().pkv_paged_attention_append(
             out.data_ptr(), queries.data_ptr(), stride,
-            query_positions.data_ptr(), query_seq.data_ptr(), num_queries,
+            query_positions.data_ptr(), query_seq.data_ptr(), num_queries, caller_ptr,
             rows_ptr, num_rows, merge_ptr, num_merge,
             key_cache.data_ptr(), value_cache.data_ptr(), kv_dtype_code(key_cache.dtype),
             key_cache.shape[0], key_cache.shape[1],
@@ -1135,7 +1149,7 @@ def paged_attention_ragged(
         return out
     rc = _native.library().pkv_paged_attention(
         out.data_ptr(), queries.data_ptr(), stride,
-        query_positions.data_ptr(), query_seq.data_ptr(), num_queries,
+        query_positions.data_ptr(), query_seq.data_ptr(), num_queries, caller_ptr,
         rows_ptr, num_rows, tiles_ptr, num_tiles, merge_ptr, num_merge,
         key_cache.data_ptr(), value_cache.data_ptr(), kv_dtype_code(key_cache.dtype),
         key_cache.shape[0], key_cache.shape[1],

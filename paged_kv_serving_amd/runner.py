@@ -163,8 +163,9 @@ class _Staging:
     pinned host buffer and copied to a device buffer of the same layout on the runner's stream by
     one C++ call (``_pkvhost.stage``: the packing and one ``hipMemcpyAsync``); the host does not
     wait for the copy. Before a later call rewrites the host buffer it waits for the copy that
-    last read it (an event), which has normally long finished. The device buffer is rewritten by
-    the next call's copy, which the stream orders after this call's kernels."""
+    last read it (a HIP event the same C++ call records), which has normally long finished. The
+    device buffer is rewritten by the next call's copy, which the stream orders after this call's
+    kernels."""
 
     def __init__(self, device: torch.device, host_ext) -> None:
         self.device = device
@@ -172,29 +173,43 @@ class _Staging:
         self.host: torch.Tensor | None = None
         self.dev: torch.Tensor | None = None
         self.base = 0  # device address of self.dev
-        self.done = torch.cuda.Event()
-        self.pending = False
         self._host_np = np.zeros(0, dtype=np.uint8)
+        self._event = 0  # the HIP event recorded after each copy (created at the first send)
 
-    def send(self, parts64: list[np.ndarray], parts32: list[np.ndarray]) -> list[int]:
-        """Copy ``parts64`` (int64 arrays) then ``parts32`` (int32 arrays) to the device; returns
-        each part's byte offset in the device buffer (see :meth:`tensor` and :attr:`base`)."""
-        if self.pending:
-            self.done.synchronize()
-        stream = torch.cuda.current_stream(self.device)
+    def __del__(self) -> None:
+        if self._event:
+            self._ext.event_destroy(self._event)
+            self._event = 0
+
+    @property
+    def host_array(self) -> np.ndarray:
+        """The pinned host buffer as a NumPy uint8 array (empty until :meth:`grow`)."""
+        return self._host_np
+
+    def grow(self, nbytes: int) -> None:
+        """Reallocate both buffers to hold at least ``nbytes``. The old ones are dropped after the
+        device has drained: the last copy from the host buffer and the kernels reading the device
+        buffer are raw HIP work that torch's allocators do not track."""
+        torch.cuda.synchronize(self.device)
+        size = max(nbytes, 2 * self._host_np.size, 1 << 16)
+        self.host = torch.empty(size, dtype=torch.uint8, pin_memory=True)
+        self.dev = torch.empty(size, dtype=torch.uint8, device=self.device)
+        self.base = self.dev.data_ptr()
+        self._host_np = self.host.numpy()
+
+    def send(self, parts64: list[np.ndarray], parts32: list[np.ndarray], stream: int | None = None) -> list[int]:
+        """Copy ``parts64`` (int64 arrays) then ``parts32`` (int32 arrays) to the device on
+        ``stream`` (default: the device's current stream); returns each part's byte offset in the
+        device buffer (see :meth:`tensor` and :attr:`base`)."""
+        if stream is None:
+            stream = ops._stream(self.device.index)
+        if not self._event:
+            self._event = self._ext.event_create(self.device.index)
         while True:
-            offsets = self._ext.stage(parts64, parts32, self._host_np, self.base, stream.cuda_stream)
+            offsets = self._ext.stage(parts64, parts32, self._host_np, self.base, stream, self._event)
             if offsets is not None:
-                break
-            nbytes = 8 * sum(p.size for p in parts64) + 4 * sum(p.size for p in parts32)
-            size = max(nbytes, 2 * self._host_np.size, 1 << 16)
-            self.host = torch.empty(size, dtype=torch.uint8, pin_memory=True)
-            self.dev = torch.empty(size, dtype=torch.uint8, device=self.device)
-            self.base = self.dev.data_ptr()
-            self._host_np = self.host.numpy()
-        self.done.record(stream)
-        self.pending = True
-        return offsets
+                return offsets
+            self.grow(8 * sum(p.size for p in parts64) + 4 * sum(p.size for p in parts32))
 
     def tensor(self, offset: int, count: int, dtype: torch.dtype) -> torch.Tensor:
         """A device tensor view of ``count`` elements of ``dtype`` (int32 or int64) at byte
@@ -206,7 +221,9 @@ class _Staging:
 @dataclass
 class _Step:
     """One iteration's device-side metadata (from :meth:`ModelRunner._prepare`), in the planner's
-    row order; ``token_order`` maps it back to batch order (None: the same). Every section lives
+    row order; ``token_order`` maps it back to batch order (None: the same), and when it is set
+    the staging buffer also holds it as int32 (``caller_rows_at``: the attention call's
+    caller_rows) and the slots in batch order (``batch_slots_at``). Every section lives
     in the staging buffer at ``staging.base`` + its byte offset; the ``*_at`` fields are those
     offsets, and :meth:`tensor` gives torch views where torch needs them."""
 
@@ -230,14 +247,18 @@ class _Step:
     flags: int
     max_context: int
     token_order: np.ndarray | None
+    caller_rows_at: int
+    batch_slots_at: int
     entries: tuple
     decode_only: bool
 
     def tensor(self, name: str) -> torch.Tensor:
-        """int64 views: ``tokens``, ``rope_positions``, ``slots``, ``logits_rows``."""
+        """int64 views: ``tokens``, ``rope_positions``, ``slots``, ``batch_slots`` (the slots in
+        batch order), ``logits_rows``."""
         offset, count = {
             "tokens": (self.tokens_at, self.total), "rope_positions": (self.rope_at, self.total),
-            "slots": (self.slots_at, self.total), "logits_rows": (self.logits_at, self.num_wanted),
+            "slots": (self.slots_at, self.total), "batch_slots": (self.batch_slots_at, self.total),
+            "logits_rows": (self.logits_at, self.num_wanted),
         }[name]  # fmt: skip
         return self.staging.tensor(offset, count, torch.int64)
 
@@ -311,7 +332,6 @@ class ModelRunner:
         shape = (config.n_layers, num_blocks, block_size, config.n_heads, config.head_dim)
         self._keys = torch.zeros(shape, dtype=kv_dtype, device=self.device)
         self._values = torch.zeros(shape, dtype=kv_dtype, device=self.device)
-        self._pending: list[tuple[int, int]] = []
         self._weights: _DeviceWeights | None = None
         self._tables = BlockTableArena(self.device)
         self._planner = ops.NativePlanner()
@@ -320,10 +340,13 @@ class ModelRunner:
         self._device_index = self.device.index
         self._stats = np.zeros(8, np.int64)
         self._kv_code = ops.kv_dtype_code(kv_dtype)
-        self._pairs = np.zeros(512, np.int64)
         self._marks = np.zeros(num_blocks, np.int32)  # one per pool block, for exclusive_writes
-        self._cow_marks = np.zeros(num_blocks, np.uint8)  # one per pool block, for cow_groups
-        self._cow_staging = _Staging(self.device, self._host)  # the queued copies' pairs
+        # Queued copy-on-write copies live in C++ (_pkvhost.CopyQueue); copy_block is its push,
+        # so a scheduler's per-block calls cost no Python frame. Their pairs travel through a
+        # pinned buffer of their own.
+        self._copies = self._host.CopyQueue(num_blocks)
+        self.copy_block = self._copies.push
+        self._cow_staging = _Staging(self.device, self._host)
         self._workspace: torch.Tensor | None = None
         self._forward_ws: torch.Tensor | None = None  # the forward pass's activations
         self._greedy_out: torch.Tensor | None = None  # its greedy token ids
@@ -334,6 +357,7 @@ class ModelRunner:
         #: arrays are views of the planner's buffers, rewritten by the next call.
         self.last_plan: ops.BatchPlan | None = None
         self._layer_bytes = self._keys[0].numel() * self._keys.element_size()
+        self._block_elems = self._keys[0, 0].numel()
 
     # --- pool ---------------------------------------------------------------------------
 
@@ -368,47 +392,38 @@ class ModelRunner:
     def copy_block(self, source: int, destination: int) -> None:
         """Copy-on-write of one block across every layer (runner.py:128-133), queued.
 
-        The copy is enqueued on the device before the pool is next read or written.
+        The copy is enqueued on the device before the pool is next read or written. A runner's
+        ``copy_block`` attribute is its C++ queue's ``push``, which makes these same checks
+        (ValueError for a copy onto itself, IndexError naming a block id outside the pool);
+        this method is what the class exposes.
         """
-        if source == destination:
-            raise ValueError("copy-on-write must not copy a block onto itself")
-        n = self.num_blocks
-        if not (0 <= source < n and 0 <= destination < n):
-            raise IndexError(f"block id {source if not 0 <= source < n else destination} is outside the pool")
-        self._pending.append((int(source), int(destination)))
+        self._copies.push(source, destination)
+
+    @property
+    def pending_copies(self) -> list[tuple[int, int]]:
+        """The queued (source, destination) copies, in queue order."""
+        return self._copies.items()
 
     def flush_copies(self) -> int:
         """Launch every queued copy-on-write copy, in order: one ``pkv_copy_blocks`` launch per
-        group of independent copies, their pairs sent in one asynchronous copy of their own.
-        Returns the number of copies."""
-        if not self._pending:
+        group of independent copies (``ops.independent_groups``'s rule), their pairs sent in one
+        asynchronous copy of their own, all from one C++ call (``CopyQueue.flush``). Returns the
+        number of copies. A failed launch raises and leaves every copy queued (a group reads no
+        block it writes, so a group that ran already leaves the same bytes when it runs again)."""
+        copies = self._copies
+        if not len(copies):
             return 0
-        pending = self._pending
-        sizes, flat = self._cow_groups(pending)
-        (offset,) = self._cow_staging.send([flat], [])
-        pairs_at = self._cow_staging.base + offset
-        k_pool, v_pool = self._keys, self._values
-        layers, num_blocks = k_pool.shape[0], k_pool.shape[1]
-        block_elems = k_pool[0, 0].numel()
-        stream = ops._stream(self._device_index)
-        start = 0
-        for size in sizes:
-            rc = self._host.copy_blocks(k_pool.data_ptr(), v_pool.data_ptr(), self._kv_code, pairs_at + 16 * start, size,
-                                        layers, num_blocks, block_elems, self._device_index, stream)  # fmt: skip
-            _native.check(rc, "pkv_copy_blocks")
-            start += size
-        # Dequeued only once every group is enqueued (a failed launch leaves them queued; a group
-        # reads no block it writes, so running it twice leaves what running it once does).
-        self._pending = []
-        return len(pending)
-
-    def _cow_groups(self, pending: list[tuple[int, int]]) -> tuple[list[int], np.ndarray]:
-        """Queued copies flattened to int64 (src, dst) pairs, and the sizes of the consecutive
-        groups that may each run as one launch (``ops.independent_groups``'s rule)."""
-        if self._pairs.size < 2 * len(pending):
-            self._pairs = np.zeros(max(2 * len(pending), 2 * self._pairs.size), np.int64)
-        sizes = self._host.cow_groups(pending, self._pairs, self._cow_marks)
-        return sizes, self._pairs[: 2 * len(pending)]
+        keys, staging = self._keys, self._cow_staging
+        while True:
+            rc, count = copies.flush(
+                keys.data_ptr(), self._values.data_ptr(), self._kv_code, keys.shape[0], self._block_elems,
+                staging.host_array, staging.base, self._device_index, ops._stream(self._device_index),
+            )  # fmt: skip
+            if count >= 0:
+                break
+            staging.grow(-count)
+        _native.check(rc, "pkv_copy_blocks")
+        return count
 
     def block_fingerprint(self, block_id: int) -> bytes:
         """BLAKE2b-16 of one block's bytes, keys then values (runner.py:135-142)."""
@@ -421,7 +436,7 @@ class ModelRunner:
 
     def reset_cache(self) -> None:
         """Zero the whole pool; queued copies are dropped (runner.py:144-147)."""
-        self._pending.clear()
+        self._copies.clear()
         self._keys.zero_()
         self._values.zero_()
 
@@ -539,6 +554,7 @@ class ModelRunner:
             else:  # entry order[r]'s tokens, consecutively: token j of run r is start + (j - run offset)
                 starts, runs = (np.cumsum(lengths) - lengths)[order], lengths[order]
                 token_order = np.repeat(starts - (np.cumsum(runs) - runs), runs) + np.arange(total)
+            batch_slots = slots
             tokens, positions, slots = tokens[token_order], positions[token_order], slots[token_order]
             rope_positions = rope_positions[token_order]
             planner_row = np.empty(total, dtype=np.int64)  # batch token index -> planner token index
@@ -558,12 +574,14 @@ class ModelRunner:
             bool(flags & _native.PKV_ATTN_SHORT_ROWS), bool(flags & _native.PKV_ATTN_DOMINANT_TILES),
         )  # fmt: skip
         parts64 = [tokens, rope_positions, slots, update.index, wanted]
-        offsets = self._staging.send(
-            parts64,
-            [query_pos, query_seq, contexts_by_row, update.values, plan_rows.ravel(), plan_tiles.ravel(), merge],
-        )  # fmt: skip
+        parts32 = [query_pos, query_seq, contexts_by_row, update.values, plan_rows.ravel(), plan_tiles.ravel(), merge]
+        if token_order is not None:  # attend's caller rows, and its slots in batch order
+            parts64.append(batch_slots)
+            parts32.append(token_order.astype(np.int32))
+        offsets = self._staging.send(parts64, parts32)
         tokens_at, rope_at, slots_at, index_at, logits_at = offsets[:5]
-        qpos_at, qseq_at, context_at, values_at, rows_at, tiles_at, merge_at = offsets[-7:]
+        qpos_at, qseq_at, context_at, values_at, rows_at, tiles_at, merge_at = offsets[len(parts64) : len(parts64) + 7]
+        batch_slots_at, caller_rows_at = (offsets[5], offsets[-1]) if token_order is not None else (slots_at, -1)
         staging = self._staging
         if update.index.size:
             self._tables.apply(staging.tensor(index_at, update.index.size, torch.int64),
@@ -584,14 +602,16 @@ class ModelRunner:
             logits_at=logits_at, qpos_at=qpos_at, qseq_at=qseq_at, contexts_at=context_at, plan_rows_at=rows_at,
             plan_tiles_at=tiles_at, merge_at=merge_at, num_plan_rows=plan_rows.shape[0],
             num_tiles=plan_tiles.shape[0], num_merge=merge.size, num_wanted=wanted.size, partition=partition,
-            flags=flags, max_context=int(context.max()), token_order=token_order, entries=entries,
-            decode_only=decode_only,
+            flags=flags, max_context=int(context.max()), token_order=token_order, caller_rows_at=caller_rows_at,
+            batch_slots_at=batch_slots_at, entries=entries, decode_only=decode_only,
         )  # fmt: skip
 
     def _attention(self, step: _Step, layer: int, queries: torch.Tensor, out: torch.Tensor, append=None) -> None:
         """Paged attention of one layer's rotated queries over the pools (and the decode append
         fused into it when ``append`` = (keys, values) rows is given), called through
-        ``_pkvhost`` with the metadata's device addresses."""
+        ``_pkvhost`` with the metadata's device addresses. ``queries``, ``out`` and the appended
+        rows are in batch order: when the plan orders the rows its own way, the call's
+        caller_rows (the staged token order) maps each planner row to its batch row."""
         config = self.model.config
         heads, dim = config.n_heads, config.head_dim
         # pkv_attention_workspace_bytes: (head_dim + 2) floats per (query, head, partition) once a
@@ -612,7 +632,8 @@ class ModelRunner:
         stream = ops._stream(device)
         common = (
             out.data_ptr(), queries.data_ptr(), queries.stride(0), step.ptr(step.qpos_at), step.ptr(step.qseq_at),
-            step.total, step.ptr(step.plan_rows_at) if step.num_plan_rows else 0, step.num_plan_rows,
+            step.total, step.ptr(step.caller_rows_at) if step.caller_rows_at >= 0 else 0,
+            step.ptr(step.plan_rows_at) if step.num_plan_rows else 0, step.num_plan_rows,
         )  # fmt: skip
         tail = (
             step.ptr(step.merge_at) if step.num_merge else 0, step.num_merge, key_at, value_at, self._kv_code,
@@ -629,7 +650,7 @@ class ModelRunner:
         keys, values = append
         rc = self._host.paged_attention_append(
             *common, *tail, keys.data_ptr(), values.data_ptr(), ops.kv_dtype_code(keys.dtype), keys.stride(0),
-            values.stride(0), step.ptr(step.slots_at), device, stream,
+            values.stride(0), step.ptr(step.batch_slots_at), device, stream,
         )  # fmt: skip
         _native.check(rc, "pkv_paged_attention_append")
 
@@ -643,8 +664,10 @@ class ModelRunner:
         (reference runner.py:184-212 for one layer). Returns float32 ``[T, heads, head_dim]`` in
         batch order, on the device (asynchronous). A decode batch (one token per entry, at its
         last position) appends inside the attention call."""
-        step = self._prepare(batch)
         config = self.model.config
+        if not 0 <= layer < config.n_layers:
+            raise IndexError(f"layer {layer} is outside the model's {config.n_layers} layers")
+        step = self._prepare(batch)
         total = 0 if step is None else step.total
         shape = (total, config.n_heads, config.head_dim)
         if out is None:
@@ -658,19 +681,20 @@ class ModelRunner:
         if not out.is_contiguous():
             raise ValueError("out must be contiguous")
         queries, keys, values = (t if t.is_contiguous() else t.contiguous() for t in (queries, keys, values))
-        if step.token_order is not None:  # the planner's row order
-            index = torch.from_numpy(step.token_order).to(self.device)
-            queries, keys, values = queries[index], keys[index], values[index]
-            result = torch.empty_like(out)
-        else:
-            result = out
+        # Everything stays in batch order: a plan in its own row order reaches the batch rows
+        # through the call's caller_rows.
         if step.decode_only:
-            self._attention(step, layer, queries, result, append=(keys, values))
-        else:
-            ops.append_kv(self._keys[layer], self._values[layer], keys, values, step.tensor("slots"))
-            self._attention(step, layer, queries, result)
-        if step.token_order is not None:
-            out[index] = result
+            self._attention(step, layer, queries, out, append=(keys, values))
+        else:  # pkv_append of the batch's keys and values at their slots, then the attention
+            offset = layer * self._layer_bytes
+            rc = self._host.append(
+                self._keys.data_ptr() + offset, self._values.data_ptr() + offset, self._kv_code,
+                self.capacity_tokens, keys.data_ptr(), values.data_ptr(), _native.PKV_F32, keys.stride(0),
+                values.stride(0), step.ptr(step.batch_slots_at), total, config.n_heads, config.head_dim,
+                self._device_index, ops._stream(self._device_index),
+            )  # fmt: skip
+            _native.check(rc, "pkv_append")
+            self._attention(step, layer, queries, out)
         return out
 
     def _forward(self, batch: ExecutionBatch, *, greedy: bool = False):

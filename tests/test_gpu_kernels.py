@@ -579,6 +579,117 @@ def test_tiles_beside_rows_equal_tiles_alone(device, dim, block, whole) -> None:
         assert np.array_equal(hinted, got), partition
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("block", [5, 16])
+@pytest.mark.parametrize("whole", [False, True], ids=["partitions", "whole"])
+def test_caller_rows_reach_the_rows_the_plan_orders(device, dim, block, whole) -> None:
+    """caller_rows[t] is the row of queries and out that planner row t reads and writes. With
+    the queries permuted and the permutation passed, the row pass, the tile pass (alone, and at
+    block 16 beside a row pass large enough for the second stream and the direct-to-LDS grid)
+    and the reduce write bit for bit what the unpermuted call writes, into the permuted rows. A
+    caller row outside the batch skips its query: its output row keeps what it held."""
+    say("caller rows", dim, block, whole)
+    rng = np.random.default_rng(dim + block + 3 * whole)
+    heads, max_ctx = 4, 700
+    kc, vc, tables, contexts, positions, seq_of, q = _ragged_case(
+        rng, heads=heads, dim=dim, block=block, pool=5 * max_ctx // block + 8, seqs=5, max_ctx=max_ctx,
+        prefill=True, max_rows=120,
+    )  # fmt: skip
+    # decode rows of 60 more sequences: at partition 64 the row pass then has more than 2,048
+    # workgroups (items x heads), so the tile pass runs beside it on the second stream
+    decode_ctx = rng.integers(600, max_ctx, 60)
+    need = [-(-int(c) // block) for c in decode_ctx]
+    first, extra = kc.shape[0], sum(need)
+    kc = np.concatenate([kc, rng.standard_normal((extra,) + kc.shape[1:]).astype(np.float32)])
+    vc = np.concatenate([vc, rng.standard_normal((extra,) + vc.shape[1:]).astype(np.float32)])
+    free = iter(range(first, first + extra))  # fresh blocks for the decode sequences
+    tables = list(tables) + [np.asarray([next(free) for _ in range(n)]) for n in need]
+    seq_of = np.concatenate([seq_of, np.arange(len(contexts), len(contexts) + decode_ctx.size)])
+    contexts = np.concatenate([contexts, decode_ctx])
+    positions = np.concatenate([positions, decode_ctx - 1])
+    q = np.concatenate([q, rng.standard_normal((decode_ctx.size, heads, dim)).astype(np.float32)])
+    total, scale = seq_of.size, dim**-0.5
+    width = max(len(t) for t in tables)
+    padded = np.full((len(tables), width), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    meta = (to(positions.astype(np.int32)), to(seq_of.astype(np.int32)), to(kc), to(vc), to(padded),
+            to(contexts.astype(np.int32)), scale)  # fmt: skip
+    rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)
+    assert tiles.shape[0] >= 2
+    if whole:
+        tiles[:, 3] = ops.TILE_WHOLE
+    visible = np.minimum(contexts[seq_of], positions + 1)
+    perm = rng.permutation(total)  # planner row t lives at caller row perm[t]
+    q_caller = np.empty_like(q)
+    q_caller[perm] = q
+    bad = perm.copy()
+    skipped = int(rng.integers(total))
+    bad[skipped] = total  # outside the batch
+    for partition in (0, 64):
+        plan = ops.upload_plan(ops.expand_rows(rows, visible, partition), tiles, device, partition_size=partition)
+        mc = int(contexts.max())
+        want = ops.paged_attention_ragged(to(q), *meta, max_context_len=mc, plan=plan)
+        got = ops.paged_attention_ragged(to(q_caller), *meta, max_context_len=mc, plan=plan,
+                                         caller_rows=to(perm.astype(np.int32)))  # fmt: skip
+        assert torch.equal(got[to(perm)], want), partition
+        held = torch.full_like(want, float("nan"))
+        ops.paged_attention_ragged(to(q_caller), *meta, max_context_len=mc, plan=plan, out=held,
+                                   caller_rows=to(bad.astype(np.int32)))  # fmt: skip
+        kept = np.delete(np.arange(total), skipped)
+        assert torch.equal(held[to(perm[kept])], want[to(kept)]), partition
+        assert bool(torch.isnan(held[int(perm[skipped])]).all()), partition
+        if partition == 64 and block == 16:
+            assert plan.num_rows * heads >= 2048, "the overlapped grid"
+
+
+@pytest.mark.parametrize("block", [16, 5])
+def test_caller_rows_with_the_fused_append(device, block) -> None:
+    """The fused decode append takes query t's new key and value from row caller_rows[t] of the
+    new rows and writes it to slot_mapping[caller_rows[t]]: permuted inputs give the same pools
+    bit for bit and the same outputs in the permuted rows (block 5 appends before the call)."""
+    say("caller rows, fused append", block)
+    rng = np.random.default_rng(40 + block)
+    heads, dim, seqs = 4, 128, 11
+    pool = seqs * -(-700 // block) + 8
+    contexts = rng.integers(1, 700, seqs)
+    ids = rng.permutation(pool)
+    tables, offset = [], 0
+    for c in contexts:
+        n = -(-int(c) // block)
+        tables.append(ids[offset : offset + n])
+        offset += n
+    padded = np.full((seqs, max(len(t) for t in tables)), -7, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    positions = contexts - 1
+    slots = np.asarray([int(t[p // block]) * block + p % block for t, p in zip(tables, positions)], np.int64)
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    kc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    vc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    q, new_k, new_v = (rng.standard_normal((seqs, heads, dim)).astype(np.float32) for _ in range(3))
+    perm = rng.permutation(seqs)  # query t at caller row perm[t]
+
+    def caller(a: np.ndarray) -> np.ndarray:
+        out = np.empty_like(a)
+        out[perm] = a
+        return out
+
+    meta = (to(padded), to(contexts.astype(np.int32)), dim**-0.5)
+    args = (to(positions.astype(np.int32)), to(np.arange(seqs, dtype=np.int32)))
+    k_plain, v_plain = to(kc), to(vc)
+    want = ops.paged_attention_ragged(to(q), *args, k_plain, v_plain, *meta, max_context_len=int(contexts.max()),
+                                      partition_size=64, append=(to(new_k), to(new_v), to(slots)))  # fmt: skip
+    k_perm, v_perm = to(kc), to(vc)
+    got = ops.paged_attention_ragged(
+        to(caller(q)), *args, k_perm, v_perm, *meta, max_context_len=int(contexts.max()), partition_size=64,
+        append=(to(caller(new_k)), to(caller(new_v)), to(caller(slots))), caller_rows=to(perm.astype(np.int32)),
+    )  # fmt: skip
+    assert torch.equal(k_perm, k_plain) and torch.equal(v_perm, v_plain)
+    assert torch.equal(got[to(perm)], want)
+
+
 @pytest.mark.parametrize("kv", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("whole", [False, True], ids=["partitions", "whole"])
 def test_nan_in_a_block_no_table_holds_reaches_no_output(device, kv, whole) -> None:

@@ -467,6 +467,9 @@ def test_attend_appends_and_attends_like_the_reference_runner(device, seed, shar
     values0 = rng.standard_normal((num_blocks, block, 4, 64)).astype(np.float32)
     runner.key_cache[1].copy_(torch.from_numpy(keys0))
     runner.value_cache[1].copy_(torch.from_numpy(values0))
+    for layer in (2, -1):  # a layer outside the pools is refused before anything is enqueued
+        with pytest.raises(IndexError, match=f"layer {layer} is outside"):
+            runner.attend(batch, *(torch.from_numpy(a).to(device) for a in (q, k, v)), layer=layer)
     out = runner.attend(batch, *(torch.from_numpy(a).to(device) for a in (q, k, v)), layer=1).cpu().numpy()
     if sharers:
         assert runner.last_plan is not None and runner.last_plan.tiles.shape[0] > 0, "prefix tiles"

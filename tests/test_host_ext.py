@@ -139,31 +139,45 @@ def _python_groups(pairs):
 
 
 @pytest.mark.parametrize("seed", range(60))
-def test_cow_groups_match_the_python_grouping(seed) -> None:
+def test_copy_queue_groups_match_the_python_grouping(seed) -> None:
     rng = np.random.default_rng(seed)
     n = int(rng.integers(0, 300))
     ids = int(rng.choice([4, 20, 1000, 100_000]))
-    pairs = [(int(a), int(b)) for a, b in rng.integers(0, ids, (n, 2))]
-    out = np.zeros(2 * n + 2, np.int64)
-    assert ext.cow_groups(pairs, out) == _python_groups(pairs)
-    assert out[: 2 * n].tolist() == [v for pair in pairs for v in pair]
-    # with the per-block marks (some ids past them fall back to the sets): the same groups, and
-    # the marks are left all zero
-    marks = np.zeros(min(ids, 900), np.uint8)
-    out2 = np.zeros(2 * n + 2, np.int64)
-    assert ext.cow_groups(pairs, out2, marks) == _python_groups(pairs)
-    assert np.array_equal(out, out2) and not marks.any()
+    pairs = [(int(a), int(b)) for a, b in rng.integers(0, ids, (n, 2)) if a != b]
+    queue = ext.CopyQueue(ids)
+    for source, destination in pairs:
+        queue.push(source, destination)
+    assert len(queue) == len(pairs) and queue.items() == pairs
+    assert queue.groups() == _python_groups(pairs)
+    assert queue.groups() == _python_groups(pairs)  # the per-block marks were left all zero
+    queue.clear()
+    assert len(queue) == 0 and queue.groups() == []
 
 
-def test_cow_groups_of_forks_are_one_group_and_bad_pairs_are_refused() -> None:
-    pairs = [(7, 100 + i) for i in range(256)]  # every child copies the same shared block
-    out = np.zeros(512, np.int64)
-    assert ext.cow_groups(pairs, out) == [256]
-    assert ext.cow_groups([(1, 2), (2, 3), (3, 1)], np.zeros(6, np.int64)) == [1, 1, 1]
+def test_copy_queue_groups_of_forks_are_one_group_and_bad_pairs_are_refused() -> None:
+    queue = ext.CopyQueue(400)
+    for i in range(256):  # every child copies the same shared block
+        queue.push(7, 100 + i)
+    assert queue.groups() == [256]
+    queue.clear()
+    for source, destination in [(1, 2), (2, 3), (3, 1)]:
+        queue.push(source, destination)
+    assert queue.groups() == [1, 1, 1]
+    # the reference's checks (runner.py:128-133), NumPy integers accepted as ids
+    queue.push(np.int64(5), np.int32(6))
+    assert queue.items()[-1] == (5, 6)
+    with pytest.raises(ValueError, match="onto itself"):
+        queue.push(4, 4)
+    for bad in [(1, 400), (-1, 2), (2**70, 1)]:
+        with pytest.raises(IndexError, match=f"block id {bad[0] if not 0 <= bad[0] < 400 else bad[1]} is outside"):
+            queue.push(*bad)
+    with pytest.raises(TypeError):
+        queue.push(1)
+    with pytest.raises(TypeError):
+        queue.push("1", 2)
+    assert len(queue) == 4  # nothing refused was queued
     with pytest.raises(ValueError):
-        ext.cow_groups([(1, 2, 3)], np.zeros(6, np.int64))
-    with pytest.raises(ValueError):
-        ext.cow_groups([(1, 2), (3, 4)], np.zeros(3, np.int64))
+        ext.CopyQueue(0)
 
 
 def test_the_bound_planner_matches_the_ctypes_planner() -> None:
@@ -250,13 +264,26 @@ def test_stage_packs_the_parts_and_issues_one_host_to_device_copy() -> None:
             host.stage([np.arange(8, dtype=np.int64)[::2]], [], buf, 4096, 77)
         with pytest.raises(ValueError):  # no device buffer for a non-empty copy
             host.stage(p64, p32, buf, 0, 77)
+        # With an event: the copy that last read the buffer is waited for before the packing,
+        # and the event is recorded on the same stream right after the new copy.
+        events = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
+        record_event = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p)(
+            lambda event, stream: calls.append(("record", event, stream)) or 0)
+        synchronize = events(lambda event: calls.append(("synchronize", event)) or 0)
+        host.bind(*entry_points, address(fake), 0, 0, 0, 0, 0, address(record_event), address(synchronize), 0)
+        del calls[:]
+        assert host.stage(p64, p32, buf, 4096, 77, 555) == offsets
+        assert calls == [("synchronize", 555), (4096, want, 1, 77), ("record", 555, 77)]
         fail = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                                 ctypes.c_void_p)(lambda *args: 1)  # fmt: skip
         host.bind(*entry_points, address(fail))
         with pytest.raises(RuntimeError, match="hipMemcpyAsync"):
             host.stage(p64, p32, buf, 4096, 77)
+        with pytest.raises(RuntimeError, match="event entry points"):  # unbound event functions
+            host.stage(p64, p32, buf, 4096, 77, 555)
     finally:
-        host.bind(*entry_points, address(lib.hipMemcpyAsync))
+        _native._BOUND = False  # bind every entry point again, the optional ones included
+        _native.bound_host()
 
 
 def exclusive_by_brute_force(tables, contexts, block_size, num_blocks) -> bool:

@@ -81,18 +81,18 @@ def test_bad_arguments_are_refused_before_any_device_work(lib) -> None:
     assert lib.pkv_copy_blocks(null, null, 9, null, 1, 1, 4, 16, 0, null) == -1
     assert lib.pkv_copy_blocks(null, null, 0, null, 0, 1, 4, 16, 0, null) == 0
     # partition size not a multiple of 16
-    args = [null, null, 8, null, null, 1, null, 0, null, 0, null, -1, null, null, 0, 4, 4, null, 1,
+    args = [null, null, 8, null, null, 1, null, null, 0, null, 0, null, -1, null, null, 0, 4, 4, null, 1,
             null, 1, 1, 8, ctypes.c_float(0.5), 8, 17, 0, null, 0, 0, null]  # fmt: skip
     assert lib.pkv_paged_attention(*args) == -1
-    args[25] = 16
-    args[26] = 2
+    args[26] = 16
+    args[27] = 2
     assert lib.pkv_paged_attention(*args) == -1  # unknown flag
-    args[26] = 1
+    args[27] = 1
     assert lib.pkv_paged_attention(*args) == -1  # null pointers
-    args[26] = 0
-    args[11] = -2
+    args[27] = 0
+    args[12] = -2
     assert lib.pkv_paged_attention(*args) == -1  # a merge count below -1
-    args[11] = 3
+    args[12] = 3
     assert lib.pkv_paged_attention(*args) == -1  # merge rows counted but not given
     assert lib.pkv_tile_head_dim_supported(128) == 1
     assert lib.pkv_tile_head_dim_supported(16) == 0
@@ -154,7 +154,7 @@ def test_fused_append_arguments_are_refused_before_any_device_work(lib) -> None:
     def call(new_keys=nk, new_values=nv, new_dtype=0, key_stride=512, value_stride=512,
              pool_dtype=0, slot_mapping=slots, head_dim=128):  # fmt: skip
         return lib.pkv_paged_attention_append(
-            out, q, 4 * head_dim, qpos, qseq, 3, None, 0, None, -1, kc, vc, pool_dtype, 100, 16,
+            out, q, 4 * head_dim, qpos, qseq, 3, None, None, 0, None, -1, kc, vc, pool_dtype, 100, 16,
             tables, 8, ctx, 3, 4, head_dim, ctypes.c_float(0.1), 100, 0, 0, ws, 1 << 20,
             new_keys, new_values, new_dtype, key_stride, value_stride, slot_mapping, 0, None,
         )  # fmt: skip

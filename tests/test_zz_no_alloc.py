@@ -33,7 +33,7 @@ def _args(batch, plan, out):
     heads, dim = batch.key_cache.shape[2], batch.key_cache.shape[3]
     return (
         out.data_ptr(), batch.queries.data_ptr(), heads * dim,
-        batch.query_positions.data_ptr(), batch.query_seq.data_ptr(), batch.num_queries,
+        batch.query_positions.data_ptr(), batch.query_seq.data_ptr(), batch.num_queries, None,
         plan.rows.data_ptr() if plan.num_rows else None, plan.num_rows,
         plan.tiles.data_ptr() if plan.num_tiles else None, plan.num_tiles,
         merge.data_ptr() if merge is not None and merge.numel() else None,
@@ -107,10 +107,10 @@ def test_a_batch_beyond_the_scratch_is_refused(device) -> None:
     small.replan(0)
     args = list(_args(small, small.plan, small.queries.clone()))
     # positions of num_queries, max_context_len and partition_size in the argument list
-    assert (args[5], args[24], args[25]) == (small.num_queries, small.max_context_len, small.plan.partition_size)
+    assert (args[5], args[25], args[26]) == (small.num_queries, small.max_context_len, small.plan.partition_size)
     args[5] = 4096  # num_queries: 4096 x 8 heads x 64 partitions x 130 floats > 64 MiB
-    args[24] = 32768  # max_context_len
-    args[25] = 512  # partition_size
+    args[25] = 32768  # max_context_len
+    args[26] = 512  # partition_size
     need = ops.attention_workspace_bytes(4096, 8, 128, 32768, 512)
     assert need > _native.STATIC_SCRATCH_BYTES
     assert lib.pkv_paged_attention_noalloc(*args, device.index, None) == _native.PKV_ETOOBIG
