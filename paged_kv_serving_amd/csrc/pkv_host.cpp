@@ -18,9 +18,10 @@
 //       caller validates, so it needs no pass of its own: [min token, max token, min position,
 //       max position, min slot, max slot, min context, 1 if two single-token entries' tables
 //       start with the same block id else 0] (slots of unformed positions count as -1).
-//   prefix_order_rows(rows, lengths, host, held_len, lead, min_rows) -> list | None
+//   prefix_order_rows(rows, lengths, host, held_len, lead, min_rows, out) -> bool
 //       The row order that puts decode entries sharing their first `lead` blocks next to each
-//       other (runner.shared_prefix_order), or None when no such run would change. Read from
+//       other (runner.shared_prefix_order), written to the int64 buffer `out` (>= one entry per
+//       row); False (out untouched) when no such run would change. Read from
 //       the block-table arena after its update: entry e has lengths[e] tokens and its table in
 //       arena row rows[e] (held_len[rows[e]] entries of host[rows[e]]), so no block id is
 //       converted from a Python object.
@@ -300,89 +301,117 @@ done:
   return result;
 }
 
-// The row order of prefix_order from the decode entries' positions in the batch and their
-// `lead` leading block ids (keys, lead per entry); None when nothing would move.
-PyObject* order_decode_entries(const std::vector<Py_ssize_t>& decode, const std::vector<int64_t>& keys,
-                               long long lead, long long min_rows, Py_ssize_t count) {
-  {
-    const Py_ssize_t nd = static_cast<Py_ssize_t>(decode.size());
-    if (nd < min_rows || lead < 1) {
-      Py_RETURN_NONE;
-    }
-    auto key = [&](Py_ssize_t k) { return keys.data() + k * lead; };
-    auto same = [&](Py_ssize_t a, Py_ssize_t b) { return std::memcmp(key(a), key(b), lead * sizeof(int64_t)) == 0; };
-    {  // sharers have the same first block; all-distinct first blocks: nothing to group
-      std::vector<int64_t> firsts(nd);
-      for (Py_ssize_t k = 0; k < nd; ++k) firsts[k] = key(k)[0];
-      std::sort(firsts.begin(), firsts.end());
-      if (std::adjacent_find(firsts.begin(), firsts.end()) == firsts.end()) {
-        Py_RETURN_NONE;
-      }
-    }
-    {  // already grouped: every key forms one run of consecutive entries, so nothing moves
-      auto hash = [&](Py_ssize_t k) {
-        uint64_t h = 1469598103934665603ull;  // FNV-1a over the key's ids
-        for (long long c = 0; c < lead; ++c) h = (h ^ static_cast<uint64_t>(key(k)[c])) * 1099511628211ull;
-        return h;
-      };
-      std::unordered_set<uint64_t> finished;  // hashes of runs that have ended
-      bool grouped_already = true;
-      uint64_t run = hash(0);
-      for (Py_ssize_t k = 1; k < nd && grouped_already; ++k) {
-        const bool continues = decode[k] == decode[k - 1] + 1 && same(k - 1, k);
-        if (continues) continue;
-        finished.insert(run);
-        run = hash(k);
-        grouped_already = finished.count(run) == 0;  // a repeated hash (or a collision): sort
-      }
-      if (grouped_already) {
-        Py_RETURN_NONE;
-      }
-    }
-    std::vector<Py_ssize_t> grouped(nd);  // positions in `decode`, stably sorted by key
-    for (Py_ssize_t k = 0; k < nd; ++k) grouped[k] = k;
-    std::stable_sort(grouped.begin(), grouped.end(), [&](Py_ssize_t a, Py_ssize_t b) {
-      return std::lexicographical_compare(key(a), key(a) + lead, key(b), key(b) + lead);
-    });
-    Py_ssize_t shared = 0, adjacent = 0;
-    for (Py_ssize_t k = 0; k + 1 < nd; ++k) {
-      shared += same(grouped[k], grouped[k + 1]);
-      if (decode[k + 1] == decode[k] + 1) adjacent += same(k, k + 1);
-    }
-    if (shared == 0 || shared == adjacent) {
-      Py_RETURN_NONE;
-    }
-    PyObject* result = PyList_New(count);
-    if (result == nullptr) return nullptr;
-    Py_ssize_t at = 0;
-    for (Py_ssize_t k = 0; k < nd; ++k) PyList_SET_ITEM(result, at++, PyLong_FromSsize_t(decode[grouped[k]]));
-    std::vector<char> is_decode(count, 0);
-    for (Py_ssize_t k = 0; k < nd; ++k) is_decode[decode[k]] = 1;
-    for (Py_ssize_t e = 0; e < count; ++e) {
-      if (!is_decode[e]) PyList_SET_ITEM(result, at++, PyLong_FromSsize_t(e));
-    }
-    return result;
+// A hash of `n` block ids: four interleaved FNV-1a lanes (independent multiply chains), folded.
+uint64_t hash_ids(const int32_t* ids, long long n) {
+  constexpr uint64_t kPrime = 1099511628211ull;
+  uint64_t h[4] = {1469598103934665603ull, 0x9e3779b97f4a7c15ull, 0xc2b2ae3d27d4eb4full, 0x165667b19e3779f9ull};
+  long long c = 0;
+  for (; c + 4 <= n; c += 4) {
+    for (int j = 0; j < 4; ++j) h[j] = (h[j] ^ static_cast<uint32_t>(ids[c + j])) * kPrime;
   }
+  for (; c < n; ++c) h[0] = (h[0] ^ static_cast<uint32_t>(ids[c])) * kPrime;
+  uint64_t x = h[0] ^ (h[1] << 16 | h[1] >> 48) ^ (h[2] << 32 | h[2] >> 32) ^ (h[3] << 48 | h[3] >> 16);
+  x ^= x >> 33;
+  x *= 0xff51afd7ed558ccdull;
+  return x ^ (x >> 33);
+}
+
+// The row order of prefix_order from the decode entries' positions in the batch (decode, in
+// batch order) and their `lead` leading block ids (keys[k] points at entry k's), written to
+// out[count]; false when nothing would move. Equal keys are found through a hash of each key
+// confirmed by comparing the ids, so each entry's key is read about twice whatever the number of
+// sharers; only the distinct keys are sorted.
+bool order_decode_entries(const std::vector<Py_ssize_t>& decode, const std::vector<const int32_t*>& keys,
+                          long long lead, long long min_rows, Py_ssize_t count, int64_t* out) {
+  const Py_ssize_t nd = static_cast<Py_ssize_t>(decode.size());
+  if (nd < min_rows || lead < 1 || nd < 2) return false;
+  const size_t key_bytes = static_cast<size_t>(lead) * sizeof(int32_t);
+  auto key = [&](Py_ssize_t k) { return keys[k]; };
+  // 1. A key id per entry (ids numbered in order of first appearance).
+  size_t slots = 4;
+  while (slots < 2 * static_cast<size_t>(nd)) slots *= 2;
+  std::vector<int32_t> table(slots, -1);  // open addressing: the first entry holding each key
+  std::vector<int32_t> id(nd), first_of;  // entry -> key id; key id -> its first entry
+  for (Py_ssize_t k = 0; k < nd; ++k) {
+    const int32_t* kk = key(k);
+    size_t at = static_cast<size_t>(hash_ids(kk, lead)) & (slots - 1);
+    while (true) {
+      const int32_t e = table[at];
+      if (e < 0) {
+        table[at] = static_cast<int32_t>(k);
+        id[k] = static_cast<int32_t>(first_of.size());
+        first_of.push_back(static_cast<int32_t>(k));
+        break;
+      }
+      if (std::memcmp(key(e), kk, key_bytes) == 0) {
+        id[k] = id[e];
+        break;
+      }
+      at = (at + 1) & (slots - 1);
+    }
+  }
+  const Py_ssize_t distinct = static_cast<Py_ssize_t>(first_of.size());
+  if (distinct == nd) return false;  // no two entries share their leading blocks
+  // 2. Already grouped: every key's entries form one run of consecutive batch entries.
+  {
+    std::vector<char> ended(distinct, 0);
+    bool grouped = true;
+    for (Py_ssize_t k = 1; k < nd && grouped; ++k) {
+      if (decode[k] == decode[k - 1] + 1 && id[k] == id[k - 1]) continue;
+      ended[id[k - 1]] = 1;
+      grouped = ended[id[k]] == 0;
+    }
+    if (grouped) return false;
+  }
+  // 3. The entries stably sorted by key: the distinct keys in lexicographic order of their ids,
+  // then a counting sort of the entries by their key's rank.
+  std::vector<int32_t> by_key(distinct);
+  for (Py_ssize_t d = 0; d < distinct; ++d) by_key[d] = static_cast<int32_t>(d);
+  std::sort(by_key.begin(), by_key.end(), [&](int32_t a, int32_t b) {
+    const int32_t* ka = key(first_of[a]);
+    const int32_t* kb = key(first_of[b]);
+    return std::lexicographical_compare(ka, ka + lead, kb, kb + lead);
+  });
+  std::vector<int32_t> start(distinct + 1, 0);  // by rank
+  std::vector<int32_t> rank(distinct);
+  for (Py_ssize_t r = 0; r < distinct; ++r) rank[by_key[r]] = static_cast<int32_t>(r);
+  for (Py_ssize_t k = 0; k < nd; ++k) ++start[rank[id[k]] + 1];
+  for (Py_ssize_t r = 0; r < distinct; ++r) start[r + 1] += start[r];
+  // 4. Nothing to gain when the entries that share are already adjacent in the batch: the sorted
+  // order has nd - distinct equal neighbours; count those the batch order already has.
+  Py_ssize_t adjacent = 0;
+  for (Py_ssize_t k = 0; k + 1 < nd; ++k) adjacent += decode[k + 1] == decode[k] + 1 && id[k] == id[k + 1];
+  if (adjacent == nd - distinct) return false;
+  for (Py_ssize_t k = 0; k < nd; ++k) out[start[rank[id[k]]]++] = decode[k];
+  std::vector<char> is_decode(count, 0);
+  for (Py_ssize_t k = 0; k < nd; ++k) is_decode[decode[k]] = 1;
+  Py_ssize_t at = nd;
+  for (Py_ssize_t e = 0; e < count; ++e) {
+    if (!is_decode[e]) out[at++] = e;
+  }
+  return true;
 }
 
 PyObject* prefix_order_rows(PyObject*, PyObject* args) {
-  PyObject *rows_o, *lengths_o, *host_o, *held_o;
+  PyObject *rows_o, *lengths_o, *host_o, *held_o, *out_o;
   long long lead, min_rows;
-  if (!PyArg_ParseTuple(args, "OOOOLL", &rows_o, &lengths_o, &host_o, &held_o, &lead, &min_rows)) return nullptr;
+  if (!PyArg_ParseTuple(args, "OOOOLLO", &rows_o, &lengths_o, &host_o, &held_o, &lead, &min_rows, &out_o)) {
+    return nullptr;
+  }
   Buf<int32_t> rows, host, held;
-  Buf<int64_t> lengths;
+  Buf<int64_t> lengths, out;
   if (!rows.get(rows_o, "rows", false) || !lengths.get(lengths_o, "lengths", false) ||
-      !host.get(host_o, "host", false) || !held.get(held_o, "held_len", false)) {
+      !host.get(host_o, "host", false) || !held.get(held_o, "held_len", false) || !out.get(out_o, "out")) {
     return nullptr;
   }
   const Py_ssize_t count = rows.size();
   const Py_ssize_t num_rows = host.dim(0), width = host.dim(1);
-  if (host.ndim() != 2 || lengths.size() < count || held.size() != num_rows) {
+  if (host.ndim() != 2 || lengths.size() < count || held.size() != num_rows || out.size() < count) {
     PyErr_SetString(PyExc_ValueError, "prefix_order_rows buffers disagree");
     return nullptr;
   }
   std::vector<Py_ssize_t> decode;
-  std::vector<int64_t> keys;
+  std::vector<const int32_t*> keys;
   if (lead >= 1) {
     for (Py_ssize_t e = 0; e < count; ++e) {
       const int32_t row = rows.data()[e];
@@ -393,10 +422,10 @@ PyObject* prefix_order_rows(PyObject*, PyObject* args) {
       if (lengths.data()[e] != 1 || held.data()[row] < lead || lead > width) continue;
       const int32_t* table = host.data() + static_cast<int64_t>(row) * width;
       decode.push_back(e);
-      for (long long c = 0; c < lead; ++c) keys.push_back(table[c]);
+      keys.push_back(table);
     }
   }
-  return order_decode_entries(decode, keys, lead, min_rows, count);
+  return PyBool_FromLong(order_decode_entries(decode, keys, lead, min_rows, count, out.data()));
 }
 
 PyObject* arena_update(PyObject*, PyObject* args) {
@@ -449,8 +478,7 @@ PyObject* arena_update(PyObject*, PyObject* args) {
     int32_t* heldp = held.data();
     int64_t* lastp = last.data();
     Py_ssize_t changed = 0, nchanged_rows = 0, reached = 0;
-    PyObject* seen = PyDict_New();  // seq id -> occurrences so far in this batch
-    if (seen == nullptr) goto done;
+    PyObject* seen = nullptr;  // seq id -> occurrences so far, built once a sequence repeats
     bool ok = true;
     for (Py_ssize_t e = 0; e < count && ok; ++e) {
       PyObject* seq_id = PyObject_GetAttr(items[e], s_seq_id);
@@ -458,24 +486,53 @@ PyObject* arena_update(PyObject*, PyObject* args) {
         ok = false;
         break;
       }
-      PyObject* key = seq_id;  // the same sequence twice in one batch gets a row per occurrence
-      PyObject* prior = PyDict_GetItemWithError(seen, seq_id);
-      long long repeat = 0;
-      if (prior != nullptr) repeat = PyLong_AsLongLong(prior);
-      else if (PyErr_Occurred()) ok = false;
-      PyObject* next = ok ? PyLong_FromLongLong(repeat + 1) : nullptr;
-      if (next == nullptr || PyDict_SetItem(seen, seq_id, next) != 0) ok = false;
-      Py_XDECREF(next);
-      if (ok && repeat > 0) {
-        key = Py_BuildValue("(OL)", seq_id, repeat);
-        if (key == nullptr) ok = false;
-      } else {
-        Py_INCREF(key);
+      // The same sequence twice in one batch gets a row per occurrence, keyed (seq_id, k) for
+      // its k-th repeat. A repeat shows as a row this iteration has used already; only then are
+      // the batch's occurrences counted.
+      PyObject* key = seq_id;
+      Py_INCREF(key);
+      PyObject* found = PyDict_GetItemWithError(row_of, key);
+      if (found == nullptr && PyErr_Occurred()) ok = false;
+      const Py_ssize_t held_row = found == nullptr ? -1 : PyLong_AsSsize_t(found);
+      const bool used = held_row >= 0 && held_row < num_rows && lastp[held_row] == step;
+      if (ok && (used || seen != nullptr)) {
+        if (seen == nullptr) {  // count the occurrences of every sequence before this entry
+          seen = PyDict_New();
+          for (Py_ssize_t f = 0; f < e && seen != nullptr; ++f) {
+            PyObject* id = PyObject_GetAttr(items[f], s_seq_id);
+            PyObject* prior = id == nullptr ? nullptr : PyDict_GetItemWithError(seen, id);
+            PyObject* next = id == nullptr || (prior == nullptr && PyErr_Occurred())
+                                 ? nullptr
+                                 : PyLong_FromLongLong(prior == nullptr ? 1 : PyLong_AsLongLong(prior) + 1);
+            if (next == nullptr || PyDict_SetItem(seen, id, next) != 0) Py_CLEAR(seen);
+            Py_XDECREF(next);
+            Py_XDECREF(id);
+          }
+          if (seen == nullptr) ok = false;
+        }
+        long long repeat = 0;
+        if (ok) {
+          PyObject* prior = PyDict_GetItemWithError(seen, seq_id);
+          if (prior != nullptr) repeat = PyLong_AsLongLong(prior);
+          else if (PyErr_Occurred()) ok = false;
+          PyObject* next = ok ? PyLong_FromLongLong(repeat + 1) : nullptr;
+          if (next == nullptr || PyDict_SetItem(seen, seq_id, next) != 0) ok = false;
+          Py_XDECREF(next);
+        }
+        if (ok && repeat > 0) {
+          Py_DECREF(key);
+          key = Py_BuildValue("(OL)", seq_id, repeat);
+          if (key == nullptr) ok = false;
+          found = key == nullptr ? nullptr : PyDict_GetItemWithError(row_of, key);
+          if (found == nullptr && PyErr_Occurred()) ok = false;
+        }
       }
       Py_DECREF(seq_id);
-      if (!ok) break;
+      if (!ok) {
+        Py_XDECREF(key);
+        break;
+      }
       Py_ssize_t row = -1;
-      PyObject* found = PyDict_GetItemWithError(row_of, key);
       if (found != nullptr) {
         row = PyLong_AsSsize_t(found);
       } else if (PyErr_Occurred()) {
@@ -559,7 +616,7 @@ PyObject* arena_update(PyObject*, PyObject* args) {
       Py_INCREF(keep);
       PyList_SetItem(held_obj, row, keep);
     }
-    Py_DECREF(seen);
+    Py_XDECREF(seen);
     if (ok) {
       result = Py_BuildValue("(nn)", changed, nchanged_rows);
     } else {

@@ -33,7 +33,6 @@
 
 #include <algorithm>
 #include <cstring>
-#include <unordered_set>
 #include <vector>
 
 #include "pkv_common.h"
@@ -313,21 +312,18 @@ extern "C" int pkv_plan_batch(const int32_t* query_seq, const int32_t* query_pos
 
   // Do two row-pass sequences start with the same block? Without that there is neither a
   // shared-prefix group nor a repeated block to look for.
-  std::vector<int32_t> row_seqs;
-  row_seqs.reserve(row_pass.size());
-  for (int32_t q : row_pass) row_seqs.push_back(seq[q]);
-  std::sort(row_seqs.begin(), row_seqs.end());
-  row_seqs.erase(std::unique(row_seqs.begin(), row_seqs.end()), row_seqs.end());
   bool may_share = false;
   {
-    std::unordered_set<int32_t> firsts;
-    firsts.reserve(row_seqs.size() * 2);
-    for (int32_t s : row_seqs) {
-      if (used[s] > 0 && !firsts.insert(block_tables[static_cast<int64_t>(s) * block_table_stride]).second) {
-        may_share = true;
-        break;
-      }
+    std::vector<char> listed(num_seqs, 0);  // each row-pass sequence's first block, once
+    std::vector<int32_t> firsts;
+    firsts.reserve(row_pass.size());
+    for (int32_t q : row_pass) {
+      const int32_t s = seq[q];
+      if (listed[s] || used[s] == 0) continue;
+      listed[s] = 1;
+      firsts.push_back(block_tables[static_cast<int64_t>(s) * block_table_stride]);
     }
+    may_share = !firsts.empty() && distinct_count(firsts) < static_cast<int64_t>(firsts.size());
   }
   std::vector<Group> groups;
   if (may_share && static_cast<int64_t>(row_pass.size()) >= kMinSharedRows && tiled) {
@@ -382,20 +378,28 @@ extern "C" int pkv_plan_batch(const int32_t* query_seq, const int32_t* query_pos
   // Rule 5: the load hint, over what the row pass still reads.
   bool shared_kv = false;
   if (!row_pass.empty() && may_share) {
-    std::vector<std::pair<int32_t, int64_t>> pairs;  // distinct (sequence, first block)
-    pairs.reserve(row_pass.size());
-    for (size_t i = 0; i < row_pass.size(); ++i) {
-      pairs.emplace_back(seq[row_pass[i]], static_cast<int64_t>(row_first[i]) * partition / block_size);
-    }
-    std::sort(pairs.begin(), pairs.end());
-    pairs.erase(std::unique(pairs.begin(), pairs.end()), pairs.end());
+    // The ids of every distinct (sequence, first block) the row pass reads from: a sequence's
+    // first such pair is found through a per-sequence slot, any further one (a sequence whose
+    // rows start at different partitions) through a sorted list.
+    std::vector<int64_t> first_of(num_seqs, -1);
+    std::vector<std::pair<int32_t, int64_t>> more;
     std::vector<int32_t> ids;
-    int64_t total_ids = 0;
-    for (const auto& [s, first] : pairs) total_ids += std::max<int64_t>(used[s] - first, 0);
-    ids.reserve(total_ids);
-    for (const auto& [s, first] : pairs) {
-      for (int64_t c = first; c < used[s]; ++c) ids.push_back(tables.at(s, c));
+    auto read_from = [&](int32_t s, int64_t first) {
+      for (int64_t c = first; c < used[s]; ++c) ids.push_back(tables.base[static_cast<int64_t>(s) * tables.stride + c]);
+    };
+    for (size_t i = 0; i < row_pass.size(); ++i) {
+      const int32_t s = seq[row_pass[i]];
+      const int64_t first = static_cast<int64_t>(row_first[i]) * partition / block_size;
+      if (first_of[s] < 0) {
+        first_of[s] = first;
+        read_from(s, first);
+      } else if (first_of[s] != first) {
+        more.emplace_back(s, first);
+      }
     }
+    std::sort(more.begin(), more.end());
+    more.erase(std::unique(more.begin(), more.end()), more.end());
+    for (const auto& [s, first] : more) read_from(s, first);
     if (!ids.empty()) {
       const int64_t n = static_cast<int64_t>(ids.size());
       shared_kv = static_cast<double>(n - distinct_count(ids)) >= kSharedKvFraction * static_cast<double>(n);

@@ -218,7 +218,7 @@ class _Staging:
         return self.dev[offset : offset + count * size].view(dtype)
 
 
-@dataclass
+@dataclass(slots=True)
 class _Step:
     """One iteration's device-side metadata (from :meth:`ModelRunner._prepare`), in the planner's
     row order; ``token_order`` maps it back to batch order (None: the same), and when it is set
@@ -341,6 +341,7 @@ class ModelRunner:
         self._stats = np.zeros(8, np.int64)
         self._kv_code = ops.kv_dtype_code(kv_dtype)
         self._marks = np.zeros(num_blocks, np.int32)  # one per pool block, for exclusive_writes
+        self._order = np.zeros(256, np.int64)  # a call's planner row order (prefix_order_rows)
         # Queued copy-on-write copies live in C++ (_pkvhost.CopyQueue); copy_block is its push,
         # so a scheduler's per-block calls cost no Python frame. Their pairs travel through a
         # pinned buffer of their own.
@@ -353,11 +354,21 @@ class ModelRunner:
         _native.init_device(self._device_index)  # the library's overlap stream on this device
         self._per_token = (np.zeros(1024, np.int64), np.zeros(1024, np.int64), np.zeros(1024, np.int64))
         self._per_entry = (np.zeros(256, np.int64), np.zeros(256, np.int32), np.zeros(256, np.int64))
-        #: The host plan of the last call (rows, tiles, merge list, partition size, hints); its
-        #: arrays are views of the planner's buffers, rewritten by the next call.
-        self.last_plan: ops.BatchPlan | None = None
+        self._last_plan: tuple | None = None  # the last call's plan pieces (see last_plan)
         self._layer_bytes = self._keys[0].numel() * self._keys.element_size()
         self._block_elems = self._keys[0, 0].numel()
+
+    @property
+    def last_plan(self) -> ops.BatchPlan | None:
+        """The host plan of the last call (rows, tiles, merge list, partition size, hints); its
+        arrays are views of the planner's buffers, rewritten by the next call."""
+        if self._last_plan is None:
+            return None
+        plan_rows, plan_tiles, partition, flags, merge = self._last_plan
+        return ops.BatchPlan(
+            plan_rows, plan_tiles, partition, bool(flags & _native.PKV_ATTN_SHARED_KV), merge,
+            bool(flags & _native.PKV_ATTN_SHORT_ROWS), bool(flags & _native.PKV_ATTN_DOMINANT_TILES),
+        )  # fmt: skip
 
     # --- pool ---------------------------------------------------------------------------
 
@@ -542,13 +553,15 @@ class ModelRunner:
         # order is read from the arena's rows, which hold every table as int32 by now.
         order = None
         if repeats:
-            order = self._host.prefix_order_rows(
+            if self._order.size < len(entries):
+                self._order = np.zeros(max(len(entries), 2 * self._order.size), np.int64)
+            if self._host.prefix_order_rows(
                 rows, lengths, self._tables.host, self._tables.held_lengths,
-                -(-ops.MIN_SHARED_TOKENS // self.block_size), ops.MIN_SHARED_ROWS,
-            )  # fmt: skip
+                -(-ops.MIN_SHARED_TOKENS // self.block_size), ops.MIN_SHARED_ROWS, self._order,
+            ):  # fmt: skip
+                order = self._order[: len(entries)]  # rewritten by the next call
         token_order = None
         if order is not None:
-            order = np.asarray(order, dtype=np.int64)
             if total == len(entries):  # one token per entry: tokens move as their entries do
                 token_order = order
             else:  # entry order[r]'s tokens, consecutively: token j of run r is start + (j - run offset)
@@ -569,10 +582,7 @@ class ModelRunner:
             query_seq, query_pos, self._tables.host, contexts_by_row, self.block_size, config.n_heads,
             config.head_dim, self.partition_size, kv_dtype=self._keys.dtype,
         )  # fmt: skip
-        self.last_plan = ops.BatchPlan(
-            plan_rows, plan_tiles, partition, bool(flags & _native.PKV_ATTN_SHARED_KV), merge,
-            bool(flags & _native.PKV_ATTN_SHORT_ROWS), bool(flags & _native.PKV_ATTN_DOMINANT_TILES),
-        )  # fmt: skip
+        self._last_plan = (plan_rows, plan_tiles, partition, flags, merge)
         parts64 = [tokens, rope_positions, slots, update.index, wanted]
         parts32 = [query_pos, query_seq, contexts_by_row, update.values, plan_rows.ravel(), plan_tiles.ravel(), merge]
         if token_order is not None:  # attend's caller rows, and its slots in batch order

@@ -26,7 +26,8 @@ __all__ = ["BlockTableArena", "TableUpdate"]
 
 class TableUpdate:
     """What one iteration changes: the arena row of every entry, and the flat (row * width +
-    column) indices and values of the table entries to write on the device."""
+    column) indices and values of the table entries to write on the device. The arrays are views
+    of the arena's buffers, valid until its next update."""
 
     __slots__ = ("rows", "index", "values")
 
@@ -111,9 +112,11 @@ class BlockTableArena:
                 self._values = np.zeros(max(extra, 2 * self._values.size), dtype=np.int32)
             else:
                 break
-        rows = self._rows[:count].copy()
+        # Views of the reused buffers: the caller consumes them before its next update (which
+        # reads _unapplied before rewriting them).
+        rows = self._rows[:count]
         self._unapplied = rows
-        return TableUpdate(rows, self._index[:changed].copy(), self._values[:changed].copy())
+        return TableUpdate(rows, self._index[:changed], self._values[:changed])
 
     def apply(self, index: torch.Tensor, values: torch.Tensor) -> None:
         """Write an update's values (device int32) at its flat indices (device int64)."""

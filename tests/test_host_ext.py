@@ -98,8 +98,11 @@ def test_prefix_order_from_the_arena_matches_the_python_grouping(seed) -> None:
         update = arena.update(entries)
         arena.apply_nothing()
         lengths = np.asarray([len(e.token_ids) for e in entries], np.int64)
-        got = ext.prefix_order_rows(update.rows, lengths, arena.host, arena.held_lengths, -(-512 // block), 16)
-        assert got == shared_prefix_order(entries, block)
+        out = np.full(len(entries) + 3, -5, np.int64)
+        moved = ext.prefix_order_rows(update.rows, lengths, arena.host, arena.held_lengths, -(-512 // block), 16, out)
+        want = shared_prefix_order(entries, block)
+        assert (out[: len(entries)].tolist() if moved else None) == want
+        assert np.all(out[len(entries) :] == -5) and (moved or np.all(out == -5))
 
 
 @pytest.mark.parametrize("seed", range(40))

@@ -62,7 +62,7 @@ def test_an_update_never_applied_is_sent_again() -> None:
 
 def test_least_recently_used_rows_are_reclaimed_and_refilled() -> None:
     arena = BlockTableArena("cpu", rows=2, width=4)
-    rows_a = step(arena, [Entry("a", (1, 2))]).rows
+    rows_a = step(arena, [Entry("a", (1, 2))]).rows.copy()  # the update's arrays are views
     step(arena, [Entry("b", (3, 4))])
     step(arena, [Entry("a", (1, 2))])  # b is now the least recently used
     rows_c = step(arena, [Entry("c", (7,))]).rows
@@ -85,6 +85,31 @@ def test_a_sequence_twice_in_one_batch_gets_two_rows() -> None:
     arena = BlockTableArena("cpu", rows=4, width=4)
     update = step(arena, [Entry("a", (1, 2)), Entry("a", (1, 3))])
     assert update.rows[0] != update.rows[1]
+
+
+@settings(max_examples=60, deadline=None)
+@given(st.data())
+def test_repeated_sequences_get_a_row_per_occurrence(data) -> None:
+    """A sequence may occur several times in one batch (each occurrence a row of its own, keyed
+    by its occurrence number); over several steps every occurrence reads back its own table, the
+    rows of one step are distinct, and a step repeating the previous one uploads nothing."""
+    arena = BlockTableArena("cpu", rows=data.draw(st.integers(1, 4)), width=data.draw(st.integers(1, 4)))
+    previous = None
+    for _ in range(data.draw(st.integers(1, 6))):
+        if previous is not None and data.draw(st.booleans()):
+            entries = previous
+        else:
+            names = data.draw(st.lists(st.sampled_from("abcd"), min_size=1, max_size=8))
+            entries = [Entry(name, tuple(data.draw(st.lists(st.integers(0, 99), min_size=1, max_size=6))))
+                       for name in names]  # fmt: skip
+        update = step(arena, entries)
+        rows = update.rows.tolist()
+        assert len(set(rows)) == len(rows)
+        for entry, row in zip(entries, rows):
+            assert arena.held(row) == entry.block_table
+        if entries is previous:
+            assert update.index.size == 0
+        previous = entries
 
 
 def test_used_blocks_concatenates_the_visible_prefix() -> None:
