@@ -299,15 +299,17 @@ int pkv_paged_attention_noalloc(float* out, const float* queries, int64_t query_
  * Replaces src/paged_kv_serving/engine/runner.py:195-196 (the append) and :198-212 (the
  * per-entry attention loop, attention.py:42-121) for a batch of decode rows.
  *
- * Arguments are pkv_paged_attention's (without tiles: every query row goes through the row pass)
- * plus new_keys / new_values ([num_queries, num_heads, head_dim] of new_dtype with token strides
+ * Arguments are pkv_paged_attention's plus new_keys / new_values ([num_queries, num_heads,
+ * head_dim] of new_dtype with token strides
  * new_key_token_stride / new_value_token_stride, 16-byte aligned rows; bfloat16 only into a
  * bfloat16 pool) and slot_mapping (int64 [num_queries]), as for pkv_append; all three in the
  * caller's row order, like queries and out (with caller_rows, query t's new token is row
  * caller_rows[t] of new_keys / new_values and goes to slot_mapping[caller_rows[t]]). Query t's
- * new token sits at query_positions[t]. Preconditions, which the caller checks: each sequence has exactly
- * one query row in the call, that row's position is below its context_len and below
- * max_context_len, and slot_mapping[t] is the slot the block table gives that position (as in
+ * new token sits at query_positions[t]. Only the row pass appends, so the tiles may cover only
+ * partitions that hold no row's new position: shared-prefix tiles over blocks no row writes,
+ * which the last rule below guarantees (a written block that one row alone reads lies in no
+ * shared prefix). Preconditions, which the caller checks: each sequence has exactly one query
+ * row in the call, that row's position is below its context_len and below max_context_len, and slot_mapping[t] is the slot the block table gives that position (as in
  * runner.py:149-159). A slot outside the pool is not written, as in pkv_append. No row may read a
  * block another row writes: the block holding each row's new slot must occur exactly once among
  * the blocks every row reads (table entries [0, ceil(visible length / block_size)) of each row's
@@ -319,8 +321,8 @@ int pkv_paged_attention_noalloc(float* out, const float* queries, int64_t query_
 int pkv_paged_attention_append(
     float* out, const float* queries, int64_t query_token_stride, const int32_t* query_positions,
     const int32_t* query_seq, int64_t num_queries, const int32_t* caller_rows, const int32_t* rows,
-    int64_t num_rows,
-    const int32_t* merge_rows, int64_t num_merge_rows, void* key_cache, void* value_cache,
+    int64_t num_rows, const int32_t* tiles, int64_t num_tiles, const int32_t* merge_rows,
+    int64_t num_merge_rows, void* key_cache, void* value_cache,
     pkv_dtype kv_dtype, int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
     int32_t block_table_stride, const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,
     int32_t head_dim, float scale, int32_t max_context_len, int32_t partition_size, int32_t flags,

@@ -278,7 +278,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pkv_paged_attention_append.argtypes = [
         _ptr, _ptr, _i64,  # out, queries, query_token_stride
         _ptr, _ptr, _i64, _ptr,  # query_positions, query_seq, num_queries, caller_rows
-        _ptr, _i64,  # rows, num_rows
+        _ptr, _i64, _ptr, _i64,  # rows, num_rows, tiles, num_tiles
         _ptr, _i64,  # merge_rows, num_merge_rows
         _ptr, _ptr, _c_int, _i64, _i32,  # key_cache, value_cache, kv_dtype, num_blocks, block_size
         _ptr, _i32, _ptr, _i32,  # block_tables, block_table_stride, context_lens, num_seqs

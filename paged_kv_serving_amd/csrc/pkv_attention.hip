@@ -423,12 +423,78 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
   const KVT* vcache = static_cast<const KVT*>(a.vcache);
   const int64_t head_off = static_cast<int64_t>(h) * D;
   const int64_t row_stride = static_cast<int64_t>(a.num_heads) * D;  // elements per token row
-  const int n_iter = (kend - kbeg + L::kIterTok - 1) / L::kIterTok;
-  // With the fused append, the key position of this row's own new token (else none), and where
-  // its head group's key and value rows start in the append source.
+  // With the fused append, the key position of this row's own new token. It is the row's last
+  // visible key (the query sits at its own position), so it lies in the row's last partition.
+  // The full-size workgroups take it from the append source inside the loop, in the load round
+  // that reaches it. The lean ones, whose workgroups must keep to the plain lean pass's
+  // registers to fit three of them beside a tile workgroup (3 x 112 + 168 <= 512 per SIMD), stop
+  // the loop one key short and take it before the loop in one lane group: a branch inside the
+  // loop takes them to 124 registers (measured: config 4's attention 0.22 -> 0.30 ms), while the
+  // full-size pass is quicker with the branch (config 2: 0.722 against 0.732 ms).
   const int own_pos = kAppend ? a.q_pos[t] : -1;
+  const bool own_here = kAppend && own_pos >= kbeg && own_pos < kend;
+  const int kloop = kLean && own_here ? own_pos : kend;
+  const int n_iter = (kloop - kbeg + L::kIterTok - 1) / L::kIterTok;
   const int64_t own_key = r * a.new_key_stride + head_off;
   const int64_t own_value = r * a.new_value_stride + head_off;
+
+  if constexpr (kAppend && kLean) {
+    // The row's own new token, in its last partition: before the loop (few registers are live
+    // yet), lane group 0 of wavefront 0 takes its key and value from the append source (in the
+    // pool's element type, as pkv_append stores them), writes them to the token's slot (the
+    // workgroup of each head group writes its slice) and starts its softmax state with them.
+    // A block id outside the pool masks the key and writes nothing (its slot, formed from the
+    // same table, lies outside too).
+    if (own_here && wave == 0) {
+      const int lb = block_of<kPow2Block>(own_pos, a) - b0;
+      const int blk = s_table[lb];
+      const bool ok = g == 0 && blk >= 0 && blk < a.num_blocks;
+      uint4 kr[L::kVpl];
+      uint4 vr[L::kVpl];
+#pragma unroll
+      for (int i = 0; i < L::kVpl; ++i) {
+        const int64_t e = static_cast<int64_t>(i * L::kLpt + j) * L::kEpv;
+        kr[i] = ok ? new_row_vector(a, a.new_keys, own_key + e, KVT{}) : make_uint4(0, 0, 0, 0);
+        vr[i] = ok ? new_row_vector(a, a.new_values, own_value + e, KVT{}) : make_uint4(0, 0, 0, 0);
+      }
+      const int64_t slot = a.new_slots[r];
+      if (ok && slot >= 0 && slot < a.num_slots) {
+        uint4* kd = reinterpret_cast<uint4*>(const_cast<KVT*>(kcache) + slot * row_stride + head_off);
+        uint4* vd = reinterpret_cast<uint4*>(const_cast<KVT*>(vcache) + slot * row_stride + head_off);
+#pragma unroll
+        for (int i = 0; i < L::kVpl; ++i) {
+          kd[i * L::kLpt + j] = kr[i];
+          vd[i * L::kLpt + j] = vr[i];
+        }
+      }
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) {
+        float dot = 0.f;
+#pragma unroll
+        for (int i = hh * L::kVph; i < (hh + 1) * L::kVph; ++i) {
+          float kf[L::kEpv];
+          widen(kr[i], kf, KVT{});
+#pragma unroll
+          for (int e = 0; e < L::kEpv; ++e) dot = fmaf(qv[i * L::kEpv + e], kf[e], dot);
+        }
+        dot = group_sum<L::kLpt>(dot);
+        const float sc = ok ? dot : -INFINITY;
+        const float mx = fmaxf(m[hh], sc);
+        const float shift = mx == -INFINITY ? 0.f : mx;
+        const float alpha = fast_exp2(m[hh] - shift);
+        const float pr = fast_exp2(sc - shift);
+        l[hh] = fmaf(l[hh], alpha, pr);
+        m[hh] = mx;
+#pragma unroll
+        for (int i = hh * L::kVph; i < (hh + 1) * L::kVph; ++i) {
+          float vf[L::kEpv];
+          widen(vr[i], vf, KVT{});
+#pragma unroll
+          for (int e = 0; e < L::kEpv; ++e) acc[i * L::kEpv + e] = fmaf(pr, vf[e], acc[i * L::kEpv + e] * alpha);
+        }
+      }
+    }
+  }
 
   for (int it = wave; it < n_iter; it += kWaves) {
     const int base = kbeg + it * L::kIterTok;
@@ -438,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
 #pragma unroll
     for (int rr = 0; rr < L::kRounds; ++rr) {
       const int kpos = base + rr * L::kTpr + g;
-      bool ok = kpos < kend;
+      bool ok = kpos < kloop;
       int64_t row = 0;
       if (ok) {
         const int lb = block_of<kPow2Block>(kpos, a) - b0;
@@ -448,7 +514,7 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
         row = (static_cast<int64_t>(blk) * a.block_size + off) * row_stride + head_off;
       }
       valid[rr] = ok;
-      if (kAppend && kpos == own_pos && kpos < kend) {
+      if (kAppend && !kLean && kpos == own_pos && kpos < kend) {
         // This row's own new token: its key and value come from the append source and are
         // written to the token's slot here (the workgroup of each head group writes its slice).
 #pragma unroll
@@ -1521,7 +1587,11 @@ int launch_all(const Params& a, int64_t num_queries, int64_t num_rows, int64_t n
     const dim3 grid(static_cast<uint32_t>(groups));
     // The lean and the appending variants exist for power-of-two block sizes only (the others
     // ignore the hint; attention_call appends separately for them).
-    if (pow2 && append && stream_kv) {
+    if (pow2 && append && short_rows && stream_kv) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, true, true>), grid, dim3(kThreads), 0, rs, a);
+    } else if (pow2 && append && short_rows) {
+      hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, true, true>), grid, dim3(kThreads), 0, rs, a);
+    } else if (pow2 && append && stream_kv) {
       hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, true, false, true>), grid, dim3(kThreads), 0, rs, a);
     } else if (pow2 && append) {
       hipLaunchKernelGGL((row_partial_kernel<KVT, D, HPW, true, false, false, true>), grid, dim3(kThreads), 0, rs, a);
@@ -1746,10 +1816,10 @@ int attention_call(float* out, const float* queries, int64_t query_token_stride,
   // The tile pass writes four dimensions of a row at a time.
   if (num_tiles > 0 && (!aligned16(out) || (ws_acc && !aligned16(ws_acc)))) return PKV_EINVAL;
   if (append != nullptr) {
-    // Only the row pass appends, so a fused append takes a plan without tiles; the source rows
-    // are read as 16-byte vectors.
+    // Only the row pass appends (tiles may cover partitions that hold no new position: a shared
+    // prefix); the source rows are read as 16-byte vectors.
     const int src_size = dtype_size(append->dtype);
-    if (num_tiles > 0 || src_size == 0 || !append->keys || !append->values || !append->slots) {
+    if (src_size == 0 || !append->keys || !append->values || !append->slots) {
       return PKV_EINVAL;
     }
     if (append->dtype == PKV_BF16 && kv_dtype == PKV_F32) return PKV_EUNSUPPORTED;
@@ -1887,7 +1957,7 @@ extern "C" int pkv_paged_attention_noalloc(
 extern "C" int pkv_paged_attention_append(
     float* out, const float* queries, int64_t query_token_stride, const int32_t* query_positions,
     const int32_t* query_seq, int64_t num_queries, const int32_t* caller_rows, const int32_t* rows,
-    int64_t num_rows,
+    int64_t num_rows, const int32_t* tiles, int64_t num_tiles,
     const int32_t* merge_rows, int64_t num_merge_rows, void* key_cache, void* value_cache,
     pkv_dtype kv_dtype, int64_t num_blocks, int32_t block_size, const int32_t* block_tables,
     int32_t block_table_stride, const int32_t* context_lens, int32_t num_seqs, int32_t num_heads,
@@ -1898,7 +1968,7 @@ extern "C" int pkv_paged_attention_append(
   const pkv::AppendSource append{new_keys, new_values, new_dtype, new_key_token_stride,
                                  new_value_token_stride, slot_mapping};
   return pkv::attention_call(out, queries, query_token_stride, query_positions, query_seq,
-                             num_queries, caller_rows, rows, num_rows, nullptr, 0, merge_rows,
+                             num_queries, caller_rows, rows, num_rows, tiles, num_tiles, merge_rows,
                              num_merge_rows,
                              key_cache, value_cache, kv_dtype, num_blocks, block_size,
                              block_tables, block_table_stride, context_lens, num_seqs, num_heads,

@@ -41,10 +41,13 @@
 //       new group when it reads a block an earlier copy of the group writes, or writes a block
 //       an earlier copy of the group reads or writes); flush(...) sends the pairs to the device
 //       and launches one pkv_copy_blocks per group; clear() and items() drop and list them.
-//   exclusive_writes(rows, contexts, host, block_size, marks) -> bool
+//   exclusive_writes(rows, contexts, host, block_size, marks[, tiles, partition]) -> bool
 //       Whether a batch of single-token entries at their last positions (entry e: arena row
 //       rows[e], context contexts[e], so it writes position contexts[e] - 1) may append inside
-//       the attention call: True when each written block occurs exactly once among the blocks
+//       the attention call: False when a tile of the plan (int32 [n, 4] records over planner
+//       rows, the entries' order here; `partition` keys per partition) covers an entry's own
+//       position, since only the row pass appends; else True when each written block occurs
+//       exactly once among the blocks
 //       every entry reads (host[rows[e]][0 .. ceil(contexts[e] / B))), which is its own writer's
 //       entry for that position. Otherwise some row reads a slot another row (or its own row,
 //       through a repeated table entry) writes in the same step, and only an append that
@@ -636,19 +639,36 @@ done:
 }
 
 PyObject* exclusive_writes(PyObject*, PyObject* args) {
-  PyObject *rows_o, *contexts_o, *host_o, *marks_o;
-  long long block_size;
-  if (!PyArg_ParseTuple(args, "OOOLO", &rows_o, &contexts_o, &host_o, &block_size, &marks_o)) return nullptr;
-  Buf<int32_t> rows, contexts, host, marks;
+  PyObject *rows_o, *contexts_o, *host_o, *marks_o, *tiles_o = Py_None;
+  long long block_size, partition = 0;
+  if (!PyArg_ParseTuple(args, "OOOLO|OL", &rows_o, &contexts_o, &host_o, &block_size, &marks_o, &tiles_o, &partition)) {
+    return nullptr;
+  }
+  Buf<int32_t> rows, contexts, host, marks, tiles;
   if (!rows.get(rows_o, "rows", false) || !contexts.get(contexts_o, "contexts", false) ||
-      !host.get(host_o, "host", false) || !marks.get(marks_o, "marks")) {
+      !host.get(host_o, "host", false) || !marks.get(marks_o, "marks") ||
+      (tiles_o != Py_None && !tiles.get(tiles_o, "tiles", false))) {
     return nullptr;
   }
   const Py_ssize_t count = rows.size();
   const Py_ssize_t num_rows = host.dim(0), width = host.dim(1);
-  if (host.ndim() != 2 || contexts.size() < count || block_size < 1) {
+  const Py_ssize_t tile_ints = tiles_o == Py_None ? 0 : tiles.size();
+  if (host.ndim() != 2 || contexts.size() < count || block_size < 1 || tile_ints % 4 != 0 ||
+      (tile_ints > 0 && partition < 1)) {
     PyErr_SetString(PyExc_ValueError, "exclusive_writes buffers disagree");
     return nullptr;
+  }
+  // 0. A tile must cover no row's own position (context - 1): only the row pass appends.
+  for (Py_ssize_t i = 0; i + 3 < tile_ints; i += 4) {
+    const int32_t* t = tiles.data() + i;
+    const bool whole = t[3] == PKV_TILE_WHOLE;
+    const int64_t lo = whole ? 0 : static_cast<int64_t>(t[2]) * partition;
+    const int64_t hi = whole || t[3] <= t[2] ? INT64_MAX : static_cast<int64_t>(t[3]) * partition;
+    for (int64_t r = t[0]; r < static_cast<int64_t>(t[0]) + t[1]; ++r) {
+      if (r < 0 || r >= count) Py_RETURN_FALSE;
+      const int64_t own = static_cast<int64_t>(contexts.data()[r]) - 1;
+      if (own >= lo && own < hi) Py_RETURN_FALSE;
+    }
   }
   const int64_t num_blocks = marks.size();
   int32_t* mark = marks.data();
@@ -682,17 +702,38 @@ PyObject* exclusive_writes(PyObject*, PyObject* args) {
     written.push_back(w);
   }
   // 2. Count the occurrences of flagged blocks among every entry's visible blocks: each written
-  // block must occur once, in its writer's own table.
+  // block must occur once, in its writer's own table. Entries that share a prefix (the common
+  // case the check serves: sequences forked from one parent) repeat the previous entry's leading
+  // blocks; those need no second look when none of them is flagged (a flagged one among them
+  // occurs in both tables, which already fails), so only the rest of each table is scanned.
+  const int32_t* prev_table = nullptr;
+  int64_t prev_nb = 0, prev_flagged = 0;  // the previous entry's first flagged index (nb: none)
   for (Py_ssize_t e = 0; e < count && ok; ++e) {
     const int32_t* table = nullptr;
     const int64_t nb = visible(e, &table);
-    for (int64_t i = 0; i < nb; ++i) {
-      const int32_t b = table[i];
-      if (b >= 0 && b < num_blocks && mark[b] != 0 && ++mark[b] > 2) {
-        ok = false;
+    int64_t start = 0;
+    if (prev_table != nullptr) {
+      const int64_t limit = std::min(nb, prev_nb);
+      while (start < limit && table[start] == prev_table[start]) ++start;
+      if (prev_flagged < start) {
+        ok = false;  // a written block in both tables
         break;
       }
     }
+    int64_t flagged = nb;
+    for (int64_t i = start; i < nb; ++i) {
+      const int32_t b = table[i];
+      if (b >= 0 && b < num_blocks && mark[b] != 0) {
+        if (flagged == nb) flagged = i;
+        if (++mark[b] > 2) {
+          ok = false;
+          break;
+        }
+      }
+    }
+    prev_table = table;
+    prev_nb = nb;
+    prev_flagged = flagged;
   }
   for (int32_t w : written) mark[w] = 0;
   return PyBool_FromLong(ok);
@@ -946,13 +987,14 @@ PyObject* paged_attention(PyObject*, PyObject* args) {
 }
 
 PyObject* paged_attention_append(PyObject*, PyObject* args) {
-  unsigned long long out, queries, qpos, qseq, caller_rows, rows, merge, kc, vc, tables, ctx, ws, new_k, new_v, slots,
-      stream;
-  long long q_stride, nq, nrows, nmerge, nblocks, ws_bytes, k_stride, v_stride;
+  unsigned long long out, queries, qpos, qseq, caller_rows, rows, tiles, merge, kc, vc, tables, ctx, ws, new_k, new_v,
+      slots, stream;
+  long long q_stride, nq, nrows, ntiles, nmerge, nblocks, ws_bytes, k_stride, v_stride;
   int dtype, block_size, table_stride, nseqs, heads, head_dim, max_ctx, partition, flags, new_dtype, device;
   float scale;
-  if (!PyArg_ParseTuple(args, "KKLKKLKKLKLKKiLiKiKiiifiiiKLKKiLLKiK", &out, &queries, &q_stride, &qpos, &qseq, &nq,
-                        &caller_rows, &rows, &nrows, &merge, &nmerge, &kc, &vc, &dtype, &nblocks, &block_size, &tables,
+  if (!PyArg_ParseTuple(args, "KKLKKLKKLKLKLKKiLiKiKiiifiiiKLKKiLLKiK", &out, &queries, &q_stride, &qpos, &qseq, &nq,
+                        &caller_rows, &rows, &nrows, &tiles, &ntiles, &merge, &nmerge, &kc, &vc, &dtype, &nblocks,
+                        &block_size, &tables,
                         &table_stride, &ctx, &nseqs, &heads, &head_dim, &scale, &max_ctx, &partition, &flags, &ws,
                         &ws_bytes, &new_k, &new_v, &new_dtype, &k_stride, &v_stride, &slots, &device, &stream)) {
     return nullptr;
@@ -960,8 +1002,8 @@ PyObject* paged_attention_append(PyObject*, PyObject* args) {
   if (!bound(reinterpret_cast<const void*>(g_paged_attention_append))) return nullptr;
   const int rc = g_paged_attention_append(
       ptr<float>(out), ptr<const float>(queries), q_stride, ptr<const int32_t>(qpos), ptr<const int32_t>(qseq), nq,
-      ptr<const int32_t>(caller_rows), ptr<const int32_t>(rows), nrows, ptr<const int32_t>(merge), nmerge,
-      ptr<void>(kc), ptr<void>(vc),
+      ptr<const int32_t>(caller_rows), ptr<const int32_t>(rows), nrows, ptr<const int32_t>(tiles), ntiles,
+      ptr<const int32_t>(merge), nmerge, ptr<void>(kc), ptr<void>(vc),
       static_cast<pkv_dtype>(dtype), nblocks, block_size, ptr<const int32_t>(tables), table_stride,
       ptr<const int32_t>(ctx), nseqs, heads, head_dim, scale, max_ctx, partition, flags, ptr<float>(ws), ws_bytes,
       ptr<const void>(new_k), ptr<const void>(new_v), static_cast<pkv_dtype>(new_dtype), k_stride, v_stride,

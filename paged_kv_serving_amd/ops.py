@@ -949,7 +949,8 @@ def launch_paged_attention(
         return
     new_keys, new_values, slot_mapping = append
     rc = lib.pkv_paged_attention_append(
-        *common, *tail, new_keys.data_ptr(), new_values.data_ptr(), kv_dtype_code(new_keys.dtype),
+        *common, plan.tiles.data_ptr() if num_tiles else None, num_tiles, *tail, new_keys.data_ptr(),
+        new_values.data_ptr(), kv_dtype_code(new_keys.dtype),
         new_keys.stride(0), new_values.stride(0), slot_mapping.data_ptr(), device, _stream(device),
     )  # fmt: skip
     _native.check(rc, "pkv_paged_attention_append")
@@ -1109,8 +1110,8 @@ def paged_attention_ragged(
         num_rows, num_tiles = plan.num_rows, plan.num_tiles
         rows_ptr = plan.rows.data_ptr() if num_rows else None
         tiles_ptr = plan.tiles.data_ptr() if num_tiles else None
-        if append is not None and (num_tiles or not num_rows):
-            raise ValueError("a fused append needs a plan whose rows all go through the row pass")
+        if append is not None and not num_rows:
+            raise ValueError("a fused append needs a plan with row-pass rows (the row pass appends)")
         if num_rows == 0 and num_tiles == 0:
             return out
         if plan.merge is not None:
@@ -1135,7 +1136,7 @@ def paged_attention_ragged(
         rc = _native.library().pkv_paged_attention_append(
             out.data_ptr(), queries.data_ptr(), stride,
             query_positions.data_ptr(), query_seq.data_ptr(), num_queries, caller_ptr,
-            rows_ptr, num_rows, merge_ptr, num_merge,
+            rows_ptr, num_rows, tiles_ptr, num_tiles, merge_ptr, num_merge,
             key_cache.data_ptr(), value_cache.data_ptr(), kv_dtype_code(key_cache.dtype),
             key_cache.shape[0], key_cache.shape[1],
             block_tables.data_ptr(), block_tables.shape[1], context_lens.data_ptr(), num_seqs,

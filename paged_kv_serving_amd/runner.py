@@ -603,9 +603,11 @@ class ModelRunner:
         # writes: the fused kernel hands a written key to its own row alone, while the reference
         # writes every slot before any attention (runner.py:195-212). A sequence twice in one
         # batch, or tables that share the block being written, take the append-then-attention
-        # path.
-        decode_only = plan_tiles.shape[0] == 0 and len(entries) == total and self._host.exclusive_writes(
-            rows, context, self._tables.host, self.block_size, self._marks
+        # path. Tiles may stay: only the row pass appends, so no tile may cover a row's new
+        # position, which exclusive_writes also checks (a decode batch's tiles are shared-prefix
+        # tiles, and a written block that one row alone reads lies past every shared prefix).
+        decode_only = len(entries) == total and self._host.exclusive_writes(
+            rows, context, self._tables.host, self.block_size, self._marks, plan_tiles, partition
         )  # fmt: skip
         return _Step(
             total=total, staging=staging, tokens_at=tokens_at, rope_at=rope_at, slots_at=slots_at,
@@ -659,7 +661,8 @@ class ModelRunner:
             return
         keys, values = append
         rc = self._host.paged_attention_append(
-            *common, *tail, keys.data_ptr(), values.data_ptr(), ops.kv_dtype_code(keys.dtype), keys.stride(0),
+            *common, step.ptr(step.plan_tiles_at) if step.num_tiles else 0, step.num_tiles, *tail, keys.data_ptr(),
+            values.data_ptr(), ops.kv_dtype_code(keys.dtype), keys.stride(0),
             values.stride(0), step.ptr(step.batch_slots_at), device, stream,
         )  # fmt: skip
         _native.check(rc, "pkv_paged_attention_append")

@@ -469,6 +469,57 @@ def test_fused_decode_append_equals_append_then_attention(device, kinds, block, 
         assert np.max(np.abs(got.cpu().numpy() - dense)) < FP32_TOL, partition
 
 
+@pytest.mark.parametrize("heads", [4, 32], ids=["alone", "overlapped"])
+def test_fused_append_beside_shared_prefix_tiles(device, heads) -> None:
+    """A decode batch whose sequences share a prefix: the plan reads the prefix as MFMA tiles and
+    the fused append writes each row's new key and value (into its private last block) from the
+    row pass, beside the tile pass (at 32 heads on the second stream). Pools bit for bit as after
+    pkv_append; outputs within 1e-6 of append-then-attention and 1e-5 of the oracle."""
+    say("fused append beside prefix tiles", heads)
+    rng = np.random.default_rng(heads)
+    dim, block, seqs = 128, 16, 64
+    prefix = 40  # blocks: 640 shared tokens
+    suffix = rng.integers(20, 300, seqs)
+    contexts = prefix * block + suffix
+    need = [-(-int(c) // block) - prefix for c in contexts]
+    pool = prefix + sum(need)
+    ids = rng.permutation(pool)
+    shared = ids[:prefix].tolist()
+    tables, offset = [], prefix
+    for n in need:
+        tables.append(np.asarray(shared + ids[offset : offset + n].tolist()))
+        offset += n
+    padded = np.zeros((seqs, max(len(t) for t in tables)), dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    positions = contexts - 1
+    slots = np.asarray([int(t[p // block]) * block + p % block for t, p in zip(tables, positions)], np.int64)
+    kc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    vc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    q, new_k, new_v = (rng.standard_normal((seqs, heads, dim)).astype(np.float32) for _ in range(3))
+    seq_of = np.arange(seqs)
+    plan = ops.plan_batch(seq_of, dim, heads, tables, contexts, block, query_positions=positions)
+    assert plan.tiles.shape[0] >= 1, "prefix tiles"
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    args = (to(q), to(positions.astype(np.int32)), to(seq_of.astype(np.int32)))
+    meta = (to(padded), to(contexts.astype(np.int32)), dim**-0.5)
+    dplan = ops.upload_batch_plan(plan, device)
+    k_sep, v_sep = to(kc), to(vc)
+    ops.append_kv(k_sep, v_sep, to(new_k), to(new_v), to(slots))
+    want = ops.paged_attention_ragged(*args, k_sep, v_sep, *meta, max_context_len=int(contexts.max()), plan=dplan)
+    k_fus, v_fus = to(kc), to(vc)
+    got = ops.paged_attention_ragged(*args, k_fus, v_fus, *meta, max_context_len=int(contexts.max()), plan=dplan,
+                                     append=(to(new_k), to(new_v), to(slots)))  # fmt: skip
+    assert torch.equal(k_fus, k_sep) and torch.equal(v_fus, v_sep)
+    assert float((got - want).abs().max()) < 1e-6
+    kh, vh = k_sep.cpu().numpy(), v_sep.cpu().numpy()
+    oracle, dense = _oracle(kh, vh, tables, contexts, positions, seq_of, q, dim**-0.5)
+    assert np.max(np.abs(got.cpu().numpy() - oracle)) < FP32_TOL
+    assert np.max(np.abs(got.cpu().numpy() - dense)) < FP32_TOL
+    if heads == 32:
+        assert plan.rows.shape[0] * heads >= 2048, "the overlapped grid"
+
+
 def _whole_tile_plan(seq_of, positions, contexts, dim, partition, device, *, explicit_merge):
     """Every run of >= 2 rows of one sequence as whole tiles; the rest in the row pass."""
     rows, tiles = ops.plan_rows(seq_of, dim, min_tile_rows=2)

@@ -330,6 +330,35 @@ def test_exclusive_writes_decides_when_the_decode_append_may_be_fused() -> None:
     assert exclusive([(0, 1, 5), (5, 6)], [20, 20], 16, 8)
 
 
+def test_exclusive_writes_refuses_tiles_over_a_new_position() -> None:
+    """Only the row pass appends, so a fused call's tiles must cover no row's own position
+    (context - 1): tile records (first row, count, first partition, end partition) over the
+    entries in the order given; end <= first partition runs through the last, -1 is whole."""
+    tables = [tuple(range(10 * i, 10 * i + 5)) for i in range(4)]  # private blocks
+    rows = np.arange(4, dtype=np.int32)
+    host = np.zeros((4, 5), np.int32)
+    for i, t in enumerate(tables):
+        host[i] = t
+    contexts = np.asarray([70, 65, 80, 33], np.int32)  # own positions 69, 64, 79, 32
+    marks = np.zeros(64, np.int32)
+
+    def fused(tiles, partition=32):
+        return ext.exclusive_writes(rows, contexts, host, 16, marks, np.asarray(tiles, np.int32).reshape(-1, 4),
+                                    partition)  # fmt: skip
+
+    assert ext.exclusive_writes(rows, contexts, host, 16, marks)
+    assert fused(np.zeros((0, 4)))
+    assert fused([[0, 3, 0, 2]])  # keys [0, 64) of rows 0-2: no own position
+    assert not fused([[0, 3, 0, 3]])  # keys [0, 96) hold row 1's position 64
+    assert fused([[3, 1, 2, 3]])  # keys [64, 96) of row 3 (position 32)
+    assert not fused([[2, 2, 1, 1]])  # from key 32 through the last: row 3's position 32
+    assert not fused([[1, 1, 0, -1]])  # a whole tile covers everything
+    assert not fused([[2, 5, 0, 1]])  # rows past the batch
+    with pytest.raises(ValueError):
+        fused([[0, 3, 0, 2]], partition=0)
+    assert not marks.any()
+
+
 @pytest.mark.parametrize("seed", range(60))
 def test_exclusive_writes_matches_the_brute_force_rule(seed) -> None:
     rng = np.random.default_rng(seed)
@@ -343,6 +372,33 @@ def test_exclusive_writes_matches_the_brute_force_rule(seed) -> None:
         tables.append(tuple(int(b) for b in rng.integers(0, num_blocks + 3, need)))
         contexts.append(ctx)
     assert exclusive(tables, contexts, block, num_blocks) == exclusive_by_brute_force(tables, contexts, block, num_blocks)
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_exclusive_writes_on_forked_tables_matches_the_brute_force_rule(seed) -> None:
+    """Tables that share leading blocks (forks of one or two parents), the case whose repeated
+    prefixes the check skips: rows ending inside a shared prefix, rows writing a block another
+    row reads past the prefix, prefixes of different lengths next to each other."""
+    rng = np.random.default_rng(1000 + seed)
+    block = int(rng.choice([1, 4, 16]))
+    ids = iter(rng.permutation(5000).tolist())
+    parents = [[next(ids) for _ in range(int(rng.integers(1, 12)))] for _ in range(2)]
+    tables, contexts = [], []
+    for _ in range(int(rng.integers(2, 25))):
+        parent = parents[int(rng.integers(2))]
+        keep = int(rng.integers(0, len(parent) + 1))
+        private = int(rng.integers(0, 4)) if rng.random() < 0.1 else int(rng.integers(1, 4))
+        table = parent[:keep] + [next(ids) for _ in range(private)]
+        if not table:
+            table = [next(ids)]
+        ctx = int(rng.integers((len(table) - 1) * block + 1, len(table) * block + 1))
+        if rng.random() < 0.05 and tables:  # write into a block some other row holds
+            other = tables[int(rng.integers(len(tables)))]
+            table = list(other[: max(1, len(other) - 1)])
+            ctx = len(table) * block
+        tables.append(tuple(table))
+        contexts.append(ctx)
+    assert exclusive(tables, contexts, block, 5000) == exclusive_by_brute_force(tables, contexts, block, 5000)
 
 
 def test_forward_refuses_bad_arguments_before_any_device_work() -> None:

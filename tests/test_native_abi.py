@@ -154,7 +154,7 @@ def test_fused_append_arguments_are_refused_before_any_device_work(lib) -> None:
     def call(new_keys=nk, new_values=nv, new_dtype=0, key_stride=512, value_stride=512,
              pool_dtype=0, slot_mapping=slots, head_dim=128):  # fmt: skip
         return lib.pkv_paged_attention_append(
-            out, q, 4 * head_dim, qpos, qseq, 3, None, None, 0, None, -1, kc, vc, pool_dtype, 100, 16,
+            out, q, 4 * head_dim, qpos, qseq, 3, None, None, 0, None, 0, None, -1, kc, vc, pool_dtype, 100, 16,
             tables, 8, ctx, 3, 4, head_dim, ctypes.c_float(0.1), 100, 0, 0, ws, 1 << 20,
             new_keys, new_values, new_dtype, key_stride, value_stride, slot_mapping, 0, None,
         )  # fmt: skip
