@@ -249,9 +249,10 @@ def run_attention_config(args, batch, *, metric: str, workload: str, dtype: str,
     def append() -> None:
         ops.append_kv(batch.key_cache, batch.value_cache, batch.new_keys, batch.new_values, batch.slot_mapping)
 
-    # A decode batch (one row per sequence, at its last position, all in the row pass) appends
-    # inside the attention call; any other batch appends first with its own launch.
-    fused = batch.decode_rows_only() and batch.plan.num_tiles == 0
+    # A decode batch (one row per sequence, at its last position) whose written blocks no other
+    # row reads appends inside the attention call, as the runner does; any other batch appends
+    # first with its own launch.
+    fused = batch.fusable_append()
     attend = attention_call(batch, args, out, workspace, fused_append=fused)
     for _ in range(args.warmup):
         if not fused:

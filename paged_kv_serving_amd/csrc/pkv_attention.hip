@@ -440,12 +440,12 @@ __global__ __launch_bounds__(kThreads) void row_partial_kernel(const Params a) {
 
   if constexpr (kAppend && kLean) {
     // The row's own new token, in its last partition: before the loop (few registers are live
-    // yet), lane group 0 of wavefront 0 takes its key and value from the append source (in the
-    // pool's element type, as pkv_append stores them), writes them to the token's slot (the
-    // workgroup of each head group writes its slice) and starts its softmax state with them.
-    // A block id outside the pool masks the key and writes nothing (its slot, formed from the
-    // same table, lies outside too).
-    if (own_here && wave == 0) {
+    // yet), lane group 0 of the last wavefront (the one the loop's round robin gives the fewest
+    // steps) takes its key and value from the append source (in the pool's element type, as
+    // pkv_append stores them), writes them to the token's slot (the workgroup of each head group
+    // writes its slice) and starts its softmax state with them. A block id outside the pool
+    // masks the key and writes nothing (its slot, formed from the same table, lies outside too).
+    if (own_here && wave == kWaves - 1) {
       const int lb = block_of<kPow2Block>(own_pos, a) - b0;
       const int blk = s_table[lb];
       const bool ok = g == 0 && blk >= 0 && blk < a.num_blocks;

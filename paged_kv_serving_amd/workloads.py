@@ -79,6 +79,30 @@ class AttentionBatch:
             return False
         return bool(np.all(self.host_positions == self.host_context[seq] - 1))
 
+    def fusable_append(self) -> bool:
+        """Whether the runner would fuse this batch's append into the attention call: the
+        decode shape, each written block read by its own row alone, and no tile of the plan over
+        a written position (the rule of ModelRunner's exclusive_writes check)."""
+        if not self.decode_rows_only():
+            return False
+        block = self.key_cache.shape[1]
+        tables = [np.asarray(self.host_tables[s]) for s in self.host_seq]
+        contexts = self.host_context[self.host_seq]
+        visible = np.concatenate([t[: -(-int(c) // block)] for t, c in zip(tables, contexts)])
+        written = np.asarray([t[(int(c) - 1) // block] for t, c in zip(tables, contexts)])
+        counts = dict(zip(*np.unique(visible, return_counts=True)))
+        if any(counts.get(int(w), 0) != 1 for w in written):
+            return False
+        tiles = self.plan.tiles.cpu().numpy() if self.plan.num_tiles else np.zeros((0, 4), np.int32)
+        part = self.plan.partition_size or 512
+        own = contexts - 1
+        for first, count, begin, end in tiles.tolist():
+            lo = 0 if end == -1 else begin * part
+            hi = np.inf if end == -1 or end <= begin else end * part
+            if np.any((own[first : first + count] >= lo) & (own[first : first + count] < hi)):
+                return False
+        return True
+
     def context_bytes(self) -> int:
         """Algorithmic K+V bytes: each query row's visible keys and values, read once."""
         heads, dim = self.key_cache.shape[2], self.key_cache.shape[3]

@@ -1140,6 +1140,12 @@ def test_config4_prefix_sharing_cow_then_decode(device) -> None:
     # a plan's partition indices belong to its partition size
     with pytest.raises(ValueError, match="partition"):
         ops.paged_attention_ragged(*common, max_context_len=d.max_context_len, plan=plan, partition_size=512)
+    # every child writes its own copied block and the prefix tiles cover no new position, so the
+    # bench and the runner fuse the append into the call; the fused step agrees with append-then-
+    # attention (the batch's rows were appended above, so this rewrites the same values)
+    assert d.fusable_append()
+    fused = _run_fused(d)
+    assert float((fused - out).abs().max()) < 1e-6
 
 
 def test_empty_inputs_leave_the_pools_alone(device) -> None:
