@@ -355,6 +355,9 @@ class ModelRunner:
         self._per_token = (np.zeros(1024, np.int64), np.zeros(1024, np.int64), np.zeros(1024, np.int64))
         self._per_entry = (np.zeros(256, np.int64), np.zeros(256, np.int32), np.zeros(256, np.int64))
         self._last_plan: tuple | None = None  # the last call's plan pieces (see last_plan)
+        #: Whether the last step's append rode inside its attention call (the decode rule of
+        #: _pkvhost.exclusive_writes), rather than a pkv_append launch before it.
+        self.last_append_fused = False
         self._layer_bytes = self._keys[0].numel() * self._keys.element_size()
         self._block_elems = self._keys[0, 0].numel()
 
@@ -696,6 +699,7 @@ class ModelRunner:
         queries, keys, values = (t if t.is_contiguous() else t.contiguous() for t in (queries, keys, values))
         # Everything stays in batch order: a plan in its own row order reaches the batch rows
         # through the call's caller_rows.
+        self.last_append_fused = step.decode_only
         if step.decode_only:
             self._attention(step, layer, queries, out, append=(keys, values))
         else:  # pkv_append of the batch's keys and values at their slots, then the attention

@@ -473,6 +473,9 @@ def test_attend_appends_and_attends_like_the_reference_runner(device, seed, shar
     out = runner.attend(batch, *(torch.from_numpy(a).to(device) for a in (q, k, v)), layer=1).cpu().numpy()
     if sharers:
         assert runner.last_plan is not None and runner.last_plan.tiles.shape[0] > 0, "prefix tiles"
+    # a decode batch whose rows write private blocks appends inside the attention call, shared-
+    # prefix tiles or not; a prefill chunk makes the runner append first
+    assert runner.last_append_fused == (not prefill)
     slots = [s for e in batch.entries for s in slots_for(e.seq_id, e.positions, e.block_table, block)]
     oracle_append(keys0, values0, slots, k, v)
     assert np.array_equal(runner.key_cache[1].cpu().numpy(), keys0)
