@@ -157,6 +157,23 @@ def test_copy_queue_groups_match_the_python_grouping(seed) -> None:
     assert len(queue) == 0 and queue.groups() == []
 
 
+def test_copy_queue_flush_checks_its_buffers_before_any_device_work() -> None:
+    """CopyQueue.flush: an empty queue does nothing; a pinned buffer too small for the pairs is
+    reported as the bytes needed (the runner grows it and calls again); a missing device buffer
+    is refused. None of these reaches the device, so they run on any machine."""
+    bound = _native.bound_host()
+    queue = bound.CopyQueue(64)
+    assert queue.flush(0, 0, 0, 1, 16, np.zeros(0, np.uint8), 0, 0, 0) == (0, 0)
+    for source, destination in [(1, 2), (3, 4), (5, 6)]:
+        queue.push(source, destination)
+    assert queue.flush(0, 0, 0, 1, 16, np.zeros(47, np.uint8), 4096, 0, 0) == (0, -48)  # 16 bytes a pair
+    with pytest.raises(ValueError, match="device buffer"):
+        queue.flush(0, 0, 0, 1, 16, np.zeros(48, np.uint8), 0, 0, 0)
+    with pytest.raises(TypeError):  # the pinned buffer must be bytes
+        queue.flush(0, 0, 0, 1, 16, np.zeros(48, np.int32), 4096, 0, 0)
+    assert queue.items() == [(1, 2), (3, 4), (5, 6)]  # nothing was dequeued
+
+
 def test_copy_queue_groups_of_forks_are_one_group_and_bad_pairs_are_refused() -> None:
     queue = ext.CopyQueue(400)
     for i in range(256):  # every child copies the same shared block
