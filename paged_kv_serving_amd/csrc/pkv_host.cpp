@@ -52,7 +52,8 @@
 //       entry for that position. Otherwise some row reads a slot another row (or its own row,
 //       through a repeated table entry) writes in the same step, and only an append that
 //       completes before attention reads it as the reference does (runner.py:195-212). `marks`
-//       is an int32 buffer with one zero per pool block; it is left all zero.
+//       is a uint8 buffer with one zero per pool block (small enough to stay in the L1 cache for
+//       tens of thousands of blocks); it is left all zero.
 //   bind(plan_batch, paged_attention, paged_attention_append, copy_blocks, rms_norm, silu_mul,
 //        rope_append, memcpy_async[, gather_rows, greedy_tokens, get_device, set_device,
 //        event_create, event_record, event_synchronize, event_destroy, append])
@@ -644,7 +645,8 @@ PyObject* exclusive_writes(PyObject*, PyObject* args) {
   if (!PyArg_ParseTuple(args, "OOOLO|OL", &rows_o, &contexts_o, &host_o, &block_size, &marks_o, &tiles_o, &partition)) {
     return nullptr;
   }
-  Buf<int32_t> rows, contexts, host, marks, tiles;
+  Buf<int32_t> rows, contexts, host, tiles;
+  Buf<uint8_t> marks;
   if (!rows.get(rows_o, "rows", false) || !contexts.get(contexts_o, "contexts", false) ||
       !host.get(host_o, "host", false) || !marks.get(marks_o, "marks") ||
       (tiles_o != Py_None && !tiles.get(tiles_o, "tiles", false))) {
@@ -671,7 +673,7 @@ PyObject* exclusive_writes(PyObject*, PyObject* args) {
     }
   }
   const int64_t num_blocks = marks.size();
-  int32_t* mark = marks.data();
+  uint8_t* mark = marks.data();
   // The visible blocks of entry e, [0, ceil(context / B)), clamped to the row; -1 on a bad row.
   auto visible = [&](Py_ssize_t e, const int32_t** table) -> int64_t {
     const int32_t row = rows.data()[e];
@@ -714,6 +716,12 @@ PyObject* exclusive_writes(PyObject*, PyObject* args) {
     int64_t start = 0;
     if (prev_table != nullptr) {
       const int64_t limit = std::min(nb, prev_nb);
+      // The common prefix, 16 ids at a time (a vectorised compare), then id by id.
+      constexpr int64_t kChunk = 16;
+      while (start + kChunk <= limit &&
+             std::memcmp(table + start, prev_table + start, kChunk * sizeof(int32_t)) == 0) {
+        start += kChunk;
+      }
       while (start < limit && table[start] == prev_table[start]) ++start;
       if (prev_flagged < start) {
         ok = false;  // a written block in both tables

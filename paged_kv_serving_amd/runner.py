@@ -340,7 +340,7 @@ class ModelRunner:
         self._device_index = self.device.index
         self._stats = np.zeros(8, np.int64)
         self._kv_code = ops.kv_dtype_code(kv_dtype)
-        self._marks = np.zeros(num_blocks, np.int32)  # one per pool block, for exclusive_writes
+        self._marks = np.zeros(num_blocks, np.uint8)  # one per pool block, for exclusive_writes
         self._order = np.zeros(256, np.int64)  # a call's planner row order (prefix_order_rows)
         # Queued copy-on-write copies live in C++ (_pkvhost.CopyQueue); copy_block is its push,
         # so a scheduler's per-block calls cost no Python frame. Their pairs travel through a

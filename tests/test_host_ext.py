@@ -322,7 +322,7 @@ def exclusive(tables, contexts, block_size, num_blocks) -> bool:
     rows = np.random.default_rng(len(tables)).permutation(host.shape[0])[: len(tables)].astype(np.int32)
     for row, table in zip(rows, tables):
         host[row, : len(table)] = table
-    marks = np.zeros(num_blocks, np.int32)
+    marks = np.zeros(num_blocks, np.uint8)
     got = ext.exclusive_writes(rows, np.asarray(contexts, np.int32), host, block_size, marks)
     assert not marks.any(), "the marks buffer is left all zero"
     return got
@@ -357,7 +357,7 @@ def test_exclusive_writes_refuses_tiles_over_a_new_position() -> None:
     for i, t in enumerate(tables):
         host[i] = t
     contexts = np.asarray([70, 65, 80, 33], np.int32)  # own positions 69, 64, 79, 32
-    marks = np.zeros(64, np.int32)
+    marks = np.zeros(64, np.uint8)
 
     def fused(tiles, partition=32):
         return ext.exclusive_writes(rows, contexts, host, 16, marks, np.asarray(tiles, np.int32).reshape(-1, 4),
