@@ -1386,12 +1386,19 @@ __device__ __forceinline__ void tile_item_dma(const Params& a, uint32_t bid, int
 // row pass the host launches one workgroup per CU instead, so the tile pass holds one wave per
 // SIMD and leaves the rest of each CU to the memory-bound row pass. The register path at
 // head_dim 128 is held to 168 VGPRs (three waves per SIMD; it needs about 170 unconstrained,
-// which allows two); the other instantiations have no occupancy target.
+// which allows two); the other instantiations have no occupancy target. Its wavefronts run at
+// instruction-arbiter priority 1 (the row pass keeps 0): beside the row pass the tile items are
+// the ones that finish last, and the memory-bound row wavefronts lose little by yielding issue
+// slots (measured: the prefix-sharing step's call 0.2333-0.2369 -> 0.2311-0.2335 ms, the mixed
+// bfloat16 call 1.105-1.110 -> 1.102-1.107 ms; alone, where every wavefront is a tile's, it
+// changes nothing). The reverse, the row pass at priority 1, starves the tiles (the mixed
+// float32 call 1.48 -> 1.97 ms).
 template <typename KVT, int D, bool kPow2Block, bool kDma>
 __global__ __launch_bounds__(kTileThreads)
 __attribute__((amdgpu_waves_per_eu(!kDma && D == 128 ? PKV_TILE_REG_WAVES : 1)))
 void tile_partial_kernel(const Params a, uint32_t num_items) {
   using S = TileShape<D>;
+  __builtin_amdgcn_s_setprio(1);
   __shared__ int s_table[kTableSlots];
   __shared__ int s_vis[kTileRows];
   if constexpr (kDma) {

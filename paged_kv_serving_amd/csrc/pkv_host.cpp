@@ -95,6 +95,10 @@
 // the returned lists.
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
+#include <structmember.h>
+#if PY_VERSION_HEX < 0x030C0000
+#include <longintrepr.h>
+#endif
 
 #include <dlfcn.h>
 
@@ -144,16 +148,71 @@ PyObject* s_positions;
 PyObject* s_block_table;
 PyObject* s_logits_index;
 
+// One attribute of the batch entries, read for a whole walk over them. For a class that keeps
+// the attribute in a __slots__ slot (BatchEntry is a slotted frozen dataclass) and uses the
+// generic attribute lookup, the slot's member descriptor gives its offset in the object, and the
+// value is read there: what getattr returns for that class, without the descriptor call (about
+// a fifth of the time per read). Objects of any other class go through PyObject_GetAttr.
+class EntryField {
+ public:
+  explicit EntryField(PyObject* name) : name_(name) {}
+  // A new reference, or null with an exception set.
+  PyObject* get(PyObject* obj) {
+    PyTypeObject* type = Py_TYPE(obj);
+    if (type != type_) resolve(type);
+    if (offset_ >= 0) {
+      PyObject* value = *reinterpret_cast<PyObject**>(reinterpret_cast<char*>(obj) + offset_);
+      if (value != nullptr) {
+        Py_INCREF(value);
+        return value;
+      }
+    }
+    return PyObject_GetAttr(obj, name_);  // an unset slot raises AttributeError here
+  }
+
+ private:
+  void resolve(PyTypeObject* type) {
+    type_ = type;
+    offset_ = -1;
+    if (type->tp_getattro != PyObject_GenericGetAttr) return;
+    PyObject* descr = _PyType_Lookup(type, name_);  // borrowed
+    if (descr == nullptr || Py_TYPE(descr) != &PyMemberDescr_Type) return;
+    const PyMemberDef* member = reinterpret_cast<PyMemberDescrObject*>(descr)->d_member;
+    if (member->type == T_OBJECT_EX && (member->flags & READ_RESTRICTED) == 0) offset_ = member->offset;
+  }
+
+  PyObject* name_;
+  PyTypeObject* type_ = nullptr;
+  Py_ssize_t offset_ = -1;
+};
+
 // A sequence attribute as a fast sequence (a new reference), or null with an exception set.
-PyObject* fast_attr(PyObject* obj, PyObject* name) {
-  PyObject* value = PyObject_GetAttr(obj, name);
+PyObject* fast_attr(PyObject* obj, EntryField& field) {
+  PyObject* value = field.get(obj);
   if (value == nullptr) return nullptr;
   PyObject* fast = PySequence_Fast(value, "a batch entry field must be a sequence");
   Py_DECREF(value);
   return fast;
 }
 
-bool as_i64(PyObject* v, int64_t* out) {
+// An int's value. Exact ints of at most one digit (|v| < 2**30: every block id, slot and
+// position of a pool) are read from the object, in the layout of CPython before 3.12
+// (longintrepr.h); anything else goes through PyLong_AsLongLong, which raises for non-ints.
+inline bool as_i64(PyObject* v, int64_t* out) {
+#if PY_VERSION_HEX < 0x030C0000
+  if (PyLong_CheckExact(v)) {
+    const Py_ssize_t size = Py_SIZE(v);
+    if (size == 0) {
+      *out = 0;
+      return true;
+    }
+    if (size == 1 || size == -1) {
+      const int64_t digit = reinterpret_cast<PyLongObject*>(v)->ob_digit[0];
+      *out = size < 0 ? -digit : digit;
+      return true;
+    }
+  }
+#endif
   const long long x = PyLong_AsLongLong(v);
   if (x == -1 && PyErr_Occurred()) return false;
   *out = x;
@@ -187,6 +246,8 @@ PyObject* gather(PyObject*, PyObject* args) {
   PyObject* result = nullptr;
   std::vector<PyObject*> toks(count, nullptr), poss(count, nullptr);
   std::vector<int64_t> firsts;  // first block ids of single-token entries
+  EntryField token_ids(s_token_ids), positions_f(s_positions), block_table(s_block_table),
+      logits_index(s_logits_index);
   int64_t total = 0;
   if (!tokens.get(tokens_o, "tokens") || !positions.get(positions_o, "positions") ||
       !slots.get(slots_o, "slots") || !lengths.get(lengths_o, "lengths") ||
@@ -202,9 +263,9 @@ PyObject* gather(PyObject*, PyObject* args) {
     goto done;
   }
   for (Py_ssize_t e = 0; e < count; ++e) {
-    toks[e] = fast_attr(items[e], s_token_ids);
+    toks[e] = fast_attr(items[e], token_ids);
     if (toks[e] == nullptr) goto done;
-    poss[e] = fast_attr(items[e], s_positions);
+    poss[e] = fast_attr(items[e], positions_f);
     if (poss[e] == nullptr) goto done;
     total += PySequence_Fast_GET_SIZE(toks[e]);
   }
@@ -227,7 +288,7 @@ PyObject* gather(PyObject*, PyObject* args) {
       }
       PyObject** tok = PySequence_Fast_ITEMS(toks[e]);
       PyObject** pos = PySequence_Fast_ITEMS(poss[e]);
-      PyObject* table = fast_attr(entry, s_block_table);
+      PyObject* table = fast_attr(entry, block_table);
       if (table == nullptr) goto done;
       const Py_ssize_t width = PySequence_Fast_GET_SIZE(table);
       PyObject** blocks = PySequence_Fast_ITEMS(table);
@@ -279,7 +340,7 @@ PyObject* gather(PyObject*, PyObject* args) {
       if (n > 0) last = positions.data()[at + n - 1];
       contexts.data()[e] = static_cast<int32_t>(last + 1);
       lo_ctx = std::min<int64_t>(lo_ctx, static_cast<int32_t>(last + 1));
-      PyObject* index = PyObject_GetAttr(entry, s_logits_index);
+      PyObject* index = logits_index.get(entry);
       if (index == nullptr) goto done;
       int64_t li = -1;
       if (index != Py_None && !as_i64(index, &li)) {
@@ -448,6 +509,7 @@ PyObject* arena_update(PyObject*, PyObject* args) {
   Buf<int64_t> last, index;
   PyObject* result = nullptr;
   std::vector<PyObject*> tables(count, nullptr);
+  EntryField block_table(s_block_table), seq_ids(s_seq_id);
   Py_ssize_t num_rows = 0, width = 0, longest = 0;
   if (!held.get(held_o, "held_len") || !last.get(last_o, "last_use") || !host.get(host_o, "host") ||
       !rows.get(rows_o, "rows") || !index.get(index_o, "index") || !values.get(values_o, "values")) {
@@ -461,7 +523,7 @@ PyObject* arena_update(PyObject*, PyObject* args) {
     goto done;
   }
   for (Py_ssize_t e = 0; e < count; ++e) {
-    tables[e] = fast_attr(items[e], s_block_table);
+    tables[e] = fast_attr(items[e], block_table);
     if (tables[e] == nullptr) goto done;
     longest = std::max(longest, PySequence_Fast_GET_SIZE(tables[e]));
   }
@@ -485,7 +547,7 @@ PyObject* arena_update(PyObject*, PyObject* args) {
     PyObject* seen = nullptr;  // seq id -> occurrences so far, built once a sequence repeats
     bool ok = true;
     for (Py_ssize_t e = 0; e < count && ok; ++e) {
-      PyObject* seq_id = PyObject_GetAttr(items[e], s_seq_id);
+      PyObject* seq_id = seq_ids.get(items[e]);
       if (seq_id == nullptr) {
         ok = false;
         break;
@@ -503,7 +565,7 @@ PyObject* arena_update(PyObject*, PyObject* args) {
         if (seen == nullptr) {  // count the occurrences of every sequence before this entry
           seen = PyDict_New();
           for (Py_ssize_t f = 0; f < e && seen != nullptr; ++f) {
-            PyObject* id = PyObject_GetAttr(items[f], s_seq_id);
+            PyObject* id = seq_ids.get(items[f]);
             PyObject* prior = id == nullptr ? nullptr : PyDict_GetItemWithError(seen, id);
             PyObject* next = id == nullptr || (prior == nullptr && PyErr_Occurred())
                                  ? nullptr
@@ -576,20 +638,20 @@ PyObject* arena_update(PyObject*, PyObject* args) {
       const Py_ssize_t n = PySequence_Fast_GET_SIZE(tables[e]);
       PyObject** blocks = PySequence_Fast_ITEMS(tables[e]);
       const bool is_tuple = PyTuple_CheckExact(tables[e]);
-      PyObject* before = PyList_GET_ITEM(held_obj, row);
-      if (is_tuple && before != Py_None && heldp[row] == n) {
-        const int same = PyObject_RichCompareBool(tables[e], before, Py_EQ);
-        if (same < 0) {
-          ok = false;
-          break;
-        }
-        if (same == 1) continue;  // the row already holds this table
-      }
+      PyObject* before = PyList_GET_ITEM(held_obj, row);  // None or the tuple the mirror holds
+      if (before == tables[e] && heldp[row] == n) continue;  // the row already holds this tuple
       int32_t* mirror = hostp + row * width;
       const Py_ssize_t old = heldp[row];
+      // The ids against the row's mirror. An id that is the very object the held tuple has at
+      // that index needs no conversion: the mirror holds that object's value (a scheduler that
+      // builds each step's tuples from the same lists of ids passes the same int objects; a
+      // comparison of the two tuples would convert every id that is not, both sides).
+      PyObject** held_ids = before != Py_None ? PySequence_Fast_ITEMS(before) : nullptr;
+      const Py_ssize_t held_n = held_ids != nullptr ? std::min(old, PyTuple_GET_SIZE(before)) : 0;
       Py_ssize_t start = 0;
       const Py_ssize_t common = std::min(old, n);
       for (; start < common; ++start) {
+        if (start < held_n && held_ids[start] == blocks[start]) continue;
         int64_t b;
         if (!as_i64(blocks[start], &b)) {
           ok = false;

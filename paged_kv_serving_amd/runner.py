@@ -43,9 +43,10 @@ __all__ = ["DEFAULT_TILE_BLOCKS", "BatchEntry", "ExecutionBatch", "ModelRunner",
 DEFAULT_TILE_BLOCKS = 8
 
 
-@dataclass(frozen=True)
+@dataclass(frozen=True, slots=True)
 class BatchEntry:
-    """One sequence's slice of an iteration (runner.py:33-68)."""
+    """One sequence's slice of an iteration (runner.py:33-68). Its fields live in __slots__, which
+    the host extension reads at their offsets when it walks a batch."""
 
     seq_id: str
     token_ids: tuple[int, ...]
@@ -178,7 +179,11 @@ class _Staging:
 
     def __del__(self) -> None:
         if self._event:
-            self._ext.event_destroy(self._event)
+            # At interpreter exit the extension module's globals may already be cleared (None);
+            # the process's end releases the event then.
+            destroy = getattr(self._ext, "event_destroy", None)
+            if callable(destroy):
+                destroy(self._event)
             self._event = 0
 
     @property

@@ -70,6 +70,71 @@ def test_gather_reports_the_first_slot_problem() -> None:
     assert problem == (2, 0, -40)
 
 
+def test_gather_reads_entries_of_any_class_as_getattr_does() -> None:
+    """BatchEntry keeps its fields in __slots__, which gather reads at their offsets; objects of
+    other classes (a plain dataclass, a namespace) and a subclass that overrides a field with a
+    property go through getattr, so each gives what its attributes say."""
+    from dataclasses import dataclass
+    from types import SimpleNamespace
+
+    @dataclass(frozen=True)
+    class PlainEntry:
+        seq_id: str
+        token_ids: tuple
+        positions: tuple
+        block_table: tuple
+        logits_index: int | None = None
+
+    class Remapped(BatchEntry):
+        @property
+        def block_table(self):  # shadows the slot of the same name, which keeps the given table
+            return (99, 98, 97)
+
+        @block_table.setter
+        def block_table(self, value):
+            BatchEntry.block_table.__set__(self, value)
+
+    assert not hasattr(BatchEntry("a", (1,), (3,), (7,)), "__dict__")
+    fields = [("a", (1, 2), (3, 4), (7,), 1), ("b", (5,), (20,), (4, 6), None), ("c", (2,), (0,), (11,), 0)]
+    plain = tuple(BatchEntry(*f) for f in fields)
+    expected = gather(plain, 16)
+    for kind in (lambda *f: PlainEntry(*f), lambda *f: SimpleNamespace(
+            seq_id=f[0], token_ids=f[1], positions=f[2], block_table=f[3], logits_index=f[4])):  # fmt: skip
+        got = gather(tuple(kind(*f) for f in fields), 16)
+        for a, b in zip(got[:6], expected[:6]):
+            assert a.tolist() == b.tolist()
+        assert got[6] == expected[6]
+    mixed = (plain[0], Remapped(*fields[1]), plain[2])  # classes change along the walk
+    *_, problem = gather(mixed, 16)
+    assert problem == (0, 0, 0)
+    slots = gather(mixed, 16)[2]
+    assert slots.tolist() == compute_slots(mixed, 16).tolist()
+    assert slots[2] == 98 * 16 + 4  # position 20 of the property's table
+
+
+def test_gather_converts_ints_of_every_size_and_kind() -> None:
+    """Small exact ints are read from the object; zero, negatives, ints past one 30-bit digit,
+    bools and NumPy integers take the general conversion and give the same values."""
+    big = 1 << 40
+    entries = (
+        BatchEntry("a", (0, True, np.int64(7)), (0, 1, 2), (3,)),
+        BatchEntry("b", (big,), (-1,), (5, 6)),  # negative: from the end of the table
+        BatchEntry("c", ((1 << 30) + 3,), ((1 << 30) + 5,), (1, 2, 9)),  # block (2**30 + 5) // 2**29 = 2
+        BatchEntry("d", (2,), (np.int32(17),), (4, big)),
+    )
+    tokens = gather(entries[:1], 16)[0]
+    assert tokens.tolist() == [0, 1, 7]
+    tokens, positions, slots, *_ = gather(entries[1:2], 16)
+    assert tokens.tolist() == [big] and positions.tolist() == [-1] and slots.tolist() == [6 * 16 + 15]
+    tokens, positions, slots, *_ = gather(entries[2:3], 1 << 29)
+    assert positions.tolist() == [(1 << 30) + 5]
+    assert slots.tolist() == [9 * (1 << 29) + 5]
+    slots = gather(entries[3:], 16)[2]
+    assert slots.tolist() == [big * 16 + 1]
+    with pytest.raises(TypeError):
+        gather((BatchEntry("e", (1,), (2.0,), (3,)),), 16)
+
+
 def _prefix_case(rng, block):
     stems = [tuple(int(b) for b in rng.integers(0, 1000, 40)) for _ in range(3)]
     entries = []

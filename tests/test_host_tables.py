@@ -159,6 +159,21 @@ def test_same_tuple_again_sends_nothing_and_an_equal_length_change_travels() -> 
     assert changed.values.tolist() == [9, 5]
 
 
+def test_rebuilt_tuples_of_the_same_ids_send_nothing_and_new_id_objects_compare_by_value() -> None:
+    """A scheduler rebuilds each step's tuples from its lists of ids: the same int objects are
+    equal without conversion; equal ids held by new int objects compare by value; a changed id
+    travels whether or not the other ids are the objects the row holds."""
+    arena = BlockTableArena("cpu", rows=2, width=6)
+    ids = [1000 + i for i in range(5)]  # past the small-int cache: each value is its own object
+    step(arena, [Entry("a", tuple(ids))])
+    assert step(arena, [Entry("a", tuple(ids))]).index.size == 0
+    assert step(arena, [Entry("a", tuple(int(str(b)) for b in ids))]).index.size == 0
+    ids[3] = 7777
+    assert step(arena, [Entry("a", tuple(ids))]).values.tolist() == [7777, 1004]
+    ids.append(8888)
+    assert step(arena, [Entry("a", tuple(int(str(b)) for b in ids))]).values.tolist() == [8888]
+
+
 def test_a_list_changed_in_place_is_compared_by_value() -> None:
     @dataclass
     class ListEntry:
