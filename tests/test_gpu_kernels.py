@@ -469,13 +469,15 @@ def test_fused_decode_append_equals_append_then_attention(device, kinds, block, 
         assert np.max(np.abs(got.cpu().numpy() - dense)) < FP32_TOL, partition
 
 
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
 @pytest.mark.parametrize("heads", [4, 32], ids=["alone", "overlapped"])
-def test_fused_append_beside_shared_prefix_tiles(device, heads) -> None:
+def test_fused_append_beside_shared_prefix_tiles(device, heads, kv) -> None:
     """A decode batch whose sequences share a prefix: the plan reads the prefix as MFMA tiles and
     the fused append writes each row's new key and value (into its private last block) from the
-    row pass, beside the tile pass (at 32 heads on the second stream). Pools bit for bit as after
-    pkv_append; outputs within 1e-6 of append-then-attention and 1e-5 of the oracle."""
-    say("fused append beside prefix tiles", heads)
+    row pass, beside the tile pass (at 32 heads on the second stream). float32 new rows into
+    float32 or bfloat16 pools (rounded to nearest even). Pools bit for bit as after pkv_append;
+    outputs within 1e-6 of append-then-attention and 1e-5 of the oracle over the pools' values."""
+    say("fused append beside prefix tiles", heads, kv)
     rng = np.random.default_rng(heads)
     dim, block, seqs = 128, 16, 64
     prefix = 40  # blocks: 640 shared tokens
@@ -498,21 +500,22 @@ def test_fused_append_beside_shared_prefix_tiles(device, heads) -> None:
     vc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
     q, new_k, new_v = (rng.standard_normal((seqs, heads, dim)).astype(np.float32) for _ in range(3))
     seq_of = np.arange(seqs)
-    plan = ops.plan_batch(seq_of, dim, heads, tables, contexts, block, query_positions=positions)
+    kv_dtype = torch.float32 if kv == "f32" else torch.bfloat16
+    plan = ops.plan_batch(seq_of, dim, heads, tables, contexts, block, query_positions=positions, kv_dtype=kv_dtype)
     assert plan.tiles.shape[0] >= 1, "prefix tiles"
     to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
     args = (to(q), to(positions.astype(np.int32)), to(seq_of.astype(np.int32)))
     meta = (to(padded), to(contexts.astype(np.int32)), dim**-0.5)
     dplan = ops.upload_batch_plan(plan, device)
-    k_sep, v_sep = to(kc), to(vc)
+    k_sep, v_sep = to(kc).to(kv_dtype), to(vc).to(kv_dtype)
     ops.append_kv(k_sep, v_sep, to(new_k), to(new_v), to(slots))
     want = ops.paged_attention_ragged(*args, k_sep, v_sep, *meta, max_context_len=int(contexts.max()), plan=dplan)
-    k_fus, v_fus = to(kc), to(vc)
+    k_fus, v_fus = to(kc).to(kv_dtype), to(vc).to(kv_dtype)
     got = ops.paged_attention_ragged(*args, k_fus, v_fus, *meta, max_context_len=int(contexts.max()), plan=dplan,
                                      append=(to(new_k), to(new_v), to(slots)))  # fmt: skip
     assert torch.equal(k_fus, k_sep) and torch.equal(v_fus, v_sep)
     assert float((got - want).abs().max()) < 1e-6
-    kh, vh = k_sep.cpu().numpy(), v_sep.cpu().numpy()
+    kh, vh = k_sep.float().cpu().numpy(), v_sep.float().cpu().numpy()
     oracle, dense = _oracle(kh, vh, tables, contexts, positions, seq_of, q, dim**-0.5)
     assert np.max(np.abs(got.cpu().numpy() - oracle)) < FP32_TOL
     assert np.max(np.abs(got.cpu().numpy() - dense)) < FP32_TOL
