@@ -643,13 +643,20 @@ PyObject* arena_update(PyObject*, PyObject* args) {
       int32_t* mirror = hostp + row * width;
       const Py_ssize_t old = heldp[row];
       // The ids against the row's mirror. An id that is the very object the held tuple has at
-      // that index needs no conversion: the mirror holds that object's value (a scheduler that
-      // builds each step's tuples from the same lists of ids passes the same int objects; a
-      // comparison of the two tuples would convert every id that is not, both sides).
+      // that index needs no conversion: the mirror holds that object's value (the reference's
+      // scheduler builds each step's tuples from its sequences' lists of ids, so the objects
+      // repeat; a comparison of the two tuples would convert every id that is not, both sides).
+      // Runs of identical objects are found by comparing the pointer arrays 16 at a time.
       PyObject** held_ids = before != Py_None ? PySequence_Fast_ITEMS(before) : nullptr;
       const Py_ssize_t held_n = held_ids != nullptr ? std::min(old, PyTuple_GET_SIZE(before)) : 0;
       Py_ssize_t start = 0;
       const Py_ssize_t common = std::min(old, n);
+      constexpr Py_ssize_t kRun = 16;
+      const Py_ssize_t same_limit = std::min(held_n, common);
+      while (start + kRun <= same_limit &&
+             std::memcmp(held_ids + start, blocks + start, kRun * sizeof(PyObject*)) == 0) {
+        start += kRun;
+      }
       for (; start < common; ++start) {
         if (start < held_n && held_ids[start] == blocks[start]) continue;
         int64_t b;

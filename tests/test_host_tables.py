@@ -172,6 +172,15 @@ def test_rebuilt_tuples_of_the_same_ids_send_nothing_and_new_id_objects_compare_
     assert step(arena, [Entry("a", tuple(ids))]).values.tolist() == [7777, 1004]
     ids.append(8888)
     assert step(arena, [Entry("a", tuple(int(str(b)) for b in ids))]).values.tolist() == [8888]
+    # Longer tables: identical objects are compared 16 pointers at a time, then one by one.
+    arena = BlockTableArena("cpu", rows=2, width=64)
+    ids = [2000 + i for i in range(40)]
+    step(arena, [Entry("b", tuple(ids))])
+    assert step(arena, [Entry("b", tuple(ids))]).index.size == 0
+    for at in (20, 35, 0, 15, 16, 39):
+        ids[at] = 9000 + at
+        moved = step(arena, [Entry("b", tuple(ids))])
+        assert moved.values.tolist() == ids[at:], at
 
 
 def test_a_list_changed_in_place_is_compared_by_value() -> None:
