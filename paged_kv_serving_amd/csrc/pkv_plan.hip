@@ -382,27 +382,57 @@ extern "C" int pkv_plan_batch(const int32_t* query_seq, const int32_t* query_pos
     // first such pair is found through a per-sequence slot, any further one (a sequence whose
     // rows start at different partitions) through a sorted list.
     std::vector<int64_t> first_of(num_seqs, -1);
-    std::vector<std::pair<int32_t, int64_t>> more;
-    std::vector<int32_t> ids;
-    auto read_from = [&](int32_t s, int64_t first) {
-      for (int64_t c = first; c < used[s]; ++c) ids.push_back(tables.base[static_cast<int64_t>(s) * tables.stride + c]);
-    };
+    std::vector<std::pair<int32_t, int64_t>> segments, more;  // (sequence, first column) read
     for (size_t i = 0; i < row_pass.size(); ++i) {
       const int32_t s = seq[row_pass[i]];
       const int64_t first = static_cast<int64_t>(row_first[i]) * partition / block_size;
       if (first_of[s] < 0) {
         first_of[s] = first;
-        read_from(s, first);
+        segments.emplace_back(s, first);
       } else if (first_of[s] != first) {
         more.emplace_back(s, first);
       }
     }
     std::sort(more.begin(), more.end());
     more.erase(std::unique(more.begin(), more.end()), more.end());
-    for (const auto& [s, first] : more) read_from(s, first);
-    if (!ids.empty()) {
-      const int64_t n = static_cast<int64_t>(ids.size());
-      shared_kv = static_cast<double>(n - distinct_count(ids)) >= kSharedKvFraction * static_cast<double>(n);
+    segments.insert(segments.end(), more.begin(), more.end());
+    // The ids are counted where they lie in the tables: their number and range first, then one
+    // bit per id of the range (distinct_count's rule, without gathering them).
+    int64_t n = 0;
+    int32_t low = INT32_MAX, high = INT32_MIN;
+    for (const auto& [s, first] : segments) {
+      const int32_t* row = tables.base + static_cast<int64_t>(s) * tables.stride;
+      for (int64_t c = first; c < used[s]; ++c) {
+        low = std::min(low, row[c]);
+        high = std::max(high, row[c]);
+      }
+      n += std::max<int64_t>(used[s] - first, 0);
+    }
+    if (n > 0) {
+      const int64_t range = static_cast<int64_t>(high) - low + 1;
+      int64_t distinct = 0;
+      if (range <= 64 * std::max<int64_t>(4096, 16 * n)) {
+        std::vector<uint64_t> seen((range + 63) / 64, 0);
+        for (const auto& [s, first] : segments) {
+          const int32_t* row = tables.base + static_cast<int64_t>(s) * tables.stride;
+          for (int64_t c = first; c < used[s]; ++c) {
+            const int64_t bit = static_cast<int64_t>(row[c]) - low;
+            uint64_t& word = seen[bit >> 6];
+            const uint64_t mask = uint64_t{1} << (bit & 63);
+            distinct += (word & mask) == 0;
+            word |= mask;
+          }
+        }
+      } else {
+        std::vector<int32_t> ids;
+        ids.reserve(static_cast<size_t>(n));
+        for (const auto& [s, first] : segments) {
+          const int32_t* row = tables.base + static_cast<int64_t>(s) * tables.stride;
+          ids.insert(ids.end(), row + first, row + std::max<int64_t>(used[s], first));
+        }
+        distinct = distinct_count(ids);
+      }
+      shared_kv = static_cast<double>(n - distinct) >= kSharedKvFraction * static_cast<double>(n);
     }
   }
 
