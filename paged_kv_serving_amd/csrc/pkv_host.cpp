@@ -14,10 +14,11 @@
 //       token ids and positions first, in the reference's order: problem 1 = a position past
 //       the table (the reference's ValueError), 2 = a negative index before its start
 //       (IndexError). Returns total = -(tokens needed), writing nothing, when the token buffers
-//       are too small. The optional int64 `stats` buffer (>= 8 entries) receives what the
-//       caller validates, so it needs no pass of its own: [min token, max token, min position,
-//       max position, min slot, max slot, min context, 1 if two single-token entries' tables
-//       start with the same block id else 0] (slots of unformed positions count as -1).
+//       are too small. The optional int64 `stats` buffer (>= 9 entries) receives what the
+//       caller validates and sizes, so it needs no pass of its own: [min token, max token, min
+//       position, max position, min slot, max slot, min context, 1 if two single-token entries'
+//       tables start with the same block id else 0, max context] (slots of unformed positions
+//       count as -1).
 //   prefix_order_rows(rows, lengths, host, held_len, lead, min_rows, out) -> bool
 //       The row order that puts decode entries sharing their first `lead` blocks next to each
 //       other (runner.shared_prefix_order), written to the int64 buffer `out` (>= one entry per
@@ -33,7 +34,8 @@
 //       changing anything, when the batch needs more rows or a wider table than it has.
 //       held_obj keeps, per row, the tuple it was last filled from: a scheduler rebuilds each
 //       table tuple from the same int objects every step, so an unchanged table compares equal
-//       by identity, element by element, without converting a single id.
+//       by identity (its pointer array against the held one's, 16 at a time) without converting
+//       a single id; ids that are other objects are converted and compared with the mirror.
 //   CopyQueue(num_blocks)
 //       A runner's queued copy-on-write copies. push(src, dst) checks and queues one copy (the
 //       runner's copy_block); groups() gives the sizes of the consecutive groups that may each
@@ -254,8 +256,8 @@ PyObject* gather(PyObject*, PyObject* args) {
       !contexts.get(contexts_o, "contexts") || !logits.get(logits_o, "logits")) {
     goto done;
   }
-  if (stats_o != Py_None && (!stats.get(stats_o, "stats") || stats.size() < 8)) {
-    if (!PyErr_Occurred()) PyErr_SetString(PyExc_ValueError, "stats must hold 8 entries");
+  if (stats_o != Py_None && (!stats.get(stats_o, "stats") || stats.size() < 9)) {
+    if (!PyErr_Occurred()) PyErr_SetString(PyExc_ValueError, "stats must hold 9 entries");
     goto done;
   }
   if (lengths.size() < count || contexts.size() < count || logits.size() < count) {
@@ -278,7 +280,7 @@ PyObject* gather(PyObject*, PyObject* args) {
     int problem = 0;
     long long bad_entry = 0, bad_position = 0;
     int64_t lo_tok = INT64_MAX, hi_tok = INT64_MIN, lo_pos = INT64_MAX, hi_pos = INT64_MIN;
-    int64_t lo_slot = INT64_MAX, hi_slot = INT64_MIN, lo_ctx = INT64_MAX;
+    int64_t lo_slot = INT64_MAX, hi_slot = INT64_MIN, lo_ctx = INT64_MAX, hi_ctx = INT64_MIN;
     for (Py_ssize_t e = 0; e < count; ++e) {
       PyObject* entry = items[e];
       const Py_ssize_t n = PySequence_Fast_GET_SIZE(toks[e]);
@@ -340,6 +342,7 @@ PyObject* gather(PyObject*, PyObject* args) {
       if (n > 0) last = positions.data()[at + n - 1];
       contexts.data()[e] = static_cast<int32_t>(last + 1);
       lo_ctx = std::min<int64_t>(lo_ctx, static_cast<int32_t>(last + 1));
+      hi_ctx = std::max<int64_t>(hi_ctx, static_cast<int32_t>(last + 1));
       PyObject* index = logits_index.get(entry);
       if (index == nullptr) goto done;
       int64_t li = -1;
@@ -354,7 +357,7 @@ PyObject* gather(PyObject*, PyObject* args) {
     if (stats_o != Py_None) {
       std::sort(firsts.begin(), firsts.end());
       const bool repeat = std::adjacent_find(firsts.begin(), firsts.end()) != firsts.end();
-      const int64_t values[8] = {lo_tok, hi_tok, lo_pos, hi_pos, lo_slot, hi_slot, lo_ctx, repeat ? 1 : 0};
+      const int64_t values[9] = {lo_tok, hi_tok, lo_pos, hi_pos, lo_slot, hi_slot, lo_ctx, repeat ? 1 : 0, hi_ctx};
       std::memcpy(stats.data(), values, sizeof(values));
     }
     result = Py_BuildValue("(LiLL)", static_cast<long long>(total), problem, bad_entry, bad_position);

@@ -43,6 +43,9 @@ __all__ = ["DEFAULT_TILE_BLOCKS", "BatchEntry", "ExecutionBatch", "ModelRunner",
 DEFAULT_TILE_BLOCKS = 8
 
 
+_NO_ROWS = np.zeros(0, dtype=np.int64)  # no logits rows (read only)
+_NO_ROWS.flags.writeable = False
+
 @dataclass(frozen=True, slots=True)
 class BatchEntry:
     """One sequence's slice of an iteration (runner.py:33-68). Its fields live in __slots__, which
@@ -343,7 +346,8 @@ class ModelRunner:
         self._host = _native.bound_host()
         self._staging = _Staging(self.device, self._host)
         self._device_index = self.device.index
-        self._stats = np.zeros(8, np.int64)
+        self._stats = np.zeros(9, np.int64)
+        self._contexts_by_row = np.zeros(0, np.int32)  # a call's context lengths by arena row
         self._kv_code = ops.kv_dtype_code(kv_dtype)
         self._marks = np.zeros(num_blocks, np.uint8)  # one per pool block, for exclusive_writes
         self._order = np.zeros(256, np.int64)  # a call's planner row order (prefix_order_rows)
@@ -512,10 +516,11 @@ class ModelRunner:
         return (tokens[:total], positions[:total], slots[:total], lengths[:count], contexts[:count],
                 logits[:count], (problem, entry, position))  # fmt: skip
 
-    def _prepare(self, batch: ExecutionBatch) -> _Step | None:
+    def _prepare(self, batch: ExecutionBatch, *, logits: bool = True) -> _Step | None:
         """Everything one iteration needs on the device before its first kernel: validation in
         the reference's order and with its messages, slots, the block-table arena update, the
-        attention plan, and one asynchronous copy of all of it (None for an empty batch)."""
+        attention plan, and one asynchronous copy of all of it (None for an empty batch). Without
+        ``logits`` (attend, which computes none) no logits rows are listed."""
         entries = batch.entries
         if not entries:
             return None
@@ -526,7 +531,7 @@ class ModelRunner:
         config = self.model.config
         tokens, positions, slots, lengths, context, logits_rows, (problem, bad, position) = self._gather(entries)
         total = tokens.size
-        low_token, high_token, low_pos, high_pos, low_slot, high_slot, low_ctx, repeats = self._stats.tolist()
+        low_token, high_token, low_pos, high_pos, low_slot, high_slot, low_ctx, repeats, high_ctx = self._stats.tolist()
         # The reference checks token ids, then positions, then forms the slots (runner.py:174-187).
         if low_token < 0 or high_token >= config.vocab_size:
             raise ValueError("token id outside the vocabulary")
@@ -551,7 +556,7 @@ class ModelRunner:
                 raise ValueError("context_len must be >= 1")
             rope_positions = np.where(positions < 0, positions + config.max_seq_len, positions)
         # Logits rows, in batch order of the entries that ask for them.
-        wanted = logits_rows[logits_rows >= 0]
+        wanted = logits_rows[logits_rows >= 0] if logits else _NO_ROWS
         # Block tables live in a device arena between calls; only changed entries travel.
         update = self._tables.update(entries)
         rows = update.rows
@@ -582,7 +587,11 @@ class ModelRunner:
             planner_row[token_order] = np.arange(total)
             wanted = planner_row[wanted]
             rows, lengths, context = rows[order], lengths[order], context[order]
-        contexts_by_row = np.zeros(self._tables.num_rows, dtype=np.int32)
+        # Context lengths by arena row; only the batch's rows are read (by the planner and the
+        # kernels), so the buffer is kept between calls and only those rows are written.
+        if self._contexts_by_row.size != self._tables.num_rows:
+            self._contexts_by_row = np.zeros(self._tables.num_rows, dtype=np.int32)
+        contexts_by_row = self._contexts_by_row
         contexts_by_row[rows] = context
         query_seq = rows if total == len(entries) else np.repeat(rows, lengths)
         query_pos = positions.astype(np.int32)
@@ -622,7 +631,7 @@ class ModelRunner:
             logits_at=logits_at, qpos_at=qpos_at, qseq_at=qseq_at, contexts_at=context_at, plan_rows_at=rows_at,
             plan_tiles_at=tiles_at, merge_at=merge_at, num_plan_rows=plan_rows.shape[0],
             num_tiles=plan_tiles.shape[0], num_merge=merge.size, num_wanted=wanted.size, partition=partition,
-            flags=flags, max_context=int(context.max()), token_order=token_order, caller_rows_at=caller_rows_at,
+            flags=flags, max_context=high_ctx, token_order=token_order, caller_rows_at=caller_rows_at,
             batch_slots_at=batch_slots_at, entries=entries, decode_only=decode_only,
         )  # fmt: skip
 
@@ -688,16 +697,16 @@ class ModelRunner:
         config = self.model.config
         if not 0 <= layer < config.n_layers:
             raise IndexError(f"layer {layer} is outside the model's {config.n_layers} layers")
-        step = self._prepare(batch)
+        step = self._prepare(batch, logits=False)
         total = 0 if step is None else step.total
         shape = (total, config.n_heads, config.head_dim)
         if out is None:
             out = torch.empty(shape, dtype=torch.float32, device=self.device)
         if step is None:
             return out
-        device = self.device
+        index = self._device_index
         for name, tensor in (("queries", queries), ("keys", keys), ("values", values), ("out", out)):
-            if tensor.shape != shape or tensor.dtype != torch.float32 or tensor.device != device:
+            if tensor.dtype is not torch.float32 or tensor.shape != shape or tensor.get_device() != index:
                 raise ValueError(f"{name} must be float32 {list(shape)} on the runner's device")
         if not out.is_contiguous():
             raise ValueError("out must be contiguous")

@@ -183,23 +183,25 @@ def test_gather_statistics_are_the_reductions_the_runner_validates(seed) -> None
     total = sum(len(e.token_ids) for e in entries)
     tokens, positions, slots = (np.zeros(total, np.int64) for _ in range(3))
     lengths, contexts, logits = np.zeros(count, np.int64), np.zeros(count, np.int32), np.zeros(count, np.int64)
-    stats = np.zeros(8, np.int64)
+    stats = np.zeros(9, np.int64)
     got = ext.gather(entries, block, tokens, positions, slots, lengths, contexts, logits, stats)
     assert got[0] == total
     decode_firsts = [e.block_table[0] for e in entries if len(e.token_ids) == 1]
     want = [tokens.min(), tokens.max(), positions.min(), positions.max(), slots.min(), slots.max(), contexts.min(),
-            int(len(set(decode_firsts)) < len(decode_firsts))]  # fmt: skip
+            int(len(set(decode_firsts)) < len(decode_firsts)), contexts.max()]  # fmt: skip
     assert stats.tolist() == [int(v) for v in want]
     assert stats[7] == (1 if seed % 4 == 1 else stats[7])
 
 
 def test_gather_statistics_count_unformed_slots_as_minus_one() -> None:
     entries = (BatchEntry("a", (3,), (5,), (7,)), BatchEntry("b", (4,), (40,), (1,)))
-    stats = np.zeros(8, np.int64)
+    stats = np.zeros(9, np.int64)
     buffers = [np.zeros(2, np.int64) for _ in range(3)] + [np.zeros(2, np.int64), np.zeros(2, np.int32), np.zeros(2, np.int64)]
     total, problem, entry, position = ext.gather(entries, 16, *buffers, stats)
     assert (total, problem, entry, position) == (2, 1, 1, 40)
-    assert stats.tolist() == [3, 4, 5, 40, -1, 7 * 16 + 5, 6, 0]
+    assert stats.tolist() == [3, 4, 5, 40, -1, 7 * 16 + 5, 6, 0, 41]
+    with pytest.raises(ValueError, match="stats must hold 9 entries"):
+        ext.gather(entries, 16, *buffers, np.zeros(8, np.int64))
 
 
 def _python_groups(pairs):
