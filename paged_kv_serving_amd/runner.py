@@ -46,10 +46,11 @@ DEFAULT_TILE_BLOCKS = 8
 _NO_ROWS = np.zeros(0, dtype=np.int64)  # no logits rows (read only)
 _NO_ROWS.flags.writeable = False
 
+
 @dataclass(frozen=True, slots=True)
 class BatchEntry:
-    """One sequence's slice of an iteration (runner.py:33-68). Its fields live in __slots__, which
-    the host extension reads at their offsets when it walks a batch."""
+    """One sequence's slice of an iteration (runner.py:33-68), slotted as the reference's is. The
+    host extension reads the fields at their slots' offsets when it walks a batch."""
 
     seq_id: str
     token_ids: tuple[int, ...]
@@ -78,7 +79,7 @@ class BatchEntry:
         return self.positions[-1] + 1
 
 
-@dataclass(frozen=True)
+@dataclass(frozen=True, slots=True)
 class ExecutionBatch:
     """The slices scheduled for one iteration (runner.py:71-87)."""
 
