@@ -106,4 +106,3 @@ def test_batched_copy_groups_equal_copies_in_order(pairs) -> None:
         for dst, value in zip(dsts, reads):
             batched[dst] = value
     assert batched == sequential
-
