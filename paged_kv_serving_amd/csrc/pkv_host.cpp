@@ -386,9 +386,10 @@ uint64_t hash_ids(const int32_t* ids, long long n) {
 
 // The row order of prefix_order from the decode entries' positions in the batch (decode, in
 // batch order) and their `lead` leading block ids (keys[k] points at entry k's), written to
-// out[count]; false when nothing would move. Equal keys are found through a hash of each key
-// confirmed by comparing the ids, so each entry's key is read about twice whatever the number of
-// sharers; only the distinct keys are sorted.
+// out[count]; false when nothing would move. An entry whose key equals the previous entry's
+// (sharers are usually adjacent) takes its id from one comparison; other keys are found through
+// a hash of the key confirmed by comparing the ids, so each entry's key is read about twice
+// whatever the number of sharers; only the distinct keys are sorted.
 bool order_decode_entries(const std::vector<Py_ssize_t>& decode, const std::vector<const int32_t*>& keys,
                           long long lead, long long min_rows, Py_ssize_t count, int64_t* out) {
   const Py_ssize_t nd = static_cast<Py_ssize_t>(decode.size());
@@ -402,6 +403,10 @@ bool order_decode_entries(const std::vector<Py_ssize_t>& decode, const std::vect
   std::vector<int32_t> id(nd), first_of;  // entry -> key id; key id -> its first entry
   for (Py_ssize_t k = 0; k < nd; ++k) {
     const int32_t* kk = key(k);
+    if (k > 0 && std::memcmp(kk, key(k - 1), key_bytes) == 0) {  // the previous entry's key
+      id[k] = id[k - 1];
+      continue;
+    }
     size_t at = static_cast<size_t>(hash_ids(kk, lead)) & (slots - 1);
     while (true) {
       const int32_t e = table[at];
