@@ -103,3 +103,85 @@ def test_random_batch_through_the_planner_matches_the_oracle(device, seed) -> No
     ).cpu().numpy()  # fmt: skip
     err = float(np.max(np.abs(got - want)))
     assert err < FP32_TOL, (seed, err, host.tiles.shape[0], host.partition_size, host.dominant_tiles)
+
+
+FUSED_CASES = int(os.environ.get("PKV_RANDOM_FUSED_CASES", "32"))  # seeds 0 .. FUSED_CASES - 1
+
+
+def _random_decode_batch(rng):
+    """One decode row per sequence at its last position, each writing a block of its own; half
+    of the cases share a leading run of whole blocks (shared-prefix tiles beside the rows)."""
+    heads = int(rng.choice([1, 2, 4, 8, 32]))
+    dim = int(rng.choice([32, 64, 128]))
+    if heads * dim > 2048:
+        heads = 2048 // dim
+    block = int(rng.choice([1, 4, 5, 16, 32]))
+    shared = rng.random() < 0.5
+    seqs = int(rng.integers(18, 41)) if shared else int(rng.integers(1, 25))
+    prefix_blocks = int(rng.integers(512, 1100)) // block if shared else 0
+    tables, contexts, next_block = [], [], prefix_blocks
+    for _ in range(seqs):
+        ctx = prefix_blocks * block + int(rng.integers(1, 300)) if shared else int(rng.integers(1, 900))
+        own = -(-ctx // block) - prefix_blocks  # the last visible block is always a private one
+        tables.append(list(range(prefix_blocks)) + list(range(next_block, next_block + own)))
+        next_block += own
+        contexts.append(ctx)
+    pool = next_block + 2
+    perm = rng.permutation(pool)
+    tables = [perm[np.asarray(t, dtype=np.int64)].astype(np.int32) for t in tables]
+    kv = torch.bfloat16 if rng.random() < 0.4 else torch.float32
+    partition = int(rng.choice([0, 0, 64, 256]))
+    return heads, dim, block, kv, partition, tables, np.asarray(contexts), pool
+
+
+@pytest.mark.parametrize("seed", range(FUSED_CASES))
+def test_random_decode_batch_with_the_fused_append_and_caller_rows(device, seed) -> None:
+    """pkv_paged_attention_append over a planned random decode batch whose rows reach the caller's
+    rows through a random caller_rows permutation: the pools equal pkv_append's bit for bit, and
+    every output row is within 1e-5 of the oracle over the appended pools (bfloat16 pools: the
+    new rows rounded to nearest even, as the append stores them)."""
+    rng = np.random.default_rng(9000 + seed)
+    heads, dim, block, kv, partition, tables, contexts, pool = _random_decode_batch(rng)
+    seqs = len(tables)
+    print("random fused decode", seed, heads, dim, block, kv, partition, seqs, flush=True)
+    positions = contexts - 1
+    seq_of = np.arange(seqs)
+    slots = np.asarray([int(t[p // block]) * block + p % block for t, p in zip(tables, positions)], np.int64)
+    kc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    vc = rng.standard_normal((pool, block, heads, dim)).astype(np.float32)
+    q, new_k, new_v = (rng.standard_normal((seqs, heads, dim)).astype(np.float32) for _ in range(3))
+    if kv == torch.bfloat16:
+        kc, vc = bf16_round(kc), bf16_round(vc)
+    kh, vh = kc.copy(), vc.copy()  # the pools after the append, as the oracle sees them
+    kh.reshape(-1, heads, dim)[slots] = bf16_round(new_k) if kv == torch.bfloat16 else new_k
+    vh.reshape(-1, heads, dim)[slots] = bf16_round(new_v) if kv == torch.bfloat16 else new_v
+    scale = dim**-0.5
+    want = np.zeros_like(q)
+    for s in range(seqs):
+        want[s] = paged_attention(q[s : s + 1], positions[s : s + 1], kh, vh, tables[s], int(contexts[s]), scale)[0]
+    host = ops.plan_batch(seq_of, dim, heads, tables, contexts, block, partition_size=partition,
+                          query_positions=positions, kv_dtype=kv)  # fmt: skip
+    width = max(len(t) for t in tables)
+    padded = np.full((seqs, width), -3, dtype=np.int32)
+    for i, t in enumerate(tables):
+        padded[i, : len(t)] = t
+    order = rng.permutation(seqs)  # planner row t reads and writes caller row order[t]
+
+    def caller(a: np.ndarray) -> np.ndarray:
+        out = np.empty_like(a)
+        out[order] = a
+        return out
+
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+    k_ref, v_ref = to(kc).to(kv), to(vc).to(kv)
+    ops.append_kv(k_ref, v_ref, to(new_k), to(new_v), to(slots))
+    k_fus, v_fus = to(kc).to(kv), to(vc).to(kv)
+    got = ops.paged_attention_ragged(
+        to(caller(q)), to(positions.astype(np.int32)), to(seq_of.astype(np.int32)), k_fus, v_fus, to(padded),
+        to(contexts.astype(np.int32)), scale, max_context_len=int(contexts.max()),
+        plan=ops.upload_batch_plan(host, device), append=(to(caller(new_k)), to(caller(new_v)), to(caller(slots))),
+        caller_rows=to(order.astype(np.int32)),
+    )  # fmt: skip
+    assert torch.equal(k_fus, k_ref) and torch.equal(v_fus, v_ref), seed
+    err = float(np.max(np.abs(got.cpu().numpy()[order] - want)))
+    assert err < FP32_TOL, (seed, err, host.tiles.shape[0], host.partition_size)
