@@ -597,3 +597,98 @@ def test_decode_rows_reading_a_block_another_row_writes(device, case) -> None:
         want = paged_attention(q[i : i + 1], np.asarray(entry.positions), keys, values, np.asarray(entry.block_table),
                                entry.context_len, 64**-0.5)  # fmt: skip
         assert float(np.max(np.abs(out[i] - want[0]))) < 1e-5, (case, entry.seq_id)
+
+
+def test_a_decode_loop_with_forks_and_copies_matches_the_oracle_step_by_step(device) -> None:
+    """Thirty steps of a serving loop through ModelRunner.attend, driven by the KV-cache manager:
+    two parents prefill their prompts, children fork from them at different steps (a first write
+    into a shared block copies it through the runner's copy_block), some finish and free their
+    blocks, and every step's batch is rebuilt from the sequences' block-table lists in a shuffled
+    order (tuple(seq.block_table), as the reference's scheduler builds its entries,
+    scheduler.py:423), so rows come and go in the arena and sharers of one prefix are interleaved
+    with the other family's. After every step the pools equal a NumPy shadow that applies the same
+    copies and appends in order, bit for bit, and every output row is within 1e-5 of the
+    oracle's paged attention over the shadow."""
+    from oracle.attention import paged_attention
+    from oracle.runner import append as oracle_append
+    from oracle.runner import copy_block as oracle_copy
+    from oracle.runner import slots_for
+
+    rng = np.random.default_rng(23)
+    heads, dim, block, num_blocks = 4, 64, 16, 640
+    config = ModelConfig(vocab_size=64, d_model=heads * dim, n_layers=1, n_heads=heads, d_ff=32, max_seq_len=2048)
+    model = LanguageModel(config, random_weights(config, seed=23))
+    runner = ModelRunner(model, num_blocks=num_blocks, block_size=block, device=device)
+    keys = rng.standard_normal((1, num_blocks, block, heads, dim)).astype(np.float32)
+    values = rng.standard_normal((1, num_blocks, block, heads, dim)).astype(np.float32)
+    runner.key_cache.copy_(torch.from_numpy(keys))
+    runner.value_cache.copy_(torch.from_numpy(values))
+    copies: list[tuple[int, int]] = []
+
+    class Store:  # the runner's copy_block, recorded for the shadow
+        def copy_block(self, source: int, destination: int) -> None:
+            runner.copy_block(source, destination)
+            copies.append((source, destination))
+
+    blocks = BlockManager(num_blocks=num_blocks, block_size=block, store=Store())
+    cache = KVCacheManager(blocks, PrefixCache(blocks, enabled=False))
+    scale = dim**-0.5
+    worst, fused_steps, tiled = 0.0, 0, 0
+
+    def run(steps):  # one attend call over [(sequence, new token count)], checked against the shadow
+        nonlocal worst, fused_steps, tiled
+        entries = []
+        for seq, n in steps:
+            start = seq.num_computed_tokens
+            cache.reserve(seq, start + n)
+            entries.append(BatchEntry(seq.seq_id, tuple(seq.token_ids[start : start + n]),
+                                      tuple(range(start, start + n)), tuple(seq.block_table), n - 1))  # fmt: skip
+        batch = ExecutionBatch(tuple(entries))
+        total = batch.num_tokens
+        q, k, v = (rng.standard_normal((total, heads, dim)).astype(np.float32) for _ in range(3))
+        out = runner.attend(batch, *(torch.from_numpy(a).to(device) for a in (q, k, v))).cpu().numpy()
+        for source, destination in copies:
+            oracle_copy(keys, values, source, destination)
+        copies.clear()
+        slots = [s for e in entries for s in slots_for(e.seq_id, e.positions, e.block_table, block)]
+        oracle_append(keys[0], values[0], slots, k, v)
+        assert np.array_equal(runner.key_cache.cpu().numpy(), keys)
+        assert np.array_equal(runner.value_cache.cpu().numpy(), values)
+        offset = 0
+        for entry in entries:
+            n = len(entry.token_ids)
+            want = paged_attention(q[offset : offset + n], np.asarray(entry.positions), keys[0], values[0],
+                                   np.asarray(entry.block_table), entry.context_len, scale)  # fmt: skip
+            worst = max(worst, float(np.max(np.abs(out[offset : offset + n] - want))))
+            offset += n
+        fused_steps += runner.last_append_fused
+        tiled += runner.last_plan is not None and runner.last_plan.tiles.shape[0] > 0
+        for seq, n in steps:
+            seq.num_computed_tokens += n
+
+    parents = []
+    for name, length in (("pa", 600), ("pb", 530)):  # 37 blocks + 8 and 33 blocks + 2: partial last blocks
+        parent = Sequence.from_request(Request(name, tuple(int(t) for t in rng.integers(0, 64, length))), 0)
+        parents.append(parent)
+    run([(p, p.num_tokens) for p in parents])
+    live, made = list(parents), 0
+    for step in range(30):
+        if step in (0, 4, 11):  # new children of both parents
+            for parent in parents:
+                for _ in range(15 if step == 0 else 4):
+                    child = Sequence.from_request(Request(f"c{made}", tuple(parent.token_ids)), 0)
+                    made += 1
+                    cache.fork(parent, child)
+                    live.append(child)
+        if step in (8, 19):  # a few children finish
+            for seq in [s for s in live if s not in parents][:5]:
+                cache.free(seq)
+                live.remove(seq)
+        for seq in live:
+            seq.token_ids.append(int(rng.integers(0, 64)))
+        order = rng.permutation(len(live))
+        run([(live[i], 1) for i in order])
+        cache.check_invariants()
+    assert worst < 1e-5
+    assert fused_steps >= 25, "decode steps append inside the attention call"
+    assert tiled >= 25, "interleaved sharers regrouped and read through prefix tiles"
