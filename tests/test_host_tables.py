@@ -146,6 +146,41 @@ def test_random_table_histories_read_back(data) -> None:
         step(arena, entries)
 
 
+@settings(max_examples=60, deadline=None)
+@given(st.data())
+def test_long_tables_of_large_ids_in_any_form_read_back(data) -> None:
+    """Tables longer than one 16-id run, of ids past the small-int cache, handed over each step as
+    a tuple of the list's own int objects, a tuple of new int objects of the same values, or a
+    list: the identity runs, the value comparison and the list path all read back exactly."""
+    arena = BlockTableArena("cpu", rows=data.draw(st.integers(1, 3)), width=data.draw(st.integers(1, 8)))
+    tables: dict[str, list[int]] = {}
+    next_block = 1000
+    for _ in range(data.draw(st.integers(1, 15))):
+        names = data.draw(st.lists(st.sampled_from("abcd"), min_size=1, max_size=4, unique=True))
+        entries = []
+        for name in names:
+            table = tables.setdefault(name, [])
+            action = data.draw(st.sampled_from(["grow", "cow", "keep", "keep", "reset"]))
+            if action == "grow" or not table:
+                for _ in range(data.draw(st.integers(1, 24))):
+                    table.append(next_block)
+                    next_block += 1
+            elif action == "cow":
+                table[data.draw(st.integers(0, len(table) - 1))] = next_block
+                next_block += 1
+            elif action == "reset":
+                table[:] = [next_block]
+                next_block += 1
+            form = data.draw(st.sampled_from(["same", "fresh", "list"]))
+            if form == "same":
+                entries.append(Entry(name, tuple(table)))
+            elif form == "fresh":
+                entries.append(Entry(name, tuple(int(str(b)) for b in table)))
+            else:
+                entries.append(Entry(name, list(table)))
+        step(arena, entries)
+
+
 def test_same_tuple_again_sends_nothing_and_an_equal_length_change_travels() -> None:
     """The walk compares a row's previous tuple with the new one before converting ids: an
     equal tuple (the same object or an equal one) sends nothing, an equal-length tuple with one
