@@ -692,3 +692,21 @@ def test_a_decode_loop_with_forks_and_copies_matches_the_oracle_step_by_step(dev
     assert worst < 1e-5
     assert fused_steps >= 25, "decode steps append inside the attention call"
     assert tiled >= 25, "interleaved sharers regrouped and read through prefix tiles"
+
+
+def test_attend_on_an_empty_batch_returns_no_rows(device) -> None:
+    """An empty ExecutionBatch: attend returns a [0, heads, head_dim] float32 tensor on the
+    device, launches nothing and leaves a queued copy-on-write copy queued; reading the pools
+    (key_cache) lands it."""
+    config = ModelConfig(vocab_size=16, d_model=64, n_layers=1, n_heads=2, d_ff=32, max_seq_len=64)
+    model = LanguageModel(config, random_weights(config, seed=3))
+    runner = ModelRunner(model, num_blocks=4, block_size=4, device=device)
+    runner.key_cache.copy_(torch.randn_like(runner.key_cache))
+    want = runner.key_cache.clone()
+    want[:, 1] = want[:, 0]
+    runner.copy_block(0, 1)
+    none = torch.zeros((0, 2, 32), device=device)
+    out = runner.attend(ExecutionBatch(()), none, none, none)
+    assert out.shape == (0, 2, 32) and out.dtype == torch.float32 and out.device == none.device
+    assert runner.pending_copies == [(0, 1)]
+    assert torch.equal(runner.key_cache, want) and runner.pending_copies == []
